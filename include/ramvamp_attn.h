@@ -1,0 +1,237 @@
+/*
+ * ramvamp_attn.h — C ABI of the MI355X (gfx950) GQA attention hot path.
+ *
+ * This is the drop-in boundary for ramvamp's per-layer attention. Every
+ * entry point below replaces one reference interface, cited as
+ * `path:line` into the ramvamp tree (crates/core/src/...). The library is
+ * `libramvamp_attn.so`, built with hipcc for gfx950 only.
+ *
+ * Conventions
+ *  - Every call returns an `int32_t` status: RV_OK (0) or one of the codes
+ *    below. When `err` is non-NULL it receives the status plus the payload
+ *    fields of the reference error variant (field meaning per code below).
+ *  - Validation runs on the host, in the reference's precedence, before any
+ *    device work is queued, so `out` is untouched on every error.
+ *  - Tensor pointers (q, k, v, out, norm weights) are device pointers on the
+ *    cache's device unless `flags` carries RV_HOST_PTRS, in which case they
+ *    are host pointers and the call copies in, computes and copies out
+ *    before it returns.
+ *  - With device pointers the call is asynchronous on the cache's stream
+ *    (rv_kv_set_stream; default: the null stream). Calls on one cache are
+ *    serialised by that stream and share its device workspace: one cache
+ *    per host thread, never two streams on one cache at once.
+ *  - Sizes and indices are `size_t`, element counts (not bytes) unless named
+ *    `*_bytes`.
+ */
+#ifndef RAMVAMP_ATTN_H
+#define RAMVAMP_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RV_ABI_VERSION 1u
+
+/* ---- status codes ------------------------------------------------------
+ * KvError variants (crates/core/src/kv/mod.rs:39-123). Payload: a..d.  */
+#define RV_OK 0
+#define RV_KV_INVALID_DIMS 1          /* a n_layers, b n_kv_heads, c head_dim, d capacity, what reason */
+#define RV_KV_LAYER_OUT_OF_RANGE 2    /* a layer, b n_layers */
+#define RV_KV_ROW_LEN_MISMATCH 3      /* what "k"|"v", a got, b expected */
+#define RV_KV_CAPACITY_EXCEEDED 4     /* a layer, b capacity */
+#define RV_KV_POSITION_OUT_OF_RANGE 5 /* a layer, b pos, c len */
+#define RV_KV_RAGGED_LAYERS 6         /* a shortest, b longest */
+#define RV_KV_TRUNCATE_BEYOND_LENGTH 7 /* a requested, b len */
+/* AttentionError variants (crates/core/src/kernels/attention.rs:218-311). A
+ * KvError raised inside attention keeps its KV code (the reference wraps it
+ * as AttentionError::Kv, which is transparent). */
+#define RV_ATTN_Q_LEN_INDIVISIBLE 16  /* a q_len, b head_dim */
+#define RV_ATTN_GQA_GROUP_MISMATCH 17 /* a n_q_heads, b n_kv_heads */
+#define RV_ATTN_OUT_LEN_MISMATCH 18   /* a out_len, b expected */
+#define RV_ATTN_EMPTY_LAYER 19        /* a layer */
+#define RV_ATTN_KV_HEAD_RANGE 20      /* a start, b end, c n_kv_heads */
+#define RV_ATTN_SCRATCH_TOO_SHORT 21  /* a len, b need */
+/* Primitive errors of the fused prologue (kernels/primitives/error.rs). */
+#define RV_PRIM_INVALID_HEAD_DIM 24   /* a head_dim (rope needs it even, nonzero) */
+#define RV_PRIM_LENGTH_MISMATCH 25    /* what, a left, b right */
+/* Errors of this library with no reference counterpart. */
+#define RV_ERR_NULL_ARG 32            /* what argument */
+#define RV_ERR_UNSUPPORTED 33         /* what, a value */
+#define RV_ERR_HIP 34                 /* what call, a hipError_t */
+#define RV_ERR_BAD_ELEM 35            /* a elem */
+
+typedef struct rv_error {
+  int32_t code;
+  uint64_t a, b, c, d;
+  const char* what; /* static string, never freed */
+} rv_error;
+
+/* Element type of the cache planes. RV_ELEM_F16 is the reference's own
+ * format (f16 bits, round-to-nearest-even on append, kv/mod.rs:336-368);
+ * RV_ELEM_F32 keeps the identical [layer][capacity][kv_dim] indexing with
+ * 4-byte elements. */
+typedef enum rv_elem { RV_ELEM_F16 = 1, RV_ELEM_F32 = 2 } rv_elem;
+
+/* flags */
+#define RV_HOST_PTRS 0x1u   /* tensor pointers are host memory */
+#define RV_SYNC 0x2u        /* synchronise the cache's stream before returning */
+/* Prefill arithmetic (rv_attention_at_rows / rv_prefill_chunk only; decode is
+ * always fp32 arithmetic). Default (0) = RV_PREFILL_EXACT. */
+#define RV_PREFILL_EXACT 0x00u /* split-f16 MFMA, fp32-equivalent products */
+#define RV_PREFILL_F16 0x10u   /* single-pass f16 MFMA inputs, fp32 accumulate */
+#define RV_PREFILL_BF16 0x20u  /* single-pass bf16 MFMA inputs, fp32 accumulate */
+#define RV_PREFILL_MODE_MASK 0x30u
+
+/* Opaque device-resident KV cache: K and V planes on one GPU, per-layer
+ * cursors on the host, one HIP stream, the decode/prefill workspace. */
+typedef struct rv_kv rv_kv;
+
+uint32_t rv_abi_version(void);
+/* Static, human-readable name of a status code ("RV_OK", ...). */
+const char* rv_status_name(int32_t code);
+
+/* attention.rs:337-353 `scratch_len`: the f32 scratch a reference CPU call
+ * needs, `(n_q_heads / n_kv_heads) * max_positions + 2 * head_dim`,
+ * saturating, division-safe. The device path keeps its own workspace; the
+ * `_in` entry points below still take the caller's scratch length and
+ * report RV_ATTN_SCRATCH_TOO_SHORT exactly where the reference does. */
+size_t rv_scratch_len(size_t n_q_heads, size_t n_kv_heads, size_t head_dim,
+                      size_t max_positions);
+
+/* ---- KV cache (crates/core/src/kv/mod.rs) ---------------------------- */
+
+/* kv/mod.rs:237-259 `KvCache::projected_bytes`, for either element type
+ * (2 planes * n_layers * capacity * n_kv_heads * head_dim * elem size). */
+int32_t rv_kv_projected_bytes(size_t n_layers, size_t n_kv_heads, size_t head_dim,
+                              size_t capacity, rv_elem elem, uint64_t* bytes,
+                              rv_error* err);
+
+/* kv/mod.rs:163-181 `KvCache::new`: zeroed planes on `device`, every cursor 0. */
+int32_t rv_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t capacity,
+                  rv_elem elem, int device, rv_kv** out, rv_error* err);
+void rv_kv_free(rv_kv* kv);
+/* Stream every later call on this cache is queued on (a hipStream_t). */
+int32_t rv_kv_set_stream(rv_kv* kv, void* hip_stream, rv_error* err);
+int32_t rv_kv_synchronize(rv_kv* kv, rv_error* err);
+
+/* kv/mod.rs:262-287 accessors. */
+size_t rv_kv_n_layers(const rv_kv* kv);
+size_t rv_kv_n_kv_heads(const rv_kv* kv);
+size_t rv_kv_head_dim(const rv_kv* kv);
+size_t rv_kv_capacity(const rv_kv* kv);
+size_t rv_kv_kv_dim(const rv_kv* kv);
+int32_t rv_kv_elem(const rv_kv* kv);
+/* kv/mod.rs:291 `len`, :297 `is_empty`, :312 `seq_len`. */
+int32_t rv_kv_len(const rv_kv* kv, size_t layer, size_t* len, rv_error* err);
+int rv_kv_is_empty(const rv_kv* kv);
+int32_t rv_kv_seq_len(const rv_kv* kv, size_t* len, rv_error* err);
+
+/* kv/mod.rs:336-368 `append`: one row of `n_kv_heads * head_dim` f32 for
+ * each of K and V, converted to the plane's element type (f16: RNE). */
+int32_t rv_kv_append(rv_kv* kv, size_t layer, const float* k, size_t k_len,
+                     const float* v, size_t v_len, uint32_t flags, rv_error* err);
+/* `rows` appends in one call: the loop at model/prefill.rs:2081-2087.
+ * k and v hold `rows * kv_dim` f32. All-or-nothing: capacity is checked for
+ * the whole chunk first (RV_KV_CAPACITY_EXCEEDED reports the layer). */
+int32_t rv_kv_append_rows(rv_kv* kv, size_t layer, const float* k, const float* v,
+                          size_t rows, size_t row_len, uint32_t flags, rv_error* err);
+/* kv/mod.rs:383-385 `clear` and :410-420 `truncate`. */
+void rv_kv_clear(rv_kv* kv);
+int32_t rv_kv_truncate(rv_kv* kv, size_t new_len, rv_error* err);
+/* kv/mod.rs:449-460 `k_layer` / `v_layer`: the device address of a layer's
+ * plane and the element count the view covers (`len(layer) * kv_dim`). */
+int32_t rv_kv_k_layer(const rv_kv* kv, size_t layer, const void** dev, size_t* n_elems,
+                      rv_error* err);
+int32_t rv_kv_v_layer(const rv_kv* kv, size_t layer, const void** dev, size_t* n_elems,
+                      rv_error* err);
+/* kv/mod.rs:428-441 `k_row` / `v_row`, copied to host memory: `dst` gets
+ * kv_dim elements of the plane's type (u16 f16 bits or f32). */
+int32_t rv_kv_read_row(const rv_kv* kv, int plane_v, size_t layer, size_t pos, void* dst,
+                       rv_error* err);
+
+/* ---- attention (crates/core/src/kernels/attention.rs) ---------------- */
+
+/* attention.rs:426 `decode_attention`: q is the full post-RoPE query
+ * (`n_q_heads * head_dim` f32), out the same length, every position the
+ * layer holds. Precedence (attention.rs:926-989): q length, GQA grouping,
+ * layer, positions, kv range, out length. */
+int32_t rv_decode_attention(const rv_kv* kv, const float* q, size_t q_len, size_t layer,
+                            float scale, float* out, size_t out_len, uint32_t flags,
+                            rv_error* err);
+/* attention.rs:484 `decode_attention_in`: also checks the caller's scratch
+ * length against rv_scratch_len, after `out`. */
+int32_t rv_decode_attention_in(const rv_kv* kv, const float* q, size_t q_len, size_t layer,
+                               float scale, size_t scratch_len, float* out, size_t out_len,
+                               uint32_t flags, rv_error* err);
+/* attention.rs:586 `decode_attention_kv_range_in`: kv heads [kv_lo, kv_hi);
+ * q is the full vector, out the range's own `(kv_hi-kv_lo)*group*head_dim`
+ * buffer from index 0. An empty in-range request is a validated no-op. */
+int32_t rv_decode_attention_kv_range_in(const rv_kv* kv, const float* q, size_t q_len,
+                                        size_t layer, float scale, size_t kv_lo, size_t kv_hi,
+                                        size_t scratch_len, float* out, size_t out_len,
+                                        uint32_t flags, rv_error* err);
+/* attention.rs:666 `attention_at`: positions 0..positions only (the causal
+ * limit is a length). positions == 0 -> RV_ATTN_EMPTY_LAYER; positions
+ * past len(layer) -> RV_KV_POSITION_OUT_OF_RANGE. */
+int32_t rv_attention_at(const rv_kv* kv, const float* q, size_t q_len, size_t layer,
+                        size_t positions, float scale, float* out, size_t out_len,
+                        uint32_t flags, rv_error* err);
+/* attention.rs:732 `attention_at_in`. */
+int32_t rv_attention_at_in(const rv_kv* kv, const float* q, size_t q_len, size_t layer,
+                           size_t positions, float scale, size_t scratch_len, float* out,
+                           size_t out_len, uint32_t flags, rv_error* err);
+/* attention.rs:807 `attention_at_kv_range_in`. */
+int32_t rv_attention_at_kv_range_in(const rv_kv* kv, const float* q, size_t q_len,
+                                    size_t layer, size_t positions, float scale, size_t kv_lo,
+                                    size_t kv_hi, size_t scratch_len, float* out,
+                                    size_t out_len, uint32_t flags, rv_error* err);
+
+/* model/prefill.rs:1322-1408 `scatter_attention`: `rows` query rows of
+ * q_dim f32 each; row r attends positions 0..start+r+1 (prefill.rs:1394).
+ * One call replaces the pool fan-out. Each row is validated as the
+ * reference's per-row attention_at_in would be, in row order, before any
+ * launch; the first failing row's error is returned and out is untouched
+ * (the reference may leave earlier rows written, prefill.rs:1310-1320).
+ * flags selects the MFMA arithmetic (RV_PREFILL_*). */
+int32_t rv_attention_at_rows(const rv_kv* kv, const float* q_rows, size_t rows, size_t q_dim,
+                             size_t layer, size_t start, float scale, float* out,
+                             uint32_t flags, rv_error* err);
+
+/* ---- fused layer steps ------------------------------------------------ */
+
+/* model/forward.rs:2622-2633, one decode token of one layer: per-head
+ * RMSNorm of q (n_q_heads heads) and k (n_kv_heads heads) with the shared
+ * [head_dim] weights and `eps` (primitives/norm.rs:18-90), NeoX RoPE of both
+ * at `position` with base `theta` (primitives/rope.rs:31-105), KvCache::append
+ * of (k, v), then decode attention over every position of the layer.
+ * q/k/v are pre-norm; q_len = n_q_heads*head_dim, k_len = v_len = kv_dim. */
+int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, const float* k,
+                       size_t k_len, const float* v, size_t v_len, const float* q_norm_w,
+                       const float* k_norm_w, float eps, float theta, size_t position,
+                       float scale, float* out, size_t out_len, uint32_t flags,
+                       rv_error* err);
+
+/* model/prefill.rs:2055-2111 steps (d)-(f) for one layer of a chunk: the
+ * same prologue per row at absolute position start+r, the whole chunk's
+ * K/V appended, then causal attention where row r sees start+r+1 positions.
+ * `start` must equal len(layer) (the chunk continues the cache). */
+int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const float* k_rows,
+                         const float* v_rows, size_t rows, size_t q_dim, const float* q_norm_w,
+                         const float* k_norm_w, float eps, float theta, size_t start,
+                         float scale, float* out, uint32_t flags, rv_error* err);
+
+/* Tuning knobs of the decode/prefill launches (0 = built-in heuristic).
+ * Exposed for benchmarking sweeps; results never depend on them beyond
+ * floating-point reassociation within the stated tolerance. */
+#define RV_TUNE_DECODE_SPLIT_LEN 1 /* positions per decode split (multiple of 16) */
+#define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill tile */
+int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAMVAMP_ATTN_H */
