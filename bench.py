@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Headline ("config 2"): one step = 48 sequential
+decode-attention calls, one per layer, each over 4,096 cached positions of a
+fp32 KV cache (GQA 32/4, head_dim 128), through the C ABI with device
+pointers; inputs are resident in HBM before timing starts. `value` is the
+unique K+V+q+out bytes of all 48 calls per second of wall time (GB/s); the
+JSON line also carries µs per layer, the dominant kernel's roofline and the
+CPU baseline, plus the prefill TFLOP/s of configs 3 and 4 and the long
+context split-K decode of config 5 under "extra".
+
+Prints exactly one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(positions: int, elem_bytes: int) -> int:
+    """Algorithmic bytes of one decode call: K and V head slices read once,
+    q read, out written (SURVEY 8d convention, benches/kernels.rs:245-270)."""
+    return 2 * positions * 512 * elem_bytes + 2 * 4096 * 4
+
+
+def prefill_flops(rows: int, start: int) -> int:
+    """4 * d * causal pairs * heads, pairs = rows*start + rows*(rows+1)/2."""
+    pairs = rows * start + rows * (rows + 1) // 2
+    return 4 * 128 * pairs * 32
+
+
+def time_region(torch, fn, iters: int):
+    """(wall seconds, event seconds) of `iters` calls on the current stream."""
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(iters):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, e0.elapsed_time(e1) / 1e3
+
+
+def bench_config2(torch, rv, synth, steps, warmup, keep_host):
+    c = synth.CONFIGS[2]
+    log(f"config 2: building 48-layer fp32 cache at ctx 4096 ...")
+    kv = rv.KvCache(48, 4, 128, 4096, "f32")
+    host_layers = []
+    for layer in range(48):
+        K, V = synth.cached_kv(2, layer, 4096)
+        kv.append_rows(layer, K, V)
+        if keep_host:
+            host_layers.append((K, V))
+    q = torch.stack([torch.from_numpy(synth.normal(synth.seed(2, synth.T_Q, l), synth.Q_DIM)) for l in range(48)]).cuda()
+    out = torch.zeros_like(q)
+    qs = [q[l] for l in range(48)]
+    outs = [out[l] for l in range(48)]
+    scale = float(synth.SCALE)
+
+    def step():
+        for l in range(48):
+            rv.decode_attention(qs[l], kv, l, scale, None, outs[l])
+
+    for _ in range(warmup):
+        step()
+    wall, ev = time_region(torch, step, steps)
+    per_step = wall / steps
+    launches = 48 * steps
+    avg_launch = ev / launches
+    byts = decode_bytes(4096, 4)
+    return {
+        "kv": kv, "host_layers": host_layers, "q": q, "out": out,
+        "ms_per_step": per_step * 1e3,
+        "value_gbs": 48 * byts / per_step / 1e9,
+        "us_per_layer_wall": per_step / 48 * 1e6,
+        "us_per_launch_event": avg_launch * 1e6,
+        "achieved_gbs": byts / avg_launch / 1e9,
+        "bytes_per_launch": byts,
+    }
+
+
+def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
+    c = synth.CONFIGS[cfg]
+    start, rows = c.context, c.rows
+    q, k, v = synth.new_rows(cfg, rows)
+    wq, wk = synth.norm_weight(cfg, synth.T_QN), synth.norm_weight(cfg, synth.T_KN)
+    dq, dk, dv = (torch.from_numpy(a).cuda() for a in (q, k, v))
+    dwq, dwk = torch.from_numpy(wq).cuda(), torch.from_numpy(wk).cuda()
+    out = torch.zeros_like(dq)
+    kv = rv.KvCache(1, 4, 128, start + rows, "f32")
+    if start:
+        K, V = synth.cached_kv(cfg, 0, start)
+        kv.append_rows(0, K, V)
+
+    def once():
+        kv.truncate(start)
+        rv.prefill_chunk(kv, 0, dq, dk, dv, dwq, dwk, synth.EPS, synth.THETA, start, synth.SCALE, out, mode=mode)
+
+    for _ in range(3):
+        once()
+    wall, ev = time_region(torch, once, iters)
+    flops = prefill_flops(rows, start)
+    return {"mode": mode, "us_per_call_wall": wall / iters * 1e6, "us_per_call_event": ev / iters * 1e6,
+            "tflops_event": flops / (ev / iters) / 1e12, "flops": flops}
+
+
+def bench_config5(torch, rv, synth, iters=50, n_caches=5):
+    """ctx 32,768 f16 KV, rotating 5 distinct caches (335 MB) past the 256 MB MALL."""
+    n = 32768
+    caches = []
+    for i in range(n_caches):
+        K, V = synth.cached_kv(5, i, n)
+        kv = rv.KvCache(1, 4, 128, n, "f16")
+        kv.append_rows(0, K, V)
+        caches.append(kv)
+    q = torch.from_numpy(synth.rope_f64(synth.normal(synth.seed(5, synth.T_Q), synth.Q_DIM), 128, n,
+                                        synth.THETA)).cuda()
+    out = torch.zeros_like(q)
+    scale = float(synth.SCALE)
+
+    def once():
+        for kv in caches:
+            rv.decode_attention(q, kv, 0, scale, None, out)
+
+    for _ in range(3):
+        once()
+    wall, ev = time_region(torch, once, iters)
+    per = ev / (iters * n_caches)
+    byts = decode_bytes(n, 2)
+    return {"us_per_call_event": per * 1e6, "achieved_gbs": byts / per / 1e9, "bytes_per_call": byts,
+            "hbm_frac": byts / per / 1e9 / HBM_PEAK_GBS}
+
+
+def cpu_baseline(synth, host_layers, budget_s=12.0):
+    """The oracle (C restatement of ramvamp's AVX2+F16C decode path with its
+    kv-head fan-out over min(4, cores) threads, forward.rs:1914-2063) on the
+    same config-2 inputs, timed on this host for a bounded sample of layers."""
+    import oracle
+
+    threads = max(1, min(4, os.cpu_count() or 1))
+    n_layers = len(host_layers)
+    caches = []
+    for (K, V) in host_layers[:8]:
+        ref = oracle.KvCache(1, 4, 128, 4096, oracle.RV_ELEM_F32)
+        ref.append_rows(0, K, V)
+        caches.append(ref)
+    qs = [synth.normal(synth.seed(2, synth.T_Q, l), synth.Q_DIM) for l in range(len(caches))]
+    times = []
+    t_end = time.perf_counter() + budget_s
+    calls = 0
+    while time.perf_counter() < t_end or calls < len(caches):
+        i = calls % len(caches)
+        t0 = time.perf_counter()
+        caches[i].pool_decode_attention(qs[i], 0, float(synth.SCALE), threads)
+        times.append(time.perf_counter() - t0)
+        calls += 1
+    per_layer = float(np.median(times))
+    return {
+        "value": decode_bytes(4096, 4) / per_layer / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "us_per_layer": per_layer * 1e6,
+        "sample": f"{calls} decode calls (ctx 4096, fp32 KV) over {len(caches)} of the {n_layers} config-2 layers, "
+                  f"median per call; oracle AVX2+F16C body, kv-head fan-out over {threads} threads",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the attention of one "
+              "layer shards by kv head, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ramvamp_amd as rv
+    from ramvamp_amd import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    r2 = bench_config2(torch, rv, synth, args.steps, args.warmup, keep_host=not args.no_cpu)
+    log(f"config 2: {r2['us_per_layer_wall']:.2f} us/layer wall, {r2['us_per_launch_event']:.2f} us/launch event, "
+        f"{r2['value_gbs']:.0f} GB/s")
+    extra = {}
+    if not args.no_extra:
+        for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
+            r = bench_prefill(torch, rv, synth, cfg, mode)
+            extra[f"config{cfg}_prefill_{mode}"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
+            log(f"config {cfg} {mode}: {r['us_per_call_event']:.1f} us, {r['tflops_event']:.1f} TFLOP/s")
+        r5 = bench_config5(torch, rv, synth)
+        extra["config5_decode_f16_ctx32768"] = {k: round(v, 4) for k, v in r5.items()}
+        log(f"config 5: {r5['us_per_call_event']:.2f} us, {r5['achieved_gbs']:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(synth, r2["host_layers"])
+        cpu = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
+    line = {
+        "metric": "decode attn µs/layer + HBM GB/s at ctx 4096; prefill attn TFLOP/s (512 tok)",
+        "value": round(r2["value_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r2["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) K/V/q, ramvamp_amd/synth.py)",
+        "config": {"workload": "config 2: 48 sequential decode-attention layers, ctx 4096, fp32 KV, GQA 32/4, d 128",
+                   "layers": 48, "context": 4096, "n_q_heads": 32, "n_kv_heads": 4, "head_dim": 128,
+                   "kv_elem": "f32", "parallelism": "single GPU"},
+        "us_per_layer": round(r2["us_per_layer_wall"], 3),
+        "roofline": {"bound": "hbm", "achieved": round(r2["achieved_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_split_kernel<float, 8, *>",
+                     "us_per_launch": round(r2["us_per_launch_event"], 3),
+                     "bytes_per_launch": r2["bytes_per_launch"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

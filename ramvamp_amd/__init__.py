@@ -1,0 +1,26 @@
+"""ramvamp_amd — MI355X-native (gfx950) GQA attention hot path of ramvamp.
+
+The product is ``libramvamp_attn.so`` (hand-written HIP kernels behind the C
+ABI in include/ramvamp_attn.h). This package builds it (``build``), loads it
+(``_lib``), mirrors the reference's Rust attention API over it
+(``attention``) and makes seeded synthetic inputs (``synth``).
+"""
+from .attention import (  # noqa: F401
+    AttentionError,
+    AttentionScratch,
+    DeviceError,
+    KvCache,
+    KvError,
+    PrimitiveError,
+    RamvampError,
+    attention_at,
+    attention_at_in,
+    attention_at_kv_range_in,
+    attention_at_rows,
+    decode_attention,
+    decode_attention_in,
+    decode_attention_kv_range_in,
+    decode_step,
+    prefill_chunk,
+    scratch_len,
+)

@@ -1,0 +1,95 @@
+"""Loads libramvamp_attn.so (the gfx950 HIP library) and declares its C ABI.
+
+The library is built in-tree by ``ramvamp_amd.build`` (hipcc --offload-arch=gfx950).
+There is no fallback: if the library is missing, importing the compute API
+raises, so nothing can silently run on the CPU instead.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libramvamp_attn.so")
+
+RV_HOST_PTRS = 0x1
+RV_SYNC = 0x2
+RV_PREFILL_EXACT = 0x00
+RV_PREFILL_F16 = 0x10
+RV_PREFILL_BF16 = 0x20
+RV_ELEM_F16 = 1
+RV_ELEM_F32 = 2
+RV_TUNE_DECODE_SPLIT_LEN = 1
+RV_TUNE_PREFILL_KV_SPLIT = 2
+
+
+class RvError(ctypes.Structure):
+    _fields_ = [("code", c_int32), ("a", c_uint64), ("b", c_uint64), ("c", c_uint64), ("d", c_uint64),
+                ("what", c_char_p)]
+
+
+# Every symbol include/ramvamp_attn.h declares: name -> (restype, argtypes).
+_E = POINTER(RvError)
+_P = c_void_p
+SIGNATURES = {
+    "rv_abi_version": (c_uint32, []),
+    "rv_status_name": (c_char_p, [c_int32]),
+    "rv_scratch_len": (c_size_t, [c_size_t, c_size_t, c_size_t, c_size_t]),
+    "rv_kv_projected_bytes": (c_int32, [c_size_t, c_size_t, c_size_t, c_size_t, c_int, POINTER(c_uint64), _E]),
+    "rv_kv_new": (c_int32, [c_size_t, c_size_t, c_size_t, c_size_t, c_int, c_int, POINTER(c_void_p), _E]),
+    "rv_kv_free": (None, [_P]),
+    "rv_kv_set_stream": (c_int32, [_P, _P, _E]),
+    "rv_kv_synchronize": (c_int32, [_P, _E]),
+    "rv_kv_n_layers": (c_size_t, [_P]),
+    "rv_kv_n_kv_heads": (c_size_t, [_P]),
+    "rv_kv_head_dim": (c_size_t, [_P]),
+    "rv_kv_capacity": (c_size_t, [_P]),
+    "rv_kv_kv_dim": (c_size_t, [_P]),
+    "rv_kv_elem": (c_int32, [_P]),
+    "rv_kv_len": (c_int32, [_P, c_size_t, POINTER(c_size_t), _E]),
+    "rv_kv_is_empty": (c_int, [_P]),
+    "rv_kv_seq_len": (c_int32, [_P, POINTER(c_size_t), _E]),
+    "rv_kv_append": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, c_uint32, _E]),
+    "rv_kv_append_rows": (c_int32, [_P, c_size_t, _P, _P, c_size_t, c_size_t, c_uint32, _E]),
+    "rv_kv_clear": (None, [_P]),
+    "rv_kv_truncate": (c_int32, [_P, c_size_t, _E]),
+    "rv_kv_k_layer": (c_int32, [_P, c_size_t, POINTER(c_void_p), POINTER(c_size_t), _E]),
+    "rv_kv_v_layer": (c_int32, [_P, c_size_t, POINTER(c_void_p), POINTER(c_size_t), _E]),
+    "rv_kv_read_row": (c_int32, [_P, c_int, c_size_t, c_size_t, _P, _E]),
+    "rv_decode_attention": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_decode_attention_in": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, c_size_t, _P, c_size_t, c_uint32, _E]),
+    "rv_decode_attention_kv_range_in": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, c_size_t, c_size_t, c_size_t,
+                                                  _P, c_size_t, c_uint32, _E]),
+    "rv_attention_at": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_attention_at_in": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_float, c_size_t, _P, c_size_t, c_uint32,
+                                     _E]),
+    "rv_attention_at_kv_range_in": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_float, c_size_t, c_size_t,
+                                              c_size_t, _P, c_size_t, c_uint32, _E]),
+    "rv_attention_at_rows": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_size_t, c_float, _P, c_uint32, _E]),
+    "rv_decode_step": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, _P, c_float, c_float,
+                                 c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, _P, c_float, c_float, c_size_t,
+                                   c_float, _P, c_uint32, _E]),
+    "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """The library with every ABI symbol typed. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} is missing: build the gfx950 HIP library first "
+            "(python -c 'import __graft_entry__ as g; g.build()'). There is no CPU fallback.")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

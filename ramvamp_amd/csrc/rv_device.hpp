@@ -1,0 +1,101 @@
+// rv_device.hpp — device helpers shared by the gfx950 kernels.
+//
+// Wave64 only (CDNA4): every lane-group reduction below assumes 64-lane
+// wavefronts and uses DPP row operations, which act within 16-lane rows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// DPP controls (GFX9 encoding).
+enum : int {
+  DPP_QUAD_XOR1 = 0xB1,       // quad_perm [1,0,3,2]
+  DPP_QUAD_XOR2 = 0x4E,       // quad_perm [2,3,0,1]
+  DPP_ROW_HALF_MIRROR = 0x141,
+  DPP_ROW_MIRROR = 0x140,
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32); every lane of a
+// group ends with the group's total. Within 16 lanes this is four DPP steps
+// (pairs, quads, half-row mirror, row mirror); 32 adds one cross-row swap.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "group size");
+  x += dpp_f32<DPP_QUAD_XOR1>(x);
+  if constexpr (N >= 4) x += dpp_f32<DPP_QUAD_XOR2>(x);
+  if constexpr (N >= 8) x += dpp_f32<DPP_ROW_HALF_MIRROR>(x);
+  if constexpr (N >= 16) x += dpp_f32<DPP_ROW_MIRROR>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
+  return x;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  x = fmaxf(x, dpp_f32<DPP_QUAD_XOR1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp_f32<DPP_QUAD_XOR2>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp_f32<DPP_ROW_HALF_MIRROR>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_f32<DPP_ROW_MIRROR>(x));
+  if constexpr (N >= 32) x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return x;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// f32 -> f16 bits, round to nearest even, with the reference's subnormal,
+// overflow and NaN encodings (crates/core/src/kernels/quants/f16.rs:39-91).
+// Integer-only, so the result never depends on the hardware rounding mode or
+// its NaN quieting.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+  uint32_t bits = __float_as_uint(x);
+  uint32_t sign = (bits >> 16) & 0x8000u;
+  int32_t exp = (int32_t)((bits >> 23) & 0xFF);
+  uint32_t frac = bits & 0x007FFFFFu;
+  if (exp == 0xFF) return (uint16_t)(frac == 0 ? (sign | 0x7C00u) : (sign | 0x7E00u | ((frac >> 13) & 0x03FFu)));
+  int32_t e16 = exp - 112;
+  if (e16 >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+  if (e16 <= 0) {
+    if (e16 < -10) return (uint16_t)sign;
+    uint32_t mant = exp == 0 ? frac : (frac | 0x00800000u);
+    uint32_t shift = (uint32_t)(14 - e16);
+    uint32_t ulp = 1u << shift, half = ulp >> 1;
+    uint32_t v = mant >> shift, rem = mant & (ulp - 1);
+    if (rem > half || (rem == half && (v & 1u))) v += 1;
+    return (uint16_t)(sign | v);
+  }
+  uint32_t v = ((uint32_t)e16 << 10) | (frac >> 13);
+  uint32_t rem = frac & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (v & 1u))) v += 1;
+  return (uint16_t)(sign | v);
+}
+
+// Eight consecutive plane elements widened to f32 (f16 widening is exact).
+__device__ __forceinline__ void load8(const float* __restrict__ p, float (&x)[8]) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+  x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+}
+__device__ __forceinline__ void load8(const _Float16* __restrict__ p, float (&x)[8]) {
+  f16x8 h = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)h[i];
+}
+
+}  // namespace rv

@@ -1,0 +1,89 @@
+// rv_internal.hpp — host-side state of a device KV cache and the kernel
+// launchers the C ABI (rv_abi.cpp) drives. Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "../../include/ramvamp_attn.h"
+
+struct rv_kv {
+  size_t n_layers = 0, n_kv_heads = 0, head_dim = 0, capacity = 0, kv_dim = 0, plane = 0;
+  int elem = RV_ELEM_F16;
+  int device = 0;
+  void* k = nullptr;  // [n_layers][capacity][kv_dim], elem-sized, device
+  void* v = nullptr;
+  std::vector<size_t> lens;  // per-layer cursors (kv/mod.rs:147), host-side
+  hipStream_t stream = nullptr;
+
+  // Device workspace, grown on first need and then reused by every call:
+  // decode split partials, the split-combine tickets, normalised q rows.
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  unsigned* tickets = nullptr;  // zeroed; each combine resets its own
+  size_t n_tickets = 0;
+  float* qbuf = nullptr;  // normalised + rotated q rows of the fused steps
+  size_t qbuf_bytes = 0;
+  // Staging for RV_HOST_PTRS calls.
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
+
+  int64_t tune_decode_split_len = 0;
+  int64_t tune_prefill_kv_split = 0;
+
+  size_t elem_size() const { return elem == RV_ELEM_F32 ? 4 : 2; }
+  char* k_layer(size_t layer) const { return (char*)k + layer * plane * elem_size(); }
+  char* v_layer(size_t layer) const { return (char*)v + layer * plane * elem_size(); }
+};
+
+namespace rv {
+
+// Result of a launch helper: hipSuccess or the first failing HIP call.
+struct HipStatus {
+  hipError_t e = hipSuccess;
+  const char* what = nullptr;
+};
+
+// Workspace (>= bytes) and tickets (>= n) on the cache's device.
+HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets);
+HipStatus ensure_qbuf(rv_kv* kv, size_t bytes);
+
+// True when the MFMA prefill kernel covers this geometry (else the ABI runs
+// each row through the decode kernel with its own position limit).
+bool prefill_supported(size_t head_dim, size_t group);
+
+// ---- prologue / append (rv_prologue.hip) ------------------------------------
+// RoPE inverse frequencies theta^(-2i/d) for i < d/2, computed on the host in
+// f64 (primitives/rope.rs:35-36) and passed by value.
+constexpr int kMaxHalf = 256;
+struct InvFreq {
+  double f[kMaxHalf];
+};
+void fill_inv_freq(InvFreq& t, size_t head_dim, float theta);
+
+// Append `rows` rows (kv_dim each) of k and v at cursor `pos0` of `layer`.
+// norm: k rows are RMSNormed per head with k_w and RoPE'd at pos0+r first
+// (model/forward.rs:2622-2631); otherwise stored as given.
+HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v,
+                        size_t rows, bool norm, const float* k_w, float eps, const InvFreq* inv,
+                        hipStream_t s);
+// q rows (rows x n_heads x head_dim): per-head RMSNorm with w then RoPE at
+// pos0 + r, written to q_out.
+HipStatus launch_q_prologue(const float* q, float* q_out, size_t rows, size_t n_heads, size_t head_dim,
+                            const float* w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s);
+
+// ---- decode (rv_decode.hip) ------------------------------------------------------
+// out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all
+// `positions` of `layer`. q is the full post-RoPE query.
+HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
+                        float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s);
+
+// ---- prefill (rv_prefill.hip) -------------------------------------------------
+// Row r of q_rows (post-RoPE, rows x q_dim) attends positions 0..start+r+1.
+HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
+                         size_t start, float scale, float* out, uint32_t mode, hipStream_t s);
+
+}  // namespace rv

@@ -1,0 +1,85 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the header
+declares, and its host-only entry points (no device work) agree with the
+oracle. No compute call is made here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from ramvamp_amd import _lib as L
+from ramvamp_amd import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ramvamp_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rv_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(L.LIB_PATH):
+        pytest.fail(f"{L.LIB_PATH} not built (run __graft_entry__.build())")
+    return L.load()
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    declared = header_functions()
+    assert len(declared) >= 30
+    assert set(declared) == set(L.SIGNATURES), set(declared) ^ set(L.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_library_is_a_gfx950_hip_build():
+    data = open(L.LIB_PATH, "rb").read()
+    assert b"gfx950" in data
+    assert b"gfx942" not in data
+
+
+def test_version_and_status_names(lib):
+    assert lib.rv_abi_version() == 1
+    names = {c: lib.rv_status_name(c).decode() for c in (0, 1, 2, 3, 4, 5, 6, 7, 16, 17, 18, 19, 20, 21, 24, 25, 32,
+                                                            33, 34, 35)}
+    assert names[0] == "RV_OK" and names[21] == "RV_ATTN_SCRATCH_TOO_SHORT"
+    assert len(set(names.values())) == len(names)
+    assert lib.rv_status_name(999).decode() == "RV_UNKNOWN"
+
+
+def test_scratch_len_matches_the_reference_carve(lib):
+    for args in [(32, 4, 128, 4096), (32, 4, 8, 17), (32, 0, 8, 17), (2 ** 63, 1, 2, 4), (8, 2, 9, 0)]:
+        assert lib.rv_scratch_len(*args) == oracle.scratch_len(*args), args
+    assert lib.rv_scratch_len(32, 4, 128, 4096) == 33_024
+
+
+def test_projected_bytes_and_dim_errors_match_the_oracle(lib):
+    for dims in [(48, 4, 128, 4096), (1, 1, 1, 1), (3, 2, 9, 13), (0, 4, 128, 8), (1, 0, 128, 8), (2, 2 ** 62, 4, 1),
+                 (2, 2 ** 61, 2, 1), (2 ** 40, 2 ** 20, 2 ** 4, 1)]:
+        for elem in (1, 2):
+            out, err = ctypes.c_uint64(), L.RvError()
+            rc = lib.rv_kv_projected_bytes(*dims, elem, ctypes.byref(out), ctypes.byref(err))
+            try:
+                want = oracle.projected_bytes(*dims, elem)
+                assert rc == 0 and out.value == want, dims
+            except oracle.OracleError as e:
+                assert (rc, err.a, err.b, err.c, err.d, err.what.decode()) == e.payload(), dims
+    out, err = ctypes.c_uint64(), L.RvError()
+    assert lib.rv_kv_projected_bytes(1, 1, 1, 1, 3, ctypes.byref(out), ctypes.byref(err)) == 35
+
+
+def test_synthetic_generator_is_deterministic_and_standard_normal():
+    a = synth.normal(synth.seed(2, synth.T_KC, 7), 1 << 20)
+    b = synth.normal(synth.seed(2, synth.T_KC, 7), 1 << 20)
+    c = synth.normal(synth.seed(2, synth.T_KC, 8), 1 << 20)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(float(a.mean())) < 5e-3 and abs(float(a.std()) - 1.0) < 5e-3
+    # prefix-stable: a shorter draw is a prefix of a longer one
+    assert np.array_equal(synth.normal(123, 1001), synth.normal(123, 5000)[:1001])
+    w = synth.norm_weight(1, synth.T_QN)
+    assert w.shape == (128,) and abs(float(w.mean()) - 1.0) < 0.01

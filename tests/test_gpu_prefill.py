@@ -1,0 +1,146 @@
+"""Chunked causal prefill on the GPU vs the oracle (model/prefill.rs:2055-2111).
+
+Modes and their stated bounds against the oracle on the same cache, each
+applied as both the reference-style elementwise gate (abs or rel) and the
+scale-normalised max|err|/max|ref| (tests/gpu_util.py `gate`):
+  exact (split-f16 MFMA): rel 1e-4 / abs 5e-5, scaled 1e-5 (the fp32-mode gate);
+  f16  (one f16 MFMA per product): rel 4e-3 / abs 4e-3, scaled 2e-3;
+  bf16 (one bf16 MFMA per product): rel 3e-2 / abs 3e-2, scaled 1.5e-2.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import ramvamp_amd as rv
+from gpu_util import dev, elem_code, gate, host, rel_err, say, torch_cuda
+from helpers import Rng
+from ramvamp_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+BOUNDS = {"exact": 1e-4, "f16": 4e-3, "bf16": 3e-2}
+ABS = {"exact": 5e-5, "f16": 4e-3, "bf16": 3e-2}  # the reference gate's abs term scales with the mode
+SCALE = {"exact": 1e-5, "f16": 2e-3, "bf16": 1.5e-2}  # max|err| / max|ref|
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def twin(rng, n_kv, hd, n_pos, cap, elem):
+    kv = rv.KvCache(1, n_kv, hd, cap, elem)
+    ref = oracle.KvCache(1, n_kv, hd, cap, elem_code(elem))
+    K = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
+    V = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
+    if n_pos:
+        kv.append_rows(0, K, V)
+        ref.append_rows(0, K, V)
+    return kv, ref
+
+
+@pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_rows_match_per_row_attention_at(mode, elem):
+    torch_cuda()
+    rng = Rng(0xC0FFEE)
+    for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (4, 32, 128, 100, 70), (2, 8, 128, 5, 16),
+                                       (1, 1, 128, 3, 50), (4, 16, 128, 0, 1), (2, 4, 128, 31, 33),
+                                       (1, 8, 16, 4, 9), (3, 6, 9, 0, 7)]:
+        say(f"case rows {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem}")
+        kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, elem)
+        q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+        out = dev(np.zeros(q.shape))
+        rv.attention_at_rows(dev(q), kv, 0, start, scale, out, mode=mode)
+        want = ref.scatter_attention(q, 0, start, scale, THREADS)
+        bound = BOUNDS[mode] if hd == 128 else 1e-4  # other head dims run the fp32 decode kernel per row
+        e = gate(host(out), want, rel=bound, abs_tol=ABS[mode] if hd == 128 else 5e-5,
+                 scale=SCALE[mode] if hd == 128 else 1e-5,
+                 what=f"rows {(n_kv, n_q, hd, start, rows)} {mode}")
+        say(f"  max rel err {e:.3e}")
+
+
+@pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
+def test_config3_prefill_chunk_matches_the_oracle(mode):
+    torch_cuda()
+    say(f"case config 3 mode={mode}")
+    kv = rv.KvCache(1, 4, 128, 512, "f32")
+    ref = oracle.KvCache(1, 4, 128, 512, oracle.RV_ELEM_F32)
+    q, k, v = synth.new_rows(3, 512)
+    wq, wk = synth.norm_weight(3, synth.T_QN), synth.norm_weight(3, synth.T_KN)
+    out = dev(np.zeros(q.shape))
+    rv.prefill_chunk(kv, 0, dev(q), dev(k), dev(v), dev(wq), dev(wk), synth.EPS, synth.THETA, 0, synth.SCALE, out,
+                     mode=mode)
+    want = ref.prefill_chunk(0, q, k, v, wq, wk, synth.EPS, synth.THETA, 0, synth.SCALE, threads=THREADS)
+    e = gate(host(out), want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode], what=f"config 3 {mode}")
+    say(f"config 3 {mode} max rel err {e:.3e}")
+    assert kv.len(0) == 512
+    for pos in (0, 511):
+        gate(kv.k_row(0, pos), ref.read_row(False, 0, pos), rel=2e-7, floor=1e-6, what="cache K")
+
+
+@pytest.mark.parametrize("mode", ["exact", "f16"])
+def test_config4_prefix_reuse_prefill_matches_the_oracle(mode):
+    torch_cuda()
+    say(f"case config 4 mode={mode}")
+    start, rows = 3449, 512
+    K, V = synth.cached_kv(4, 0, start)
+    kv = rv.KvCache(1, 4, 128, start + rows, "f32")
+    ref = oracle.KvCache(1, 4, 128, start + rows, oracle.RV_ELEM_F32)
+    kv.append_rows(0, K, V)
+    ref.append_rows(0, K, V)
+    q, k, v = synth.new_rows(4, rows)
+    wq, wk = synth.norm_weight(4, synth.T_QN), synth.norm_weight(4, synth.T_KN)
+    out = dev(np.zeros(q.shape))
+    rv.prefill_chunk(kv, 0, dev(q), dev(k), dev(v), dev(wq), dev(wk), synth.EPS, synth.THETA, start, synth.SCALE,
+                     out, mode=mode)
+    got = host(out)
+    # Oracle: the same prologue and append for every row, attention for a sample of rows.
+    qn = np.stack([oracle.norm_rope_heads(q[r], 32, 128, wq, synth.EPS, synth.THETA, start + r) for r in range(rows)])
+    for r in range(rows):
+        ref.append(0, oracle.norm_rope_heads(k[r], 4, 128, wk, synth.EPS, synth.THETA, start + r), v[r])
+    sample = [0, 1, 2, 63, 64, 200, 255, 256, 383, 509, 510, 511]
+    want = np.stack([ref.attention(qn[r], 0, synth.SCALE, positions=start + r + 1) for r in sample])
+    e = gate(got[sample], want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode], what=f"config 4 {mode}")
+    say(f"config 4 {mode} max rel err (sampled rows) {e:.3e}")
+
+
+def test_prefill_rows_equal_decode_with_the_row_limit():
+    # attention.rs:2019-2058 in spirit: the masked (prefill) form equals the
+    # position-limited decode form row by row (two different device kernels).
+    torch_cuda()
+    say("case prefill vs attention_at")
+    rng = Rng(0xCA5A)
+    kv, _ = twin(rng, 4, 128, 900, 900, "f32")
+    start, rows = 700, 200
+    q = rng.vec_in(rows * 4096, -1.0, 1.0).reshape(rows, -1)
+    out = np.zeros(q.shape, np.float32)
+    rv.attention_at_rows(q, kv, 0, start, 0.1, out, mode="exact")
+    for r in (0, 1, 99, 199):
+        one = np.zeros(4096, np.float32)
+        rv.attention_at(q[r], kv, 0, start + r + 1, 0.1, None, one)
+        gate(out[r], one, rel=1e-4, what=f"row {r}")
+
+
+def test_prefill_errors_and_first_row_semantics():
+    torch_cuda()
+    say("case prefill errors")
+    kv = rv.KvCache(2, 4, 128, 64, "f32")
+    rng = Rng(3)
+    K = rng.vec_in(10 * 512, -1, 1).reshape(10, -1)
+    kv.append_rows(0, K, K)
+    q = rng.vec_in(8 * 4096, -1, 1).reshape(8, -1)
+    out = np.full(q.shape, np.nan, np.float32)
+    with pytest.raises(rv.KvError) as e:  # row 7 would attend 11 positions of 10
+        rv.attention_at_rows(q, kv, 0, 3, 0.1, out)
+    assert e.value.variant == "PositionOutOfRange" and e.value.fields["pos"] == 10 and e.value.fields["len"] == 10
+    assert np.all(np.isnan(out))
+    with pytest.raises(rv.KvError):
+        rv.attention_at_rows(q, kv, 2, 0, 0.1, out)
+    with pytest.raises(rv.AttentionError) as e:
+        rv.attention_at_rows(np.ascontiguousarray(q[:, :100]), kv, 0, 0, 0.1, np.zeros((8, 100), np.float32))
+    assert e.value.variant == "QLenIndivisible"
+    rv.attention_at_rows(q[:0], kv, 0, 0, 0.1, out[:0])  # zero rows: a no-op
+    rv.attention_at_rows(q[:1], kv, 0, 0, 0.1, out[:1])  # row 0 at start 0 sees only position 0
+    # split-f16 reproduces V to ~2^-22 relative (hi + lo of one f32)
+    assert np.allclose(out[0].reshape(4, 8, 128), np.broadcast_to(K[0].reshape(4, 1, 128), (4, 8, 128)), rtol=1e-6,
+                       atol=0)
