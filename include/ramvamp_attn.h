@@ -226,8 +226,12 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
 /* Tuning knobs of the decode/prefill launches (0 = built-in heuristic).
  * Exposed for benchmarking sweeps; results never depend on them beyond
  * floating-point reassociation within the stated tolerance. */
-#define RV_TUNE_DECODE_SPLIT_LEN 1 /* positions per decode split (multiple of 16) */
-#define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill tile */
+#define RV_TUNE_DECODE_SPLIT_LEN 1 /* positions per decode split (rounded to the workgroup step) */
+#define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill row tile (1..8) */
+#define RV_TUNE_DECODE_WAVES 3     /* waves per decode workgroup: 4 or 8 */
+#define RV_TUNE_PREFILL_ROWS 4     /* query rows per prefill tile: 8 or 16 */
+#define RV_TUNE_DECODE_HG 5        /* query heads per VALU decode workgroup: 1, 2, 4 or 8 */
+#define RV_TUNE_DECODE_IMPL 6      /* decode kernel: 0 auto, 1 VALU subgroups, 2 MFMA */
 int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
 
 #ifdef __cplusplus

@@ -687,6 +687,10 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
   switch (knob) {
     case RV_TUNE_DECODE_SPLIT_LEN: kv->tune_decode_split_len = value; break;
     case RV_TUNE_PREFILL_KV_SPLIT: kv->tune_prefill_kv_split = value; break;
+    case RV_TUNE_DECODE_WAVES: kv->tune_decode_waves = value; break;
+    case RV_TUNE_PREFILL_ROWS: kv->tune_prefill_rows = value; break;
+    case RV_TUNE_DECODE_HG: kv->tune_decode_hg = value; break;
+    case RV_TUNE_DECODE_IMPL: kv->tune_decode_impl = value; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }
   return ok(err);
