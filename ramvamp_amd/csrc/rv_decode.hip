@@ -4,23 +4,23 @@
 // (crates/core/src/kernels/attention.rs:1075-1303) for the decode and
 // position-limited forms.
 //
-// Fast path (head_dim 128, any group): one workgroup of W waves per (kv
-// head, subgroup of G query heads, split of the position axis). A K or V
-// row's 128-element head slice is read by one 16-lane group, 8 elements (16
-// or 32 bytes) per lane, and serves the subgroup's G heads from registers.
-// QK dots reduce over the 16 lanes with DPP; softmax is online (running max
-// and sum per query head, exp2 with log2(e) folded into q). The 4*W row
-// groups of a workgroup merge through LDS; the splits of one (kv head,
-// subgroup) are merged by a second kernel with an fp32 log-sum-exp combine
-// (the kernel boundary makes the partials visible: an in-kernel hand-off
-// would need agent-scope fences, which write back and invalidate the L2 and
-// cost more than the second launch).
+// Fast path (head_dim 128, group <= 16): decode_tile_kernel, one workgroup
+// of W waves per (kv head, split of the position axis). The group's query
+// heads are the columns of fp32 MFMA tiles over 16-position tiles of K and V,
+// loaded straight into registers in the MFMA operand layouts; softmax is
+// online (running max and sum per query head, exp2 with log2(e) folded into
+// q). The splits of one kv head are merged by a second kernel with an fp32
+// log-sum-exp combine. The kernel boundary is what makes the partials
+// visible: the workgroups of one kv head run on different XCDs, whose L2s are
+// not coherent, and an in-kernel hand-off would need agent-scope release and
+// acquire fences (an L2 write-back and invalidate each), measured dearer
+// than the second launch.
 //
-// Why subgroups: one CU streams only ~10-25 GB/s, so the merge must read
-// little (splits x G x 520 bytes) while the grid stays wide enough to put
-// every CU on the K/V stream. Subgroups of one (kv head, split) read the same
-// rows; the grid places them on one XCD so its L2 serves the repeats and HBM
-// sees each K/V byte once.
+// VALU path (head_dim 128, any group; groups over 16 use it by default):
+// decode_split_kernel, one workgroup per (kv head, subgroup of G query heads,
+// split); a K or V row's head slice is read by one 16-lane group, 8 elements
+// per lane, and serves the subgroup's G heads from registers; QK dots reduce
+// over the 16 lanes with DPP. Same merge kernel.
 //
 // Generic path (any head_dim, any group): scores, softmax and the V
 // reduction as three kernels in the reference's own order — f32 dots with
@@ -36,7 +36,6 @@ namespace {
 
 constexpr int kD = 128;                     // head_dim of the fast path
 constexpr int kLPR = 16;                    // lanes per K/V row (8 elements each)
-constexpr int kMaxSplits = 256;             // splits per kv head the merge stages in LDS
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegSentinel = -1.0e30f;    // finite "no position yet" max
 
@@ -78,11 +77,10 @@ __device__ __forceinline__ void load_row8<_Float16>(const _Float16* __restrict__
 }
 
 // One workgroup per (kv head, subgroup of G query heads, split). The 1-D
-// grid puts the n_hg subgroups of one (kv head, split) unit on the same XCD
-// (workgroups are dispatched round-robin over the 8 XCDs, so equal block ids
-// mod 8 share an L2) and in the same dispatch round: the subgroups read the
-// same K/V rows, and L2 serves all but the first. With one split the
-// workgroup writes `out`; otherwise its partial (o, max, sum) row, merged by
+// grid numbers the n_hg subgroups of one (kv head, split) unit 8 apart, so
+// they are dispatched in the same round and their repeated reads of the same
+// K/V rows can hit in the shared cache levels. With one split the workgroup
+// writes `out`; otherwise its partial (o, max, sum) row, merged by
 // decode_merge_kernel.
 template <typename T, int G, int R, int W>
 __global__ __launch_bounds__(W * 64) void decode_split_kernel(const float* __restrict__ q,
@@ -250,198 +248,153 @@ __global__ __launch_bounds__(W * 64) void decode_split_kernel(const float* __res
   }
 }
 
-// ---- MFMA path ------------------------------------------------------------------
+// ---- MFMA path ----------------------------------------------------------------------
 
-// 32 consecutive plane elements widened to f32.
+// 16-byte vector of plane elements: 4 fp32 or 8 f16.
 template <typename T>
-__device__ __forceinline__ void load32(const T* __restrict__ p, float (&x)[32]);
+struct Chunk;
 template <>
-__device__ __forceinline__ void load32<float>(const float* __restrict__ p, float (&x)[32]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const f32x4 a = reinterpret_cast<const f32x4*>(p)[i];
-    x[4 * i] = a[0];
-    x[4 * i + 1] = a[1];
-    x[4 * i + 2] = a[2];
-    x[4 * i + 3] = a[3];
-  }
-}
-template <>
-__device__ __forceinline__ void load32<_Float16>(const _Float16* __restrict__ p, float (&x)[32]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f16x8 a = reinterpret_cast<const f16x8*>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)a[j];
-  }
-}
-
-// LDS row stride of a staged 16 x 128 tile, in floats: 4 words of padding
-// put the 16 rows read at one column into 16 different bank groups.
-constexpr int kTileStride = kD + 4;
-
-// One 16-position K or V tile (16 rows x 128 elements of one kv head) in
-// staging registers, loaded with whole rows per instruction: f32 lane i of
-// step j holds row 2j + i/32, columns 4*(i%32)..+3; f16 lane i of step j
-// holds row 4j + i/16, columns 8*(i%16)..+7.
-template <typename T>
-struct TileRegs;
-template <>
-struct TileRegs<float> {
-  static constexpr int kSteps = 8;
-  f32x4 r[8];
-  __device__ void load(const float* __restrict__ plane, int kv_dim, size_t col, int t0, int t_last, int lane) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = min(t0 + 2 * j + (lane >> 5), t_last);
-      r[j] = *reinterpret_cast<const f32x4*>(plane + (size_t)row * kv_dim + col + 4 * (lane & 31));
-    }
-  }
-  __device__ void store(float (*lds)[kTileStride], int lane) const {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4*>(&lds[2 * j + (lane >> 5)][4 * (lane & 31)]) = r[j];
-  }
+struct Chunk<float> {
+  typedef f32x4 type;
+  static constexpr int n = 4;
 };
 template <>
-struct TileRegs<_Float16> {
-  f16x8 r[4];
-  __device__ void load(const _Float16* __restrict__ plane, int kv_dim, size_t col, int t0, int t_last, int lane) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = min(t0 + 4 * j + (lane >> 4), t_last);
-      r[j] = *reinterpret_cast<const f16x8*>(plane + (size_t)row * kv_dim + col + 8 * (lane & 15));
-    }
-  }
-  __device__ void store(float (*lds)[kTileStride], int lane) const {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f32x4 a, b;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        a[e] = (float)r[j][e];
-        b[e] = (float)r[j][4 + e];
-      }
-      float* dst = &lds[4 * j + (lane >> 4)][8 * (lane & 15)];
-      *reinterpret_cast<f32x4*>(dst) = a;
-      *reinterpret_cast<f32x4*>(dst + 4) = b;
-    }
-  }
+struct Chunk<_Float16> {
+  typedef f16x8 type;
+  static constexpr int n = 8;
 };
 
-// One workgroup of W waves per (kv head, split); all `group` (<= 16) query
+// One workgroup of W waves per (kv head, split); the `group` (<= 16) query
 // heads of the kv head are the 16 columns of fp32 MFMA tiles
 // (v_mfma_f32_16x16x4_f32: exact fp32 products, fp32 accumulation). Wave w
-// takes the split's 16-position tiles w, w+W, ...; each tile's K and V rows
-// are read whole-row-per-instruction into registers (the next tile's loads
-// are issued before the current tile is computed), converted to f32 and
-// staged in the wave's own LDS region, from which the MFMA operands are read:
-//   S^T[t][m] = sum_d K[t][d] Q[m][d]: 32 MFMAs; A slot (lane t + 16*kg,
-//     step s) is K[t][32*kg + s], B is q (loaded once, log2(e)*scale folded);
-//   online softmax on the accumulator: lane l holds rows 4*(l/16) + i of
+// takes the split's 16-position tiles w, w+W, ...; every operand comes
+// straight from global memory into registers, 16 bytes per load, in the
+// layout the MFMA consumes, so nothing is staged through LDS:
+//   S^T[t][m] = sum_d K[t][d] Q[m][d]: 32 MFMAs; lane (t, k) holds K row t
+//     and lane (m, k) holds q head m at d = E*(k + 4*(s/E)) + s%E for step
+//     s (E = elements per 16-byte chunk), i.e. chunks k, k+4, ... of the row;
+//     log2(e)*scale is folded into q;
+//   online softmax on the accumulator: lane l holds rows 4*(l/16) + r of
 //     column l % 16, so a column's max needs two cross-lane swaps and every
 //     exp is computed once;
-//   O^T[d][m] += sum_t V[t][d] P[m][t]: 8 x 4 MFMAs; the accumulator layout
-//     of S^T is exactly the B layout P^T needs, so P never moves.
-// The waves merge through LDS; the workgroup writes `out` (one split) or its
-// partial (o, max, sum) row for decode_merge_kernel.
+//   O^T[d][m] += sum_t V[t][d] P^T[t][m]: 8 x 4 MFMAs; the accumulator layout
+//     of S^T is exactly the B layout P^T needs (step r takes rows 4k + r), and
+//     lane (i, k) holds V[4k + r][8i .. 8i+7], so output block b is d = 8i + b.
+// The first tile's loads are issued before anything waits (a scheduling
+// barrier keeps the compiler from sinking them to their uses), the next
+// tile's after the current one is computed. The waves merge through LDS; the
+// workgroup writes `out` (one split) or its partial (o, max, sum) row for
+// decode_merge_kernel.
 template <typename T, int W>
-__global__ __launch_bounds__(W * 64) void decode_mfma_kernel(const float* __restrict__ q, const T* __restrict__ kl,
+__global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __restrict__ q, const T* __restrict__ kl,
                                                              const T* __restrict__ vl, int kv_dim, int positions,
                                                              int split_len, int n_splits, int group, int kv_lo,
                                                              float qscale, float* __restrict__ part,
                                                              float* __restrict__ out) {
+  typedef typename Chunk<T>::type CT;
+  constexpr int E = Chunk<T>::n;
+  constexpr int NKC = 32 / E;  // K chunks per lane per tile
+  constexpr int NVC = 32 / E;  // V chunks per lane per tile (4 rows x 8 elements)
   constexpr int NT = W * 64;
-  __shared__ __attribute__((aligned(16))) float sm_kv[W][2][16][kTileStride];
-  __shared__ float sm_ml[W][16][2];
   const int split = blockIdx.x % n_splits;
   const int hidx = blockIdx.x / n_splits;  // kv head within the range
   const int kvh = kv_lo + hidx;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lm = lane & 15, kg = lane >> 4;
+  const int li = lane & 15, lk = lane >> 4;
   const int t_begin = split * split_len;
   const int t_end = min(positions, t_begin + split_len);
-  const bool col_ok = lm < group;
+  const int n_tiles = (t_end - t_begin + 15) / 16;
+  const int my_tiles = n_tiles > wave ? (n_tiles - wave + W - 1) / W : 0;
   const size_t col = (size_t)kvh * kD;
+  const bool col_ok = li < group;
 
-  float qb[32];
+  float qv[32];
   {
-    const float* qp = q + (size_t)(kvh * group + (col_ok ? lm : 0)) * kD + kg * 32;
+    const float* qp = q + (size_t)(kvh * group + (col_ok ? li : 0)) * kD;
 #pragma unroll
-    for (int s = 0; s < 32; ++s) qb[s] = col_ok ? qp[s] * qscale : 0.f;
+    for (int c = 0; c < NKC; ++c)
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(qp + E * (lk + 4 * c) + e);
+        qv[c * E + e] = x[0];
+        qv[c * E + e + 1] = x[1];
+        qv[c * E + e + 2] = x[2];
+        qv[c * E + e + 3] = x[3];
+      }
   }
+  CT kb[NKC], vb[NVC];
+  // Rows past the split re-read its last row (in bounds, branch-free); their
+  // scores are masked below.
+  auto load_tile = [&](int j) {
+    const int t0 = t_begin + (wave + j * W) * 16;
+    const T* kp = kl + (size_t)min(t0 + li, t_end - 1) * kv_dim + col + E * lk;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) kb[c] = *reinterpret_cast<const CT*>(kp + 4 * E * c);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const T* vp = vl + (size_t)min(t0 + 4 * lk + r, t_end - 1) * kv_dim + col + 8 * li;
+#pragma unroll
+      for (int h = 0; h < 8 / E; ++h) vb[r * (8 / E) + h] = *reinterpret_cast<const CT*>(vp + E * h);
+    }
+  };
+  if (my_tiles > 0) load_tile(0);
+  __builtin_amdgcn_sched_barrier(0);
+  const float qsc = col_ok ? qscale : 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) qv[i] *= qsc;
+
   f32x4 o[8];
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) o[ds] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegSentinel, l_run = 0.f;
-
-  float (*ks)[kTileStride] = sm_kv[wave][0];
-  float (*vs)[kTileStride] = sm_kv[wave][1];
-  TileRegs<T> kr, vr;
-  int t0 = t_begin + wave * 16;
-  if (t0 < t_end) {
-    kr.load(kl, kv_dim, col, t0, t_end - 1, lane);
-    vr.load(vl, kv_dim, col, t0, t_end - 1, lane);
-  }
-  for (; t0 < t_end; t0 += W * 16) {
-    // The wave's LDS region is its own, and one wave's LDS accesses complete
-    // in order, so no barrier is needed between the store and the reads.
-    kr.store(ks, lane);
-    vr.store(vs, lane);
-    const int tn = t0 + W * 16;
-    if (tn < t_end) {
-      kr.load(kl, kv_dim, col, tn, t_end - 1, lane);
-      vr.load(vl, kv_dim, col, tn, t_end - 1, lane);
-    }
-    float ka[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(&ks[lm][kg * 32 + 4 * i]);
-      ka[4 * i] = a[0];
-      ka[4 * i + 1] = a[1];
-      ka[4 * i + 2] = a[2];
-      ka[4 * i + 3] = a[3];
-    }
+  for (int j = 0; j < my_tiles; ++j) {
+    const int t0 = t_begin + (wave + j * W) * 16;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 32; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[s], qb[s], acc, 0, 0, 0);
+    for (int c = 0; c < NKC; ++c)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kb[c][e], qv[c * E + e], acc, 0, 0, 0);
     float x[4], mx = kNegSentinel;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[i] = (t0 + kg * 4 + i < t_end) ? acc[i] : -INFINITY;
-      mx = fmaxf(mx, x[i]);
+    for (int r = 0; r < 4; ++r) {
+      x[r] = (t0 + 4 * lk + r < t_end) ? acc[r] : -INFINITY;
+      mx = fmaxf(mx, x[r]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mn = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - mn);
+    // v_exp_f32 directly: results below 2^-126 flush to zero, which only
+    // drops weights that are negligible next to the running maximum's 1.
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
     m_run = mn;
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = exp2f(x[i] - mn);
+    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - mn);
     l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) {
-      o[ds] *= alpha;
+    for (int b = 0; b < 8; ++b) {
+      o[b] *= alpha;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        o[ds] = __builtin_amdgcn_mfma_f32_16x16x4f32(vs[kg * 4 + s][ds * 16 + lm], p[s], o[ds], 0, 0, 0);
+      for (int r = 0; r < 4; ++r)
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vb[(r * 8 + b) / E][(r * 8 + b) % E], p[r], o[b], 0, 0, 0);
     }
+    if (j + 1 < my_tiles) load_tile(j + 1);
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // Merge the W waves through LDS (the tile regions are reused).
-  __syncthreads();
-  float (*so)[kTileStride] = sm_kv[wave][0];  // [16 heads][128 d]
-  if (col_ok) {
+  // o[b][r] = O^T[d = 8*(4*lk + r) + b][m = li]. Merge the W waves in LDS.
+  __shared__ __attribute__((aligned(16))) float sm_o[W][16][kD + 4];
+  __shared__ float sm_ml[W][16][2];
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) so[lm][ds * 16 + kg * 4 + i] = o[ds][i];
-    if (kg == 0) {
-      sm_ml[wave][lm][0] = m_run;
-      sm_ml[wave][lm][1] = l_run;
-    }
+  for (int r = 0; r < 4; ++r) {
+    float* dst = &sm_o[wave][li][8 * (4 * lk + r)];
+    *reinterpret_cast<f32x4*>(dst) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
+  }
+  if (lk == 0) {
+    sm_ml[wave][li][0] = m_run;
+    sm_ml[wave][li][1] = l_run;
   }
   __syncthreads();
   const int stride = part_stride_of(group);
@@ -455,9 +408,9 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(const float* __rest
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float a = exp2f(sm_ml[w][g][0] - M);
+      const float a = __builtin_amdgcn_exp2f(sm_ml[w][g][0] - M);
       L += sm_ml[w][g][1] * a;
-      O += *reinterpret_cast<const f32x4*>(&sm_kv[w][0][g][d]) * a;
+      O += *reinterpret_cast<const f32x4*>(&sm_o[w][g][d]) * a;
     }
     if (n_splits == 1) {
       const f32x4 r = O / L;  // out may be only 4-byte aligned
@@ -477,48 +430,67 @@ __global__ __launch_bounds__(W * 64) void decode_mfma_kernel(const float* __rest
 }
 
 // fp32 log-sum-exp merge of the splits of every (kv head, subgroup of G
-// heads): one 256-thread workgroup per (subgroup, head, 64-column half). The
-// four waves take every fourth split and fold them online; their loads do
-// not depend on one another, so one round trip brings them all. The waves
-// then merge through LDS.
+// heads) partial row set: one 256-thread workgroup per (query head, block of
+// kMergeCols output columns), its threads a grid of 256/kMergeCols split
+// lanes x kMergeCols columns. Each thread loads a chunk of kMergeChunk splits
+// (o, max, sum) before it folds any of them, so a chunk costs one memory
+// round trip; the split lanes then merge through LDS.
+constexpr int kMergeCols = 32;
+constexpr int kMergeChunk = 8;
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, int n_splits, int stride,
                                                            int G, int group, int n_hg, float* __restrict__ out) {
-  const int b = blockIdx.x;
-  const int half = b & 1, jg = b >> 1;
+  constexpr int NS = 256 / kMergeCols;
+  constexpr int NB = kD / kMergeCols;
+  const int blk = blockIdx.x % NB, jg = blockIdx.x / NB;
   const int g = jg % G, job = jg / G;
   const int hidx = job / n_hg, hg = job % n_hg;
   const int h = hidx * group + hg * G + g;  // q head within the range
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int d = half * 64 + lane;
+  const int tid = threadIdx.x, ci = tid % kMergeCols, sl = tid / kMergeCols;
+  const int d = blk * kMergeCols + ci;
   const float* base = part + (size_t)job * n_splits * stride;
   float M = kNegSentinel, L = 0.f, O = 0.f;
-#pragma unroll 16
-  for (int sp = wave; sp < n_splits; sp += 4) {
-    const float* ps = base + (size_t)sp * stride;
-    const float m = ps[G * kD + 2 * g], l = ps[G * kD + 2 * g + 1], o = ps[g * kD + d];
-    const float mn = fmaxf(M, m);
-    const float a = exp2f(M - mn), c = exp2f(m - mn);
-    L = L * a + l * c;
-    O = O * a + o * c;
-    M = mn;
-  }
-  __shared__ float sm[3][4][64];
-  sm[0][wave][lane] = M;
-  sm[1][wave][lane] = L;
-  sm[2][wave][lane] = O;
-  __syncthreads();
-  if (wave == 0) {
-    float Mt = sm[0][0][lane];
+  for (int b0 = 0; b0 < n_splits; b0 += NS * kMergeChunk) {
+    float ov[kMergeChunk], mv[kMergeChunk], lv[kMergeChunk];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) Mt = fmaxf(Mt, sm[0][w][lane]);
+    for (int i = 0; i < kMergeChunk; ++i) {
+      const float* ps = base + (size_t)min(b0 + NS * i + sl, n_splits - 1) * stride;
+      ov[i] = ps[g * kD + d];
+      mv[i] = ps[G * kD + 2 * g];
+      lv[i] = ps[G * kD + 2 * g + 1];
+    }
+    float mc = M;
+#pragma unroll
+    for (int i = 0; i < kMergeChunk; ++i)
+      if (b0 + NS * i + sl < n_splits) mc = fmaxf(mc, mv[i]);
+    const float a = __builtin_amdgcn_exp2f(M - mc);
+    L *= a;
+    O *= a;
+#pragma unroll
+    for (int i = 0; i < kMergeChunk; ++i)
+      if (b0 + NS * i + sl < n_splits) {
+        const float c = __builtin_amdgcn_exp2f(mv[i] - mc);
+        L += lv[i] * c;
+        O += ov[i] * c;
+      }
+    M = mc;
+  }
+  __shared__ float sm[3][NS][kMergeCols + 1];
+  sm[0][sl][ci] = M;
+  sm[1][sl][ci] = L;
+  sm[2][sl][ci] = O;
+  __syncthreads();
+  if (tid < kMergeCols) {
+    float Mt = sm[0][0][tid];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) Mt = fmaxf(Mt, sm[0][i][tid]);
     float Lt = 0.f, Ot = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float a = exp2f(sm[0][w][lane] - Mt);
-      Lt += sm[1][w][lane] * a;
-      Ot += sm[2][w][lane] * a;
+    for (int i = 0; i < NS; ++i) {
+      const float a = __builtin_amdgcn_exp2f(sm[0][i][tid] - Mt);
+      Lt += sm[1][i][tid] * a;
+      Ot += sm[2][i][tid] * a;
     }
-    out[(size_t)h * kD + d] = Ot / Lt;
+    out[(size_t)h * kD + blk * kMergeCols + tid] = Ot / Lt;
   }
 }
 
@@ -641,11 +613,11 @@ void launch_split_g(int hg_size, const SplitArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Launch shape of the fast path: query heads per workgroup (the largest of
-// 8/4/2/1 that divides the group and does not exceed the tuned size, default
-// 2), waves per workgroup (default 4) and positions per split (default: about
-// 512 workgroups in all, at least 64 positions each, at most kMaxSplits
-// splits per kv head), rounded to the workgroup's row step.
+// Launch shape of the VALU subgroup path: query heads per workgroup (the
+// largest of 8/4/2/1 that divides the group and does not exceed the tuned
+// size, default 2), waves per workgroup (default 8) and positions per split
+// (default: about 256 workgroups in all, at least 64 positions each), rounded
+// to the workgroup's row step.
 struct DecodeShape {
   int hg_size, waves, split_len;
 };
@@ -663,15 +635,30 @@ static DecodeShape pick_shape(const rv_kv* kv, int positions, int n_heads, int g
   const int step = d.waves * 4;
   long len = kv->tune_decode_split_len;
   if (len <= 0) {
-    // ~256 workgroups in all (measured best at ctx 4096, fp32: 16 splits of
-    // 256 positions for each of 16 (kv head, pair of heads) jobs).
     const long jobs = (long)n_heads * (group / d.hg_size);
     const long splits = std::max<long>(1, 256 / jobs);
     len = std::max<long>(64, ((long)positions + splits - 1) / splits);
   }
-  len = std::max<long>(len, ((long)positions + kMaxSplits - 1) / kMaxSplits);
   d.split_len = (int)((len + step - 1) / step * step);
   return d;
+}
+
+static void launch_merge(const float* part, int n_splits, int G, int group, int n_hg, int n_q, float* out,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(n_q * (kD / kMergeCols))), dim3(256), 0, s, part, n_splits,
+                     part_stride_of(G), G, group, n_hg, out);
+}
+
+template <typename T>
+static void launch_tile(int waves, dim3 grid, hipStream_t s, const float* q, const void* kl, const void* vl,
+                        int kv_dim, int positions, int split_len, int n_splits, int group, int kv_lo, float qscale,
+                        float* part, float* out) {
+  if (waves == 8)
+    hipLaunchKernelGGL((decode_tile_kernel<T, 8>), grid, dim3(512), 0, s, q, (const T*)kl, (const T*)vl, kv_dim,
+                       positions, split_len, n_splits, group, kv_lo, qscale, part, out);
+  else
+    hipLaunchKernelGGL((decode_tile_kernel<T, 4>), grid, dim3(256), 0, s, q, (const T*)kl, (const T*)vl, kv_dim,
+                       positions, split_len, n_splits, group, kv_lo, qscale, part, out);
 }
 
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
@@ -682,50 +669,32 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const void* kl = kv->k_layer(layer);
   const void* vl = kv->v_layer(layer);
-  // Kernel choice, from sweeps on MI355X: the MFMA kernel for f16 planes and
-  // very long contexts (where it streams fastest), the VALU subgroup kernel
-  // for fp32 planes up to 16K positions (where its shorter per-workgroup
-  // critical path wins).
-  const bool mfma = kv->tune_decode_impl == 2 ||
-                    (kv->tune_decode_impl == 0 && (kv->elem == RV_ELEM_F16 || positions > 16384));
-  if (kv->head_dim == kD && group <= 16 && mfma) {
-    // MFMA path: ~512 positions per split (at least one 16-position tile per
-    // wave), at most kMaxSplits splits.
-    const int waves = kv->tune_decode_waves == 8 ? 8 : 4;
+  const float qscale = scale * kLog2e;
+  if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1) {
+    // MFMA tile kernel. Default shape, from sweeps on MI355X: about 512
+    // workgroups in all, 4 waves (one tile each, 64 positions at ctx 4096)
+    // while splits stay short, 8 waves from 256 positions per split (ctx
+    // 32768: two tiles per wave); never less than one tile per wave.
+    const long want = ((long)positions * n_heads + 511) / 512;
+    const int waves = kv->tune_decode_waves == 8 || kv->tune_decode_waves == 4 ? (int)kv->tune_decode_waves
+                                                                               : (want >= 256 ? 8 : 4);
     const int step = waves * 16;
     long len = kv->tune_decode_split_len;
-    if (len <= 0) len = std::max<long>(step, std::min<long>(512, ((long)positions * n_heads + 255) / 256));
-    len = std::max<long>(len, ((long)positions + kMaxSplits - 1) / kMaxSplits);
+    if (len <= 0) len = want;
+    len = std::max<long>(len, step);
     const int split_len = (int)((len + step - 1) / step * step);
     const int n_splits = (int)((positions + split_len - 1) / split_len);
-    const size_t part_bytes = (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float);
-    st = ensure_workspace(kv, part_bytes, 0);
+    st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float), 0);
     if (st.e != hipSuccess) return st;
-    const dim3 grid((unsigned)(n_heads * n_splits));
     float* part = (float*)kv->ws;
-    const float qscale = scale * kLog2e;
-    if (kv->elem == RV_ELEM_F32) {
-      if (waves == 4)
-        hipLaunchKernelGGL((decode_mfma_kernel<float, 4>), grid, dim3(256), 0, s, q, (const float*)kl,
-                           (const float*)vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group, (int)kv_lo,
-                           qscale, part, out);
-      else
-        hipLaunchKernelGGL((decode_mfma_kernel<float, 8>), grid, dim3(512), 0, s, q, (const float*)kl,
-                           (const float*)vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group, (int)kv_lo,
-                           qscale, part, out);
-    } else {
-      if (waves == 4)
-        hipLaunchKernelGGL((decode_mfma_kernel<_Float16, 4>), grid, dim3(256), 0, s, q, (const _Float16*)kl,
-                           (const _Float16*)vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
-                           (int)kv_lo, qscale, part, out);
-      else
-        hipLaunchKernelGGL((decode_mfma_kernel<_Float16, 8>), grid, dim3(512), 0, s, q, (const _Float16*)kl,
-                           (const _Float16*)vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
-                           (int)kv_lo, qscale, part, out);
-    }
-    if (n_splits > 1)
-      hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(n_heads * group * 2)), dim3(256), 0, s,
-                         (const float*)part, n_splits, part_stride_of(group), group, group, 1, out);
+    const dim3 grid((unsigned)(n_heads * n_splits));
+    if (kv->elem == RV_ELEM_F32)
+      launch_tile<float>(waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
+                         (int)kv_lo, qscale, part, out);
+    else
+      launch_tile<_Float16>(waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
+                            (int)kv_lo, qscale, part, out);
+    if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
   } else if (kv->head_dim == kD) {
     const DecodeShape d = pick_shape(kv, (int)positions, n_heads, group);
     const int n_hg = group / d.hg_size;
@@ -735,7 +704,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     st = ensure_workspace(kv, part_bytes, 0);
     if (st.e != hipSuccess) return st;
     SplitArgs a{q, kl, vl, (int)kv->kv_dim, (int)positions, d.split_len, n_splits, n_heads * n_splits, group,
-                n_hg, (int)kv_lo, scale * kLog2e, (float*)kv->ws, out};
+                n_hg, (int)kv_lo, qscale, (float*)kv->ws, out};
     if (kv->elem == RV_ELEM_F32) {
       if (d.waves == 4) launch_split_g<float, 4>(d.hg_size, a, s);
       else launch_split_g<float, 8>(d.hg_size, a, s);
@@ -743,9 +712,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
       if (d.waves == 4) launch_split_g<_Float16, 4>(d.hg_size, a, s);
       else launch_split_g<_Float16, 8>(d.hg_size, a, s);
     }
-    if (n_splits > 1)
-      hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(n_jobs * d.hg_size * 2)), dim3(256), 0, s,
-                         (const float*)kv->ws, n_splits, part_stride_of(d.hg_size), d.hg_size, group, n_hg, out);
+    if (n_splits > 1) launch_merge((const float*)kv->ws, n_splits, d.hg_size, group, n_hg, n_jobs * d.hg_size, out, s);
   } else {
     const size_t hd = kv->head_dim;
     const int n_qr = n_heads * group;

@@ -36,7 +36,7 @@ struct rv_kv {
   int64_t tune_decode_waves = 0;
   int64_t tune_prefill_rows = 0;
   int64_t tune_decode_hg = 0;
-  int64_t tune_decode_impl = 0;  // 0 auto, 1 VALU subgroups, 2 MFMA (head_dim 128, group <= 16)
+  int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups
 
   size_t elem_size() const { return elem == RV_ELEM_F32 ? 4 : 2; }
   char* k_layer(size_t layer) const { return (char*)k + layer * plane * elem_size(); }
