@@ -6,11 +6,23 @@
 Headline ("config 2"): one step = 48 sequential
 decode-attention calls, one per layer, each over 4,096 cached positions of a
 fp32 KV cache (GQA 32/4, head_dim 128), through the C ABI with device
-pointers; inputs are resident in HBM before timing starts. `value` is the
-unique K+V+q+out bytes of all 48 calls per second of wall time (GB/s); the
-JSON line also carries µs per layer, the dominant kernel's roofline and the
-CPU baseline, plus the prefill TFLOP/s of configs 3 and 4 and the long
-context split-K decode of config 5 under "extra".
+pointers. The step is captured once into a HIP graph and replayed, the way a
+serving loop runs its per-token layer sequence; inputs are resident in HBM
+before timing starts. `value` is the unique K+V+q+out bytes of all 48 calls
+per second of wall time (GB/s). The eager (one host call per layer) step time
+is reported beside it.
+
+`roofline` is for the dominant kernel (the decode tile kernel): algorithmic
+bytes per launch over its average duration, timed live over eager steps with
+HIP events that the kernel launch itself fills with the kernel's start and
+end on the launch stream (RV_TUNE_KERNEL_TIMING, hipExtLaunchKernelGGL).
+`traffic` is the HBM bytes per launch read from the committed rocprofv3
+counter summary, when present.
+
+`extra` carries the other configurations: prefill TFLOP/s of configs 3 and 4
+in the three arithmetic modes and the long-context f16 decode of config 5.
+`cpu_baseline` is the C restatement of the reference's CPU decode path
+(oracle/, AVX2+F16C, kv-head fan-out) on a bounded sample of config 2.
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -19,6 +31,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -29,6 +42,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+DECODE_PROFILE = os.path.join(ROOT, "profiles", "decode_tile_ctx4096_f32.md")
 
 
 def log(*a):
@@ -36,8 +50,8 @@ def log(*a):
 
 
 def decode_bytes(positions: int, elem_bytes: int) -> int:
-    """Algorithmic bytes of one decode call: K and V head slices read once,
-    q read, out written (SURVEY 8d convention, benches/kernels.rs:245-270)."""
+    """Algorithmic bytes of one decode call: the layer's K and V head slices
+    read once, q read, out written (benches/kernels.rs:245-270 convention)."""
     return 2 * positions * 512 * elem_bytes + 2 * 4096 * 4
 
 
@@ -47,24 +61,40 @@ def prefill_flops(rows: int, start: int) -> int:
     return 4 * 128 * pairs * 32
 
 
-def time_region(torch, fn, iters: int):
-    """(wall seconds, event seconds) of `iters` calls on the current stream."""
-    s = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+def timed(torch, fn, iters: int) -> float:
+    """Wall seconds of `iters` calls, synchronised on both sides."""
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    e0.record(s)
     for _ in range(iters):
         fn()
-    e1.record(s)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return wall, e0.elapsed_time(e1) / 1e3
+    return time.perf_counter() - t0
+
+
+def kernel_avg(torch, kv, fn, iters: int):
+    """Average dominant-kernel duration (s) over `iters` eager calls of fn,
+    from the library's HIP events on the launch stream."""
+    kv.set_tuning(7, 1)
+    kv.kernel_time()  # reset
+    for _ in range(iters):
+        fn()
+    ms, n = kv.kernel_time()
+    kv.set_tuning(7, 0)
+    return (ms / 1e3 / n) if n else None, n
+
+
+def traffic_from_profile(path: str):
+    """HBM bytes per launch recorded in a committed counter summary."""
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", f.read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def bench_config2(torch, rv, synth, steps, warmup, keep_host):
-    c = synth.CONFIGS[2]
-    log(f"config 2: building 48-layer fp32 cache at ctx 4096 ...")
+    log("config 2: building 48-layer fp32 cache at ctx 4096 ...")
     kv = rv.KvCache(48, 4, 128, 4096, "f32")
     host_layers = []
     for layer in range(48):
@@ -84,18 +114,35 @@ def bench_config2(torch, rv, synth, steps, warmup, keep_host):
 
     for _ in range(warmup):
         step()
-    wall, ev = time_region(torch, step, steps)
-    per_step = wall / steps
-    launches = 48 * steps
-    avg_launch = ev / launches
+    eager = timed(torch, step, steps) / steps
+    ref = out.clone()
+
+    # The same step captured once and replayed.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    per_step = timed(torch, graph.replay, steps) / steps
+    graph_ok = bool(torch.equal(out, ref))
+
     byts = decode_bytes(4096, 4)
+    k_avg, k_n = kernel_avg(torch, kv, step, max(1, min(steps, 50)))
     return {
-        "kv": kv, "host_layers": host_layers, "q": q, "out": out,
+        "kv": kv, "host_layers": host_layers, "graph": graph, "graph_matches_eager": graph_ok,
         "ms_per_step": per_step * 1e3,
         "value_gbs": 48 * byts / per_step / 1e9,
-        "us_per_layer_wall": per_step / 48 * 1e6,
-        "us_per_launch_event": avg_launch * 1e6,
-        "achieved_gbs": byts / avg_launch / 1e9,
+        "us_per_layer": per_step / 48 * 1e6,
+        "eager_us_per_layer": eager / 48 * 1e6,
+        "eager_gbs": 48 * byts / eager / 1e9,
+        "kernel_us": k_avg * 1e6 if k_avg else None,
+        "kernel_launches_timed": k_n,
+        "achieved_gbs": byts / k_avg / 1e9 if k_avg else None,
         "bytes_per_launch": byts,
     }
 
@@ -119,10 +166,12 @@ def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
 
     for _ in range(3):
         once()
-    wall, ev = time_region(torch, once, iters)
+    wall = timed(torch, once, iters) / iters
+    k_avg, _ = kernel_avg(torch, kv, once, iters)
     flops = prefill_flops(rows, start)
-    return {"mode": mode, "us_per_call_wall": wall / iters * 1e6, "us_per_call_event": ev / iters * 1e6,
-            "tflops_event": flops / (ev / iters) / 1e12, "flops": flops}
+    return {"mode": mode, "us_per_call": round(wall * 1e6, 2), "us_attention_kernel": round(k_avg * 1e6, 2),
+            "tflops_call": round(flops / wall / 1e12, 2), "tflops_kernel": round(flops / k_avg / 1e12, 2),
+            "mfma_frac_kernel": round(flops / k_avg / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops}
 
 
 def bench_config5(torch, rv, synth, iters=50, n_caches=5):
@@ -145,11 +194,27 @@ def bench_config5(torch, rv, synth, iters=50, n_caches=5):
 
     for _ in range(3):
         once()
-    wall, ev = time_region(torch, once, iters)
-    per = ev / (iters * n_caches)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        once()
+    graph.replay()
+    per = timed(torch, graph.replay, iters) / (iters * n_caches)
+    tot, cnt = 0.0, 0
+    for kv in caches:
+        kv.set_tuning(7, 1)
+        kv.kernel_time()
+    for _ in range(iters):
+        once()
+    for kv in caches:
+        ms, c = kv.kernel_time()
+        kv.set_tuning(7, 0)
+        tot += ms
+        cnt += c
+    k_avg = tot / 1e3 / cnt
     byts = decode_bytes(n, 2)
-    return {"us_per_call_event": per * 1e6, "achieved_gbs": byts / per / 1e9, "bytes_per_call": byts,
-            "hbm_frac": byts / per / 1e9 / HBM_PEAK_GBS}
+    return {"us_per_call": round(per * 1e6, 3), "gbs_call": round(byts / per / 1e9, 1),
+            "us_kernel": round(k_avg * 1e6, 3), "gbs_kernel": round(byts / k_avg / 1e9, 1),
+            "hbm_frac_kernel": round(byts / k_avg / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": byts}
 
 
 def cpu_baseline(synth, host_layers, budget_s=12.0):
@@ -177,8 +242,8 @@ def cpu_baseline(synth, host_layers, budget_s=12.0):
         calls += 1
     per_layer = float(np.median(times))
     return {
-        "value": decode_bytes(4096, 4) / per_layer / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-        "us_per_layer": per_layer * 1e6,
+        "value": round(decode_bytes(4096, 4) / per_layer / 1e9, 3), "unit": "GB/s", "cores": threads,
+        "kind": "port", "us_per_layer": round(per_layer * 1e6, 1),
         "sample": f"{calls} decode calls (ctx 4096, fp32 KV) over {len(caches)} of the {n_layers} config-2 layers, "
                   f"median per call; oracle AVX2+F16C body, kv-head fan-out over {threads} threads",
     }
@@ -191,10 +256,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (the attention of one "
-              "layer shards by kv head, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (one layer's attention would "
+              "shard by kv head, one GPU per head group, with no exchange); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -203,23 +271,34 @@ def main():
     from ramvamp_amd import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        a = torch.ones(16 << 20, device="cuda")  # 64 MiB of f32
+        b = torch.empty_like(a)
+        for _ in range(10):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copied 10 x 64 MiB")
+        return
     r2 = bench_config2(torch, rv, synth, args.steps, args.warmup, keep_host=not args.no_cpu)
-    log(f"config 2: {r2['us_per_layer_wall']:.2f} us/layer wall, {r2['us_per_launch_event']:.2f} us/launch event, "
-        f"{r2['value_gbs']:.0f} GB/s")
-    extra = {}
+    log(f"config 2: {r2['us_per_layer']:.2f} us/layer (graph), {r2['eager_us_per_layer']:.2f} us/layer (eager), "
+        f"kernel {r2['kernel_us']:.2f} us, {r2['value_gbs']:.0f} GB/s")
+    extra = {"config2_eager": {"us_per_layer": round(r2["eager_us_per_layer"], 3),
+                               "gbs": round(r2["eager_gbs"], 1)},
+             "config2_graph_matches_eager": r2["graph_matches_eager"]}
     if not args.no_extra:
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
             r = bench_prefill(torch, rv, synth, cfg, mode)
-            extra[f"config{cfg}_prefill_{mode}"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}
-            log(f"config {cfg} {mode}: {r['us_per_call_event']:.1f} us, {r['tflops_event']:.1f} TFLOP/s")
+            extra[f"config{cfg}_prefill_{mode}"] = r
+            log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
+                f"{r['tflops_kernel']:.1f} TFLOP/s")
         r5 = bench_config5(torch, rv, synth)
-        extra["config5_decode_f16_ctx32768"] = {k: round(v, 4) for k, v in r5.items()}
-        log(f"config 5: {r5['us_per_call_event']:.2f} us, {r5['achieved_gbs']:.0f} GB/s")
+        extra["config5_decode_f16_ctx32768"] = r5
+        log(f"config 5: {r5['us_per_call']:.2f} us/call, kernel {r5['us_kernel']:.2f} us, {r5['gbs_kernel']:.0f} GB/s")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline(synth, r2["host_layers"])
-        cpu = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in cpu.items()}
+    traffic = traffic_from_profile(DECODE_PROFILE)
     line = {
         "metric": "decode attn µs/layer + HBM GB/s at ctx 4096; prefill attn TFLOP/s (512 tok)",
         "value": round(r2["value_gbs"], 2),
@@ -233,14 +312,15 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded N(0,1) K/V/q, ramvamp_amd/synth.py)",
-        "config": {"workload": "config 2: 48 sequential decode-attention layers, ctx 4096, fp32 KV, GQA 32/4, d 128",
+        "config": {"workload": "config 2: 48 sequential decode-attention layers, ctx 4096, fp32 KV, GQA 32/4, d 128, "
+                               "graph-replayed step",
                    "layers": 48, "context": 4096, "n_q_heads": 32, "n_kv_heads": 4, "head_dim": 128,
                    "kv_elem": "f32", "parallelism": "single GPU"},
-        "us_per_layer": round(r2["us_per_layer_wall"], 3),
+        "us_per_layer": round(r2["us_per_layer"], 3),
         "roofline": {"bound": "hbm", "achieved": round(r2["achieved_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_split_kernel<float, 8, *>",
-                     "us_per_launch": round(r2["us_per_launch_event"], 3),
+                     "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "decode_tile_kernel<float, 4>",
+                     "us_per_launch": round(r2["kernel_us"], 3), "launches_timed": r2["kernel_launches_timed"],
                      "bytes_per_launch": r2["bytes_per_launch"]},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -232,7 +232,18 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
 #define RV_TUNE_PREFILL_ROWS 4     /* query rows per prefill tile: 8 or 16 */
 #define RV_TUNE_DECODE_HG 5        /* query heads per VALU decode workgroup: 1, 2, 4 or 8 */
 #define RV_TUNE_DECODE_IMPL 6      /* decode kernel: 0 auto (MFMA tiles when head_dim 128 and group <= 16), 1 VALU subgroups */
+#define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
 int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
+
+/* No reference counterpart: benchmark instrumentation. With
+ * RV_TUNE_KERNEL_TIMING on, every decode/prefill call that is not being
+ * captured into a graph launches its dominant kernel (the tile/split decode
+ * kernel, the prefill kernel) with a pair of HIP events that record that
+ * kernel's own start and end on the cache's stream (hipExtLaunchKernelGGL).
+ * This synchronises the stream, returns the summed event time in
+ * milliseconds and the number of timed launches since the last read, and
+ * resets both. */
+int32_t rv_kv_kernel_time(rv_kv* kv, double* total_ms, uint64_t* launches, rv_error* err);
 
 #ifdef __cplusplus
 }

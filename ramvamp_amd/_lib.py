@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libramvamp_attn.so")
@@ -22,6 +22,11 @@ RV_ELEM_F16 = 1
 RV_ELEM_F32 = 2
 RV_TUNE_DECODE_SPLIT_LEN = 1
 RV_TUNE_PREFILL_KV_SPLIT = 2
+RV_TUNE_DECODE_WAVES = 3
+RV_TUNE_PREFILL_ROWS = 4
+RV_TUNE_DECODE_HG = 5
+RV_TUNE_DECODE_IMPL = 6
+RV_TUNE_KERNEL_TIMING = 7
 
 
 class RvError(ctypes.Structure):
@@ -72,6 +77,7 @@ SIGNATURES = {
     "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, _P, c_float, c_float, c_size_t,
                                    c_float, _P, c_uint32, _E]),
     "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
+    "rv_kv_kernel_time": (c_int32, [_P, POINTER(c_double), POINTER(c_uint64), _E]),
 }
 
 _lib = None

@@ -20,7 +20,7 @@ reference read the same here. Differences, all forced by the device:
 from __future__ import annotations
 
 import ctypes
-from ctypes import byref, c_size_t, c_uint64, c_void_p
+from ctypes import byref, c_double, c_size_t, c_uint64, c_void_p
 
 import numpy as np
 
@@ -270,6 +270,13 @@ class KvCache:
     def synchronize(self):
         err = L.RvError()
         _check(_lib().rv_kv_synchronize(self._h, byref(err)), err)
+
+    def kernel_time(self):
+        """(total milliseconds, launches) of the dominant kernels timed since
+        the last read (RV_TUNE_KERNEL_TIMING on); resets the tally."""
+        ms, n, err = c_double(), c_uint64(), L.RvError()
+        _check(_lib().rv_kv_kernel_time(self._h, byref(ms), byref(n), byref(err)), err)
+        return ms.value, n.value
 
 
 def scratch_len(n_q_heads: int, n_kv_heads: int, head_dim: int, max_positions: int) -> int:

@@ -211,6 +211,41 @@ int32_t check_rope_dim(const rv_kv* kv, rv_error* err) {
 
 namespace rv {
 
+constexpr size_t kMaxTimedPairs = 4096;  // pairs held before they are folded
+
+static bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+void timing_fold(rv_kv* kv) {
+  for (size_t i = 0; i + 1 < kv->ev_used; i += 2) {
+    float ms = 0.f;
+    if (hipEventSynchronize(kv->ev[i + 1]) == hipSuccess && hipEventElapsedTime(&ms, kv->ev[i], kv->ev[i + 1]) == hipSuccess) {
+      kv->timed_ms += ms;
+      kv->timed_n += 1;
+    }
+  }
+  kv->ev_used = 0;
+}
+
+TimedPair timing_pair(rv_kv* kv, hipStream_t s) {
+  TimedPair tp;
+  if (!kv->timing || capturing(s)) return tp;
+  if (kv->ev_used + 2 > 2 * kMaxTimedPairs) timing_fold(kv);
+  while (kv->ev.size() < kv->ev_used + 2) {
+    // Timing-only events: no system-scope fence when they complete, so the
+    // timed kernel ends as it would untimed (no extra L2 write-back).
+    hipEvent_t e;
+    if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return tp;
+    kv->ev.push_back(e);
+  }
+  tp.start = kv->ev[kv->ev_used];
+  tp.stop = kv->ev[kv->ev_used + 1];
+  kv->ev_used += 2;
+  return tp;
+}
+
 HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets) {
   HipStatus st;
   if (bytes > kv->ws_bytes) {
@@ -357,6 +392,7 @@ void rv_kv_free(rv_kv* kv) {
     else (void)hipDeviceSynchronize();
     for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->tickets, (void*)kv->qbuf, kv->stage})
       if (p) (void)hipFree(p);
+    for (hipEvent_t e : kv->ev) (void)hipEventDestroy(e);
   }
   delete kv;
 }
@@ -691,8 +727,23 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_PREFILL_ROWS: kv->tune_prefill_rows = value; break;
     case RV_TUNE_DECODE_HG: kv->tune_decode_hg = value; break;
     case RV_TUNE_DECODE_IMPL: kv->tune_decode_impl = value; break;
+    case RV_TUNE_KERNEL_TIMING: kv->timing = value != 0; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }
+  return ok(err);
+}
+
+int32_t rv_kv_kernel_time(rv_kv* kv, double* total_ms, uint64_t* launches, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  if (!total_ms || !launches) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, !total_ms ? "total_ms" : "launches");
+  DeviceGuard dg(kv->device);
+  const hipError_t e = kv->stream ? hipStreamSynchronize(kv->stream) : hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(err, e, "synchronize before reading kernel times");
+  rv::timing_fold(kv);
+  *total_ms = kv->timed_ms;
+  *launches = kv->timed_n;
+  kv->timed_ms = 0;
+  kv->timed_n = 0;
   return ok(err);
 }
 

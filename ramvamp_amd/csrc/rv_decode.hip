@@ -580,14 +580,15 @@ struct SplitArgs {
   float qscale;
   float* part;
   float* out;
+  TimedPair tp;
 };
 
 template <typename T, int G, int R, int W>
 void launch_split(const SplitArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8 * a.n_hg);
-  hipLaunchKernelGGL((decode_split_kernel<T, G, R, W>), dim3(blocks), dim3(W * 64), 0, s, a.q, (const T*)a.kl,
-                     (const T*)a.vl, a.kv_dim, a.positions, a.split_len, a.n_splits, a.n_units, a.group, a.n_hg,
-                     a.kv_lo, a.qscale, a.part, a.out);
+  launch_timed(a.tp, decode_split_kernel<T, G, R, W>, dim3(blocks), dim3(W * 64), s, a.q, (const T*)a.kl,
+               (const T*)a.vl, a.kv_dim, a.positions, a.split_len, a.n_splits, a.n_units, a.group, a.n_hg, a.kv_lo,
+               a.qscale, a.part, a.out);
 }
 
 template <typename T, int G, int W>
@@ -650,15 +651,15 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 }
 
 template <typename T>
-static void launch_tile(int waves, dim3 grid, hipStream_t s, const float* q, const void* kl, const void* vl,
-                        int kv_dim, int positions, int split_len, int n_splits, int group, int kv_lo, float qscale,
-                        float* part, float* out) {
+static void launch_tile(const TimedPair& tp, int waves, dim3 grid, hipStream_t s, const float* q, const void* kl,
+                        const void* vl, int kv_dim, int positions, int split_len, int n_splits, int group, int kv_lo,
+                        float qscale, float* part, float* out) {
   if (waves == 8)
-    hipLaunchKernelGGL((decode_tile_kernel<T, 8>), grid, dim3(512), 0, s, q, (const T*)kl, (const T*)vl, kv_dim,
-                       positions, split_len, n_splits, group, kv_lo, qscale, part, out);
+    launch_timed(tp, decode_tile_kernel<T, 8>, grid, dim3(512), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
+                 split_len, n_splits, group, kv_lo, qscale, part, out);
   else
-    hipLaunchKernelGGL((decode_tile_kernel<T, 4>), grid, dim3(256), 0, s, q, (const T*)kl, (const T*)vl, kv_dim,
-                       positions, split_len, n_splits, group, kv_lo, qscale, part, out);
+    launch_timed(tp, decode_tile_kernel<T, 4>, grid, dim3(256), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
+                 split_len, n_splits, group, kv_lo, qscale, part, out);
 }
 
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
@@ -688,11 +689,12 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     if (st.e != hipSuccess) return st;
     float* part = (float*)kv->ws;
     const dim3 grid((unsigned)(n_heads * n_splits));
+    const TimedPair tp = timing_pair(kv, s);
     if (kv->elem == RV_ELEM_F32)
-      launch_tile<float>(waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
+      launch_tile<float>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
                          (int)kv_lo, qscale, part, out);
     else
-      launch_tile<_Float16>(waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
+      launch_tile<_Float16>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
                             (int)kv_lo, qscale, part, out);
     if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
   } else if (kv->head_dim == kD) {
@@ -704,7 +706,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     st = ensure_workspace(kv, part_bytes, 0);
     if (st.e != hipSuccess) return st;
     SplitArgs a{q, kl, vl, (int)kv->kv_dim, (int)positions, d.split_len, n_splits, n_heads * n_splits, group,
-                n_hg, (int)kv_lo, qscale, (float*)kv->ws, out};
+                n_hg, (int)kv_lo, qscale, (float*)kv->ws, out, timing_pair(kv, s)};
     if (kv->elem == RV_ELEM_F32) {
       if (d.waves == 4) launch_split_g<float, 4>(d.hg_size, a, s);
       else launch_split_g<float, 8>(d.hg_size, a, s);

@@ -2,6 +2,7 @@
 // launchers the C ABI (rv_abi.cpp) drives. Not part of the public ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -38,6 +39,14 @@ struct rv_kv {
   int64_t tune_decode_hg = 0;
   int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups
 
+  // RV_TUNE_KERNEL_TIMING: event pairs around the dominant kernel of each
+  // call, folded into timed_ms / timed_n when read (or when the pool fills).
+  bool timing = false;
+  std::vector<hipEvent_t> ev;
+  size_t ev_used = 0;
+  double timed_ms = 0;
+  uint64_t timed_n = 0;
+
   size_t elem_size() const { return elem == RV_ELEM_F32 ? 4 : 2; }
   char* k_layer(size_t layer) const { return (char*)k + layer * plane * elem_size(); }
   char* v_layer(size_t layer) const { return (char*)v + layer * plane * elem_size(); }
@@ -54,6 +63,25 @@ struct HipStatus {
 // Workspace (>= bytes) and tickets (>= n) on the cache's device.
 HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets);
 HipStatus ensure_qbuf(rv_kv* kv, size_t bytes);
+
+// RV_TUNE_KERNEL_TIMING: the event pair the next dominant-kernel launch
+// records its own start and end into (hipExtLaunchKernelGGL), or two nulls
+// when timing is off or the stream is being captured.
+struct TimedPair {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+TimedPair timing_pair(rv_kv* kv, hipStream_t s);
+// Adds every recorded pair to timed_ms / timed_n (waits for the last one).
+void timing_fold(rv_kv* kv);
+
+// Launch that fills `tp` with the kernel's start and end when it is set.
+template <typename F, typename... Args>
+inline void launch_timed(const TimedPair& tp, F kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
+  if (tp.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, tp.start, tp.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
 
 // True when the MFMA prefill kernel covers this geometry (else the ABI runs
 // each row through the decode kernel with its own position limit).

@@ -373,13 +373,13 @@ struct PrefillArgs {
   float* part;
   unsigned* tickets;
   float* out;
+  TimedPair tp;
 };
 
 template <int MODE, typename T, int MT, int ROWS>
 void launch_one(const PrefillArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((prefill_kernel<MODE, T, MT, ROWS>), a.grid, dim3(kWG), 0, s, a.q, (const T*)a.kl,
-                     (const T*)a.vl, a.kv_dim, a.q_stride, a.rows, a.start, a.group, a.kv_splits, a.qscale, a.part,
-                     a.tickets, a.out);
+  launch_timed(a.tp, prefill_kernel<MODE, T, MT, ROWS>, a.grid, dim3(kWG), s, a.q, (const T*)a.kl, (const T*)a.vl,
+               a.kv_dim, a.q_stride, a.rows, a.start, a.group, a.kv_splits, a.qscale, a.part, a.tickets, a.out);
 }
 
 // MT = column blocks per wave = ceil(group * ROWS / 16 / 4).
@@ -442,7 +442,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   }
   PrefillArgs a{dim3((unsigned)kv_splits, (unsigned)n_rt, (unsigned)n_kv), q_rows, kv->k_layer(layer),
                 kv->v_layer(layer), (int)kv->kv_dim, (int)(n_q_heads * kD), (int)rows, (int)start, group,
-                kv_splits, scale * kLog2e, (float*)kv->ws, kv->tickets, out};
+                kv_splits, scale * kLog2e, (float*)kv->ws, kv->tickets, out, timing_pair(kv, s)};
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
   if (kv->elem == RV_ELEM_F32)
     launch_t<float>(m, rows_per_tile, mt, a, s);

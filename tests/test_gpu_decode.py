@@ -236,6 +236,26 @@ def test_split_lengths_agree_within_tolerance(split_len):
     gate(out, want, what="decode")
 
 
+@pytest.mark.parametrize("impl,waves", [(0, 4), (0, 8), (1, 4), (1, 8)])
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_kernel_variants_agree_with_the_oracle(impl, waves, elem):
+    """Both fast kernels (MFMA tiles, VALU subgroups) at both workgroup sizes,
+    with splits of one and of several tiles per wave."""
+    torch_cuda()
+    say(f"case impl={impl} waves={waves} elem={elem}")
+    rng = Rng(0x7EA1 + 16 * impl + waves)
+    kv, ref = twin_caches(rng, 1, 4, 128, 2049, elem)
+    kv.set_tuning(6, impl)
+    kv.set_tuning(3, waves)
+    q = rng.vec_in(32 * 128, -2.0, 2.0)
+    for split_len in (0, 64, 200, 4096):
+        kv.set_tuning(1, split_len)
+        for p in (1, 15, 16, 65, 2049):
+            out = np.zeros(q.size, np.float32)
+            rv.attention_at(q, kv, 0, p, 0.3, None, out)
+            gate(out, ref.attention(q, 0, 0.3, positions=p), what=f"impl {impl} waves {waves} split {split_len} p {p}")
+
+
 def test_config1_decode_step_matches_the_oracle():
     # BASELINE config 1: cached rows 0..511 built by the fused prefill prologue,
     # then the fused decode step at position 512 (prologue + append + decode).

@@ -1,0 +1,75 @@
+"""Decode calls captured into a HIP graph: every replay matches the eager
+result bit for bit (the calls queue no memset and allocate nothing once the
+cache's workspace exists), with eager work and synchronisations between
+replays; and the kernel-timing instrumentation counts what it brackets."""
+import numpy as np
+import pytest
+
+import ramvamp_amd as rv
+from gpu_util import dev, host, say, torch_cuda
+from helpers import Rng
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_graph_replays_match_eager(elem):
+    torch = torch_cuda()
+    say(f"case graph replay elem={elem}")
+    rng = Rng(0x6A7F)
+    n_layers, n_pos = 3, 1000
+    kv = rv.KvCache(n_layers, 4, 128, n_pos, elem)
+    for layer in range(n_layers):
+        K = rng.vec_in(n_pos * 512, -1.0, 1.0).reshape(n_pos, -1)
+        V = rng.vec_in(n_pos * 512, -1.0, 1.0).reshape(n_pos, -1)
+        kv.append_rows(layer, K, V)
+    q = dev(rng.vec_in(n_layers * 4096, -1.0, 1.0).reshape(n_layers, 4096))
+    out = torch.zeros_like(q)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+    def eager_ref():
+        out.zero_()
+        for layer in range(n_layers):
+            rv.decode_attention(q[layer], kv, layer, scale, None, out[layer])
+        return host(out).copy()
+
+    want = eager_ref()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for layer in range(n_layers):
+            rv.decode_attention(q[layer], kv, layer, scale, None, out[layer])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for layer in range(n_layers):
+            rv.decode_attention(q[layer], kv, layer, scale, None, out[layer])
+    for rep in range(5):
+        out.fill_(float("nan"))
+        g.replay()
+        got = host(out)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}"
+        again = eager_ref()  # eager work between replays
+        assert np.array_equal(again.view(np.uint32), want.view(np.uint32)), f"eager after replay {rep}"
+
+
+def test_kernel_timing_counts_bracketed_launches():
+    torch = torch_cuda()
+    say("case kernel timing")
+    rng = Rng(0x71E)
+    kv = rv.KvCache(1, 4, 128, 512, "f32")
+    K = rng.vec_in(512 * 512, -1.0, 1.0).reshape(512, -1)
+    kv.append_rows(0, K, K)
+    q = dev(rng.vec_in(4096, -1.0, 1.0))
+    out = torch.zeros_like(q)
+    assert kv.kernel_time() == (0.0, 0)
+    rv.decode_attention(q, kv, 0, 0.1, None, out)
+    assert kv.kernel_time() == (0.0, 0)  # timing off: nothing recorded
+    kv.set_tuning(7, 1)
+    for _ in range(3):
+        rv.decode_attention(q, kv, 0, 0.1, None, out)
+    ms, n = kv.kernel_time()
+    assert n == 3 and ms > 0.0, (ms, n)
+    assert kv.kernel_time() == (0.0, 0)  # reset by the read
+    kv.set_tuning(7, 0)
