@@ -10,37 +10,40 @@ import math
 import numpy as np
 import pytest
 
+import json
+import os
+
 import oracle
 from helpers import Rng, assert_close, reference_attention, round_trip
+
+# Known answers the reference's own tests assert, kept as data.
+with open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")) as _f:
+    KATS = json.load(_f)
 
 F16_SUBNORMAL_ULP = np.float32(2.0 ** -24)
 
 
 # ---- f16 (kernels/quants/f16.rs:97-160) ---------------------------------------
 
+def _f32(bits_hex):
+    return np.array([int(bits_hex, 16)], dtype=np.uint32).view(np.float32)[0]
+
+
 def test_f16_to_f32_known_vectors():
-    # f16.rs:97-113
-    cases = {0x0000: 0.0, 0x3C00: 1.0, 0xC100: -2.5, 0x7BFF: 65504.0, 0x0001: F16_SUBNORMAL_ULP,
-             0x03FF: 1023.0 * F16_SUBNORMAL_ULP, 0x8001: -F16_SUBNORMAL_ULP, 0x7C00: np.inf, 0xFC00: -np.inf,
-             0x3555: np.float32(0.33325195)}
-    for bits, want in cases.items():
-        assert oracle.f16_to_f32([bits])[0] == np.float32(want), hex(bits)
-    neg0 = oracle.f16_to_f32([0x8000])[0]
-    assert neg0 == 0.0 and math.copysign(1.0, neg0) < 0
-    assert np.isnan(oracle.f16_to_f32([0x7E00])[0]) and np.isnan(oracle.f16_to_f32([0xFE01])[0])
+    kat = KATS["f16_to_f32"]  # f16.rs:97-113
+    for case in kat["cases"]:
+        got = oracle.f16_to_f32([int(case["f16"], 16)])[0]
+        assert np.float32(got).view(np.uint32) == _f32(case["f32_bits"]).view(np.uint32), case
+    for bits in kat["nan_inputs"]:
+        assert np.isnan(oracle.f16_to_f32([int(bits, 16)])[0])
 
 
 def test_f32_to_f16_known_vectors():
-    # f16.rs:116-133
-    cases = [(0.0, 0x0000), (-0.0, 0x8000), (1.0, 0x3C00), (-2.5, 0xC100), (65504.0, 0x7BFF), (65520.0, 0x7C00),
-             (1e9, 0x7C00), (np.inf, 0x7C00), (-np.inf, 0xFC00), (F16_SUBNORMAL_ULP, 0x0001),
-             (0.5 * F16_SUBNORMAL_ULP, 0x0000), (0.75 * F16_SUBNORMAL_ULP, 0x0001), (1e-10, 0x0000),
-             (-1e-10, 0x8000)]
-    for x, want in cases:
-        assert int(oracle.f32_to_f16([x])[0]) == want, x
-    assert np.isnan(oracle.f16_to_f32(oracle.f32_to_f16([np.nan]))[0])
-    payload = np.array([0x7F800001], dtype=np.uint32).view(np.float32)
-    assert np.isnan(oracle.f16_to_f32(oracle.f32_to_f16(payload))[0])
+    kat = KATS["f32_to_f16"]  # f16.rs:116-133, ties to even :153-160
+    for case in kat["cases"]:
+        assert int(oracle.f32_to_f16([_f32(case["f32_bits"])])[0]) == int(case["f16"], 16), case
+    for bits in kat["nan_inputs_f32_bits"]:
+        assert np.isnan(oracle.f16_to_f32(oracle.f32_to_f16([_f32(bits)]))[0])
 
 
 def test_f16_round_trip_all_finite_and_ties_to_even():
@@ -73,7 +76,8 @@ def test_f16_matches_ieee_library_conversion():
 # ---- softmax / rmsnorm / rope ----------------------------------------------------
 
 def test_softmax_closed_forms_and_f64_reference():
-    assert oracle.softmax([-1234.5])[0] == np.float32(1.0)  # softmax.rs:103-107
+    kat = KATS["softmax_single_element"]  # softmax.rs:103-107
+    assert oracle.softmax(kat["input"])[0] == np.float32(kat["expected"][0])
     for n in (1, 3, 1000):  # softmax.rs:90-100
         assert_close(oracle.softmax(np.full(n, 42.5, np.float32)), np.full(n, 1.0 / n), 1e-6, 0.0, "all equal")
     a = np.float32(0.7)
@@ -97,17 +101,16 @@ def test_rmsnorm_closed_forms():
         xd = x.astype(np.float64)
         want = xd / np.sqrt(np.mean(xd * xd) + float(eps)) * w
         assert_close(oracle.rmsnorm(x, w, eps), want, 1e-6, 1e-30, f"rmsnorm n={n}")
-    assert np.all(oracle.rmsnorm([1, 2, 3, 4], np.zeros(4), eps) == 0.0)  # norm.rs:184-191
+    kat = KATS["rmsnorm_zero_weight"]  # norm.rs:184-191
+    assert np.array_equal(oracle.rmsnorm(kat["input"], kat["weight"], eps), np.asarray(kat["expected"], np.float32))
     assert_close(oracle.rmsnorm(np.full(512, 3.0), np.ones(512), eps), np.ones(512), 1e-6, 0.0, "all equal")
 
 
 def test_rope_known_angles_head_dim_4_theta_1e7():
-    # rope.rs:144-175: hand-computed f64 values for [1, 2, 3, 4].
-    cases = [(1, [-1.9841106485555495, 1.9987349889570154, 2.4623779024123156, 4.000632255521494]),
-             (3, [-1.413352520780047, 1.9962043673770753, -2.828857481741469, 4.001895566311631])]
-    for pos, want in cases:
-        got = oracle.rope_neox_heads([1.0, 2.0, 3.0, 4.0], 1, 4, pos, 1e7)
-        assert_close(got, want, 1e-6, 1e-30, f"rope pos {pos}")
+    kat = KATS["rope_neox_head_dim4_theta_1e7"]  # rope.rs:144-175: hand-computed f64 values
+    for case in kat["cases"]:
+        got = oracle.rope_neox_heads(kat["input"], 1, 4, case["position"], kat["theta"])
+        assert_close(got, case["expected"], kat["tolerance"]["rel"], 1e-30, f"rope pos {case['position']}")
 
 
 def test_rope_identity_magnitude_and_f64_reference():
@@ -289,7 +292,8 @@ def test_doubling_scale_squares_the_odds_ratio():
 
 
 def test_scratch_len_pins():
-    assert oracle.scratch_len(32, 4, 128, 4096) == 33_024  # attention.rs:2330-2342
+    kat = KATS["scratch_len"]  # attention.rs:2330-2342
+    assert oracle.scratch_len(*kat["args"]) == kat["expected"]
     assert oracle.scratch_len(32, 4, 8, 17) == 8 * 17 + 2 * 8
     assert oracle.scratch_len(32, 0, 8, 17) == 16
     assert oracle.scratch_len(2 ** 63, 1, 2, 4) == 2 ** 64 - 1
@@ -449,3 +453,56 @@ def test_scatter_attention_matches_per_row_attention_at():
     for threads in (1, 2, 3, 8):
         got = kv.scatter_attention(q, 0, start, scale, threads)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), threads
+
+
+# ---- fused callers (model/forward.rs:2622-2633, model/prefill.rs:2057-2109) -------------
+
+def _norm_rope_f64(x, n_heads, hd, w, eps, theta, pos):
+    """f64 textbook of one token's per-head RMSNorm then NeoX RoPE at `pos`."""
+    h = np.asarray(x, np.float64).reshape(n_heads, hd)
+    h = h / np.sqrt(np.mean(h * h, axis=1, keepdims=True) + float(eps)) * np.asarray(w, np.float64)
+    half = hd // 2
+    i = np.arange(half, dtype=np.float64)
+    ang = pos * np.power(float(np.float32(theta)), -2.0 * i / hd)
+    a, b = h[:, :half], h[:, half:]
+    return np.concatenate([a * np.cos(ang) - b * np.sin(ang), a * np.sin(ang) + b * np.cos(ang)], axis=1).reshape(-1)
+
+
+def test_decode_step_and_prefill_chunk_match_the_f64_composition():
+    # The order the callers fix: q and k heads normed, then rotated at the
+    # token's position (= the layer's length before the append), k and v
+    # appended, then attention over every position including the new one; a
+    # prefill row r sits at start + r and attends start + r + 1 positions.
+    n_kv, n_q, hd, eps, theta = 2, 8, 16, np.float32(1e-6), np.float32(1e6)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    rng = Rng(0xF05E)
+    wq, wk = rng.vec_in(hd, 0.5, 1.5), rng.vec_in(hd, 0.5, 1.5)
+    start = 9
+    cached_k = rng.vec_in(start * n_kv * hd, -1.0, 1.0).reshape(start, -1)
+    cached_v = rng.vec_in(start * n_kv * hd, -1.0, 1.0).reshape(start, -1)
+    # decode step
+    kv = oracle.KvCache(1, n_kv, hd, start + 8, oracle.RV_ELEM_F32)
+    kv.append_rows(0, cached_k, cached_v)
+    q, k, v = rng.vec_in(n_q * hd, -2.0, 2.0), rng.vec_in(n_kv * hd, -2.0, 2.0), rng.vec_in(n_kv * hd, -1.0, 1.0)
+    got = kv.decode_step(0, q, k, v, wq, wk, eps, theta, start, scale)
+    kn = _norm_rope_f64(k, n_kv, hd, wk, eps, theta, start)
+    qn = _norm_rope_f64(q, n_q, hd, wq, eps, theta, start)
+    assert kv.len(0) == start + 1
+    assert_close(kv.read_row(False, 0, start), kn, 1e-5, 1e-6, "appended k row")
+    assert np.array_equal(kv.read_row(True, 0, start), v)
+    want = reference_attention(qn, np.vstack([cached_k, kn]), np.vstack([cached_v, v]), n_kv, hd, scale)
+    assert_close(got, want, 1e-4, 5e-5, "decode step")
+    # prefill chunk of 5 rows after the same prefix
+    rows = 5
+    kv = oracle.KvCache(1, n_kv, hd, start + rows, oracle.RV_ELEM_F32)
+    kv.append_rows(0, cached_k, cached_v)
+    qr = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+    kr = rng.vec_in(rows * n_kv * hd, -2.0, 2.0).reshape(rows, -1)
+    vr = rng.vec_in(rows * n_kv * hd, -1.0, 1.0).reshape(rows, -1)
+    got = kv.prefill_chunk(0, qr, kr, vr, wq, wk, eps, theta, start, scale)
+    kall = np.vstack([cached_k] + [_norm_rope_f64(kr[r], n_kv, hd, wk, eps, theta, start + r) for r in range(rows)])
+    vall = np.vstack([cached_v, vr])
+    for r in range(rows):
+        qn = _norm_rope_f64(qr[r], n_q, hd, wq, eps, theta, start + r)
+        n = start + r + 1
+        assert_close(got[r], reference_attention(qn, kall[:n], vall[:n], n_kv, hd, scale), 1e-4, 5e-5, f"row {r}")
