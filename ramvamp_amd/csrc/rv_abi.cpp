@@ -584,7 +584,7 @@ static int32_t rows_plan(const rv_kv* kv, size_t rows, size_t q_dim, size_t laye
 static int32_t run_rows(rv_kv* kv, const float* dq, size_t rows, size_t q_dim, size_t layer, size_t start,
                         const Plan& p, float scale, float* dout, uint32_t flags, rv_error* err) {
   rv::HipStatus hs;
-  if (rv::prefill_supported(kv->head_dim, p.group)) {
+  if (rv::prefill_supported(kv, p.group, start + rows)) {
     hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, kv->stream);
   } else {
     for (size_t r = 0; r < rows && hs.e == hipSuccess; ++r)

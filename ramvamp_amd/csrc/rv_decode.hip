@@ -310,17 +310,12 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
 
   float qv[32];
   {
+    // q may be only 4-byte aligned: scalar loads (once per workgroup).
     const float* qp = q + (size_t)(kvh * group + (col_ok ? li : 0)) * kD;
 #pragma unroll
     for (int c = 0; c < NKC; ++c)
 #pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(qp + E * (lk + 4 * c) + e);
-        qv[c * E + e] = x[0];
-        qv[c * E + e + 1] = x[1];
-        qv[c * E + e + 2] = x[2];
-        qv[c * E + e + 3] = x[3];
-      }
+      for (int e = 0; e < E; ++e) qv[c * E + e] = qp[E * (lk + 4 * c) + e];
   }
   CT kb[NKC], vb[NVC];
   // Rows past the split re-read its last row (in bounds, branch-free); their

@@ -83,9 +83,9 @@ inline void launch_timed(const TimedPair& tp, F kernel, dim3 grid, dim3 block, h
     hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
 }
 
-// True when the MFMA prefill kernel covers this geometry (else the ABI runs
-// each row through the decode kernel with its own position limit).
-bool prefill_supported(size_t head_dim, size_t group);
+// True when the MFMA prefill kernel covers this geometry and extent (else the
+// ABI runs each row through the decode kernel with its own position limit).
+bool prefill_supported(const rv_kv* kv, size_t group, size_t positions);
 
 // ---- prologue / append (rv_prologue.hip) ------------------------------------
 // RoPE inverse frequencies theta^(-2i/d) for i < d/2, computed on the host in

@@ -4,28 +4,41 @@
 // (crates/core/src/model/prefill.rs:1322-1408 -> kernels/attention.rs:732):
 // query row r of the chunk attends cache positions 0..start+r+1.
 //
-// Tiling. One workgroup (4 waves) per (kv head, tile of ROWS query rows, kv
-// split). The tile's query vectors are its ROWS rows of every q head of the
-// GQA group, so each K/V tile staged in LDS serves all `group` heads. A 16x16
-// MFMA column block holds 16/ROWS heads x ROWS rows; wave w owns column
-// blocks w, w+4, .... Per 32-position K/V tile:
-//   S^T[t][m] = sum_d K[t][d] Q[m][d]      (A = K from LDS, B = Q in VGPRs)
-//   O^T[d][m] += sum_t V[t][d] P[m][t]     (A = V^T from LDS, B = P in VGPRs)
-// on v_mfma_f32_16x16x32_{f16,bf16}. Computing S transposed puts each query
-// vector's scores in one lane (4 consecutive t per 16x16 block), which is
-// exactly the B-operand layout P^T needs, so P never leaves registers.
+// Two kernels per call (plus a merge when the KV axis is split):
+//
+// 1. prefill_stage_kernel converts the layer's K and V rows [0, positions)
+//    once into the MFMA element type (f16 / bf16, or hi + lo f16 for the
+//    split mode) and lays each 64-position tile out exactly as the attention
+//    kernel wants it in LDS: K row-major, V transposed with its positions
+//    permuted into the order the S^T accumulator produces P, both with their
+//    16-byte chunks XOR-swizzled so the MFMA operand reads are free of bank
+//    conflicts. Every row block of the chunk then re-reads this compact copy
+//    (half the bytes of an fp32 cache) instead of converting on the fly.
+//
+// 2. prefill_kernel: one workgroup (4 waves) per (kv head, block of M/group
+//    query rows, KV split). Its M = 128 (or 64) query vectors are every q head
+//    of the GQA group for each of its rows, so each staged K/V tile feeds all
+//    heads: column m is head m / qr, row m % qr (qr = M / group); wave w owns
+//    columns [16*MT*w, 16*MT*(w+1)). Tiles stream into a ring of NS LDS
+//    stages with direct-to-LDS loads (global_load_lds_dwordx4: no registers,
+//    no conversion), NS - 1 tiles ahead of the one being computed. Per tile:
+//      S^T[t][m] = sum_d K[t][d] Q[m][d]      (A = K from LDS, B = Q in VGPRs)
+//      O^T[d][m] += sum_t V[t][d] P[m][t]     (A = V^T from LDS, B = P in VGPRs)
+//    on v_mfma_f32_16x16x32_{f16,bf16}. Computing S transposed puts a query
+//    vector's scores in one lane (4 consecutive t per 16x16 block), which is
+//    the B-operand layout P^T needs, so P never leaves registers.
 //
 // Arithmetic modes (flags RV_PREFILL_*):
 //   EXACT: each operand split as hi + lo f16 (lo = f16(x - hi)); products
 //          hi*hi + hi*lo + lo*hi, fp32 accumulate: ~2^-21 relative products,
 //          the fp32 parity mode.
 //   F16 / BF16: one MFMA per product, fp32 accumulate.
-// Softmax is online in fp32 (exp2, log2(e) folded into the score scale).
+// Softmax is online in fp32 (exp2, log2(e) folded into the score scale), with
+// the running maximum moved only when a tile exceeds it by 2^8.
 //
-// KV splits are used only when the row tiles alone leave most of the chip
-// idle (short chunks): each split writes partial (O, max, sum) rows and the
-// last workgroup of a (kv head, row tile) to finish merges them, with split
-// maxima and weights staged in LDS and 16-byte partial loads.
+// KV splits (short chunks, too few row blocks to fill the chip): each split
+// writes partial (O, max, sum) columns; prefill_merge_kernel folds them with
+// an fp32 log-sum-exp in a further launch (the splits run on different XCDs).
 #include "rv_device.hpp"
 #include "rv_internal.hpp"
 
@@ -36,12 +49,13 @@ namespace {
 
 constexpr int kWG = 256;
 constexpr int kD = 128;
-constexpr int kBT = 32;          // positions per K/V tile
-constexpr int kKPad = kD + 8;    // LDS row stride of K (halves)
-constexpr int kVPad = kBT + 8;   // LDS row stride of V^T (halves)
+constexpr int kBT = 64;             // positions per K/V tile
+constexpr int kPlaneBytes = 16384;  // one staged 64 x 128 plane of 2-byte elements
 constexpr int kMaxKvSplits = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegSentinel = -1.0e30f;
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 enum Mode { kExact = 0, kF16 = 1, kBF16 = 2 };
 
@@ -51,6 +65,7 @@ template <>
 struct Op<kExact> {
   typedef _Float16 E;
   typedef f16x8 V8;
+  typedef f16x4 V4;
   static constexpr bool kSplit = true;
   __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 };
@@ -58,6 +73,7 @@ template <>
 struct Op<kF16> {
   typedef _Float16 E;
   typedef f16x8 V8;
+  typedef f16x4 V4;
   static constexpr bool kSplit = false;
   __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 };
@@ -65,224 +81,314 @@ template <>
 struct Op<kBF16> {
   typedef __bf16 E;
   typedef bf16x8 V8;
+  typedef bf16x4 V4;
   static constexpr bool kSplit = false;
   __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 };
 
-// hi = round(x), lo = round(x - hi) (lo only matters in the split mode).
-template <typename E>
-__device__ __forceinline__ void split2(float x, E& hi, E& lo) {
-  hi = (E)x;
-  lo = (E)(x - (float)hi);
+// hi = round(x); lo = round(x - hi), into element e of two vectors.
+template <typename E, typename V>
+__device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
+  const E h = (E)x;
+  hi[e] = h;
+  lo[e] = (E)(x - (float)h);
 }
 
-template <typename T>
-__device__ __forceinline__ void load16(const T* p, float (&x)[16]);
-template <>
-__device__ __forceinline__ void load16<float>(const float* p, float (&x)[16]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f32x4 a = reinterpret_cast<const f32x4*>(p)[i];
-    x[4 * i] = a[0];
-    x[4 * i + 1] = a[1];
-    x[4 * i + 2] = a[2];
-    x[4 * i + 3] = a[3];
-  }
-}
-template <>
-__device__ __forceinline__ void load16<_Float16>(const _Float16* p, float (&x)[16]) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    f16x8 a = reinterpret_cast<const f16x8*>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)a[j];
-  }
+// ---- staged tile layout -------------------------------------------------------------
+// One tile = P planes of K, then P planes of V^T (P = 2 in the split mode:
+// hi, lo), each plane 16 KiB of 16-byte chunks (8 elements).
+//   K plane: row t (64) x chunk c (16): elements d = 8c .. 8c+7, stored at
+//     byte 256 t + 16 (c ^ (t & 15)).
+//   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot
+//     j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
+//     (j >= 4); stored at byte 128 d + 16 (c ^ ((d >> 1) & 7)).
+// The swizzles put the 16 lanes of one operand read on 16 distinct 16-byte
+// bank groups.
+__device__ __forceinline__ int k_off(int t, int c) { return 256 * t + 16 * (c ^ (t & 15)); }
+__device__ __forceinline__ int vt_off(int d, int c) { return 128 * d + 16 * (c ^ ((d >> 1) & 7)); }
+__device__ __forceinline__ int vt_pos(int c, int j) {
+  const int s2 = c >> 2, k = c & 3;
+  return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
 }
 
-// Partial layout per (kv head, row tile, split): O[g][r][d], then (max, sum)[g][r],
-// padded to a 16-byte multiple.
-__host__ __device__ constexpr size_t part_stride(int group, int rows) {
-  return (size_t)group * rows * kD + ((size_t)2 * group * rows + 3) / 4 * 4;
-}
-
-template <int MODE, typename T, int MT, int ROWS>
-__global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ q, const T* __restrict__ kl,
-                                                      const T* __restrict__ vl, int kv_dim, int q_stride,
-                                                      int rows, int start, int group, int kv_splits,
-                                                      float qscale, float* __restrict__ part,
-                                                      unsigned* __restrict__ tickets, float* __restrict__ out) {
+// Stage kernel: one workgroup per (kv head, tile). Rows at or past
+// `positions` are staged as zeros.
+template <int MODE, typename T>
+__global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict__ kl, const T* __restrict__ vl,
+                                                            int kv_dim, int positions, int n_tiles,
+                                                            char* __restrict__ stage) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
+  constexpr int P = Op<MODE>::kSplit ? 2 : 1;
+  const int tile = blockIdx.x % n_tiles, kvh = blockIdx.x / n_tiles;
+  const int tid = threadIdx.x;
+  char* dst = stage + ((size_t)kvh * n_tiles + tile) * (2 * P * kPlaneBytes);
+  const int t0 = tile * kBT;
+  const size_t col = (size_t)kvh * kD;
+  __shared__ float vt[kBT][kD + 1];
+
+  // Thread -> row r = tid / 4, elements 32 (tid % 4) .. +31 of K and of V.
+  const int r = tid >> 2, cb = (tid & 3) * 4;
+  const bool live = t0 + r < positions;
+  const T* kp = kl + (size_t)(live ? t0 + r : 0) * kv_dim + col + 8 * cb;
+  const T* vp = vl + (size_t)(live ? t0 + r : 0) * kv_dim + col + 8 * cb;
+  float kx[32], vx[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    kx[i] = live ? (float)kp[i] : 0.f;
+    vx[i] = live ? (float)vp[i] : 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    V8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split2v<E>(kx[8 * c + e], hi, lo, e);
+    *reinterpret_cast<V8*>(dst + k_off(r, cb + c)) = hi;
+    if constexpr (P == 2) *reinterpret_cast<V8*>(dst + kPlaneBytes + k_off(r, cb + c)) = lo;
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) vt[r][8 * cb + i] = vx[i];
+  __syncthreads();
+  // Thread -> V^T row d = tid / 2, chunks 4 (tid % 2) .. +3.
+  const int d = tid >> 1;
+  char* vdst = dst + P * kPlaneBytes;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    const int c = 4 * (tid & 1) + cc;
+    V8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) split2v<E>(vt[vt_pos(c, j)][d], hi, lo, j);
+    *reinterpret_cast<V8*>(vdst + vt_off(d, c)) = hi;
+    if constexpr (P == 2) *reinterpret_cast<V8*>(vdst + kPlaneBytes + vt_off(d, c)) = lo;
+  }
+}
+
+// 16 bytes per lane from global memory straight into LDS at the wave-uniform
+// base `l` + 16 * lane (global_load_lds_dwordx4). The device-only guard keeps
+// the host pass, which has no such builtin, from dropping the kernels' stubs.
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void lds_load16(const void* g, lds_void* l) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Partial layout per (kv head, row block, split): O[128 columns][kD], then
+// (max, sum)[128 columns].
+constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
+
+template <int MODE, int MT, int NS>
+__global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ q, const char* __restrict__ stage,
+                                                      int n_stage_tiles, int q_stride, int rows, int start, int group,
+                                                      int n_rb, int n_units, int kv_splits, float qscale,
+                                                      float* __restrict__ part, float* __restrict__ out) {
+  typedef typename Op<MODE>::E E;
+  typedef typename Op<MODE>::V8 V8;
+  typedef typename Op<MODE>::V4 V4;
   constexpr bool kSplit = Op<MODE>::kSplit;
-  constexpr int kPlanes = kSplit ? 2 : 1;
-  constexpr int HPT = 16 / ROWS;  // heads per 16-column block
+  constexpr int P = kSplit ? 2 : 1;
+  constexpr int M = 64 * MT;              // query vectors per workgroup
+  constexpr int TB = 2 * P * kPlaneBytes;  // bytes per staged tile
+  constexpr int LPW = TB / 1024 / 4;       // direct-to-LDS loads per wave per tile
+  // Scores are kept relative to a running maximum that only moves when a
+  // tile's maximum exceeds it by more than this (log2 units): P values stay
+  // below 2^8 and most tiles skip rescaling the accumulators.
+  constexpr float kRescale = 8.0f;
 
-  __shared__ __attribute__((aligned(16))) E k_lds[kPlanes][kBT][kKPad];
-  __shared__ __attribute__((aligned(16))) E v_lds[kPlanes][kD][kVPad];
+  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
 
-  const int split = blockIdx.x, rt = blockIdx.y, kvh = blockIdx.z;
+  // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
+  // XCD b % 8). Units (kv head, row block, split) are numbered kv-head-major
+  // and each XCD takes a contiguous run of them, so the workgroups sharing an
+  // XCD's L2 stream the same kv head's tiles at about the same time.
+  const int per_xcd = (n_units + 7) / 8;
+  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if ((int)(blockIdx.x / 8) >= per_xcd || unit >= n_units) return;
+  const int split = unit % kv_splits, rb = (unit / kv_splits) % n_rb, kvh = unit / (kv_splits * n_rb);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lm = lane & 15, kg = lane >> 4;
-  const int r0 = rt * ROWS;
-  const int rows_here = min(ROWS, rows - r0);
-  const int tile_limit = start + r0 + rows_here;  // positions the last row of the tile sees
-  const int n_tt = (tile_limit + kBT - 1) / kBT;
-  const int tt_lo = (int)((long)n_tt * split / kv_splits);
-  const int tt_hi = (int)((long)n_tt * (split + 1) / kv_splits);
+  const int lm = lane & 15, kk = lane >> 4;
+  const int qr = M / group;  // rows per workgroup
+  const int r0 = rb * qr;
+  const int rows_here = min(qr, rows - r0);
+  const int wg_limit = start + r0 + rows_here;  // positions the block's last row sees
+  const int all_see = start + r0 + 1;           // positions every row of the block sees
+  const int n_tiles = (wg_limit + kBT - 1) / kBT;
+  const int tt_lo = (int)((long)n_tiles * split / kv_splits);
+  const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
+  const int n = tt_hi - tt_lo;
 
-  // This lane's query vector (column lm of every 16x16 block): a row and a
-  // head offset inside the block.
-  const int rsub = lm % ROWS, hsub = lm / ROWS;
-  const int my_row = r0 + rsub;
-  const bool row_ok = my_row < rows;
-  const int my_limit = start + my_row + 1;  // attends t < my_limit
+  // Tile j of this workgroup (clamped to its last, so every wave issues the
+  // same number of loads per iteration) into stage s: wave w copies the
+  // 1 KiB pieces w, w + 4, ...; lane l's 16 bytes land at piece + 16 l.
+  const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
+  auto issue = [&](int j, int s) {
+    const char* g = src + (size_t)(tt_lo + min(j, n - 1)) * TB;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int piece = 1024 * (wave + 4 * i);
+      lds_load16(g + piece, (lds_void*)&lds[s][piece]);
+    }
+  };
+  if (n > 0) {
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) issue(j, j);
+  }
 
+  // This lane's query vector in column block mt: column m = 16*(wave*MT + mt) + lm.
+  int my_row[MT], my_head[MT], my_limit[MT];
+  bool col_ok[MT];
   V8 qh[MT][4], ql[MT][4];
   f32x4 o[MT][8];
   float m_run[MT], l_run[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int g = (wave + 4 * mt) * HPT + hsub;
-    const bool g_ok = g < group && row_ok;
-    const float* qp = q + (size_t)my_row * q_stride + (size_t)(kvh * group + g) * kD;
+    const int m = 16 * (wave * MT + mt) + lm;
+    my_head[mt] = m / qr;
+    my_row[mt] = r0 + m % qr;
+    col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
+    my_limit[mt] = col_ok[mt] ? start + my_row[mt] + 1 : 0;
+    const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
+                      (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
+    // q rows may be only 4-byte aligned: scalar loads (once per workgroup).
+    // log2(e) * scale is folded in before rounding to the MFMA type, except
+    // in the split mode, where rounding the scaled q would cost low bits of
+    // the lo half and the scores are scaled in fp32 instead.
+    const float qs = col_ok[mt] ? (kSplit ? 1.f : qscale) : 0.f;
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float x = g_ok ? qp[ds * 32 + kg * 8 + j] : 0.f;
-        E hi, lo;
-        split2(x, hi, lo);
-        qh[mt][ds][j] = hi;
-        ql[mt][ds][j] = lo;
-      }
-    }
+      for (int e = 0; e < 8; ++e) split2v<E>(qp[32 * s + e] * qs, qh[mt][s], ql[mt][s], e);
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) o[mt][ds] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
     l_run[mt] = 0.f;
   }
 
-  // K/V tile loader mapping: thread -> (position, 16-element d chunk).
-  const int ld_t = tid >> 3, ld_d = (tid & 7) * 16;
-
-  for (int tt = tt_lo; tt < tt_hi; ++tt) {
-    const int t0 = tt * kBT;
+  for (int i = 0; i < n; ++i) {
+    const int s = i % NS;
+    // This wave's loads of tile i are done once at most NS - 2 tiles of its
+    // loads remain in flight; the barrier makes every wave's part visible
+    // and retires the stage the loads below overwrite (computed last
+    // iteration).
+    wait_vmcnt<(NS - 2) * LPW>();
     __syncthreads();
-    {
-      const int t = t0 + ld_t;
-      float kx[16], vx[16];
-      if (t < tile_limit) {
-        load16<T>(kl + (size_t)t * kv_dim + (size_t)kvh * kD + ld_d, kx);
-        load16<T>(vl + (size_t)t * kv_dim + (size_t)kvh * kD + ld_d, vx);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) kx[i] = vx[i] = 0.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        E kh, klo, vh, vlo;
-        split2(kx[i], kh, klo);
-        split2(vx[i], vh, vlo);
-        k_lds[0][ld_t][ld_d + i] = kh;
-        v_lds[0][ld_d + i][ld_t] = vh;
-        if constexpr (kSplit) {
-          k_lds[kPlanes - 1][ld_t][ld_d + i] = klo;
-          v_lds[kPlanes - 1][ld_d + i][ld_t] = vlo;
-        }
-      }
-    }
-    __syncthreads();
+    issue(i + NS - 1, (i + NS - 1) % NS);
+    const char* kt = lds[s];
+    const char* vt = lds[s] + P * kPlaneBytes;
+    const int t0 = (tt_lo + i) * kBT;
 
-    // S^T for both 16-position halves of the tile.
-    f32x4 s[MT][2];
+    // S^T for the tile's four 16-position blocks.
+    f32x4 sc[MT][4];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s[mt][0] = s[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int ts = 0; ts < 2; ++ts) {
+      for (int pb = 0; pb < 4; ++pb) sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const V8 a = *reinterpret_cast<const V8*>(&k_lds[0][ts * 16 + lm][ds * 32 + kg * 8]);
+    for (int pb = 0; pb < 4; ++pb) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int off = k_off(16 * pb + lm, 4 * ks + kk);
+        const V8 a = *reinterpret_cast<const V8*>(kt + off);
         V8 alo;
-        if constexpr (kSplit) alo = *reinterpret_cast<const V8*>(&k_lds[kPlanes - 1][ts * 16 + lm][ds * 32 + kg * 8]);
+        if constexpr (kSplit) alo = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          s[mt][ts] = Op<MODE>::mfma(a, qh[mt][ds], s[mt][ts]);
+          sc[mt][pb] = Op<MODE>::mfma(a, qh[mt][ks], sc[mt][pb]);
           if constexpr (kSplit) {
-            s[mt][ts] = Op<MODE>::mfma(alo, qh[mt][ds], s[mt][ts]);
-            s[mt][ts] = Op<MODE>::mfma(a, ql[mt][ds], s[mt][ts]);
+            sc[mt][pb] = Op<MODE>::mfma(alo, qh[mt][ks], sc[mt][pb]);
+            sc[mt][pb] = Op<MODE>::mfma(a, ql[mt][ks], sc[mt][pb]);
           }
         }
       }
     }
-
-    // Online softmax per query vector (lane column lm); scores for t0 + ts*16 + kg*4 + i.
-    V8 pb[MT], pl[MT];
+    if constexpr (kSplit) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] *= qscale;
+    }
+    // Causal mask only where some row of the block stops inside the tile.
+    if (t0 + kBT > all_see) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
+    }
+    // Online softmax per query vector; this lane holds t0 + 16pb + 4kk + e.
+    // P^T operand for PV step s2: slots j<4 are t = 32s2 + 4kk + j, slots
+    // j>=4 are t = 32s2 + 16 + 4kk + j - 4 (blocks 2s2 and 2s2 + 1).
+    V8 ph[MT][2], pl[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      float sv[8];
-      float mx = kNegSentinel;
+      float mx = sc[mt][0][0];
 #pragma unroll
-      for (int ts = 0; ts < 2; ++ts) {
+      for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = t0 + ts * 16 + kg * 4 + i;
-          const float x = (t < my_limit) ? s[mt][ts][i] * qscale : -INFINITY;
-          sv[ts * 4 + i] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
+        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sc[mt][pb][e]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m_run[mt], mx);
-      const float alpha = exp2f(m_run[mt] - mn);
-      m_run[mt] = mn;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[mt] + kRescale)) {
+        const float mn = fmaxf(m_run[mt], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - mn);
+        m_run[mt] = mn;
+        l_run[mt] *= alpha;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
+      }
       float psum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p = exp2f(sv[j] - mn);
-        psum += p;
-        E hi, lo;
-        split2(p, hi, lo);
-        pb[mt][j] = hi;
-        pl[mt][j] = lo;
-      }
-      l_run[mt] = l_run[mt] * alpha + psum;
+      for (int pb = 0; pb < 4; ++pb) {
+        f32x4 p;
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds) o[mt][ds] *= alpha;
+        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e] - m_run[mt]);
+        psum += (p[0] + p[1]) + (p[2] + p[3]);
+        const V4 hi = __builtin_convertvector(p, V4);
+        V4 lo;
+        if constexpr (kSplit) lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
+          if constexpr (kSplit) pl[mt][pb / 2][4 * (pb % 2) + e] = lo[e];
+        }
+      }
+      l_run[mt] += psum;
     }
-
-    // O^T += V^T P^T: A row d = ds*16 + lm, slots t = kg*4 + {0..3} and 16 + kg*4 + {0..3}.
+    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's).
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) {
-      V8 a, alo;
-      {
-        const E* vr = &v_lds[0][ds * 16 + lm][0];
+    for (int b = 0; b < 8; ++b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          a[i] = vr[kg * 4 + i];
-          a[4 + i] = vr[16 + kg * 4 + i];
-        }
-        if constexpr (kSplit) {
-          const E* vl2 = &v_lds[kPlanes - 1][ds * 16 + lm][0];
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int off = vt_off(16 * b + lm, 4 * s2 + kk);
+        const V8 a = *reinterpret_cast<const V8*>(vt + off);
+        V8 alo;
+        if constexpr (kSplit) alo = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            alo[i] = vl2[kg * 4 + i];
-            alo[4 + i] = vl2[16 + kg * 4 + i];
+        for (int mt = 0; mt < MT; ++mt) {
+          o[mt][b] = Op<MODE>::mfma(a, ph[mt][s2], o[mt][b]);
+          if constexpr (kSplit) {
+            o[mt][b] = Op<MODE>::mfma(alo, ph[mt][s2], o[mt][b]);
+            o[mt][b] = Op<MODE>::mfma(a, pl[mt][s2], o[mt][b]);
           }
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        o[mt][ds] = Op<MODE>::mfma(a, pb[mt], o[mt][ds]);
-        if constexpr (kSplit) {
-          o[mt][ds] = Op<MODE>::mfma(alo, pb[mt], o[mt][ds]);
-          o[mt][ds] = Op<MODE>::mfma(a, pl[mt], o[mt][ds]);
         }
       }
     }
   }
+  // The clamped prefetches past the last tile may still be landing in LDS:
+  // retire them before the workgroup ends.
+  wait_vmcnt<0>();
 
-  // Row sums: each lane holds a quarter of its vector's positions.
+  // Column sums: each lane holds a quarter of its column's positions.
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     l_run[mt] += __shfl_xor(l_run[mt], 16, 64);
@@ -292,127 +398,101 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
   if (kv_splits == 1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int g = (wave + 4 * mt) * HPT + hsub;
-      if (g >= group || !row_ok) continue;
+      if (!col_ok[mt]) continue;
       const float inv = 1.0f / l_run[mt];
-      float* op = out + (size_t)my_row * q_stride + (size_t)(kvh * group + g) * kD;
+      float* op = out + (size_t)my_row[mt] * q_stride + (size_t)(kvh * group + my_head[mt]) * kD;
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds)
+      for (int b = 0; b < 8; ++b)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) op[ds * 16 + kg * 4 + i] = o[mt][ds][i] * inv;
+        for (int e = 0; e < 4; ++e) op[16 * b + 4 * kk + e] = o[mt][b][e] * inv;
     }
     return;
   }
-
-  // Partial (O, max, sum) for this split.
-  const int n_rt = gridDim.y;
-  const size_t tile_idx = (size_t)kvh * n_rt + rt;
-  const size_t stride = part_stride(group, ROWS);
-  const size_t ml_off = (size_t)group * ROWS * kD;
-  float* mine = part + (tile_idx * kv_splits + split) * stride;
+  // Partial (O, max, sum) of this split; o[mt][b][e] is O^T[16b + 4kk + e][m].
+  float* mine = part + (((size_t)kvh * n_rb + rb) * kv_splits + split) * kPartStride;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int g = (wave + 4 * mt) * HPT + hsub;
-    if (g >= group) continue;
-    const size_t v = (size_t)g * ROWS + rsub;
+    const int m = 16 * (wave * MT + mt) + lm;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-      *reinterpret_cast<f32x4*>(&mine[v * kD + ds * 16 + kg * 4]) = o[mt][ds];
-    if (kg == 0) {
-      mine[ml_off + v * 2] = m_run[mt];
-      mine[ml_off + v * 2 + 1] = l_run[mt];
+    for (int b = 0; b < 8; ++b) *reinterpret_cast<f32x4*>(&mine[(size_t)m * kD + 16 * b + 4 * kk]) = o[mt][b];
+    if (kk == 0) {
+      mine[128 * kD + 2 * m] = m_run[mt];
+      mine[128 * kD + 2 * m + 1] = l_run[mt];
     }
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ unsigned s_last;
-  if (tid == 0) s_last = atomicAdd(&tickets[tile_idx], 1u) == (unsigned)(kv_splits - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+}
 
-  // Merge: split weights per query vector in LDS, then 16-byte partial rows.
-  const float* base = part + tile_idx * kv_splits * stride;
-  const int nv = group * ROWS;  // query vectors of the tile
-  __shared__ float sm_w[kMaxKvSplits][16 * 16];
-  __shared__ float sm_inv[16 * 16];
-  for (int v = tid; v < nv; v += kWG) {
-    float M = kNegSentinel;
-    for (int sp = 0; sp < kv_splits; ++sp) M = fmaxf(M, base[sp * stride + ml_off + v * 2]);
-    float L = 0.f;
-    for (int sp = 0; sp < kv_splits; ++sp) {
-      const float w = exp2f(base[sp * stride + ml_off + v * 2] - M);
-      sm_w[sp][v] = w;
-      L += w * base[sp * stride + ml_off + v * 2 + 1];
-    }
-    sm_inv[v] = 1.0f / L;
+// Log-sum-exp merge of the KV splits: one 256-thread workgroup per (kv head,
+// row block, pair of columns), thread -> (column, d).
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int kv_splits, int n_rb,
+                                                            int qr, int rows, int group, int q_stride,
+                                                            float* __restrict__ out) {
+  const int pair = blockIdx.x % 64, rb = (blockIdx.x / 64) % n_rb, kvh = blockIdx.x / (64 * n_rb);
+  const int m = 2 * pair + (threadIdx.x >> 7), d = threadIdx.x & 127;
+  const int head = m / qr, row = rb * qr + m % qr;
+  if (head >= group || row >= rows) return;
+  const float* base = part + ((size_t)kvh * n_rb + rb) * kv_splits * kPartStride;
+  float M = kNegSentinel;
+  for (int sp = 0; sp < kv_splits; ++sp) M = fmaxf(M, base[sp * kPartStride + 128 * kD + 2 * m]);
+  float L = 0.f, O = 0.f;
+  for (int sp = 0; sp < kv_splits; ++sp) {
+    const float* ps = base + sp * kPartStride;
+    const float w = __builtin_amdgcn_exp2f(ps[128 * kD + 2 * m] - M);
+    L += ps[128 * kD + 2 * m + 1] * w;
+    O += ps[(size_t)m * kD + d] * w;
   }
-  __syncthreads();
-  for (int idx = tid; idx < nv * (kD / 4); idx += kWG) {
-    const int v = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
-    const int g = v / ROWS, r = v % ROWS;
-    if (r0 + r >= rows) continue;
-    f32x4 O = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < kv_splits; ++sp)
-      O += *reinterpret_cast<const f32x4*>(&base[sp * stride + (size_t)v * kD + d]) * sm_w[sp][v];
-    O *= sm_inv[v];
-    float* op = out + (size_t)(r0 + r) * q_stride + (size_t)(kvh * group + g) * kD + d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) op[i] = O[i];
-  }
-  if (tid == 0) __hip_atomic_store(&tickets[tile_idx], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  out[(size_t)row * q_stride + (size_t)(kvh * group + head) * kD + d] = O / L;
 }
 
 struct PrefillArgs {
-  dim3 grid;
   const float* q;
-  const void* kl;
-  const void* vl;
-  int kv_dim, q_stride, rows, start, group, kv_splits;
+  char* stage;
+  int n_kv, n_stage_tiles, kv_dim, positions, q_stride, rows, start, group, n_rb, n_units, kv_splits;
   float qscale;
   float* part;
-  unsigned* tickets;
   float* out;
   TimedPair tp;
 };
 
-template <int MODE, typename T, int MT, int ROWS>
-void launch_one(const PrefillArgs& a, hipStream_t s) {
-  launch_timed(a.tp, prefill_kernel<MODE, T, MT, ROWS>, a.grid, dim3(kWG), s, a.q, (const T*)a.kl, (const T*)a.vl,
-               a.kv_dim, a.q_stride, a.rows, a.start, a.group, a.kv_splits, a.qscale, a.part, a.tickets, a.out);
-}
-
-// MT = column blocks per wave = ceil(group * ROWS / 16 / 4).
-template <int MODE, typename T, int ROWS>
-void launch_rows(int mt, const PrefillArgs& a, hipStream_t s) {
-  if (mt <= 1)
-    launch_one<MODE, T, 1, ROWS>(a, s);
-  else if (mt == 2)
-    launch_one<MODE, T, 2, ROWS>(a, s);
-  else
-    launch_one<MODE, T, 4, ROWS>(a, s);
+template <int MODE, int MT>
+void launch_main(const PrefillArgs& a, hipStream_t s) {
+  // LDS ring: four 32 KiB stages for single-plane modes, two 64 KiB
+  // stages for the split mode.
+  constexpr int NS = Op<MODE>::kSplit ? 2 : 4;
+  const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
+  launch_timed(a.tp, prefill_kernel<MODE, MT, NS>, dim3(blocks), dim3(kWG), s, a.q, (const char*)a.stage,
+               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale, a.part,
+               a.out);
 }
 
 template <int MODE, typename T>
-void launch_mode(int rows_per_tile, int mt, const PrefillArgs& a, hipStream_t s) {
-  if (rows_per_tile == 8)
-    launch_rows<MODE, T, 8>(mt, a, s);
+void launch_mode(int mt, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles)), dim3(kWG), 0, s, kl,
+                     vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
+  if (mt == 1)
+    launch_main<MODE, 1>(a, s);
   else
-    launch_rows<MODE, T, 16>(mt, a, s);
+    launch_main<MODE, 2>(a, s);
 }
 
 template <typename T>
-void launch_t(uint32_t mode, int rows_per_tile, int mt, const PrefillArgs& a, hipStream_t s) {
+void launch_t(uint32_t mode, int mt, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
   switch (mode) {
-    case RV_PREFILL_F16: launch_mode<kF16, T>(rows_per_tile, mt, a, s); break;
-    case RV_PREFILL_BF16: launch_mode<kBF16, T>(rows_per_tile, mt, a, s); break;
-    default: launch_mode<kExact, T>(rows_per_tile, mt, a, s);
+    case RV_PREFILL_F16: launch_mode<kF16, T>(mt, kl, vl, a, s); break;
+    case RV_PREFILL_BF16: launch_mode<kBF16, T>(mt, kl, vl, a, s); break;
+    default: launch_mode<kExact, T>(mt, kl, vl, a, s);
   }
 }
 
 }  // namespace
 
-bool prefill_supported(size_t head_dim, size_t group) { return head_dim == kD && group >= 1 && group <= 16; }
+// head_dim 128 and a group that divides 64 (so a workgroup's 64 or 128
+// columns are whole rows of the group); any other geometry runs each row
+// through the decode kernels.
+bool prefill_supported(const rv_kv* kv, size_t group, size_t positions) {
+  (void)positions;
+  return kv->head_dim == kD && group >= 1 && 64 % group == 0;
+}
 
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
                          size_t start, float scale, float* out, uint32_t mode, hipStream_t s) {
@@ -420,34 +500,41 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   if (rows == 0) return st;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const int n_kv = (int)kv->n_kv_heads;
-  // Row tiles of 8 (two heads per MFMA column block) when the group is even,
-  // so a 512-row chunk fills the chip without splitting the KV axis.
-  int rows_per_tile = (kv->tune_prefill_rows == 16 || group % 2) ? 16 : 8;
-  if (kv->tune_prefill_rows == 8 && group % 2 == 0) rows_per_tile = 8;
-  const int n_rt = (int)((rows + rows_per_tile - 1) / rows_per_tile);
-  const int mt = (group * rows_per_tile / 16 + 3) / 4;
+  const uint32_t m = mode & RV_PREFILL_MODE_MASK;
+  const int planes = (m == RV_PREFILL_F16 || m == RV_PREFILL_BF16) ? 1 : 2;
+  // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
+  // the tuning asks for it.
+  const int vectors = kv->tune_prefill_rows > 0 && kv->tune_prefill_rows * group <= 64 ? 64 : 128;
+  const int mt = vectors / 64;
+  const int qr = vectors / group;
+  const int n_rb = (int)((rows + qr - 1) / qr);
+  const size_t positions = start + rows;
+  const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);
   int kv_splits = (int)kv->tune_prefill_kv_split;
   if (kv_splits <= 0) {
-    // Split the KV axis only when the tiles cover under half the chip, and
-    // keep at least 4 K/V tiles per split.
-    const long tiles = (long)n_rt * n_kv;
-    const long longest = ((long)start + (long)rows + kBT - 1) / kBT;
-    kv_splits = tiles >= 128 ? 1 : (int)std::min<long>(256 / tiles, std::max<long>(1, longest / 4));
+    // Split the KV axis until about 256 workgroups are in flight, keeping at
+    // least 4 K/V tiles per split of the longest block.
+    const long wgs = (long)n_rb * n_kv;
+    kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 4));
   }
   kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
-  const size_t n_tiles = (size_t)n_kv * n_rt;
-  if (kv_splits > 1) {
-    st = ensure_workspace(kv, n_tiles * kv_splits * part_stride(group, rows_per_tile) * sizeof(float), n_tiles);
-    if (st.e != hipSuccess) return st;
-  }
-  PrefillArgs a{dim3((unsigned)kv_splits, (unsigned)n_rt, (unsigned)n_kv), q_rows, kv->k_layer(layer),
-                kv->v_layer(layer), (int)kv->kv_dim, (int)(n_q_heads * kD), (int)rows, (int)start, group,
-                kv_splits, scale * kLog2e, (float*)kv->ws, kv->tickets, out, timing_pair(kv, s)};
-  const uint32_t m = mode & RV_PREFILL_MODE_MASK;
+  // Workspace: staged tiles, then the split partials.
+  const size_t stage_bytes = (size_t)n_kv * n_stage_tiles * 2 * planes * kPlaneBytes;
+  const size_t part_bytes = kv_splits > 1 ? (size_t)n_kv * n_rb * kv_splits * kPartStride * sizeof(float) : 0;
+  st = ensure_workspace(kv, stage_bytes + part_bytes, 0);
+  if (st.e != hipSuccess) return st;
+  char* stage = (char*)kv->ws;
+  float* part = (float*)(stage + stage_bytes);
+  PrefillArgs a{q_rows, stage, n_kv, n_stage_tiles, (int)kv->kv_dim, (int)positions, (int)(n_q_heads * kD), (int)rows,
+                (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e, part, out,
+                timing_pair(kv, s)};
   if (kv->elem == RV_ELEM_F32)
-    launch_t<float>(m, rows_per_tile, mt, a, s);
+    launch_t<float>(m, mt, (const float*)kv->k_layer(layer), (const float*)kv->v_layer(layer), a, s);
   else
-    launch_t<_Float16>(m, rows_per_tile, mt, a, s);
+    launch_t<_Float16>(m, mt, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), a, s);
+  if (kv_splits > 1)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * 64)), dim3(256), 0, s, (const float*)part,
+                       kv_splits, n_rb, qr, (int)rows, group, (int)(n_q_heads * kD), out);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
   return st;

@@ -44,6 +44,7 @@ def test_rows_match_per_row_attention_at(mode, elem):
     rng = Rng(0xC0FFEE)
     for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (4, 32, 128, 100, 70), (2, 8, 128, 5, 16),
                                        (1, 1, 128, 3, 50), (4, 16, 128, 0, 1), (2, 4, 128, 31, 33),
+                                       (1, 16, 128, 7, 21), (1, 32, 128, 64, 9), (3, 9, 128, 2, 5),
                                        (1, 8, 16, 4, 9), (3, 6, 9, 0, 7)]:
         say(f"case rows {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem}")
         kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, elem)
@@ -144,3 +145,26 @@ def test_prefill_errors_and_first_row_semantics():
     # split-f16 reproduces V to ~2^-22 relative (hi + lo of one f32)
     assert np.allclose(out[0].reshape(4, 8, 128), np.broadcast_to(K[0].reshape(4, 1, 128), (4, 8, 128)), rtol=1e-6,
                        atol=0)
+
+
+@pytest.mark.parametrize("mode", ["exact", "f16"])
+@pytest.mark.parametrize("vectors_rows,splits", [(0, 0), (8, 1), (16, 1), (16, 2), (8, 3), (16, 8)])
+def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits):
+    """64 or 128 query vectors per workgroup and 1..8 KV splits (some empty),
+    over a chunk whose rows cross several 64-position tiles and end in a
+    partial row block."""
+    torch_cuda()
+    say(f"case tiles rows={vectors_rows} splits={splits} mode={mode}")
+    rng = Rng(0x711E + 31 * splits + vectors_rows)
+    n_kv, n_q, hd, start, rows = 4, 32, 128, 200, 130
+    kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, "f32")
+    kv.set_tuning(4, vectors_rows)
+    kv.set_tuning(2, splits)
+    q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = dev(np.full(q.shape, np.nan))
+    rv.attention_at_rows(dev(q), kv, 0, start, scale, out, mode=mode)
+    want = ref.scatter_attention(q, 0, start, scale, THREADS)
+    e = gate(host(out), want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode],
+             what=f"tiles {vectors_rows}/{splits} {mode}")
+    say(f"  max rel err {e:.3e}")
