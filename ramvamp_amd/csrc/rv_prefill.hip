@@ -15,7 +15,7 @@
 //    conflicts. Every row block of the chunk then re-reads this compact copy
 //    (half the bytes of an fp32 cache) instead of converting on the fly.
 //
-// 2. prefill_kernel: one workgroup (4 waves) per (kv head, block of M/group
+// 2. prefill_kernel: one workgroup (W waves) per (kv head, block of M/group
 //    query rows, KV split). Its M = 128 (or 64) query vectors are every q head
 //    of the GQA group for each of its rows, so each staged K/V tile feeds all
 //    heads: column m is head m / qr, row m % qr (qr = M / group); wave w owns
@@ -111,43 +111,81 @@ __device__ __forceinline__ int vt_pos(int c, int j) {
   return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
 }
 
-// Stage kernel: one workgroup per (kv head, tile). Rows at or past
-// `positions` are staged as zeros.
+// Stage kernel: one workgroup per (kv head, tile, plane K or V). Rows at or
+// past `positions` are staged as zeros. Loads are whole rows per wave
+// instruction (fp32: thread i reads row 8j + i/32, elements 4(i%32)..+3 for
+// j < 8; f16: row 16j + i/16, elements 8(i%16)..+7 for j < 4), all issued
+// before any is used. K goes straight to its swizzled rows; V is transposed
+// through LDS.
+template <typename T>
+struct StageLoad;
+template <>
+struct StageLoad<float> {
+  static constexpr int kN = 8, kE = 4;
+  f32x4 x[8];
+  __device__ static int row(int j, int tid) { return 8 * j + tid / 32; }
+  __device__ static int col(int tid) { return 4 * (tid % 32); }
+  __device__ void load(const float* __restrict__ base, int kv_dim, int t0, int positions, int tid) {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int t = t0 + row(j, tid);
+      x[j] = t < positions ? *reinterpret_cast<const f32x4*>(base + (size_t)t * kv_dim + col(tid))
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ float get(int j, int e) const { return x[j][e]; }
+};
+template <>
+struct StageLoad<_Float16> {
+  static constexpr int kN = 4, kE = 8;
+  f16x8 x[4];
+  __device__ static int row(int j, int tid) { return 16 * j + tid / 16; }
+  __device__ static int col(int tid) { return 8 * (tid % 16); }
+  __device__ void load(const _Float16* __restrict__ base, int kv_dim, int t0, int positions, int tid) {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int t = t0 + row(j, tid);
+      x[j] = t < positions ? *reinterpret_cast<const f16x8*>(base + (size_t)t * kv_dim + col(tid)) : f16x8{};
+    }
+  }
+  __device__ float get(int j, int e) const { return (float)x[j][e]; }
+};
+
 template <int MODE, typename T>
 __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict__ kl, const T* __restrict__ vl,
                                                             int kv_dim, int positions, int n_tiles,
                                                             char* __restrict__ stage) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
+  typedef E EN __attribute__((ext_vector_type(StageLoad<T>::kE)));
   constexpr int P = Op<MODE>::kSplit ? 2 : 1;
-  const int tile = blockIdx.x % n_tiles, kvh = blockIdx.x / n_tiles;
+  constexpr int NE = StageLoad<T>::kE;
+  const int plane = blockIdx.x & 1, tile = (blockIdx.x >> 1) % n_tiles, kvh = (blockIdx.x >> 1) / n_tiles;
   const int tid = threadIdx.x;
   char* dst = stage + ((size_t)kvh * n_tiles + tile) * (2 * P * kPlaneBytes);
   const int t0 = tile * kBT;
-  const size_t col = (size_t)kvh * kD;
+  StageLoad<T> ld;
+  ld.load((plane ? vl : kl) + (size_t)kvh * kD, kv_dim, t0, positions, tid);
+  if (plane == 0) {
+    // NE elements = a half (fp32) or a whole (f16) 16-byte chunk of row r.
+    const int c = StageLoad<T>::col(tid);
+#pragma unroll
+    for (int j = 0; j < StageLoad<T>::kN; ++j) {
+      const int r = StageLoad<T>::row(j, tid);
+      EN hi, lo;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) split2v<E>(ld.get(j, e), hi, lo, e);
+      const int off = k_off(r, c / 8) + 2 * (c % 8);
+      *reinterpret_cast<EN*>(dst + off) = hi;
+      if constexpr (P == 2) *reinterpret_cast<EN*>(dst + kPlaneBytes + off) = lo;
+    }
+    return;
+  }
   __shared__ float vt[kBT][kD + 1];
-
-  // Thread -> row r = tid / 4, elements 32 (tid % 4) .. +31 of K and of V.
-  const int r = tid >> 2, cb = (tid & 3) * 4;
-  const bool live = t0 + r < positions;
-  const T* kp = kl + (size_t)(live ? t0 + r : 0) * kv_dim + col + 8 * cb;
-  const T* vp = vl + (size_t)(live ? t0 + r : 0) * kv_dim + col + 8 * cb;
-  float kx[32], vx[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    kx[i] = live ? (float)kp[i] : 0.f;
-    vx[i] = live ? (float)vp[i] : 0.f;
-  }
+  for (int j = 0; j < StageLoad<T>::kN; ++j)
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    V8 hi, lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) split2v<E>(kx[8 * c + e], hi, lo, e);
-    *reinterpret_cast<V8*>(dst + k_off(r, cb + c)) = hi;
-    if constexpr (P == 2) *reinterpret_cast<V8*>(dst + kPlaneBytes + k_off(r, cb + c)) = lo;
-  }
-#pragma unroll
-  for (int i = 0; i < 32; ++i) vt[r][8 * cb + i] = vx[i];
+    for (int e = 0; e < NE; ++e) vt[StageLoad<T>::row(j, tid)][StageLoad<T>::col(tid) + e] = ld.get(j, e);
   __syncthreads();
   // Thread -> V^T row d = tid / 2, chunks 4 (tid % 2) .. +3.
   const int d = tid >> 1;
@@ -185,8 +223,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 // (max, sum)[128 columns].
 constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
 
-template <int MODE, int MT, int NS>
-__global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ q, const char* __restrict__ stage,
+template <int MODE, int W, int MT, int NS>
+__global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict__ q, const char* __restrict__ stage,
                                                       int n_stage_tiles, int q_stride, int rows, int start, int group,
                                                       int n_rb, int n_units, int kv_splits, float qscale,
                                                       float* __restrict__ part, float* __restrict__ out) {
@@ -195,9 +233,10 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
   typedef typename Op<MODE>::V4 V4;
   constexpr bool kSplit = Op<MODE>::kSplit;
   constexpr int P = kSplit ? 2 : 1;
-  constexpr int M = 64 * MT;              // query vectors per workgroup
+  constexpr int M = 16 * W * MT;           // query vectors per workgroup
   constexpr int TB = 2 * P * kPlaneBytes;  // bytes per staged tile
-  constexpr int LPW = TB / 1024 / 4;       // direct-to-LDS loads per wave per tile
+  constexpr int LPW = TB / 1024 / W;       // direct-to-LDS loads per wave per tile
+  static_assert(LPW % 8 == 0, "pieces split evenly over the QK and PV loops");
   // Scores are kept relative to a running maximum that only moves when a
   // tile's maximum exceeds it by more than this (log2 units): P values stay
   // below 2^8 and most tiles skip rescaling the accumulators.
@@ -227,15 +266,16 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
 
   // Tile j of this workgroup (clamped to its last, so every wave issues the
   // same number of loads per iteration) into stage s: wave w copies the
-  // 1 KiB pieces w, w + 4, ...; lane l's 16 bytes land at piece + 16 l.
+  // 1 KiB pieces w, w + W, ...; lane l's 16 bytes land at piece + 16 l.
   const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
-  auto issue = [&](int j, int s) {
+  auto issue_piece = [&](int j, int s, int i) {
     const char* g = src + (size_t)(tt_lo + min(j, n - 1)) * TB;
+    const int piece = 1024 * (wave + W * i);
+    lds_load16(g + piece, (lds_void*)&lds[s][piece]);
+  };
+  auto issue = [&](int j, int s) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int piece = 1024 * (wave + 4 * i);
-      lds_load16(g + piece, (lds_void*)&lds[s][piece]);
-    }
+    for (int i = 0; i < LPW; ++i) issue_piece(j, s, i);
   };
   if (n > 0) {
 #pragma unroll
@@ -280,34 +320,41 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
     // iteration).
     wait_vmcnt<(NS - 2) * LPW>();
     __syncthreads();
-    issue(i + NS - 1, (i + NS - 1) % NS);
     const char* kt = lds[s];
     const char* vt = lds[s] + P * kPlaneBytes;
     const int t0 = (tt_lo + i) * kBT;
+    const int nxt = (i + NS - 1) % NS;
 
-    // S^T for the tile's four 16-position blocks.
-    f32x4 sc[MT][4];
+    // S^T for the tile's four 16-position blocks. The tile's K operands are
+    // read from LDS ahead of the MFMAs; the next tile's loads are issued
+    // between them, so the address queue drains while the MFMAs run.
+    V8 ka[4][4], kal[4][4];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
+    for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int off = k_off(16 * pb + lm, 4 * ks + kk);
-        const V8 a = *reinterpret_cast<const V8*>(kt + off);
-        V8 alo;
-        if constexpr (kSplit) alo = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
+        ka[pb][ks] = *reinterpret_cast<const V8*>(kt + off);
+        if constexpr (kSplit) kal[pb][ks] = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
+      }
+    f32x4 sc[MT][4];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          sc[mt][pb] = Op<MODE>::mfma(a, qh[mt][ks], sc[mt][pb]);
+    for (int pb = 0; pb < 4; ++pb) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          sc[mt][pb] = Op<MODE>::mfma(ka[pb][ks], qh[mt][ks], sc[mt][pb]);
           if constexpr (kSplit) {
-            sc[mt][pb] = Op<MODE>::mfma(alo, qh[mt][ks], sc[mt][pb]);
-            sc[mt][pb] = Op<MODE>::mfma(a, ql[mt][ks], sc[mt][pb]);
+            sc[mt][pb] = Op<MODE>::mfma(kal[pb][ks], qh[mt][ks], sc[mt][pb]);
+            sc[mt][pb] = Op<MODE>::mfma(ka[pb][ks], ql[mt][ks], sc[mt][pb]);
           }
         }
       }
+      // Pieces [0, LPW/2) of the next tile, spread over the four blocks.
+#pragma unroll
+      for (int j = pb * (LPW / 2) / 4; j < (pb + 1) * (LPW / 2) / 4; ++j) issue_piece(i + NS - 1, nxt, j);
     }
     if constexpr (kSplit) {
 #pragma unroll
@@ -326,26 +373,38 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
             if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
     }
     // Online softmax per query vector; this lane holds t0 + 16pb + 4kk + e.
-    // P^T operand for PV step s2: slots j<4 are t = 32s2 + 4kk + j, slots
-    // j>=4 are t = 32s2 + 16 + 4kk + j - 4 (blocks 2s2 and 2s2 + 1).
-    V8 ph[MT][2], pl[MT][2];
+    // Column maxima over the lane's 16 values, then across the four lanes of
+    // the column (lanes 16 and 32 apart) with permlane swaps.
+    float mx[MT];
+    bool grow = false;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      float mx = sc[mt][0][0];
+      float x = fmaxf(fmaxf(sc[mt][0][0], sc[mt][0][1]), fmaxf(sc[mt][0][2], sc[mt][0][3]));
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb)
+      for (int pb = 1; pb < 4; ++pb)
+        x = fmaxf(x, fmaxf(fmaxf(sc[mt][pb][0], sc[mt][pb][1]), fmaxf(sc[mt][pb][2], sc[mt][pb][3])));
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      mx[mt] = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      grow = grow || mx[mt] > m_run[mt] + kRescale;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sc[mt][pb][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[mt] + kRescale)) {
-        const float mn = fmaxf(m_run[mt], mx);
+      for (int mt = 0; mt < MT; ++mt) {
+        const float mn = fmaxf(m_run[mt], mx[mt]);
         const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - mn);
         m_run[mt] = mn;
         l_run[mt] *= alpha;
 #pragma unroll
         for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
       }
+    }
+    // P^T operand for PV step s2: slots j<4 are t = 32s2 + 4kk + j, slots
+    // j>=4 are t = 32s2 + 16 + 4kk + j - 4 (blocks 2s2 and 2s2 + 1).
+    V8 ph[MT][2], pl[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
       float psum = 0.f;
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
@@ -364,24 +423,33 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
       }
       l_run[mt] += psum;
     }
-    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's).
+    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's);
+    // the V operands are read ahead of the MFMAs.
+    V8 va[8][2], val[8][2];
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int off = vt_off(16 * b + lm, 4 * s2 + kk);
+        va[b][s2] = *reinterpret_cast<const V8*>(vt + off);
+        if constexpr (kSplit) val[b][s2] = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
+      }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int off = vt_off(16 * b + lm, 4 * s2 + kk);
-        const V8 a = *reinterpret_cast<const V8*>(vt + off);
-        V8 alo;
-        if constexpr (kSplit) alo = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          o[mt][b] = Op<MODE>::mfma(a, ph[mt][s2], o[mt][b]);
+          o[mt][b] = Op<MODE>::mfma(va[b][s2], ph[mt][s2], o[mt][b]);
           if constexpr (kSplit) {
-            o[mt][b] = Op<MODE>::mfma(alo, ph[mt][s2], o[mt][b]);
-            o[mt][b] = Op<MODE>::mfma(a, pl[mt][s2], o[mt][b]);
+            o[mt][b] = Op<MODE>::mfma(val[b][s2], ph[mt][s2], o[mt][b]);
+            o[mt][b] = Op<MODE>::mfma(va[b][s2], pl[mt][s2], o[mt][b]);
           }
         }
       }
+      // Pieces [LPW/2, LPW), spread over the eight d blocks.
+#pragma unroll
+      for (int j = b * (LPW / 2) / 8; j < (b + 1) * (LPW / 2) / 8; ++j) issue_piece(i + NS - 1, nxt, LPW / 2 + j);
     }
   }
   // The clamped prefetches past the last tile may still be landing in LDS:
@@ -425,9 +493,9 @@ __global__ __launch_bounds__(kWG) void prefill_kernel(const float* __restrict__ 
 // Log-sum-exp merge of the KV splits: one 256-thread workgroup per (kv head,
 // row block, pair of columns), thread -> (column, d).
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int kv_splits, int n_rb,
-                                                            int qr, int rows, int group, int q_stride,
+                                                            int pairs, int qr, int rows, int group, int q_stride,
                                                             float* __restrict__ out) {
-  const int pair = blockIdx.x % 64, rb = (blockIdx.x / 64) % n_rb, kvh = blockIdx.x / (64 * n_rb);
+  const int pair = blockIdx.x % pairs, rb = (blockIdx.x / pairs) % n_rb, kvh = blockIdx.x / (pairs * n_rb);
   const int m = 2 * pair + (threadIdx.x >> 7), d = threadIdx.x & 127;
   const int head = m / qr, row = rb * qr + m % qr;
   if (head >= group || row >= rows) return;
@@ -454,33 +522,39 @@ struct PrefillArgs {
   TimedPair tp;
 };
 
-template <int MODE, int MT>
+template <int MODE, int W, int MT, int NS>
 void launch_main(const PrefillArgs& a, hipStream_t s) {
-  // LDS ring: four 32 KiB stages for single-plane modes, two 64 KiB
-  // stages for the split mode.
-  constexpr int NS = Op<MODE>::kSplit ? 2 : 4;
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
-  launch_timed(a.tp, prefill_kernel<MODE, MT, NS>, dim3(blocks), dim3(kWG), s, a.q, (const char*)a.stage,
+  launch_timed(a.tp, prefill_kernel<MODE, W, MT, NS>, dim3(blocks), dim3(W * 64), s, a.q, (const char*)a.stage,
                a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale, a.part,
                a.out);
 }
 
+// 128 query vectors: 4 waves x 2 column blocks with a ring of four 32 KiB
+// stages (two 64 KiB stages in the split mode), one workgroup per CU.
+// 64 query vectors (single-plane modes): 2 waves x 2 column blocks with two
+// 32 KiB stages, two workgroups per CU; the split mode keeps 4 waves x 1.
 template <int MODE, typename T>
-void launch_mode(int mt, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles)), dim3(kWG), 0, s, kl,
-                     vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
-  if (mt == 1)
-    launch_main<MODE, 1>(a, s);
-  else
-    launch_main<MODE, 2>(a, s);
+void launch_mode(int vectors, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles * 2)), dim3(kWG), 0, s,
+                     kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
+  constexpr bool kSplit = Op<MODE>::kSplit;
+  if (vectors == 64) {
+    if constexpr (kSplit)
+      launch_main<MODE, 4, 1, 2>(a, s);
+    else
+      launch_main<MODE, 2, 2, 2>(a, s);
+  } else {
+    launch_main<MODE, 4, 2, kSplit ? 2 : 4>(a, s);
+  }
 }
 
 template <typename T>
-void launch_t(uint32_t mode, int mt, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+void launch_t(uint32_t mode, int vectors, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
   switch (mode) {
-    case RV_PREFILL_F16: launch_mode<kF16, T>(mt, kl, vl, a, s); break;
-    case RV_PREFILL_BF16: launch_mode<kBF16, T>(mt, kl, vl, a, s); break;
-    default: launch_mode<kExact, T>(mt, kl, vl, a, s);
+    case RV_PREFILL_F16: launch_mode<kF16, T>(vectors, kl, vl, a, s); break;
+    case RV_PREFILL_BF16: launch_mode<kBF16, T>(vectors, kl, vl, a, s); break;
+    default: launch_mode<kExact, T>(vectors, kl, vl, a, s);
   }
 }
 
@@ -505,7 +579,6 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
   // the tuning asks for it.
   const int vectors = kv->tune_prefill_rows > 0 && kv->tune_prefill_rows * group <= 64 ? 64 : 128;
-  const int mt = vectors / 64;
   const int qr = vectors / group;
   const int n_rb = (int)((rows + qr - 1) / qr);
   const size_t positions = start + rows;
@@ -529,12 +602,12 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
                 (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e, part, out,
                 timing_pair(kv, s)};
   if (kv->elem == RV_ELEM_F32)
-    launch_t<float>(m, mt, (const float*)kv->k_layer(layer), (const float*)kv->v_layer(layer), a, s);
+    launch_t<float>(m, vectors, (const float*)kv->k_layer(layer), (const float*)kv->v_layer(layer), a, s);
   else
-    launch_t<_Float16>(m, mt, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), a, s);
+    launch_t<_Float16>(m, vectors, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), a, s);
   if (kv_splits > 1)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * 64)), dim3(256), 0, s, (const float*)part,
-                       kv_splits, n_rb, qr, (int)rows, group, (int)(n_q_heads * kD), out);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 2)), dim3(256), 0, s,
+                       (const float*)part, kv_splits, n_rb, vectors / 2, qr, (int)rows, group, (int)(n_q_heads * kD), out);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
   return st;
