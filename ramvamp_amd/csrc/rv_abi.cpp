@@ -463,7 +463,7 @@ int32_t rv_kv_append_rows(rv_kv* kv, size_t layer, const float* k, const float* 
     dv = st.in(v, n);
     if (st.e != hipSuccess) return hip_fail(err, st.e, "hipMemcpyAsync H2D");
   }
-  rv::HipStatus hs = rv::launch_append(kv, layer, len, dk, dv, rows, false, nullptr, 0.f, nullptr, kv->stream);
+  rv::HipStatus hs = rv::launch_append(kv, layer, len, dk, dv, rows, kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   kv->lens[layer] = len + rows;
   if (flags & (RV_HOST_PTRS | RV_SYNC)) {
@@ -659,10 +659,10 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
   rv::InvFreq inv;
   rv::fill_inv_freq(inv, hd, theta);
   const size_t n_q = q_len / hd;
-  hs = rv::launch_q_prologue(dq, kv->qbuf, 1, n_q, hd, dwq, eps, inv, position, kv->stream);
-  if (hs.e == hipSuccess) hs = rv::launch_append(kv, layer, len, dk, dv, 1, true, dwk, eps, &inv, kv->stream);
-  // position is the RoPE angle's position; the row lands at the cursor.
-  (void)position;
+  // q and k rotate at `position` (forward.rs:2628-2629); the row lands at
+  // the layer's cursor.
+  hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, n_q, dk, dv, 1, dwq, dwk, eps, inv, position,
+                               kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   kv->lens[layer] = len + 1;
   hs = rv::launch_decode(kv, kv->qbuf, n_q, layer, len + 1, scale, 0, kv->n_kv_heads, dout, kv->stream);
@@ -708,8 +708,8 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   rv::InvFreq inv;
   rv::fill_inv_freq(inv, hd, theta);
-  hs = rv::launch_q_prologue(dq, kv->qbuf, rows, q_dim / hd, hd, dwq, eps, inv, start, kv->stream);
-  if (hs.e == hipSuccess) hs = rv::launch_append(kv, layer, len, dk, dv, rows, true, dwk, eps, &inv, kv->stream);
+  hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, q_dim / hd, dk, dv, rows, dwq, dwk, eps, inv, start,
+                               kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   kv->lens[layer] = len + rows;
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};

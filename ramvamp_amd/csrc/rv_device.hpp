@@ -52,10 +52,39 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(x), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(x), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+// x + (x of the lane 16 or 32 apart): a permlane swap pairs every lane with
+// that partner, and the pair's two values are summed (the same sum on both
+// lanes, addition being commutative).
+template <int D>
+__device__ __forceinline__ double swap_sum_f64(double x) {
+  const unsigned lo = (unsigned)__double2loint(x), hi = (unsigned)__double2hiint(x);
+  if constexpr (D == 16) {
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __hiloint2double((int)h[0], (int)l[0]) + __hiloint2double((int)h[1], (int)l[1]);
+  } else {
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return __hiloint2double((int)h[0], (int)l[0]) + __hiloint2double((int)h[1], (int)l[1]);
+  }
+}
+
+// Wave total in f64 on every lane: DPP within 16-lane rows, then the two
+// cross-row swaps (all VALU, no LDS round trips).
 __device__ __forceinline__ double wave_sum_f64(double x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
+  x += dpp_f64<DPP_QUAD_XOR1>(x);
+  x += dpp_f64<DPP_QUAD_XOR2>(x);
+  x += dpp_f64<DPP_ROW_HALF_MIRROR>(x);
+  x += dpp_f64<DPP_ROW_MIRROR>(x);
+  x = swap_sum_f64<16>(x);
+  return swap_sum_f64<32>(x);
 }
 
 // f32 -> f16 bits, round to nearest even, with the reference's subnormal,

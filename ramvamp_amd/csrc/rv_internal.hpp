@@ -96,16 +96,16 @@ struct InvFreq {
 };
 void fill_inv_freq(InvFreq& t, size_t head_dim, float theta);
 
-// Append `rows` rows (kv_dim each) of k and v at cursor `pos0` of `layer`.
-// norm: k rows are RMSNormed per head with k_w and RoPE'd at pos0+r first
-// (model/forward.rs:2622-2631); otherwise stored as given.
-HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v,
-                        size_t rows, bool norm, const float* k_w, float eps, const InvFreq* inv,
+// Append `rows` rows (kv_dim each) of k and v, as given, at cursor `pos0` of
+// `layer`.
+HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v, size_t rows,
                         hipStream_t s);
-// q rows (rows x n_heads x head_dim): per-head RMSNorm with w then RoPE at
-// pos0 + r, written to q_out.
-HipStatus launch_q_prologue(const float* q, float* q_out, size_t rows, size_t n_heads, size_t head_dim,
-                            const float* w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s);
+// Rows of (q, k, v) at RoPE positions pos0 + r: q heads RMSNormed with q_w
+// and rotated into q_out (rows x n_q x head_dim), k heads RMSNormed with k_w
+// and rotated into the cache at cache_row + r, v heads copied there.
+HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
+                              size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
+                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s);
 
 // ---- decode (rv_decode.hip) ------------------------------------------------------
 // out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all

@@ -491,25 +491,44 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
 }
 
 // Log-sum-exp merge of the KV splits: one 256-thread workgroup per (kv head,
-// row block, pair of columns), thread -> (column, d).
+// row block, 8 columns), thread -> (column, 4 consecutive d). Every split's
+// partial is loaded before any is folded (one memory round trip).
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int kv_splits, int n_rb,
-                                                            int pairs, int qr, int rows, int group, int q_stride,
+                                                            int n_cb, int qr, int rows, int group, int q_stride,
                                                             float* __restrict__ out) {
-  const int pair = blockIdx.x % pairs, rb = (blockIdx.x / pairs) % n_rb, kvh = blockIdx.x / (pairs * n_rb);
-  const int m = 2 * pair + (threadIdx.x >> 7), d = threadIdx.x & 127;
+  const int cb = blockIdx.x % n_cb, rb = (blockIdx.x / n_cb) % n_rb, kvh = blockIdx.x / (n_cb * n_rb);
+  const int m = 8 * cb + (threadIdx.x >> 5), d = 4 * (threadIdx.x & 31);
   const int head = m / qr, row = rb * qr + m % qr;
   if (head >= group || row >= rows) return;
   const float* base = part + ((size_t)kvh * n_rb + rb) * kv_splits * kPartStride;
-  float M = kNegSentinel;
-  for (int sp = 0; sp < kv_splits; ++sp) M = fmaxf(M, base[sp * kPartStride + 128 * kD + 2 * m]);
-  float L = 0.f, O = 0.f;
-  for (int sp = 0; sp < kv_splits; ++sp) {
-    const float* ps = base + sp * kPartStride;
-    const float w = __builtin_amdgcn_exp2f(ps[128 * kD + 2 * m] - M);
-    L += ps[128 * kD + 2 * m + 1] * w;
-    O += ps[(size_t)m * kD + d] * w;
+  f32x4 o[kMaxKvSplits];
+  float2 ml[kMaxKvSplits];
+#pragma unroll
+  for (int sp = 0; sp < kMaxKvSplits; ++sp) {
+    if (sp < kv_splits) {
+      o[sp] = *reinterpret_cast<const f32x4*>(base + sp * kPartStride + (size_t)m * kD + d);
+      ml[sp] = *reinterpret_cast<const float2*>(base + sp * kPartStride + 128 * kD + 2 * m);
+    }
   }
-  out[(size_t)row * q_stride + (size_t)(kvh * group + head) * kD + d] = O / L;
+  float M = kNegSentinel;
+#pragma unroll
+  for (int sp = 0; sp < kMaxKvSplits; ++sp)
+    if (sp < kv_splits) M = fmaxf(M, ml[sp].x);
+  float L = 0.f;
+  f32x4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < kMaxKvSplits; ++sp) {
+    if (sp < kv_splits) {
+      const float w = __builtin_amdgcn_exp2f(ml[sp].x - M);
+      L += ml[sp].y * w;
+      O += o[sp] * w;
+    }
+  }
+  // The caller's rows may be only 4-byte aligned: scalar stores.
+  float* op = out + (size_t)row * q_stride + (size_t)(kvh * group + head) * kD + d;
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) op[e] = O[e] * inv;
 }
 
 struct PrefillArgs {
@@ -586,9 +605,9 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   int kv_splits = (int)kv->tune_prefill_kv_split;
   if (kv_splits <= 0) {
     // Split the KV axis until about 256 workgroups are in flight, keeping at
-    // least 4 K/V tiles per split of the longest block.
+    // least 8 K/V tiles per split of the longest block.
     const long wgs = (long)n_rb * n_kv;
-    kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 4));
+    kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 8));
   }
   kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
   // Workspace: staged tiles, then the split partials.
@@ -606,8 +625,8 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   else
     launch_t<_Float16>(m, vectors, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), a, s);
   if (kv_splits > 1)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 2)), dim3(256), 0, s,
-                       (const float*)part, kv_splits, n_rb, vectors / 2, qr, (int)rows, group, (int)(n_q_heads * kD), out);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 8)), dim3(256), 0, s,
+                       (const float*)part, kv_splits, n_rb, vectors / 8, qr, (int)rows, group, (int)(n_q_heads * kD), out);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
   return st;

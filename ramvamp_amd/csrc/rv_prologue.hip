@@ -5,8 +5,8 @@
 // (primitives/rope.rs:31-45, :82-105) and KvCache::append (kv/mod.rs:336-368),
 // as called at model/forward.rs:2622-2631 and model/prefill.rs:2057-2087.
 //
-// One wavefront per (row, head). The f32 arithmetic is the reference's, op
-// for op and with contraction off: `x * inv * w` left to right, the rotation
+// One wavefront per 8 heads of a row (q, k and v heads in one launch). The
+// f32 arithmetic is the reference's, op for op and with contraction off: `x * inv * w` left to right, the rotation
 // as two separately rounded products and a subtraction/addition. The mean of
 // squares is summed in f64 (a tree, not the reference's sequential order: the
 // two agree to f64 rounding before the cast to f32). RoPE angles are
@@ -27,39 +27,6 @@ void fill_inv_freq(InvFreq& t, size_t head_dim, float theta) {
 
 namespace {
 
-// Normalise (optional) and rotate one head of `hd` elements held in `x`
-// (global memory, read once), returning the results through `emit(i, y)`.
-template <typename Emit>
-__device__ __forceinline__ void norm_rope_head(const float* __restrict__ x, int hd, const float* __restrict__ w,
-                                               float eps, bool norm, const InvFreq& inv, double pos, Emit emit) {
-#pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const int half = hd / 2;
-  float inv_rms = 1.0f;
-  if (norm) {
-    double ss = 0.0;
-    for (int i = lane; i < hd; i += 64) {
-      const double v = (double)x[i];
-      ss += v * v;
-    }
-    ss = wave_sum_f64(ss);
-    const double mean = ss / (double)hd;
-    inv_rms = (float)(1.0 / sqrt(mean + (double)eps));
-  }
-  for (int i = lane; i < half; i += 64) {
-    float x0 = x[i], x1 = x[i + half];
-    if (norm) {
-      x0 = x0 * inv_rms * w[i];
-      x1 = x1 * inv_rms * w[i + half];
-    }
-    const double ang = pos * inv.f[i];
-    const float sn = (float)sin(ang), cs = (float)cos(ang);
-    const float a = x0 * cs, b = x1 * sn, c = x0 * sn, d = x1 * cs;
-    emit(i, a - b);
-    emit(i + half, c + d);
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ void store_elem(T* p, float v);
 template <>
@@ -71,68 +38,185 @@ __device__ __forceinline__ void store_elem<uint16_t>(uint16_t* p, float v) {
   *p = f32_to_f16_bits(v);
 }
 
-// grid (rows, n_kv_heads), one wave each: K head normalised + rotated (or
-// copied), V head copied, both converted to the plane's element type.
+// grid (rows, n_kv_heads), one wave each: K and V heads copied into the
+// cache, converted to the plane's element type (KvCache::append as is).
 template <typename T>
 __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k, const float* __restrict__ v,
-                                                    T* __restrict__ kp, T* __restrict__ vp, int kv_dim, int hd,
-                                                    bool norm, const float* __restrict__ k_w, float eps,
-                                                    InvFreq inv, long pos0) {
-  const int r = blockIdx.x, h = blockIdx.y;
-  const int lane = threadIdx.x;
-  const size_t src = (size_t)r * kv_dim + (size_t)h * hd;
-  T* kd = kp + src;
-  T* vd = vp + src;
-  if (norm) {
-    norm_rope_head(k + src, hd, k_w, eps, true, inv, (double)(pos0 + r),
-                   [&](int i, float y) { store_elem<T>(kd + i, y); });
-  } else {
-    for (int i = lane; i < hd; i += 64) store_elem<T>(kd + i, k[src + i]);
+                                                    T* __restrict__ kp, T* __restrict__ vp, int kv_dim, int hd) {
+  const size_t src = (size_t)blockIdx.x * kv_dim + (size_t)blockIdx.y * hd;
+  for (int i = threadIdx.x; i < hd; i += 64) {
+    store_elem<T>(kp + src + i, k[src + i]);
+    store_elem<T>(vp + src + i, v[src + i]);
   }
-  for (int i = lane; i < hd; i += 64) store_elem<T>(vd + i, v[src + i]);
 }
 
-__global__ __launch_bounds__(64) void q_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
-                                                        int n_heads, int hd, const float* __restrict__ w, float eps,
-                                                        InvFreq inv, long pos0) {
-  const int r = blockIdx.x, h = blockIdx.y;
-  const size_t off = ((size_t)r * n_heads + h) * hd;
-  float* dst = q_out + off;
-  norm_rope_head(q + off, hd, w, eps, true, inv, (double)(pos0 + r), [&](int i, float y) { dst[i] = y; });
+// One decode or prefill row's prologue: q heads RMSNormed + rotated into
+// q_out, k heads RMSNormed + rotated into the cache, v heads copied into the
+// cache. grid (rows, slot blocks), one wave per 8 head slots of the row's
+// list [q heads | k heads | v heads]. Lane l owns the element pairs
+// (i, i + half) with i = l + 64 j, j < NP, for every head of its slots, so
+// the row's sin/cos (f64, cast to f32) are computed once per wave rather than
+// once per head, while the wave's head loads are in flight.
+constexpr int kSlots = 8;
+
+template <typename T, int NP>
+__global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
+                                                          int n_q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, T* __restrict__ kp,
+                                                          T* __restrict__ vp, int n_kv, int hd,
+                                                          const float* __restrict__ q_w,
+                                                          const float* __restrict__ k_w, float eps, InvFreq inv,
+                                                          long pos0) {
+#pragma clang fp contract(off)
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const int half = hd / 2;
+  const int n_slots = n_q + 2 * n_kv;
+  const int s0 = (int)blockIdx.y * kSlots;
+  // Source of slot s (q, k or v head of row r); its destination is below.
+  auto src = [&](int s) -> const float* {
+    if (s < n_q) return q + ((size_t)r * n_q + s) * hd;
+    if (s < n_q + n_kv) return k + ((size_t)r * n_kv + (s - n_q)) * hd;
+    return v + ((size_t)r * n_kv + (s - n_q - n_kv)) * hd;
+  };
+  // inv_freq first: the sin/cos below wait only for it, not the heads.
+  double freq[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) freq[p] = inv.f[min(lane + 64 * p, half - 1)];
+  float x0[kSlots][NP], x1[kSlots][NP];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const bool live = s0 + j < n_slots;
+    const float* x = src(live ? s0 + j : 0);
+    // Unconditional loads from clamped (valid) addresses, so the wait
+    // counts stay exact; dead lanes and slots are zeroed afterwards.
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int i = min(lane + 64 * p, half - 1);
+      const bool in = live && lane + 64 * p < half;
+      const float a0 = x[i], a1 = x[i + half];
+      x0[j][p] = in ? a0 : 0.f;
+      x1[j][p] = in ? a1 : 0.f;
+    }
+  }
+  float wq0[NP], wq1[NP], wk0[NP], wk1[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = min(lane + 64 * p, half - 1);
+    wq0[p] = q_w[i];
+    wq1[p] = q_w[i + half];
+    wk0[p] = k_w[i];
+    wk1[p] = k_w[i + half];
+  }
+  // Every load above is issued before the first use (the scheduler would
+  // otherwise sink each head's loads to its arithmetic, one round trip each).
+  __builtin_amdgcn_sched_barrier(0);
+  const double pos = (double)(pos0 + r);
+  float sn[NP], cs[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = lane + 64 * p;
+    double sd = 0.0, cd = 1.0;
+    if (i < half) sincos(pos * freq[p], &sd, &cd);
+    sn[p] = (float)sd;
+    cs[p] = (float)cd;
+  }
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const int s = s0 + j;
+    if (s >= n_slots) break;
+    if (s >= n_q + n_kv) {  // v head: copied into the cache
+      T* d = vp + ((size_t)r * n_kv + (s - n_q - n_kv)) * hd;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int i = lane + 64 * p;
+        if (i < half) {
+          store_elem<T>(d + i, x0[j][p]);
+          store_elem<T>(d + i + half, x1[j][p]);
+        }
+      }
+      continue;
+    }
+    const bool is_q = s < n_q;
+    double ss = 0.0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) ss += (double)x0[j][p] * (double)x0[j][p] + (double)x1[j][p] * (double)x1[j][p];
+    ss = wave_sum_f64(ss);
+    const float inv_rms = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int i = lane + 64 * p;
+      if (i >= half) continue;
+      const float a0 = x0[j][p] * inv_rms * (is_q ? wq0[p] : wk0[p]);
+      const float a1 = x1[j][p] * inv_rms * (is_q ? wq1[p] : wk1[p]);
+      const float ya = a0 * cs[p] - a1 * sn[p], yb = a0 * sn[p] + a1 * cs[p];
+      if (is_q) {
+        float* d = q_out + ((size_t)r * n_q + s) * hd;
+        d[i] = ya;
+        d[i + half] = yb;
+      } else {
+        T* d = kp + ((size_t)r * n_kv + (s - n_q)) * hd;
+        store_elem<T>(d + i, ya);
+        store_elem<T>(d + i + half, yb);
+      }
+    }
+  }
+}
+
+template <typename T>
+void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int n_q, const float* k, const float* v,
+                           T* kp, T* vp, int n_kv, int hd, const float* q_w, const float* k_w, float eps,
+                           const InvFreq& inv, long pos0, hipStream_t s) {
+  if (np == 1)
+    hipLaunchKernelGGL((row_prologue_kernel<T, 1>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
+                       k_w, eps, inv, pos0);
+  else if (np == 2)
+    hipLaunchKernelGGL((row_prologue_kernel<T, 2>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
+                       k_w, eps, inv, pos0);
+  else
+    hipLaunchKernelGGL((row_prologue_kernel<T, 4>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
+                       k_w, eps, inv, pos0);
 }
 
 }  // namespace
 
 HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v, size_t rows,
-                        bool norm, const float* k_w, float eps, const InvFreq* inv, hipStream_t s) {
+                        hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
   const size_t off = pos0 * kv->kv_dim;
-  static const InvFreq kZero = {};
-  const InvFreq& f = inv ? *inv : kZero;
   const dim3 grid((unsigned)rows, (unsigned)kv->n_kv_heads);
   if (kv->elem == RV_ELEM_F32) {
     hipLaunchKernelGGL(append_kernel<float>, grid, dim3(64), 0, s, k, v, (float*)kv->k_layer(layer) + off,
-                       (float*)kv->v_layer(layer) + off, (int)kv->kv_dim, (int)kv->head_dim, norm, k_w, eps, f,
-                       (long)pos0);
+                       (float*)kv->v_layer(layer) + off, (int)kv->kv_dim, (int)kv->head_dim);
   } else {
     hipLaunchKernelGGL(append_kernel<uint16_t>, grid, dim3(64), 0, s, k, v, (uint16_t*)kv->k_layer(layer) + off,
-                       (uint16_t*)kv->v_layer(layer) + off, (int)kv->kv_dim, (int)kv->head_dim, norm, k_w, eps,
-                       f, (long)pos0);
+                       (uint16_t*)kv->v_layer(layer) + off, (int)kv->kv_dim, (int)kv->head_dim);
   }
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "append launch";
   return st;
 }
 
-HipStatus launch_q_prologue(const float* q, float* q_out, size_t rows, size_t n_heads, size_t head_dim,
-                            const float* w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s) {
+HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
+                              size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
+                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
-  hipLaunchKernelGGL(q_prologue_kernel, dim3((unsigned)rows, (unsigned)n_heads), dim3(64), 0, s, q, q_out,
-                     (int)n_heads, (int)head_dim, w, eps, inv, (long)pos0);
+  const int hd = (int)kv->head_dim, n_kv = (int)kv->n_kv_heads;
+  const int half = hd / 2;
+  const int np = half <= 64 ? 1 : half <= 128 ? 2 : 4;
+  const int n_slots = (int)n_q + 2 * n_kv;
+  const dim3 grid((unsigned)rows, (unsigned)((n_slots + kSlots - 1) / kSlots));
+  const size_t off = cache_row * kv->kv_dim;
+  if (kv->elem == RV_ELEM_F32)
+    launch_row_prologue_t<float>(grid, np, q, q_out, (int)n_q, k, v, (float*)kv->k_layer(layer) + off,
+                                 (float*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0, s);
+  else
+    launch_row_prologue_t<uint16_t>(grid, np, q, q_out, (int)n_q, k, v, (uint16_t*)kv->k_layer(layer) + off,
+                                    (uint16_t*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0,
+                                    s);
   st.e = hipGetLastError();
-  if (st.e != hipSuccess) st.what = "q prologue launch";
+  if (st.e != hipSuccess) st.what = "prologue launch";
   return st;
 }
 

@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 import ramvamp_amd as rv
-from gpu_util import FP32_FLOOR, dev, elem_code, gate, host, rel_err, say, torch_cuda
+from gpu_util import FP32_FLOOR, FP32_REL, dev, elem_code, gate, host, rel_err, say, torch_cuda
 from helpers import Rng, assert_close, reference_attention, round_trip
 from ramvamp_amd import synth
 
@@ -286,6 +286,31 @@ def test_config1_decode_step_matches_the_oracle():
     e = gate(out, want, what="config 1")
     say(f"config 1 max rel err {e:.3e}")
     assert kv.len(0) == 513
+
+
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_decode_step_rotates_q_and_k_at_the_given_position(elem):
+    # forward.rs:2628-2629 rotates q and k at the same rope_pos; the row still
+    # lands at the layer's cursor. Head dims 128/256/512 cover one, two and
+    # four element pairs per lane in the fused prologue.
+    torch_cuda()
+    rng = Rng(0x5EED)
+    for n_kv, n_q, hd, n_pos, position in ((4, 32, 128, 5, 700), (2, 6, 256, 3, 3), (1, 3, 512, 2, 41)):
+        say(f"case decode_step {(n_kv, n_q, hd, n_pos, position)} elem={elem}")
+        kv, ref = twin_caches(rng, 1, n_kv, hd, n_pos, elem, cap=n_pos + 1)
+        wq, wk = rng.vec_in(hd, 0.9, 1.1), rng.vec_in(hd, 0.9, 1.1)
+        q, k, v = rng.vec_in(n_q * hd, -2, 2), rng.vec_in(n_kv * hd, -2, 2), rng.vec_in(n_kv * hd, -2, 2)
+        out = np.zeros(q.size, np.float32)
+        rv.decode_step(kv, 0, q, k, v, wq, wk, 1e-6, 1e6, position, 0.125, out)
+        want = ref.decode_step(0, q, k, v, wq, wk, 1e-6, 1e6, position, 0.125)
+        # f16: the new K row may round one ulp apart (f64 sin/cos of two libms).
+        f16 = elem == "f16"
+        gate(out, want, rel=1e-3 if f16 else FP32_REL, abs_tol=1.5e-3 if f16 else FP32_FLOOR,
+             what=f"decode_step hd {hd}")
+        got_k, want_k = kv.k_row(0, n_pos), ref.read_row(False, 0, n_pos)
+        gate(got_k, want_k, rel=1e-3 if f16 else 2e-7, floor=1e-6, what=f"rotated K row hd {hd}")
+        assert np.array_equal(kv.v_row(0, n_pos), ref.read_row(True, 0, n_pos))
+        assert kv.len(0) == n_pos + 1
 
 
 def test_config2_layers_match_the_oracle_at_ctx_4096():
