@@ -223,11 +223,42 @@ __device__ __forceinline__ void wait_vmcnt() {
 // (max, sum)[128 columns].
 constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
 
-template <int MODE, int W, int MT, int NS>
-__global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict__ q, const char* __restrict__ stage,
-                                                      int n_stage_tiles, int q_stride, int rows, int start, int group,
-                                                      int n_rb, int n_units, int kv_splits, float qscale,
-                                                      float* __restrict__ part, float* __restrict__ out) {
+// NaN-propagating max of three (v_maximum3_f32: unlike fmaxf it needs no
+// operand canonicalisation).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
+// Sum of the 8 P values of a B operand in fp32 (v_dot2 with (1, 1)): the
+// softmax denominator of exactly the rounded P the PV products use.
+__device__ __forceinline__ float sum8(f16x8 v, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 0, 1), h2{1, 1}, acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 2, 3), h2{1, 1}, acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 4, 5), h2{1, 1}, acc, false);
+  return __builtin_amdgcn_fdot2(__builtin_shufflevector(v, v, 6, 7), h2{1, 1}, acc, false);
+}
+__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+}
+
+// G groups of W waves. Every group covers all M = 16 W MT columns of the
+// workgroup; group g computes the tiles tt_lo + G j + g of the workgroup's
+// range from its own ring of NS stages, all groups in lockstep (one barrier
+// per iteration), and the groups' (O, max, sum) are merged through LDS at the
+// end. With G = 2 two waves share each SIMD, so one's softmax overlaps the
+// other's MFMAs.
+template <int MODE, int G, int W, int MT, int NS>
+__global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __restrict__ q,
+                                                             const char* __restrict__ stage, int n_stage_tiles,
+                                                             int q_stride, int rows, int start, int group, int n_rb,
+                                                             int n_units, int kv_splits, float qscale,
+                                                             float* __restrict__ part, float* __restrict__ out) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   typedef typename Op<MODE>::V4 V4;
@@ -241,8 +272,11 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
   // tile's maximum exceeds it by more than this (log2 units): P values stay
   // below 2^8 and most tiles skip rescaling the accumulators.
   constexpr float kRescale = 8.0f;
+  // Per-lane floats a later group hands to group 0: O, then (max, sum) per mt.
+  constexpr int kX = MT * 32 + 2 * MT;
+  static_assert((size_t)(G - 1) * W * 64 * kX * 4 <= (size_t)G * NS * TB, "group exchange fits the ring");
 
-  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
+  __shared__ __attribute__((aligned(1024))) char lds[G][NS][TB];
 
   // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
   // XCD b % 8). Units (kv head, row block, split) are numbered kv-head-major
@@ -252,7 +286,9 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
   const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
   if ((int)(blockIdx.x / 8) >= per_xcd || unit >= n_units) return;
   const int split = unit % kv_splits, rb = (unit / kv_splits) % n_rb, kvh = unit / (kv_splits * n_rb);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave / W, wv = wave % W;
   const int lm = lane & 15, kk = lane >> 4;
   const int qr = M / group;  // rows per workgroup
   const int r0 = rb * qr;
@@ -263,34 +299,37 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
   const int tt_lo = (int)((long)n_tiles * split / kv_splits);
   const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
   const int n = tt_hi - tt_lo;
+  const int n_mine = (n - grp + G - 1) / G;  // this group's tiles: tt_lo + G j + grp
+  const int n_iter = (n + G - 1) / G;        // iterations (every group, lockstep)
 
-  // Tile j of this workgroup (clamped to its last, so every wave issues the
-  // same number of loads per iteration) into stage s: wave w copies the
-  // 1 KiB pieces w, w + W, ...; lane l's 16 bytes land at piece + 16 l.
+  // The group's tile j (clamped to its last, so every wave issues the same
+  // number of loads per iteration) into stage s: wave w copies the 1 KiB
+  // pieces w, w + W, ...; lane l's 16 bytes land at piece + 16 l.
   const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
   auto issue_piece = [&](int j, int s, int i) {
-    const char* g = src + (size_t)(tt_lo + min(j, n - 1)) * TB;
-    const int piece = 1024 * (wave + W * i);
-    lds_load16(g + piece, (lds_void*)&lds[s][piece]);
+    if (n_mine <= 0) return;
+    const char* g = src + (size_t)(tt_lo + G * min(j, n_mine - 1) + grp) * TB;
+    const int piece = 1024 * (wv + W * i);
+    lds_load16(g + piece, (lds_void*)&lds[grp][s][piece]);
   };
-  auto issue = [&](int j, int s) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) issue_piece(j, s, i);
-  };
-  if (n > 0) {
+  for (int j = 0; j < NS - 1; ++j)
 #pragma unroll
-    for (int j = 0; j < NS - 1; ++j) issue(j, j);
-  }
+    for (int i = 0; i < LPW; ++i) issue_piece(j, j, i);
 
-  // This lane's query vector in column block mt: column m = 16*(wave*MT + mt) + lm.
+  // This lane's query vector in column block mt: column m = 16*(wv*MT + mt) + lm.
   int my_row[MT], my_head[MT], my_limit[MT];
   bool col_ok[MT];
   V8 qh[MT][4], ql[MT][4];
   f32x4 o[MT][8];
   float m_run[MT], l_run[MT];
+  // -m_run, or 0 while a column has seen no unmasked position: the non-split
+  // modes start their QK MFMAs from it, so S^T arrives relative to the
+  // running max; the split mode adds it after scaling.
+  f32x4 negm[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * (wave * MT + mt) + lm;
+    const int m = 16 * (wv * MT + mt) + lm;
     my_head[mt] = m / qr;
     my_row[mt] = r0 + m % qr;
     col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
@@ -310,20 +349,26 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
     for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
     l_run[mt] = 0.f;
+    negm[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int i = 0; i < n; ++i) {
-    const int s = i % NS;
-    // This wave's loads of tile i are done once at most NS - 2 tiles of its
-    // loads remain in flight; the barrier makes every wave's part visible
-    // and retires the stage the loads below overwrite (computed last
-    // iteration).
+  for (int j = 0; j < n_iter; ++j) {
+    const int s = j % NS;
+    // This wave's loads of the group's tile j are done once at most NS - 2
+    // tiles of its loads remain in flight; the barrier makes every wave's
+    // part visible and retires the stage the loads below overwrite
+    // (computed last iteration).
     wait_vmcnt<(NS - 2) * LPW>();
     __syncthreads();
-    const char* kt = lds[s];
-    const char* vt = lds[s] + P * kPlaneBytes;
-    const int t0 = (tt_lo + i) * kBT;
-    const int nxt = (i + NS - 1) % NS;
+    const int nxt = (j + NS - 1) % NS;
+    if (j >= n_mine) {  // this group has no tile this iteration (wave-uniform)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) issue_piece(j + NS - 1, nxt, i);
+      continue;
+    }
+    const char* kt = lds[grp][s];
+    const char* vt = lds[grp][s] + P * kPlaneBytes;
+    const int t0 = (tt_lo + G * j + grp) * kBT;
 
     // S^T for the tile's four 16-position blocks. The tile's K operands are
     // read from LDS ahead of the MFMAs; the next tile's loads are issued
@@ -342,7 +387,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
     for (int pb = 0; pb < 4; ++pb) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sc[mt][pb] = kSplit ? f32x4{0.f, 0.f, 0.f, 0.f} : negm[mt];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           sc[mt][pb] = Op<MODE>::mfma(ka[pb][ks], qh[mt][ks], sc[mt][pb]);
@@ -354,13 +399,13 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
       }
       // Pieces [0, LPW/2) of the next tile, spread over the four blocks.
 #pragma unroll
-      for (int j = pb * (LPW / 2) / 4; j < (pb + 1) * (LPW / 2) / 4; ++j) issue_piece(i + NS - 1, nxt, j);
+      for (int i = pb * (LPW / 2) / 4; i < (pb + 1) * (LPW / 2) / 4; ++i) issue_piece(j + NS - 1, nxt, i);
     }
     if constexpr (kSplit) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] *= qscale;
+        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] = sc[mt][pb] * qscale + negm[mt];
     }
     // Causal mask only where some row of the block stops inside the tile.
     if (t0 + kBT > all_see) {
@@ -372,32 +417,48 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
           for (int e = 0; e < 4; ++e)
             if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
     }
-    // Online softmax per query vector; this lane holds t0 + 16pb + 4kk + e.
-    // Column maxima over the lane's 16 values, then across the four lanes of
-    // the column (lanes 16 and 32 apart) with permlane swaps.
+    // Online softmax per query vector; this lane holds t0 + 16pb + 4kk + e,
+    // relative to m_run (absolute while m_run is the sentinel). Column maxima
+    // over the lane's 16 values, then across the four lanes of the column
+    // (lanes 16 and 32 apart) with permlane swaps.
     float mx[MT];
     bool grow = false;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      float x = fmaxf(fmaxf(sc[mt][0][0], sc[mt][0][1]), fmaxf(sc[mt][0][2], sc[mt][0][3]));
-#pragma unroll
-      for (int pb = 1; pb < 4; ++pb)
-        x = fmaxf(x, fmaxf(fmaxf(sc[mt][pb][0], sc[mt][pb][1]), fmaxf(sc[mt][pb][2], sc[mt][pb][3])));
+      float x = max3f(sc[mt][0][0], sc[mt][0][1], sc[mt][0][2]);
+      x = max3f(x, sc[mt][0][3], sc[mt][1][0]);
+      x = max3f(x, sc[mt][1][1], sc[mt][1][2]);
+      x = max3f(x, sc[mt][1][3], sc[mt][2][0]);
+      x = max3f(x, sc[mt][2][1], sc[mt][2][2]);
+      x = max3f(x, sc[mt][2][3], sc[mt][3][0]);
+      x = max3f(x, sc[mt][3][1], sc[mt][3][2]);
+      x = __builtin_elementwise_maximum(x, sc[mt][3][3]);
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      x = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      mx[mt] = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-      grow = grow || mx[mt] > m_run[mt] + kRescale;
+      mx[mt] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      grow = grow || mx[mt] > kRescale || m_run[mt] == kNegSentinel;
     }
     if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const float mn = fmaxf(m_run[mt], mx[mt]);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[mt] - mn);
-        m_run[mt] = mn;
-        l_run[mt] *= alpha;
+        // A column still at the sentinel takes the tile's maximum outright
+        // (its O and sum are zero); others move up by d >= 0 and rescale.
+        const bool fresh = m_run[mt] == kNegSentinel;
+        const float d = fresh ? fmaxf(mx[mt], kNegSentinel) : fmaxf(mx[mt], 0.f);
+        if (!fresh) {
+          const float alpha = __builtin_amdgcn_exp2f(-d);
+          l_run[mt] *= alpha;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
+          for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
+          m_run[mt] += d;
+        } else {
+          m_run[mt] = d;
+        }
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] -= d;
+        const float nm = m_run[mt] == kNegSentinel ? 0.f : -m_run[mt];
+        negm[mt] = f32x4{nm, nm, nm, nm};
       }
     }
     // P^T operand for PV step s2: slots j<4 are t = 32s2 + 4kk + j, slots
@@ -410,17 +471,20 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
       for (int pb = 0; pb < 4; ++pb) {
         f32x4 p;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e] - m_run[mt]);
-        psum += (p[0] + p[1]) + (p[2] + p[3]);
+        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e]);
         const V4 hi = __builtin_convertvector(p, V4);
         V4 lo;
-        if constexpr (kSplit) lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
+        if constexpr (kSplit) {
+          psum += (p[0] + p[1]) + (p[2] + p[3]);
+          lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
           if constexpr (kSplit) pl[mt][pb / 2][4 * (pb % 2) + e] = lo[e];
         }
       }
+      if constexpr (!kSplit) psum = sum8(ph[mt][1], sum8(ph[mt][0], 0.f));
       l_run[mt] += psum;
     }
     // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's);
@@ -449,11 +513,11 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
       }
       // Pieces [LPW/2, LPW), spread over the eight d blocks.
 #pragma unroll
-      for (int j = b * (LPW / 2) / 8; j < (b + 1) * (LPW / 2) / 8; ++j) issue_piece(i + NS - 1, nxt, LPW / 2 + j);
+      for (int i = b * (LPW / 2) / 8; i < (b + 1) * (LPW / 2) / 8; ++i) issue_piece(j + NS - 1, nxt, LPW / 2 + i);
     }
   }
   // The clamped prefetches past the last tile may still be landing in LDS:
-  // retire them before the workgroup ends.
+  // retire them before the ring is reused or the workgroup ends.
   wait_vmcnt<0>();
 
   // Column sums: each lane holds a quarter of its column's positions.
@@ -461,6 +525,43 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
   for (int mt = 0; mt < MT; ++mt) {
     l_run[mt] += __shfl_xor(l_run[mt], 16, 64);
     l_run[mt] += __shfl_xor(l_run[mt], 32, 64);
+  }
+
+  if constexpr (G > 1) {
+    // Groups 1.. hand (O, max, sum) to group 0 through the ring: item i of
+    // wave w's lane l at float (w * kX + i) * 64 + l (conflict-free).
+    float* xch = reinterpret_cast<float*>(&lds[0][0][0]);
+    __syncthreads();
+    if (grp > 0) {
+      float* mine = xch + (size_t)((grp - 1) * W + wv) * kX * 64 + lane;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mine[((mt * 8 + b) * 4 + e) * 64] = o[mt][b][e];
+        mine[(MT * 32 + 2 * mt) * 64] = m_run[mt];
+        mine[(MT * 32 + 2 * mt + 1) * 64] = l_run[mt];
+      }
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int g2 = 1; g2 < G; ++g2) {
+      const float* theirs = xch + (size_t)((g2 - 1) * W + wv) * kX * 64 + lane;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float m2 = theirs[(MT * 32 + 2 * mt) * 64], l2 = theirs[(MT * 32 + 2 * mt + 1) * 64];
+        const float mn = fmaxf(m_run[mt], m2);
+        const float a1 = __builtin_amdgcn_exp2f(m_run[mt] - mn), a2 = __builtin_amdgcn_exp2f(m2 - mn);
+        m_run[mt] = mn;
+        l_run[mt] = l_run[mt] * a1 + l2 * a2;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[mt][b][e] = o[mt][b][e] * a1 + theirs[((mt * 8 + b) * 4 + e) * 64] * a2;
+      }
+    }
   }
 
   if (kv_splits == 1) {
@@ -480,7 +581,7 @@ __global__ __launch_bounds__(W * 64) void prefill_kernel(const float* __restrict
   float* mine = part + (((size_t)kvh * n_rb + rb) * kv_splits + split) * kPartStride;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * (wave * MT + mt) + lm;
+    const int m = 16 * (wv * MT + mt) + lm;
 #pragma unroll
     for (int b = 0; b < 8; ++b) *reinterpret_cast<f32x4*>(&mine[(size_t)m * kD + 16 * b + 4 * kk]) = o[mt][b];
     if (kk == 0) {
@@ -541,31 +642,27 @@ struct PrefillArgs {
   TimedPair tp;
 };
 
-template <int MODE, int W, int MT, int NS>
+template <int MODE, int G, int W, int MT, int NS>
 void launch_main(const PrefillArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
-  launch_timed(a.tp, prefill_kernel<MODE, W, MT, NS>, dim3(blocks), dim3(W * 64), s, a.q, (const char*)a.stage,
-               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale, a.part,
-               a.out);
+  launch_timed(a.tp, prefill_kernel<MODE, G, W, MT, NS>, dim3(blocks), dim3(G * W * 64), s, a.q,
+               (const char*)a.stage, a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units,
+               a.kv_splits, a.qscale, a.part, a.out);
 }
 
-// 128 query vectors: 4 waves x 2 column blocks with a ring of four 32 KiB
-// stages (two 64 KiB stages in the split mode), one workgroup per CU.
-// 64 query vectors (single-plane modes): 2 waves x 2 column blocks with two
-// 32 KiB stages, two workgroups per CU; the split mode keeps 4 waves x 1.
+// F16 / BF16: two groups of 4 waves (2 per SIMD), each with two 32 KiB
+// stages; 128 query vectors = 2 column blocks per wave, 64 = 1. The split
+// mode's 64 KiB tiles allow one group: 4 waves with two stages.
 template <int MODE, typename T>
 void launch_mode(int vectors, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles * 2)), dim3(kWG), 0, s,
                      kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
   constexpr bool kSplit = Op<MODE>::kSplit;
-  if (vectors == 64) {
-    if constexpr (kSplit)
-      launch_main<MODE, 4, 1, 2>(a, s);
-    else
-      launch_main<MODE, 2, 2, 2>(a, s);
-  } else {
-    launch_main<MODE, 4, 2, kSplit ? 2 : 4>(a, s);
-  }
+  constexpr int G = kSplit ? 1 : 2;
+  if (vectors == 64)
+    launch_main<MODE, G, 4, 1, 2>(a, s);
+  else
+    launch_main<MODE, G, 4, 2, 2>(a, s);
 }
 
 template <typename T>
@@ -596,8 +693,13 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
   const int planes = (m == RV_PREFILL_F16 || m == RV_PREFILL_BF16) ? 1 : 2;
   // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
-  // the tuning asks for it.
-  const int vectors = kv->tune_prefill_rows > 0 && kv->tune_prefill_rows * group <= 64 ? 64 : 128;
+  // 128-vector blocks would leave CUs idle (fewer than 256 workgroups) or the
+  // tuning asks for it.
+  int vectors = 128;
+  if (kv->tune_prefill_rows > 0)
+    vectors = kv->tune_prefill_rows * group <= 64 ? 64 : 128;
+  else if ((long)((rows * group + 127) / 128) * n_kv < 256)
+    vectors = 64;
   const int qr = vectors / group;
   const int n_rb = (int)((rows + qr - 1) / qr);
   const size_t positions = start + rows;
