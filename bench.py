@@ -256,6 +256,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the prefill legs (configs 3 and 4, every mode), log them and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -278,6 +280,12 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log("copied 10 x 64 MiB")
+        return
+    if args.prefill_only:
+        for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
+            r = bench_prefill(torch, rv, synth, cfg, mode)
+            log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
+                f"{r['tflops_kernel']:.1f} TFLOP/s")
         return
     r2 = bench_config2(torch, rv, synth, args.steps, args.warmup, keep_host=not args.no_cpu)
     log(f"config 2: {r2['us_per_layer']:.2f} us/layer (graph), {r2['eager_us_per_layer']:.2f} us/layer (eager), "

@@ -27,6 +27,7 @@ RV_TUNE_PREFILL_ROWS = 4
 RV_TUNE_DECODE_HG = 5
 RV_TUNE_DECODE_IMPL = 6
 RV_TUNE_KERNEL_TIMING = 7
+RV_TUNE_PREFILL_IMPL = 8
 
 
 class RvError(ctypes.Structure):

@@ -12,24 +12,44 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libramvamp_attn.so")
 SOURCES = ["rv_abi.cpp", "rv_prologue.hip", "rv_decode.hip", "rv_prefill.hip"]
+# Per-source extra flags. The prefill kernels hold MFMA accumulators and
+# their softmax operands together; the default heuristic places the
+# accumulators in AGPRs and copies them through VGPRs every tile, so their
+# MFMAs are forced to the VGPR form.
+EXTRA = {"rv_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+NOISE = "is not a recognized feature for this target"
+
+
+def _run(cmd: list[str]) -> list[str]:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if NOISE not in ln]
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + "\n".join(msgs))
+    return msgs
 
 
 def build(verbose: bool = False) -> str:
+    """Compile every source to an object (in parallel), then link the library."""
+    objdir = os.path.join(HERE, "_obj")
+    os.makedirs(objdir, exist_ok=True)
+    objs, cmds = [], []
+    for src in SOURCES:
+        obj = os.path.join(objdir, src + ".o")
+        objs.append(obj)
+        cmds.append([HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", "-o", obj, os.path.join(CSRC, src)])
+    with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+        msgs = [m for ms in pool.map(_run, cmds) for m in ms]
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
-    if proc.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + "\n".join(msgs))
+    msgs += _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     if verbose and msgs:
         print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, OUT)

@@ -727,6 +727,7 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_PREFILL_ROWS: kv->tune_prefill_rows = value; break;
     case RV_TUNE_DECODE_HG: kv->tune_decode_hg = value; break;
     case RV_TUNE_DECODE_IMPL: kv->tune_decode_impl = value; break;
+    case RV_TUNE_PREFILL_IMPL: kv->tune_prefill_impl = value; break;
     case RV_TUNE_KERNEL_TIMING: kv->timing = value != 0; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }

@@ -37,6 +37,7 @@ struct rv_kv {
   int64_t tune_decode_waves = 0;
   int64_t tune_prefill_rows = 0;
   int64_t tune_decode_hg = 0;
+  int64_t tune_prefill_impl = 0;  // 0 auto, 1 two wave groups, 2 software-pipelined
   int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups
 
   // RV_TUNE_KERNEL_TIMING: event pairs around the dominant kernel of each

@@ -591,6 +591,275 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   }
 }
 
+// Software-pipelined single-group kernel (F16 / BF16): 4 waves, one per
+// SIMD, each owning MT column blocks; tiles stream through a ring of NS
+// 32 KiB stages. Iteration j, after one barrier:
+//   (rare) rescale O, the sum and S(j) when S(j)'s maximum moved m_run;
+//   QK(j+1) on the MFMAs   || P(j) = exp2(S(j)) and its sums on the VALU;
+//   PV(j) on the MFMAs     || mask and column maxima of S(j+1) on the VALU;
+// with tile j + NS - 1's loads issued among the QK MFMAs. One wave's MFMA
+// and VALU streams are independent within each step, so they overlap.
+template <int MODE, int MT, int NS>
+__global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict__ q,
+                                                        const char* __restrict__ stage, int n_stage_tiles,
+                                                        int q_stride, int rows, int start, int group, int n_rb,
+                                                        int n_units, int kv_splits, float qscale,
+                                                        float* __restrict__ part, float* __restrict__ out) {
+  typedef typename Op<MODE>::E E;
+  typedef typename Op<MODE>::V8 V8;
+  typedef typename Op<MODE>::V4 V4;
+  static_assert(!Op<MODE>::kSplit, "one plane per operand");
+  static_assert(NS >= 3, "K(j+1), V(j) and the loads of a later tile need three stages");
+  constexpr int W = 4;
+  constexpr int M = 16 * W * MT;
+  constexpr int TB = 2 * kPlaneBytes;
+  constexpr int LPW = TB / 1024 / W;  // 8
+  constexpr float kRescale = 8.0f;
+
+  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
+
+  const int per_xcd = (n_units + 7) / 8;
+  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if ((int)(blockIdx.x / 8) >= per_xcd || unit >= n_units) return;
+  const int split = unit % kv_splits, rb = (unit / kv_splits) % n_rb, kvh = unit / (kv_splits * n_rb);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lm = lane & 15, kk = lane >> 4;
+  const int qr = M / group;
+  const int r0 = rb * qr;
+  const int rows_here = min(qr, rows - r0);
+  const int wg_limit = start + r0 + rows_here;
+  const int all_see = start + r0 + 1;
+  const int n_tiles = (wg_limit + kBT - 1) / kBT;
+  const int tt_lo = (int)((long)n_tiles * split / kv_splits);
+  const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
+  const int n = tt_hi - tt_lo;
+
+  // Tile j (clamped to the last, so every iteration issues LPW loads per
+  // wave and the wait counts stay exact) into stage j % NS.
+  const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
+  auto issue_piece = [&](int j, int i) {
+    const char* g = src + (size_t)(tt_lo + min(j, n - 1)) * TB;
+    const int piece = 1024 * (wave + W * i);
+    lds_load16(g + piece, (lds_void*)&lds[j % NS][piece]);
+  };
+  if (n > 0) {
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) issue_piece(j, i);
+  }
+
+  int my_row[MT], my_head[MT], my_limit[MT];
+  bool col_ok[MT];
+  V8 qh[MT][4];
+  f32x4 o[MT][8];
+  float m_run[MT], l_run[MT];
+  f32x4 negm[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * (wave * MT + mt) + lm;
+    my_head[mt] = m / qr;
+    my_row[mt] = r0 + m % qr;
+    col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
+    my_limit[mt] = col_ok[mt] ? start + my_row[mt] + 1 : 0;
+    const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
+                      (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
+    const float qs = col_ok[mt] ? qscale : 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qh[mt][s2][e] = (E)(qp[32 * s2 + e] * qs);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[mt] = kNegSentinel;
+    l_run[mt] = 0.f;
+    negm[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // S^T of tile j into dst (relative to the running max); with `loads`,
+  // tile j + NS - 2's pieces are issued among the MFMAs (the caller is
+  // iteration j - 1, whose loads target tile (j - 1) + NS - 1).
+  auto qk = [&](int j, f32x4 (&dst)[MT][4], bool loads) {
+    const char* kt = lds[j % NS];
+    V8 ka[2][4];
+    auto read_k = [&](int pb, int buf) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) ka[buf][ks] = *reinterpret_cast<const V8*>(kt + k_off(16 * pb + lm, 4 * ks + kk));
+    };
+    read_k(0, 0);
+#pragma unroll
+    for (int pb = 0; pb < 4; ++pb) {
+      if (pb < 3) read_k(pb + 1, (pb + 1) & 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        dst[mt][pb] = negm[mt];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) dst[mt][pb] = Op<MODE>::mfma(ka[pb & 1][ks], qh[mt][ks], dst[mt][pb]);
+      }
+      if (loads) {
+#pragma unroll
+        for (int i = pb * LPW / 4; i < (pb + 1) * LPW / 4; ++i) issue_piece(j + NS - 2, i);
+      }
+    }
+  };
+  // Mask (only where a row of the block stops inside the tile) and column
+  // maxima of S(j); returns whether any column must move its maximum.
+  float mx[MT];
+  auto scan = [&](int j, f32x4 (&sc)[MT][4]) -> bool {
+    const int t0 = (tt_lo + j) * kBT;
+    if (t0 + kBT > all_see) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int pb = 0; pb < 4; ++pb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
+    }
+    bool grow = false;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float x = max3f(sc[mt][0][0], sc[mt][0][1], sc[mt][0][2]);
+      x = max3f(x, sc[mt][0][3], sc[mt][1][0]);
+      x = max3f(x, sc[mt][1][1], sc[mt][1][2]);
+      x = max3f(x, sc[mt][1][3], sc[mt][2][0]);
+      x = max3f(x, sc[mt][2][1], sc[mt][2][2]);
+      x = max3f(x, sc[mt][2][3], sc[mt][3][0]);
+      x = max3f(x, sc[mt][3][1], sc[mt][3][2]);
+      x = __builtin_elementwise_maximum(x, sc[mt][3][3]);
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      x = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      mx[mt] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      grow = grow || mx[mt] > kRescale || m_run[mt] == kNegSentinel;
+    }
+    return __builtin_amdgcn_ballot_w64(grow) != 0;
+  };
+  // Move the running maxima to S(j)'s (see prefill_kernel) and rescale.
+  auto rescale = [&](f32x4 (&sc)[MT][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const bool fresh = m_run[mt] == kNegSentinel;
+      const float d = fresh ? fmaxf(mx[mt], kNegSentinel) : fmaxf(mx[mt], 0.f);
+      if (!fresh) {
+        const float alpha = __builtin_amdgcn_exp2f(-d);
+        l_run[mt] *= alpha;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
+        m_run[mt] += d;
+      } else {
+        m_run[mt] = d;
+      }
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) sc[mt][pb] -= d;
+      const float nm = m_run[mt] == kNegSentinel ? 0.f : -m_run[mt];
+      negm[mt] = f32x4{nm, nm, nm, nm};
+    }
+  };
+  V8 ph[MT][2];
+  auto make_p = [&](f32x4 (&sc)[MT][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) {
+        f32x4 p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e]);
+        const V4 hi = __builtin_convertvector(p, V4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
+      }
+      l_run[mt] = sum8(ph[mt][1], sum8(ph[mt][0], l_run[mt]));
+    }
+  };
+  auto pv = [&](int j) {
+    const char* vt = lds[j % NS] + kPlaneBytes;
+    V8 va[2][2];
+    auto read_v = [&](int b, int buf) {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) va[buf][s2] = *reinterpret_cast<const V8*>(vt + vt_off(16 * b + lm, 4 * s2 + kk));
+    };
+    read_v(0, 0);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (b < 7) read_v(b + 1, (b + 1) & 1);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[mt][b] = Op<MODE>::mfma(va[b & 1][s2], ph[mt][s2], o[mt][b]);
+    }
+  };
+
+  f32x4 sa[MT][4], sb[MT][4];
+  bool grow = false;
+  if (n > 0) {
+    wait_vmcnt<(NS - 2) * LPW>();
+    __syncthreads();
+    qk(0, sa, false);
+    grow = scan(0, sa);
+  }
+  // One iteration with cur = S(j), nxt <- S(j + 1); tile j + 1 is resident
+  // once at most NS - 3 tiles of loads are in flight.
+  auto step = [&](int j, f32x4 (&cur)[MT][4], f32x4 (&nxt)[MT][4]) {
+    wait_vmcnt<(NS - 3) * LPW>();
+    __syncthreads();
+    if (grow) rescale(cur);
+    qk(j + 1, nxt, true);
+    make_p(cur);
+    pv(j);
+    grow = scan(j + 1, nxt);
+  };
+  int j = 0;
+  for (; j + 2 < n; j += 2) {
+    step(j, sa, sb);
+    step(j + 1, sb, sa);
+  }
+  if (j + 1 < n) {
+    step(j, sa, sb);
+    ++j;
+    // Last tile, from sb.
+    if (grow) rescale(sb);
+    make_p(sb);
+    pv(j);
+  } else if (j < n) {
+    if (grow) rescale(sa);
+    make_p(sa);
+    pv(j);
+  }
+  wait_vmcnt<0>();
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    l_run[mt] += __shfl_xor(l_run[mt], 16, 64);
+    l_run[mt] += __shfl_xor(l_run[mt], 32, 64);
+  }
+  if (kv_splits == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!col_ok[mt]) continue;
+      const float inv = 1.0f / l_run[mt];
+      float* op = out + (size_t)my_row[mt] * q_stride + (size_t)(kvh * group + my_head[mt]) * kD;
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) op[16 * b + 4 * kk + e] = o[mt][b][e] * inv;
+    }
+    return;
+  }
+  float* mine = part + (((size_t)kvh * n_rb + rb) * kv_splits + split) * kPartStride;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * (wave * MT + mt) + lm;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) *reinterpret_cast<f32x4*>(&mine[(size_t)m * kD + 16 * b + 4 * kk]) = o[mt][b];
+    if (kk == 0) {
+      mine[128 * kD + 2 * m] = m_run[mt];
+      mine[128 * kD + 2 * m + 1] = l_run[mt];
+    }
+  }
+}
+
 // Log-sum-exp merge of the KV splits: one 256-thread workgroup per (kv head,
 // row block, 8 columns), thread -> (column, 4 consecutive d). Every split's
 // partial is loaded before any is folded (one memory round trip).
@@ -653,11 +922,28 @@ void launch_main(const PrefillArgs& a, hipStream_t s) {
 // F16 / BF16: two groups of 4 waves (2 per SIMD), each with two 32 KiB
 // stages; 128 query vectors = 2 column blocks per wave, 64 = 1. The split
 // mode's 64 KiB tiles allow one group: 4 waves with two stages.
+template <int MODE, int MT, int NS>
+void launch_sp(const PrefillArgs& a, hipStream_t s) {
+  const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
+  launch_timed(a.tp, prefill_sp_kernel<MODE, MT, NS>, dim3(blocks), dim3(256), s, a.q, (const char*)a.stage,
+               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale, a.part,
+               a.out);
+}
+
 template <int MODE, typename T>
-void launch_mode(int vectors, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+void launch_mode(int vectors, int impl, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles * 2)), dim3(kWG), 0, s,
                      kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
   constexpr bool kSplit = Op<MODE>::kSplit;
+  if constexpr (!kSplit) {
+    if (impl == 2) {
+      if (vectors == 64)
+        launch_sp<MODE, 1, 4>(a, s);
+      else
+        launch_sp<MODE, 2, 4>(a, s);
+      return;
+    }
+  }
   constexpr int G = kSplit ? 1 : 2;
   if (vectors == 64)
     launch_main<MODE, G, 4, 1, 2>(a, s);
@@ -666,11 +952,11 @@ void launch_mode(int vectors, const T* kl, const T* vl, const PrefillArgs& a, hi
 }
 
 template <typename T>
-void launch_t(uint32_t mode, int vectors, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+void launch_t(uint32_t mode, int vectors, int impl, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
   switch (mode) {
-    case RV_PREFILL_F16: launch_mode<kF16, T>(vectors, kl, vl, a, s); break;
-    case RV_PREFILL_BF16: launch_mode<kBF16, T>(vectors, kl, vl, a, s); break;
-    default: launch_mode<kExact, T>(vectors, kl, vl, a, s);
+    case RV_PREFILL_F16: launch_mode<kF16, T>(vectors, impl, kl, vl, a, s); break;
+    case RV_PREFILL_BF16: launch_mode<kBF16, T>(vectors, impl, kl, vl, a, s); break;
+    default: launch_mode<kExact, T>(vectors, impl, kl, vl, a, s);
   }
 }
 
@@ -722,10 +1008,18 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   PrefillArgs a{q_rows, stage, n_kv, n_stage_tiles, (int)kv->kv_dim, (int)positions, (int)(n_q_heads * kD), (int)rows,
                 (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e, part, out,
                 timing_pair(kv, s)};
+  // Attention kernel: the software-pipelined one for short KV ranges (at most
+  // 16 tiles per split, e.g. a chunk on an empty cache), where its single
+  // barrier per tile and four-wave workgroups finish sooner; the two-group
+  // one for long ranges.
+  int impl = (int)kv->tune_prefill_impl;
+  if (impl <= 0) impl = (n_stage_tiles + kv_splits - 1) / kv_splits <= 16 ? 2 : 1;
   if (kv->elem == RV_ELEM_F32)
-    launch_t<float>(m, vectors, (const float*)kv->k_layer(layer), (const float*)kv->v_layer(layer), a, s);
+    launch_t<float>(m, vectors, impl, (const float*)kv->k_layer(layer),
+                    (const float*)kv->v_layer(layer), a, s);
   else
-    launch_t<_Float16>(m, vectors, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), a, s);
+    launch_t<_Float16>(m, vectors, impl, (const _Float16*)kv->k_layer(layer),
+                       (const _Float16*)kv->v_layer(layer), a, s);
   if (kv_splits > 1)
     hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 8)), dim3(256), 0, s,
                        (const float*)part, kv_splits, n_rb, vectors / 8, qr, (int)rows, group, (int)(n_q_heads * kD), out);

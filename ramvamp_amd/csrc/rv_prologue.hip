@@ -120,6 +120,17 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
     sn[p] = (float)sd;
     cs[p] = (float)cd;
   }
+  // The eight slots' norms first, branch-free (v and dead slots compute a
+  // norm they do not use), so their f64 reductions and square roots overlap.
+  float inv_rms[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    double ss = 0.0;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) ss += (double)x0[j][p] * (double)x0[j][p] + (double)x1[j][p] * (double)x1[j][p];
+    ss = wave_sum_f64(ss);
+    inv_rms[j] = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
+  }
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
     const int s = s0 + j;
@@ -137,17 +148,12 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
       continue;
     }
     const bool is_q = s < n_q;
-    double ss = 0.0;
-#pragma unroll
-    for (int p = 0; p < NP; ++p) ss += (double)x0[j][p] * (double)x0[j][p] + (double)x1[j][p] * (double)x1[j][p];
-    ss = wave_sum_f64(ss);
-    const float inv_rms = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int i = lane + 64 * p;
       if (i >= half) continue;
-      const float a0 = x0[j][p] * inv_rms * (is_q ? wq0[p] : wk0[p]);
-      const float a1 = x1[j][p] * inv_rms * (is_q ? wq1[p] : wk1[p]);
+      const float a0 = x0[j][p] * inv_rms[j] * (is_q ? wq0[p] : wk0[p]);
+      const float a1 = x1[j][p] * inv_rms[j] * (is_q ? wq1[p] : wk1[p]);
       const float ya = a0 * cs[p] - a1 * sn[p], yb = a0 * sn[p] + a1 * cs[p];
       if (is_q) {
         float* d = q_out + ((size_t)r * n_q + s) * hd;

@@ -37,9 +37,12 @@ def twin(rng, n_kv, hd, n_pos, cap, elem):
     return kv, ref
 
 
+@pytest.mark.parametrize("impl", [1, 2])
 @pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
 @pytest.mark.parametrize("elem", ["f32", "f16"])
-def test_rows_match_per_row_attention_at(mode, elem):
+def test_rows_match_per_row_attention_at(mode, elem, impl):
+    # impl (RV_TUNE_PREFILL_IMPL): 1 two wave groups, 2 software-pipelined
+    # (f16/bf16; the split mode has one kernel).
     torch_cuda()
     rng = Rng(0xC0FFEE)
     for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (4, 32, 128, 100, 70), (2, 8, 128, 5, 16),
@@ -48,6 +51,7 @@ def test_rows_match_per_row_attention_at(mode, elem):
                                        (1, 8, 16, 4, 9), (3, 6, 9, 0, 7)]:
         say(f"case rows {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem}")
         kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, elem)
+        kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
         q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
         scale = np.float32(1.0) / np.sqrt(np.float32(hd))
         out = dev(np.zeros(q.shape))
@@ -147,19 +151,21 @@ def test_prefill_errors_and_first_row_semantics():
                        atol=0)
 
 
+@pytest.mark.parametrize("impl", [1, 2])
 @pytest.mark.parametrize("mode", ["exact", "f16"])
 @pytest.mark.parametrize("vectors_rows,splits", [(0, 0), (8, 1), (16, 1), (16, 2), (8, 3), (16, 8)])
-def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits):
+def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits, impl):
     """64 or 128 query vectors per workgroup and 1..8 KV splits (some empty),
     over a chunk whose rows cross several 64-position tiles and end in a
-    partial row block."""
+    partial row block, for both f16/bf16 attention kernels."""
     torch_cuda()
-    say(f"case tiles rows={vectors_rows} splits={splits} mode={mode}")
+    say(f"case tiles rows={vectors_rows} splits={splits} mode={mode} impl={impl}")
     rng = Rng(0x711E + 31 * splits + vectors_rows)
     n_kv, n_q, hd, start, rows = 4, 32, 128, 200, 130
     kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, "f32")
     kv.set_tuning(4, vectors_rows)
     kv.set_tuning(2, splits)
+    kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
     q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     out = dev(np.full(q.shape, np.nan))
