@@ -585,7 +585,7 @@ static int32_t run_rows(rv_kv* kv, const float* dq, size_t rows, size_t q_dim, s
                         const Plan& p, float scale, float* dout, uint32_t flags, rv_error* err) {
   rv::HipStatus hs;
   if (rv::prefill_supported(kv, p.group, start + rows)) {
-    hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, kv->stream);
+    hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, nullptr, kv->stream);
   } else {
     for (size_t r = 0; r < rows && hs.e == hipSuccess; ++r)
       hs = rv::launch_decode(kv, dq + r * q_dim, p.n_q_heads, layer, start + r + 1, scale, 0, kv->n_kv_heads,
@@ -661,7 +661,7 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
   const size_t n_q = q_len / hd;
   // q and k rotate at `position` (forward.rs:2628-2629); the row lands at
   // the layer's cursor.
-  hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, n_q, dk, dv, 1, dwq, dwk, eps, inv, position,
+  hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, n_q, dk, dv, 1, dwq, dwk, eps, inv, position, nullptr,
                                kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   kv->lens[layer] = len + 1;
@@ -704,17 +704,32 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
     dout = st.carve(nq);
     if (st.e != hipSuccess) return hip_fail(err, st.e, "hipMemcpyAsync H2D");
   }
-  rv::HipStatus hs = rv::ensure_qbuf(kv, nq * sizeof(float));
-  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   rv::InvFreq inv;
   rv::fill_inv_freq(inv, hd, theta);
-  hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, q_dim / hd, dk, dv, rows, dwq, dwk, eps, inv, start,
-                               kv->stream);
-  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
-  kv->lens[layer] = len + rows;
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};
-  rc = run_rows(kv, kv->qbuf, rows, q_dim, layer, start, p, scale, dout, flags, err);
-  if (rc) return rc;
+  rv::HipStatus hs;
+  if (rv::prefill_supported(kv, p.group, start + rows)) {
+    // k/v prologue + append and the rows' (cos, sin) table; the q prologue
+    // runs inside the attention kernel's query loads.
+    hs = rv::ensure_qbuf(kv, rows * hd * sizeof(float));
+    if (hs.e == hipSuccess)
+      hs = rv::launch_row_prologue(kv, layer, len, nullptr, nullptr, 0, dk, dv, rows, nullptr, dwk, eps, inv, start,
+                                   kv->qbuf, kv->stream);
+    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+    kv->lens[layer] = len + rows;
+    const rv::QNorm qn{dwq, eps, kv->qbuf};
+    hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, &qn, kv->stream);
+    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  } else {
+    hs = rv::ensure_qbuf(kv, nq * sizeof(float));
+    if (hs.e == hipSuccess)
+      hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, q_dim / hd, dk, dv, rows, dwq, dwk, eps, inv, start,
+                                   nullptr, kv->stream);
+    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+    kv->lens[layer] = len + rows;
+    rc = run_rows(kv, kv->qbuf, rows, q_dim, layer, start, p, scale, dout, flags, err);
+    if (rc) return rc;
+  }
   return finish(kv, flags, dout, out, nq, err);
 }
 

@@ -102,11 +102,14 @@ void fill_inv_freq(InvFreq& t, size_t head_dim, float theta);
 HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v, size_t rows,
                         hipStream_t s);
 // Rows of (q, k, v) at RoPE positions pos0 + r: q heads RMSNormed with q_w
-// and rotated into q_out (rows x n_q x head_dim), k heads RMSNormed with k_w
-// and rotated into the cache at cache_row + r, v heads copied there.
+// and rotated into q_out (rows x n_q x head_dim; n_q may be 0), k heads
+// RMSNormed with k_w and rotated into the cache at cache_row + r, v heads
+// copied there. With rope_tab, each row's (cos, sin) pairs as f32 are also
+// written there (rows x head_dim/2 x 2), for a fused q prologue downstream.
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
-                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s);
+                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
+                              hipStream_t s);
 
 // ---- decode (rv_decode.hip) ------------------------------------------------------
 // out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all
@@ -115,8 +118,17 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
                         float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s);
 
 // ---- prefill (rv_prefill.hip) -------------------------------------------------
-// Row r of q_rows (post-RoPE, rows x q_dim) attends positions 0..start+r+1.
+// The q prologue fused into the prefill kernels' query loads: RMSNorm with
+// w and eps, rotation with the rows' (cos, sin) table from
+// launch_row_prologue.
+struct QNorm {
+  const float* w = nullptr;
+  float eps = 0.f;
+  const float* tab = nullptr;
+};
+// Row r of q_rows (rows x q_dim) attends positions 0..start+r+1; q_rows are
+// post-RoPE, or the raw projections when qn is given.
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
-                         size_t start, float scale, float* out, uint32_t mode, hipStream_t s);
+                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s);
 
 }  // namespace rv

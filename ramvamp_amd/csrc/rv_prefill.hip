@@ -223,6 +223,40 @@ __device__ __forceinline__ void wait_vmcnt() {
 // (max, sum)[128 columns].
 constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
 
+// This lane's 32 elements of one query vector, d = 8kk + 32s + e, from qp
+// (already offset by 8kk). With qn_w, qp is the raw projection and the q
+// prologue runs here, as the row prologue would: RMSNorm with an f64 sum of
+// squares over the column's four lanes (lanes 16 and 32 apart), then
+// `x * inv * w` and the rotation of the pairs (i, i + 64) - both in this
+// lane, s and s + 2 - in the reference's separately rounded f32 operations,
+// with the row's (cos, sin) from tab_row.
+__device__ __forceinline__ void load_q(const float* qp, int kk, const float* __restrict__ qn_w, float qn_eps,
+                                       const float* __restrict__ tab_row, float (&x)[4][8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[s][e] = qp[32 * s + e];
+  if (!qn_w) return;
+  double ss = 0.0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += (double)x[s][e] * (double)x[s][e];
+  ss = swap_sum_f64<32>(swap_sum_f64<16>(ss));
+  const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)qn_eps));
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * kk + 32 * s + e;
+      const float a0 = x[s][e] * inv * qn_w[i], a1 = x[s + 2][e] * inv * qn_w[i + 64];
+      const float cs = tab_row[2 * i], sn = tab_row[2 * i + 1];
+      x[s][e] = a0 * cs - a1 * sn;
+      x[s + 2][e] = a0 * sn + a1 * cs;
+    }
+}
+
 // NaN-propagating max of three (v_maximum3_f32: unlike fmaxf it needs no
 // operand canonicalisation).
 __device__ __forceinline__ float max3f(float a, float b, float c) {
@@ -258,6 +292,8 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
                                                              const char* __restrict__ stage, int n_stage_tiles,
                                                              int q_stride, int rows, int start, int group, int n_rb,
                                                              int n_units, int kv_splits, float qscale,
+                                                             const float* __restrict__ qn_w, float qn_eps,
+                                                             const float* __restrict__ qn_tab,
                                                              float* __restrict__ part, float* __restrict__ out) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
@@ -341,10 +377,12 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     // in the split mode, where rounding the scaled q would cost low bits of
     // the lo half and the scores are scaled in fp32 instead.
     const float qs = col_ok[mt] ? (kSplit ? 1.f : qscale) : 0.f;
+    float x[4][8];
+    load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) split2v<E>(qp[32 * s + e] * qs, qh[mt][s], ql[mt][s], e);
+      for (int e = 0; e < 8; ++e) split2v<E>(x[s][e] * qs, qh[mt][s], ql[mt][s], e);
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
@@ -604,6 +642,8 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
                                                         const char* __restrict__ stage, int n_stage_tiles,
                                                         int q_stride, int rows, int start, int group, int n_rb,
                                                         int n_units, int kv_splits, float qscale,
+                                                        const float* __restrict__ qn_w, float qn_eps,
+                                                        const float* __restrict__ qn_tab,
                                                         float* __restrict__ part, float* __restrict__ out) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
@@ -666,10 +706,12 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
     const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
                       (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
     const float qs = col_ok[mt] ? qscale : 0.f;
+    float x[4][8];
+    load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qh[mt][s2][e] = (E)(qp[32 * s2 + e] * qs);
+      for (int e = 0; e < 8; ++e) qh[mt][s2][e] = (E)(x[s2][e] * qs);
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
@@ -906,6 +948,9 @@ struct PrefillArgs {
   char* stage;
   int n_kv, n_stage_tiles, kv_dim, positions, q_stride, rows, start, group, n_rb, n_units, kv_splits;
   float qscale;
+  const float* qn_w;
+  float qn_eps;
+  const float* qn_tab;
   float* part;
   float* out;
   TimedPair tp;
@@ -916,7 +961,7 @@ void launch_main(const PrefillArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
   launch_timed(a.tp, prefill_kernel<MODE, G, W, MT, NS>, dim3(blocks), dim3(G * W * 64), s, a.q,
                (const char*)a.stage, a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units,
-               a.kv_splits, a.qscale, a.part, a.out);
+               a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
 // F16 / BF16: two groups of 4 waves (2 per SIMD), each with two 32 KiB
@@ -926,8 +971,8 @@ template <int MODE, int MT, int NS>
 void launch_sp(const PrefillArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
   launch_timed(a.tp, prefill_sp_kernel<MODE, MT, NS>, dim3(blocks), dim3(256), s, a.q, (const char*)a.stage,
-               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale, a.part,
-               a.out);
+               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale,
+               a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
 template <int MODE, typename T>
@@ -971,7 +1016,7 @@ bool prefill_supported(const rv_kv* kv, size_t group, size_t positions) {
 }
 
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
-                         size_t start, float scale, float* out, uint32_t mode, hipStream_t s) {
+                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
@@ -1006,8 +1051,8 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   char* stage = (char*)kv->ws;
   float* part = (float*)(stage + stage_bytes);
   PrefillArgs a{q_rows, stage, n_kv, n_stage_tiles, (int)kv->kv_dim, (int)positions, (int)(n_q_heads * kD), (int)rows,
-                (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e, part, out,
-                timing_pair(kv, s)};
+                (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
+                qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s)};
   // Attention kernel: the software-pipelined one for short KV ranges (at most
   // 16 tiles per split, e.g. a chunk on an empty cache), where its single
   // barrier per tile and four-wave workgroups finish sooner; the two-group

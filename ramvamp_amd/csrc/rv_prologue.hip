@@ -66,7 +66,7 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
                                                           T* __restrict__ vp, int n_kv, int hd,
                                                           const float* __restrict__ q_w,
                                                           const float* __restrict__ k_w, float eps, InvFreq inv,
-                                                          long pos0) {
+                                                          long pos0, float* __restrict__ tab) {
 #pragma clang fp contract(off)
   const int r = blockIdx.x, lane = threadIdx.x;
   const int half = hd / 2;
@@ -119,6 +119,10 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
     if (i < half) sincos(pos * freq[p], &sd, &cd);
     sn[p] = (float)sd;
     cs[p] = (float)cd;
+    if (tab && blockIdx.y == 0 && i < half) {
+      tab[((size_t)r * half + i) * 2] = cs[p];
+      tab[((size_t)r * half + i) * 2 + 1] = sn[p];
+    }
   }
   // The eight slots' norms first, branch-free (v and dead slots compute a
   // norm they do not use), so their f64 reductions and square roots overlap.
@@ -171,16 +175,16 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
 template <typename T>
 void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int n_q, const float* k, const float* v,
                            T* kp, T* vp, int n_kv, int hd, const float* q_w, const float* k_w, float eps,
-                           const InvFreq& inv, long pos0, hipStream_t s) {
+                           const InvFreq& inv, long pos0, float* tab, hipStream_t s) {
   if (np == 1)
     hipLaunchKernelGGL((row_prologue_kernel<T, 1>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0);
+                       k_w, eps, inv, pos0, tab);
   else if (np == 2)
     hipLaunchKernelGGL((row_prologue_kernel<T, 2>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0);
+                       k_w, eps, inv, pos0, tab);
   else
     hipLaunchKernelGGL((row_prologue_kernel<T, 4>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0);
+                       k_w, eps, inv, pos0, tab);
 }
 
 }  // namespace
@@ -205,22 +209,27 @@ HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float*
 
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
-                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, hipStream_t s) {
+                              const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
+                              hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
   const int hd = (int)kv->head_dim, n_kv = (int)kv->n_kv_heads;
   const int half = hd / 2;
+  // Without q heads the kernel still reads its q weights (unused): point
+  // them at the k weights.
+  if (n_q == 0) q_w = k_w;
   const int np = half <= 64 ? 1 : half <= 128 ? 2 : 4;
   const int n_slots = (int)n_q + 2 * n_kv;
   const dim3 grid((unsigned)rows, (unsigned)((n_slots + kSlots - 1) / kSlots));
   const size_t off = cache_row * kv->kv_dim;
   if (kv->elem == RV_ELEM_F32)
     launch_row_prologue_t<float>(grid, np, q, q_out, (int)n_q, k, v, (float*)kv->k_layer(layer) + off,
-                                 (float*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0, s);
+                                 (float*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0, rope_tab,
+                                 s);
   else
     launch_row_prologue_t<uint16_t>(grid, np, q, q_out, (int)n_q, k, v, (uint16_t*)kv->k_layer(layer) + off,
                                     (uint16_t*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0,
-                                    s);
+                                    rope_tab, s);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prologue launch";
   return st;
