@@ -5,7 +5,7 @@
 // (primitives/rope.rs:31-45, :82-105) and KvCache::append (kv/mod.rs:336-368),
 // as called at model/forward.rs:2622-2631 and model/prefill.rs:2057-2087.
 //
-// One wavefront per 8 heads of a row (q, k and v heads in one launch). The
+// One wavefront per 4 heads of a row (q, k and v heads in one launch). The
 // f32 arithmetic is the reference's, op for op and with contraction off: `x * inv * w` left to right, the rotation
 // as two separately rounded products and a subtraction/addition. The mean of
 // squares is summed in f64 (a tree, not the reference's sequential order: the
@@ -52,12 +52,12 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
 
 // One decode or prefill row's prologue: q heads RMSNormed + rotated into
 // q_out, k heads RMSNormed + rotated into the cache, v heads copied into the
-// cache. grid (rows, slot blocks), one wave per 8 head slots of the row's
+// cache. grid (rows, slot blocks), one wave per 4 head slots of the row's
 // list [q heads | k heads | v heads]. Lane l owns the element pairs
 // (i, i + half) with i = l + 64 j, j < NP, for every head of its slots, so
 // the row's sin/cos (f64, cast to f32) are computed once per wave rather than
 // once per head, while the wave's head loads are in flight.
-constexpr int kSlots = 8;
+constexpr int kSlots = 4;
 
 template <typename T, int NP>
 __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
@@ -111,12 +111,14 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
   // otherwise sink each head's loads to its arithmetic, one round trip each).
   __builtin_amdgcn_sched_barrier(0);
   const double pos = (double)(pos0 + r);
+  // Blocks of v heads only need no angles.
+  const bool rotates = s0 < n_q + n_kv;
   float sn[NP], cs[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int i = lane + 64 * p;
     double sd = 0.0, cd = 1.0;
-    if (i < half) sincos(pos * freq[p], &sd, &cd);
+    if (rotates && i < half) sincos(pos * freq[p], &sd, &cd);
     sn[p] = (float)sd;
     cs[p] = (float)cd;
     if (tab && blockIdx.y == 0 && i < half) {
@@ -124,11 +126,14 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
       tab[((size_t)r * half + i) * 2 + 1] = sn[p];
     }
   }
-  // The eight slots' norms first, branch-free (v and dead slots compute a
-  // norm they do not use), so their f64 reductions and square roots overlap.
+  // The slots' norms first, branch-free within a block that rotates (its v
+  // and dead slots compute a norm they do not use), so the f64 reductions
+  // and square roots overlap.
   float inv_rms[kSlots];
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
+    inv_rms[j] = 1.0f;
+    if (!rotates) continue;
     double ss = 0.0;
 #pragma unroll
     for (int p = 0; p < NP; ++p) ss += (double)x0[j][p] * (double)x0[j][p] + (double)x1[j][p] * (double)x1[j][p];
