@@ -29,9 +29,9 @@ THREADS = min(16, os.cpu_count() or 1)
 def twin(rng, n_kv, hd, n_pos, cap, elem):
     kv = rv.KvCache(1, n_kv, hd, cap, elem)
     ref = oracle.KvCache(1, n_kv, hd, cap, elem_code(elem))
-    K = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
-    V = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
     if n_pos:
+        K = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
+        V = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
         kv.append_rows(0, K, V)
         ref.append_rows(0, K, V)
     return kv, ref
@@ -81,6 +81,42 @@ def test_config3_prefill_chunk_matches_the_oracle(mode):
     assert kv.len(0) == 512
     for pos in (0, 511):
         gate(kv.k_row(0, pos), ref.read_row(False, 0, pos), rel=2e-7, floor=1e-6, what="cache K")
+
+
+@pytest.mark.parametrize("impl", [1, 2])
+@pytest.mark.parametrize("mode", ["exact", "f16"])
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_prefill_chunk_matches_the_oracle_across_geometries(mode, elem, impl):
+    """The fused path (k/v prologue + append, q prologue inside the attention
+    kernels' query loads) for groups 1..8, and the fallback path (full row
+    prologue, then per-row decode) where the prefill kernels do not apply
+    (group 3, head_dim 16 and 256)."""
+    torch_cuda()
+    rng = Rng(0xFEED + 7 * impl + (elem == "f16"))
+    for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (2, 8, 128, 5, 16), (1, 1, 128, 3, 20),
+                                       (4, 16, 128, 100, 9), (2, 4, 128, 31, 33), (3, 9, 128, 2, 5),
+                                       (1, 8, 16, 4, 9), (2, 4, 256, 7, 6)]:
+        say(f"case prefill_chunk {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem} impl={impl}")
+        kv, ref = twin(rng, n_kv, hd, start, start + rows, elem)
+        kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
+        q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+        k = rng.vec_in(rows * n_kv * hd, -2.0, 2.0).reshape(rows, -1)
+        v = rng.vec_in(rows * n_kv * hd, -1.0, 1.0).reshape(rows, -1)
+        wq, wk = rng.vec_in(hd, 0.9, 1.1), rng.vec_in(hd, 0.9, 1.1)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+        out = dev(np.full(q.shape, np.nan))
+        rv.prefill_chunk(kv, 0, dev(q), dev(k), dev(v), dev(wq), dev(wk), 1e-6, 1e6, start, scale, out, mode=mode)
+        want = ref.prefill_chunk(0, q, k, v, wq, wk, 1e-6, 1e6, start, scale, threads=THREADS)
+        fast = hd == 128 and 64 % (n_q // n_kv) == 0
+        # f16 planes: a new K row may round one ulp apart (f64 sin/cos of two libms).
+        loose = elem == "f16"
+        rel = BOUNDS[mode] if fast else 1e-4
+        e = gate(host(out), want, rel=max(rel, 1e-3) if loose else rel,
+                 abs_tol=max(ABS[mode] if fast else 5e-5, 1.5e-3 if loose else 0),
+                 scale=max(SCALE[mode] if fast else 1e-5, 1e-3 if loose else 0),
+                 what=f"prefill_chunk {(n_kv, n_q, hd, start, rows)} {mode}")
+        say(f"  max rel err {e:.3e}")
+        assert kv.len(0) == start + rows
 
 
 @pytest.mark.parametrize("mode", ["exact", "f16"])
