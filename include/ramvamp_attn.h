@@ -79,7 +79,10 @@ typedef enum rv_elem { RV_ELEM_F16 = 1, RV_ELEM_F32 = 2 } rv_elem;
 #define RV_HOST_PTRS 0x1u   /* tensor pointers are host memory */
 #define RV_SYNC 0x2u        /* synchronise the cache's stream before returning */
 /* Prefill arithmetic (rv_attention_at_rows / rv_prefill_chunk only; decode is
- * always fp32 arithmetic). Default (0) = RV_PREFILL_EXACT. */
+ * always fp32 arithmetic). Default (0) = RV_PREFILL_EXACT. EXACT and F16 take
+ * their operands (q, K, V, and P <= 2^8) through f16: values must stay below
+ * 65504 in magnitude, and EXACT keeps its ~2^-21 relative products only for
+ * values above f16's normal minimum (2^-14); BF16 has fp32's range. */
 #define RV_PREFILL_EXACT 0x00u /* split-f16 MFMA, fp32-equivalent products */
 #define RV_PREFILL_F16 0x10u   /* single-pass f16 MFMA inputs, fp32 accumulate */
 #define RV_PREFILL_BF16 0x20u  /* single-pass bf16 MFMA inputs, fp32 accumulate */

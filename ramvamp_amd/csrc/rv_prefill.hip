@@ -31,7 +31,8 @@
 // Arithmetic modes (flags RV_PREFILL_*):
 //   EXACT: each operand split as hi + lo f16 (lo = f16(x - hi)); products
 //          hi*hi + hi*lo + lo*hi, fp32 accumulate: ~2^-21 relative products,
-//          the fp32 parity mode.
+//          the fp32 parity mode, for operands within f16's range (below
+//          65504 in magnitude; full relative precision above 2^-14).
 //   F16 / BF16: one MFMA per product, fp32 accumulate.
 // Softmax is online in fp32 (exp2, log2(e) folded into the score scale), with
 // the running maximum moved only when a tile exceeds it by 2^8.
