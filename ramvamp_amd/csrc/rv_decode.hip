@@ -317,10 +317,9 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[c * E + e] = qp[E * (lk + 4 * c) + e];
   }
-  CT kb[NKC], vb[NVC];
   // Rows past the split re-read its last row (in bounds, branch-free); their
   // scores are masked below.
-  auto load_tile = [&](int j) {
+  auto load_tile = [&](int j, CT (&kb)[NKC], CT (&vb)[NVC]) {
     const int t0 = t_begin + (wave + j * W) * 16;
     const T* kp = kl + (size_t)min(t0 + li, t_end - 1) * kv_dim + col + E * lk;
 #pragma unroll
@@ -332,17 +331,19 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       for (int h = 0; h < 8 / E; ++h) vb[r * (8 / E) + h] = *reinterpret_cast<const CT*>(vp + E * h);
     }
   };
-  if (my_tiles > 0) load_tile(0);
-  __builtin_amdgcn_sched_barrier(0);
+  // q is scaled once the first tile's loads are in flight (its own loads
+  // then complete under theirs).
   const float qsc = col_ok ? qscale : 0.f;
+  auto scale_q = [&]() {
 #pragma unroll
-  for (int i = 0; i < 32; ++i) qv[i] *= qsc;
+    for (int i = 0; i < 32; ++i) qv[i] *= qsc;
+  };
 
   f32x4 o[8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegSentinel, l_run = 0.f;
-  for (int j = 0; j < my_tiles; ++j) {
+  auto compute = [&](int j, const CT (&kb)[NKC], const CT (&vb)[NVC]) {
     const int t0 = t_begin + (wave + j * W) * 16;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -373,7 +374,30 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       for (int r = 0; r < 4; ++r)
         o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vb[(r * 8 + b) / E][(r * 8 + b) % E], p[r], o[b], 0, 0, 0);
     }
-    if (j + 1 < my_tiles) load_tile(j + 1);
+  };
+  // Every load of a tile is issued unconditionally before the tile is used
+  // (exact wait counts: its first MFMAs start as its first chunks land); the
+  // sched_barrier keeps the compiler from sinking them to their first use.
+  // 4-wave workgroups take tiles in pairs (two in flight per wave); 8-wave
+  // ones one at a time, keeping their registers within four waves per SIMD.
+  CT ka[NKC], va[NVC];
+  int j = 0;
+  if constexpr (W == 4) {
+    CT kb2[NKC], vb2[NVC];
+    for (; j + 1 < my_tiles; j += 2) {
+      load_tile(j, ka, va);
+      load_tile(j + 1, kb2, vb2);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j == 0) scale_q();
+      compute(j, ka, va);
+      compute(j + 1, kb2, vb2);
+    }
+  }
+  for (; j < my_tiles; ++j) {
+    load_tile(j, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j == 0) scale_q();
+    compute(j, ka, va);
   }
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
