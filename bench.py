@@ -71,25 +71,22 @@ def timed(torch, fn, iters: int) -> float:
     return time.perf_counter() - t0
 
 
-def kernel_avg(torch, kv, fn, iters: int, lead_bytes: int = 0):
+def kernel_avg(torch, kv, fn, iters: int, lead_cycles: int = 0):
     """Average dominant-kernel duration (s) over `iters` eager calls of fn,
     from the library's HIP events on the launch stream.
 
-    With lead_bytes, each call is queued behind a device copy of that size
-    (not timed), so the host gets ahead of the GPU and the timed kernels run
-    back to back as in a graph replay; without it, a host that submits more
-    slowly than the GPU drains leaves the GPU idle between launches and the
-    event spans grow by ~3 us (seen on some boxes, with unchanged kernel
-    execution windows in the trace)."""
-    src = dst = None
-    if lead_bytes:
-        src = torch.empty(lead_bytes // 4, device="cuda")
-        dst = torch.empty_like(src)
+    With lead_cycles, each call is queued behind a bounded spin of that many
+    GPU clock cycles (torch.cuda._sleep: no memory traffic, not timed), so the
+    host gets ahead of the GPU and the timed kernels run back to back as in a
+    graph replay; without it, a host that submits more slowly than the GPU
+    drains leaves the GPU idle between launches and the event spans grow by
+    ~3 us (seen on some boxes, with unchanged kernel execution windows in the
+    trace)."""
     kv.set_tuning(7, 1)
     kv.kernel_time()  # reset
     for _ in range(iters):
-        if src is not None:
-            dst.copy_(src)
+        if lead_cycles:
+            torch.cuda._sleep(lead_cycles)
         fn()
     ms, n = kv.kernel_time()
     kv.set_tuning(7, 0)
@@ -143,9 +140,9 @@ def bench_config2(torch, rv, synth, steps, warmup):
     graph_ok = bool(torch.equal(out, ref))
 
     byts = decode_bytes(4096, 4)
-    # 4 GiB copied ahead of each 48-layer step: ~1.6 ms of GPU work, longer
-    # than the host needs to queue the step.
-    k_avg, k_n = kernel_avg(torch, kv, step, max(1, min(steps, 50)), lead_bytes=4 << 30)
+    # ~1 ms of GPU spin ahead of each 48-layer step, longer than the host
+    # needs to queue the step.
+    k_avg, k_n = kernel_avg(torch, kv, step, max(1, min(steps, 50)), lead_cycles=2_000_000)
     return {
         "kv": kv, "graph": graph, "graph_matches_eager": graph_ok,
         "ms_per_step": per_step * 1e3,
@@ -180,7 +177,7 @@ def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
     for _ in range(3):
         once()
     wall = timed(torch, once, iters) / iters
-    k_avg, _ = kernel_avg(torch, kv, once, iters, lead_bytes=1 << 30)
+    k_avg, _ = kernel_avg(torch, kv, once, iters, lead_cycles=400_000)
     flops = prefill_flops(rows, start)
     return {"mode": mode, "us_per_call": round(wall * 1e6, 2), "us_attention_kernel": round(k_avg * 1e6, 2),
             "tflops_call": round(flops / wall / 1e12, 2), "tflops_kernel": round(flops / k_avg / 1e12, 2),

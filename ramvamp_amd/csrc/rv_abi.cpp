@@ -213,7 +213,7 @@ namespace rv {
 
 constexpr size_t kMaxTimedPairs = 4096;  // pairs held before they are folded
 
-static bool capturing(hipStream_t s) {
+bool capturing(hipStream_t s) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
@@ -246,7 +246,7 @@ TimedPair timing_pair(rv_kv* kv, hipStream_t s) {
   return tp;
 }
 
-HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets) {
+HipStatus ensure_workspace(rv_kv* kv, size_t bytes) {
   HipStatus st;
   if (bytes > kv->ws_bytes) {
     if (kv->ws) {
@@ -263,22 +263,6 @@ HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets) {
       return st;
     }
     kv->ws_bytes = want;
-  }
-  if (n_tickets > kv->n_tickets) {
-    if (kv->tickets) {
-      (void)hipStreamSynchronize(kv->stream);
-      (void)hipFree(kv->tickets);
-      kv->tickets = nullptr;
-      kv->n_tickets = 0;
-    }
-    const size_t want = std::max<size_t>(n_tickets, 1024);
-    st.e = hipMalloc(&kv->tickets, want * sizeof(unsigned));
-    if (st.e == hipSuccess) st.e = hipMemset(kv->tickets, 0, want * sizeof(unsigned));
-    if (st.e != hipSuccess) {
-      st.what = "hipMalloc tickets";
-      return st;
-    }
-    kv->n_tickets = want;
   }
   return st;
 }
@@ -370,6 +354,10 @@ int32_t rv_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t ca
   kv->elem = elem;
   kv->device = device;
   kv->lens.assign(n_layers, 0);
+  kv->staged.assign(n_layers, nullptr);
+  kv->staged_bytes.assign(n_layers, 0);
+  kv->staged_pos.assign(n_layers, 0);
+  kv->staged_mode.assign(n_layers, 0);
   DeviceGuard dg(device);
   const size_t plane_bytes = total * elem_size(elem);
   hipError_t e = hipMalloc(&kv->k, plane_bytes);
@@ -390,7 +378,9 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->tickets, (void*)kv->qbuf, kv->stage})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage})
+      if (p) (void)hipFree(p);
+    for (void* p : kv->staged)
       if (p) (void)hipFree(p);
     for (hipEvent_t e : kv->ev) (void)hipEventDestroy(e);
   }
@@ -486,7 +476,9 @@ int32_t rv_kv_append(rv_kv* kv, size_t layer, const float* k, size_t k_len, cons
 }
 
 void rv_kv_clear(rv_kv* kv) {
-  if (kv) std::fill(kv->lens.begin(), kv->lens.end(), 0);
+  if (!kv) return;
+  std::fill(kv->lens.begin(), kv->lens.end(), 0);
+  std::fill(kv->staged_pos.begin(), kv->staged_pos.end(), 0);
 }
 
 // kv/mod.rs:410-420: ragged first, then an upward target.
@@ -496,6 +488,8 @@ int32_t rv_kv_truncate(rv_kv* kv, size_t new_len, rv_error* err) {
   if (rc) return rc;
   if (new_len > len) return fail(err, RV_KV_TRUNCATE_BEYOND_LENGTH, new_len, len);
   std::fill(kv->lens.begin(), kv->lens.end(), new_len);
+  // Rows from new_len on will be rewritten: their staged copies are stale.
+  for (size_t& sp : kv->staged_pos) sp = std::min(sp, new_len);
   return ok(err);
 }
 

@@ -704,7 +704,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     len = std::max<long>(len, step);
     const int split_len = (int)((len + step - 1) / step * step);
     const int n_splits = (int)((positions + split_len - 1) / split_len);
-    st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float), 0);
+    st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float));
     if (st.e != hipSuccess) return st;
     float* part = (float*)kv->ws;
     const dim3 grid((unsigned)(n_heads * n_splits));
@@ -722,7 +722,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     const int n_splits = (int)((positions + d.split_len - 1) / d.split_len);
     const int n_jobs = n_heads * n_hg;
     const size_t part_bytes = (size_t)n_jobs * n_splits * part_stride_of(d.hg_size) * sizeof(float);
-    st = ensure_workspace(kv, part_bytes, 0);
+    st = ensure_workspace(kv, part_bytes);
     if (st.e != hipSuccess) return st;
     SplitArgs a{q, kl, vl, (int)kv->kv_dim, (int)positions, d.split_len, n_splits, n_heads * n_splits, group,
                 n_hg, (int)kv_lo, qscale, (float*)kv->ws, out, timing_pair(kv, s)};
@@ -737,7 +737,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   } else {
     const size_t hd = kv->head_dim;
     const int n_qr = n_heads * group;
-    st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float), 0);
+    st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float));
     if (st.e != hipSuccess) return st;
     float* scores = (float*)kv->ws;
     const dim3 g1((unsigned)((positions + 255) / 256), (unsigned)n_qr);

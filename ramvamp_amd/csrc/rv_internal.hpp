@@ -21,13 +21,19 @@ struct rv_kv {
   hipStream_t stream = nullptr;
 
   // Device workspace, grown on first need and then reused by every call:
-  // decode split partials, the split-combine tickets, normalised q rows.
+  // decode and prefill split partials, normalised q rows / RoPE tables.
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  unsigned* tickets = nullptr;  // zeroed; each combine resets its own
-  size_t n_tickets = 0;
   float* qbuf = nullptr;  // normalised + rotated q rows of the fused steps
   size_t qbuf_bytes = 0;
+  // Prefill's staged copy of each layer's K/V tiles (MFMA type and LDS
+  // layout), kept across calls so a reused prefix is converted once:
+  // positions [0, staged_pos[layer]) are current for staged_mode[layer].
+  // Every write below a layer's staged_pos (truncate, clear) lowers it;
+  // appends land at or above it.
+  std::vector<void*> staged;
+  std::vector<size_t> staged_bytes, staged_pos;
+  std::vector<uint32_t> staged_mode;
   // Staging for RV_HOST_PTRS calls.
   void* stage = nullptr;
   size_t stage_bytes = 0;
@@ -62,7 +68,9 @@ struct HipStatus {
 };
 
 // Workspace (>= bytes) and tickets (>= n) on the cache's device.
-HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t n_tickets);
+HipStatus ensure_workspace(rv_kv* kv, size_t bytes);
+// Whether work on s is being captured into a graph.
+bool capturing(hipStream_t s);
 HipStatus ensure_qbuf(rv_kv* kv, size_t bytes);
 
 // RV_TUNE_KERNEL_TIMING: the event pair the next dominant-kernel launch

@@ -112,8 +112,9 @@ __device__ __forceinline__ int vt_pos(int c, int j) {
   return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
 }
 
-// Stage kernel: one workgroup per (kv head, tile, plane K or V). Rows at or
-// past `positions` are staged as zeros. Loads are whole rows per wave
+// Stage kernel: one workgroup per (kv head, tile in [tile_lo, tile_lo +
+// n_tiles), plane K or V); a kv head's tiles are tile_stride apart. Rows at
+// or past `positions` are staged as zeros. Loads are whole rows per wave
 // instruction (fp32: thread i reads row 8j + i/32, elements 4(i%32)..+3 for
 // j < 8; f16: row 16j + i/16, elements 8(i%16)..+7 for j < 4), all issued
 // before any is used. K goes straight to its swizzled rows; V is transposed
@@ -154,16 +155,17 @@ struct StageLoad<_Float16> {
 
 template <int MODE, typename T>
 __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict__ kl, const T* __restrict__ vl,
-                                                            int kv_dim, int positions, int n_tiles,
-                                                            char* __restrict__ stage) {
+                                                            int kv_dim, int positions, int tile_stride, int tile_lo,
+                                                            int n_tiles, char* __restrict__ stage) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   typedef E EN __attribute__((ext_vector_type(StageLoad<T>::kE)));
   constexpr int P = Op<MODE>::kSplit ? 2 : 1;
   constexpr int NE = StageLoad<T>::kE;
-  const int plane = blockIdx.x & 1, tile = (blockIdx.x >> 1) % n_tiles, kvh = (blockIdx.x >> 1) / n_tiles;
+  const int plane = blockIdx.x & 1;
+  const int tile = tile_lo + (int)(blockIdx.x >> 1) % n_tiles, kvh = (int)(blockIdx.x >> 1) / n_tiles;
   const int tid = threadIdx.x;
-  char* dst = stage + ((size_t)kvh * n_tiles + tile) * (2 * P * kPlaneBytes);
+  char* dst = stage + ((size_t)kvh * tile_stride + tile) * (2 * P * kPlaneBytes);
   const int t0 = tile * kBT;
   StageLoad<T> ld;
   ld.load((plane ? vl : kl) + (size_t)kvh * kD, kv_dim, t0, positions, tid);
@@ -947,7 +949,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
 struct PrefillArgs {
   const float* q;
   char* stage;
-  int n_kv, n_stage_tiles, kv_dim, positions, q_stride, rows, start, group, n_rb, n_units, kv_splits;
+  // n_stage_tiles: a kv head's stride in the staged copy (the layer's
+  // capacity in tiles); [stage_lo, stage_hi): the tiles this call restages.
+  int n_kv, n_stage_tiles, stage_lo, stage_hi, kv_dim, positions, q_stride, rows, start, group, n_rb, n_units,
+      kv_splits;
   float qscale;
   const float* qn_w;
   float qn_eps;
@@ -978,8 +983,10 @@ void launch_sp(const PrefillArgs& a, hipStream_t s) {
 
 template <int MODE, typename T>
 void launch_mode(int vectors, int impl, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * a.n_stage_tiles * 2)), dim3(kWG), 0, s,
-                     kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage);
+  if (a.stage_hi > a.stage_lo)
+    hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * (a.stage_hi - a.stage_lo) * 2)),
+                       dim3(kWG), 0, s, kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage_lo,
+                       a.stage_hi - a.stage_lo, a.stage);
   constexpr bool kSplit = Op<MODE>::kSplit;
   if constexpr (!kSplit) {
     if (impl == 2) {
@@ -1035,7 +1042,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const int qr = vectors / group;
   const int n_rb = (int)((rows + qr - 1) / qr);
   const size_t positions = start + rows;
-  const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);
+  const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);  // tiles this call reads
   int kv_splits = (int)kv->tune_prefill_kv_split;
   if (kv_splits <= 0) {
     // Split the KV axis until about 256 workgroups are in flight, keeping at
@@ -1044,14 +1051,57 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
     kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 8));
   }
   kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
-  // Workspace: staged tiles, then the split partials.
-  const size_t stage_bytes = (size_t)n_kv * n_stage_tiles * 2 * planes * kPlaneBytes;
   const size_t part_bytes = kv_splits > 1 ? (size_t)n_kv * n_rb * kv_splits * kPartStride * sizeof(float) : 0;
-  st = ensure_workspace(kv, stage_bytes + part_bytes, 0);
+  const size_t tile_bytes = (size_t)2 * planes * kPlaneBytes;
+  // Workspace: the split partials, then room to stage every tile this call
+  // reads, which only a captured call uses; eager calls reserve it too, so
+  // capturing a call of a shape already run eagerly allocates nothing.
+  const size_t call_stage_bytes = (size_t)n_kv * n_stage_tiles * tile_bytes;
+  st = ensure_workspace(kv, part_bytes + call_stage_bytes);
   if (st.e != hipSuccess) return st;
-  char* stage = (char*)kv->ws;
-  float* part = (float*)(stage + stage_bytes);
-  PrefillArgs a{q_rows, stage, n_kv, n_stage_tiles, (int)kv->kv_dim, (int)positions, (int)(n_q_heads * kD), (int)rows,
+  char* stage;
+  int tile_stride, stage_lo;
+  float* part = (float*)kv->ws;
+  if (capturing(s)) {
+    // A captured graph may be replayed at any later time, so it stages
+    // every tile it reads into the workspace and leaves the layer's
+    // persistent copy alone.
+    stage = (char*)kv->ws + part_bytes;
+    tile_stride = n_stage_tiles;
+    stage_lo = 0;
+  } else {
+    // The layer's persistent staged copy (whole capacity, so tile addresses
+    // never move): only tiles from the first one at or past the current
+    // prefix are (re)staged; a change of arithmetic mode restages everything.
+    const int cap_tiles = (int)((kv->capacity + kBT - 1) / kBT);
+    const size_t stage_bytes = (size_t)n_kv * cap_tiles * tile_bytes;
+    if (kv->staged_mode[layer] != m || stage_bytes > kv->staged_bytes[layer]) {
+      kv->staged_pos[layer] = 0;
+      kv->staged_mode[layer] = m;
+    }
+    if (stage_bytes > kv->staged_bytes[layer]) {
+      if (kv->staged[layer]) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(kv->staged[layer]);
+        kv->staged[layer] = nullptr;
+        kv->staged_bytes[layer] = 0;
+      }
+      st.e = hipMalloc(&kv->staged[layer], stage_bytes);
+      if (st.e != hipSuccess) {
+        kv->staged[layer] = nullptr;
+        st.what = "hipMalloc prefill staging";
+        return st;
+      }
+      kv->staged_bytes[layer] = stage_bytes;
+    }
+    size_t& staged_pos = kv->staged_pos[layer];
+    stage_lo = staged_pos >= positions ? n_stage_tiles : (int)(staged_pos / kBT);
+    staged_pos = std::max(staged_pos, positions);
+    stage = (char*)kv->staged[layer];
+    tile_stride = cap_tiles;
+  }
+  PrefillArgs a{q_rows, stage, n_kv, tile_stride, stage_lo, n_stage_tiles, (int)kv->kv_dim, (int)positions,
+                (int)(n_q_heads * kD), (int)rows,
                 (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
                 qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s)};
   // Attention kernel: the software-pipelined one for short KV ranges (at most

@@ -73,3 +73,47 @@ def test_kernel_timing_counts_bracketed_launches():
     assert n == 3 and ms > 0.0, (ms, n)
     assert kv.kernel_time() == (0.0, 0)  # reset by the read
     kv.set_tuning(7, 0)
+
+
+@pytest.mark.parametrize("mode", ["f16", "exact"])
+def test_prefill_graph_replays_match_eager_and_leave_the_staged_copy_sound(mode):
+    """Prefill keeps a staged copy of the layer's K/V across eager calls; a
+    captured call stages what it reads into the workspace on every replay and
+    leaves that copy alone. Replays interleaved with eager calls over a longer
+    prefix (before and after the capture) match eager results bit for bit."""
+    torch = torch_cuda()
+    say(f"case prefill graph mode={mode}")
+    rng = Rng(0x9A9F)
+    n_pos = 300
+    kv = rv.KvCache(1, 4, 128, 700, "f32")
+    kv.append_rows(0, rng.vec_in(n_pos * 512, -1.0, 1.0).reshape(n_pos, -1),
+                   rng.vec_in(n_pos * 512, -1.0, 1.0).reshape(n_pos, -1))
+    q = dev(rng.vec_in(40 * 4096, -1.0, 1.0).reshape(40, 4096))
+    out = torch.zeros_like(q)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+    def eager(start):
+        out.fill_(float("nan"))
+        rv.attention_at_rows(q, kv, 0, start, scale, out, mode=mode)
+        return host(out).copy()
+
+    want_long = eager(260)  # stages every tile of positions 0..299
+    want_short = eager(100)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        rv.attention_at_rows(q, kv, 0, 100, scale, out, mode=mode)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rv.attention_at_rows(q, kv, 0, 100, scale, out, mode=mode)
+    again = eager(260)
+    assert np.array_equal(again.view(np.uint32), want_long.view(np.uint32)), "eager after capture"
+    for rep in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        got = host(out)
+        assert np.array_equal(got.view(np.uint32), want_short.view(np.uint32)), f"replay {rep}"
+        again = eager(260)  # restages past the replay's zeroed rows
+        assert np.array_equal(again.view(np.uint32), want_long.view(np.uint32)), f"eager after replay {rep}"

@@ -119,6 +119,55 @@ def test_prefill_chunk_matches_the_oracle_across_geometries(mode, elem, impl):
         assert kv.len(0) == start + rows
 
 
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_chunked_prefill_truncation_and_mode_changes_keep_the_staged_copy_current(elem):
+    """The prefill kernels keep a staged copy of each layer's K/V across calls
+    and restage only from the first tile at or past the current prefix. A
+    sequence of chunks, a truncation (server prefix reuse), a change of
+    arithmetic mode, attention over a shorter prefix and a cleared cache must
+    each match the oracle running the same sequence."""
+    torch_cuda()
+    rng = Rng(0x57A6E + (elem == "f16"))
+    n_kv, n_q, hd = 2, 16, 128
+    kv = rv.KvCache(2, n_kv, hd, 400, elem)
+    ref = oracle.KvCache(2, n_kv, hd, 400, elem_code(elem))
+    wq, wk = rng.vec_in(hd, 0.9, 1.1), rng.vec_in(hd, 0.9, 1.1)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    loose = elem == "f16"
+
+    def chunk(layer, start, rows, mode):
+        q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+        k = rng.vec_in(rows * n_kv * hd, -2.0, 2.0).reshape(rows, -1)
+        v = rng.vec_in(rows * n_kv * hd, -1.0, 1.0).reshape(rows, -1)
+        out = dev(np.full(q.shape, np.nan))
+        rv.prefill_chunk(kv, layer, dev(q), dev(k), dev(v), dev(wq), dev(wk), 1e-6, 1e6, start, scale, out, mode=mode)
+        want = ref.prefill_chunk(layer, q, k, v, wq, wk, 1e-6, 1e6, start, scale, threads=THREADS)
+        gate(host(out), want, rel=max(BOUNDS[mode], 1e-3 if loose else 0), abs_tol=max(ABS[mode], 1.5e-3 if loose else 0),
+             scale=max(SCALE[mode], 1e-3 if loose else 0), what=f"chunk {layer} {start}+{rows} {mode}")
+
+    for layer in (0, 1):
+        say(f"case chunked prefill layer {layer} elem={elem}")
+        chunk(layer, 0, 100, "f16")     # tiles 0-1 staged, tile 1 partly
+        chunk(layer, 100, 70, "f16")    # restage from tile 1
+    kv.truncate(130)
+    ref.truncate(130)
+    for layer in (0, 1):
+        chunk(layer, 130, 90, "f16")    # rows 130.. rewritten: restage from tile 2
+        chunk(layer, 220, 33, "exact")  # a mode change restages everything
+    # attention over a shorter prefix of the staged layer, then the full one
+    q = rng.vec_in(20 * n_q * hd, -2.0, 2.0).reshape(20, -1)
+    for start in (40, 233):
+        out = dev(np.full(q.shape, np.nan))
+        rv.attention_at_rows(dev(q), kv, 1, start, scale, out, mode="f16")
+        want = ref.scatter_attention(q, 1, start, scale, THREADS)
+        gate(host(out), want, rel=max(BOUNDS["f16"], 1e-3 if loose else 0), abs_tol=ABS["f16"],
+             scale=SCALE["f16"], what=f"attention_at_rows start {start}")
+    kv.clear()
+    ref.clear()
+    chunk(0, 0, 64, "f16")
+    assert kv.len(0) == 64
+
+
 @pytest.mark.parametrize("mode", ["exact", "f16"])
 def test_config4_prefix_reuse_prefill_matches_the_oracle(mode):
     torch_cuda()
