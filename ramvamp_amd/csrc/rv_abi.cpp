@@ -656,7 +656,7 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
   // q and k rotate at `position` (forward.rs:2628-2629); the row lands at
   // the layer's cursor.
   hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, n_q, dk, dv, 1, dwq, dwk, eps, inv, position, nullptr,
-                               kv->stream);
+                               nullptr, kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   kv->lens[layer] = len + 1;
   hs = rv::launch_decode(kv, kv->qbuf, n_q, layer, len + 1, scale, 0, kv->n_kv_heads, dout, kv->stream);
@@ -703,12 +703,15 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};
   rv::HipStatus hs;
   if (rv::prefill_supported(kv, p.group, start + rows)) {
-    // k/v prologue + append and the rows' (cos, sin) table; the q prologue
-    // runs inside the attention kernel's query loads.
+    // k/v prologue + append (also into the layer's staged tiles) and the
+    // rows' (cos, sin) table; the q prologue runs inside the attention
+    // kernel's query loads.
+    rv::StageDst sd;
     hs = rv::ensure_qbuf(kv, rows * hd * sizeof(float));
+    if (hs.e == hipSuccess) hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
     if (hs.e == hipSuccess)
       hs = rv::launch_row_prologue(kv, layer, len, nullptr, nullptr, 0, dk, dv, rows, nullptr, dwk, eps, inv, start,
-                                   kv->qbuf, kv->stream);
+                                   kv->qbuf, &sd, kv->stream);
     if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
     kv->lens[layer] = len + rows;
     const rv::QNorm qn{dwq, eps, kv->qbuf};
@@ -718,7 +721,7 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
     hs = rv::ensure_qbuf(kv, nq * sizeof(float));
     if (hs.e == hipSuccess)
       hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, q_dim / hd, dk, dv, rows, dwq, dwk, eps, inv, start,
-                                   nullptr, kv->stream);
+                                   nullptr, nullptr, kv->stream);
     if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
     kv->lens[layer] = len + rows;
     rc = run_rows(kv, kv->qbuf, rows, q_dim, layer, start, p, scale, dout, flags, err);

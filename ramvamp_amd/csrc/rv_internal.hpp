@@ -109,15 +109,25 @@ void fill_inv_freq(InvFreq& t, size_t head_dim, float theta);
 // `layer`.
 HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float* k, const float* v, size_t rows,
                         hipStream_t s);
+// A layer's staged K/V tiles (prefill's MFMA-typed copy) that a row
+// prologue also writes its k and v rows into; base == nullptr: none.
+struct StageDst {
+  char* base = nullptr;
+  int tile_stride = 0;  // tiles between consecutive kv heads
+  uint32_t mode = 0;    // RV_PREFILL_EXACT / F16 / BF16
+};
 // Rows of (q, k, v) at RoPE positions pos0 + r: q heads RMSNormed with q_w
 // and rotated into q_out (rows x n_q x head_dim; n_q may be 0), k heads
 // RMSNormed with k_w and rotated into the cache at cache_row + r, v heads
 // copied there. With rope_tab, each row's (cos, sin) pairs as f32 are also
 // written there (rows x head_dim/2 x 2), for a fused q prologue downstream.
+// With sd (head_dim 128 only), the k and v rows as the cache holds them are
+// also written into the staged tiles at cache_row + r, and the rest of the
+// last tile is zeroed.
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
                               const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
-                              hipStream_t s);
+                              const StageDst* sd, hipStream_t s);
 
 // ---- decode (rv_decode.hip) ------------------------------------------------------
 // out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all
@@ -134,6 +144,15 @@ struct QNorm {
   float eps = 0.f;
   const float* tab = nullptr;
 };
+// Before a prefill chunk appends `rows` rows at pos0 = len(layer) and runs
+// launch_prefill: readies the layer's persistent staged copy in `mode`
+// (stages the rows the prefix gained since it was last current, up to pos0)
+// and marks [0, pos0 + rows) current, so that the chunk's row prologue
+// writes its own rows there (sd) and launch_prefill stages nothing. Under
+// graph capture sd->base stays null: a captured call stages into the
+// workspace instead.
+HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t rows, uint32_t mode,
+                                hipStream_t s, StageDst* sd);
 // Row r of q_rows (rows x q_dim) attends positions 0..start+r+1; q_rows are
 // post-RoPE, or the raw projections when qn is given.
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,

@@ -42,6 +42,7 @@
 // an fp32 log-sum-exp in a further launch (the splits run on different XCDs).
 #include "rv_device.hpp"
 #include "rv_internal.hpp"
+#include "rv_staged.hpp"
 
 #include <algorithm>
 
@@ -50,71 +51,9 @@ namespace {
 
 constexpr int kWG = 256;
 constexpr int kD = 128;
-constexpr int kBT = 64;             // positions per K/V tile
-constexpr int kPlaneBytes = 16384;  // one staged 64 x 128 plane of 2-byte elements
 constexpr int kMaxKvSplits = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegSentinel = -1.0e30f;
-
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-
-enum Mode { kExact = 0, kF16 = 1, kBF16 = 2 };
-
-template <int MODE>
-struct Op;
-template <>
-struct Op<kExact> {
-  typedef _Float16 E;
-  typedef f16x8 V8;
-  typedef f16x4 V4;
-  static constexpr bool kSplit = true;
-  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-};
-template <>
-struct Op<kF16> {
-  typedef _Float16 E;
-  typedef f16x8 V8;
-  typedef f16x4 V4;
-  static constexpr bool kSplit = false;
-  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-};
-template <>
-struct Op<kBF16> {
-  typedef __bf16 E;
-  typedef bf16x8 V8;
-  typedef bf16x4 V4;
-  static constexpr bool kSplit = false;
-  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
-};
-
-// hi = round(x); lo = round(x - hi), into element e of two vectors.
-template <typename E, typename V>
-__device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
-  const E h = (E)x;
-  hi[e] = h;
-  lo[e] = (E)(x - (float)h);
-}
-
-// ---- staged tile layout -------------------------------------------------------------
-// One tile = P planes of K, then P planes of V^T (P = 2 in the split mode:
-// hi, lo), each plane 16 KiB of 16-byte chunks (8 elements).
-//   K plane: row t (64) x chunk c (16): elements d = 8c .. 8c+7, stored at
-//     byte 256 t + 16 (c ^ (t & 15)).
-//   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot
-//     j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
-//     (j >= 4); stored at byte 8192 s2 + 64 d + 16 (k ^ ((d >> 2) & 3)), so
-//     each 32-position half of the tile (s2) is 8 KiB of its own.
-// The rows of K's first and second 32 positions are likewise contiguous
-// halves. The swizzles put the 16 lanes of one operand read on 16 distinct
-// 16-byte bank groups.
-__device__ __forceinline__ int k_off(int t, int c) { return 256 * t + 16 * (c ^ (t & 15)); }
-__device__ __forceinline__ int vt_off(int d, int c) {
-  return 8192 * (c >> 2) + 64 * d + 16 * ((c & 3) ^ ((d >> 2) & 3));
-}
-__device__ __forceinline__ int vt_pos(int c, int j) {
-  const int s2 = c >> 2, k = c & 3;
-  return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
-}
 
 // Stage kernel: one workgroup per (kv head, tile in [tile_lo, tile_lo +
 // n_tiles), plane K or V); a kv head's tiles are tile_stride apart. Rows at
@@ -953,10 +892,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
 struct PrefillArgs {
   const float* q;
   char* stage;
-  // n_stage_tiles: a kv head's stride in the staged copy (the layer's
-  // capacity in tiles); [stage_lo, stage_hi): the tiles this call restages.
-  int n_kv, n_stage_tiles, stage_lo, stage_hi, kv_dim, positions, q_stride, rows, start, group, n_rb, n_units,
-      kv_splits;
+  // n_stage_tiles: a kv head's stride in the staged copy.
+  int n_stage_tiles, q_stride, rows, start, group, n_rb, n_units, kv_splits;
   float qscale;
   const float* qn_w;
   float qn_eps;
@@ -985,12 +922,8 @@ void launch_sp(const PrefillArgs& a, hipStream_t s) {
                a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
-template <int MODE, typename T>
-void launch_mode(int vectors, int impl, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
-  if (a.stage_hi > a.stage_lo)
-    hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(a.n_kv * (a.stage_hi - a.stage_lo) * 2)),
-                       dim3(kWG), 0, s, kl, vl, a.kv_dim, a.positions, a.n_stage_tiles, a.stage_lo,
-                       a.stage_hi - a.stage_lo, a.stage);
+template <int MODE>
+void launch_mode(int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
   constexpr bool kSplit = Op<MODE>::kSplit;
   if constexpr (!kSplit) {
     if (impl == 2) {
@@ -1008,13 +941,72 @@ void launch_mode(int vectors, int impl, const T* kl, const T* vl, const PrefillA
     launch_main<MODE, G, 4, 2, 2>(a, s);
 }
 
-template <typename T>
-void launch_t(uint32_t mode, int vectors, int impl, const T* kl, const T* vl, const PrefillArgs& a, hipStream_t s) {
+void launch_attention(uint32_t mode, int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
   switch (mode) {
-    case RV_PREFILL_F16: launch_mode<kF16, T>(vectors, impl, kl, vl, a, s); break;
-    case RV_PREFILL_BF16: launch_mode<kBF16, T>(vectors, impl, kl, vl, a, s); break;
-    default: launch_mode<kExact, T>(vectors, impl, kl, vl, a, s);
+    case RV_PREFILL_F16: launch_mode<kF16>(vectors, impl, a, s); break;
+    case RV_PREFILL_BF16: launch_mode<kBF16>(vectors, impl, a, s); break;
+    default: launch_mode<kExact>(vectors, impl, a, s);
   }
+}
+
+// Stage tiles [lo, hi) of every kv head of `layer` (positions at or past
+// `positions` as zeros) into `stage`, kv heads tile_stride tiles apart.
+template <int MODE, typename T>
+void launch_stage_t(const T* kl, const T* vl, int n_kv, int kv_dim, int positions, int tile_stride, int lo, int hi,
+                    char* stage, hipStream_t s) {
+  hipLaunchKernelGGL((prefill_stage_kernel<MODE, T>), dim3((unsigned)(n_kv * (hi - lo) * 2)), dim3(kWG), 0, s, kl, vl,
+                     kv_dim, positions, tile_stride, lo, hi - lo, stage);
+}
+template <typename T>
+void launch_stage_m(uint32_t mode, const T* kl, const T* vl, int n_kv, int kv_dim, int positions, int tile_stride,
+                    int lo, int hi, char* stage, hipStream_t s) {
+  switch (mode) {
+    case RV_PREFILL_F16: launch_stage_t<kF16, T>(kl, vl, n_kv, kv_dim, positions, tile_stride, lo, hi, stage, s); break;
+    case RV_PREFILL_BF16: launch_stage_t<kBF16, T>(kl, vl, n_kv, kv_dim, positions, tile_stride, lo, hi, stage, s); break;
+    default: launch_stage_t<kExact, T>(kl, vl, n_kv, kv_dim, positions, tile_stride, lo, hi, stage, s);
+  }
+}
+void launch_stage(const rv_kv* kv, size_t layer, uint32_t mode, size_t positions, int tile_stride, int lo, int hi,
+                  char* stage, hipStream_t s) {
+  if (hi <= lo) return;
+  const int n_kv = (int)kv->n_kv_heads, kv_dim = (int)kv->kv_dim;
+  if (kv->elem == RV_ELEM_F32)
+    launch_stage_m<float>(mode, (const float*)kv->k_layer(layer), (const float*)kv->v_layer(layer), n_kv, kv_dim,
+                          (int)positions, tile_stride, lo, hi, stage, s);
+  else
+    launch_stage_m<_Float16>(mode, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), n_kv,
+                             kv_dim, (int)positions, tile_stride, lo, hi, stage, s);
+}
+
+int planes_of(uint32_t mode) { return (mode == RV_PREFILL_F16 || mode == RV_PREFILL_BF16) ? 1 : 2; }
+
+// The layer's persistent staged copy in `mode` (whole capacity, so tile
+// addresses never move), allocated or grown on need; a change of mode or a
+// new allocation marks nothing current. Sets *cap_tiles to its tile stride.
+HipStatus ready_persistent(rv_kv* kv, size_t layer, uint32_t mode, hipStream_t s, int* cap_tiles) {
+  HipStatus st;
+  *cap_tiles = (int)((kv->capacity + kBT - 1) / kBT);
+  const size_t stage_bytes = (size_t)kv->n_kv_heads * *cap_tiles * 2 * planes_of(mode) * kPlaneBytes;
+  if (kv->staged_mode[layer] != mode || stage_bytes > kv->staged_bytes[layer]) {
+    kv->staged_pos[layer] = 0;
+    kv->staged_mode[layer] = mode;
+  }
+  if (stage_bytes > kv->staged_bytes[layer]) {
+    if (kv->staged[layer]) {
+      (void)hipStreamSynchronize(s);
+      (void)hipFree(kv->staged[layer]);
+      kv->staged[layer] = nullptr;
+      kv->staged_bytes[layer] = 0;
+    }
+    st.e = hipMalloc(&kv->staged[layer], stage_bytes);
+    if (st.e != hipSuccess) {
+      kv->staged[layer] = nullptr;
+      st.what = "hipMalloc prefill staging";
+      return st;
+    }
+    kv->staged_bytes[layer] = stage_bytes;
+  }
+  return st;
 }
 
 }  // namespace
@@ -1034,7 +1026,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const int n_kv = (int)kv->n_kv_heads;
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
-  const int planes = (m == RV_PREFILL_F16 || m == RV_PREFILL_BF16) ? 1 : 2;
+  const int planes = planes_of(m);
   // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
   // 128-vector blocks would leave CUs idle (fewer than 256 workgroups) or the
   // tuning asks for it.
@@ -1074,38 +1066,16 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
     tile_stride = n_stage_tiles;
     stage_lo = 0;
   } else {
-    // The layer's persistent staged copy (whole capacity, so tile addresses
-    // never move): only tiles from the first one at or past the current
-    // prefix are (re)staged; a change of arithmetic mode restages everything.
-    const int cap_tiles = (int)((kv->capacity + kBT - 1) / kBT);
-    const size_t stage_bytes = (size_t)n_kv * cap_tiles * tile_bytes;
-    if (kv->staged_mode[layer] != m || stage_bytes > kv->staged_bytes[layer]) {
-      kv->staged_pos[layer] = 0;
-      kv->staged_mode[layer] = m;
-    }
-    if (stage_bytes > kv->staged_bytes[layer]) {
-      if (kv->staged[layer]) {
-        (void)hipStreamSynchronize(s);
-        (void)hipFree(kv->staged[layer]);
-        kv->staged[layer] = nullptr;
-        kv->staged_bytes[layer] = 0;
-      }
-      st.e = hipMalloc(&kv->staged[layer], stage_bytes);
-      if (st.e != hipSuccess) {
-        kv->staged[layer] = nullptr;
-        st.what = "hipMalloc prefill staging";
-        return st;
-      }
-      kv->staged_bytes[layer] = stage_bytes;
-    }
+    // The layer's persistent staged copy: only tiles from the first one at
+    // or past its current prefix are (re)staged.
+    st = ready_persistent(kv, layer, m, s, &tile_stride);
+    if (st.e != hipSuccess) return st;
     size_t& staged_pos = kv->staged_pos[layer];
     stage_lo = staged_pos >= positions ? n_stage_tiles : (int)(staged_pos / kBT);
     staged_pos = std::max(staged_pos, positions);
     stage = (char*)kv->staged[layer];
-    tile_stride = cap_tiles;
   }
-  PrefillArgs a{q_rows, stage, n_kv, tile_stride, stage_lo, n_stage_tiles, (int)kv->kv_dim, (int)positions,
-                (int)(n_q_heads * kD), (int)rows,
+  PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
                 (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
                 qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s)};
   // Attention kernel: the software-pipelined one for short KV ranges (at most
@@ -1114,17 +1084,38 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   // one for long ranges.
   int impl = (int)kv->tune_prefill_impl;
   if (impl <= 0) impl = (n_stage_tiles + kv_splits - 1) / kv_splits <= 16 ? 2 : 1;
-  if (kv->elem == RV_ELEM_F32)
-    launch_t<float>(m, vectors, impl, (const float*)kv->k_layer(layer),
-                    (const float*)kv->v_layer(layer), a, s);
-  else
-    launch_t<_Float16>(m, vectors, impl, (const _Float16*)kv->k_layer(layer),
-                       (const _Float16*)kv->v_layer(layer), a, s);
+  launch_stage(kv, layer, m, positions, tile_stride, stage_lo, n_stage_tiles, stage, s);
+  launch_attention(m, vectors, impl, a, s);
   if (kv_splits > 1)
     hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 8)), dim3(256), 0, s,
                        (const float*)part, kv_splits, n_rb, vectors / 8, qr, (int)rows, group, (int)(n_q_heads * kD), out);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
+  return st;
+}
+
+HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t rows, uint32_t mode,
+                                hipStream_t s, StageDst* sd) {
+  HipStatus st;
+  *sd = StageDst{};
+  if (rows == 0 || kv->head_dim != kD || capturing(s)) return st;
+  const uint32_t m = mode & RV_PREFILL_MODE_MASK;
+  int tile_stride;
+  st = ready_persistent(kv, layer, m, s, &tile_stride);
+  if (st.e != hipSuccess) return st;
+  size_t& staged_pos = kv->staged_pos[layer];
+  // Rows below pos0 not yet current (decode steps, plain appends, a new
+  // mode): staged from the cache, their last tile zero-filled from pos0 on,
+  // which the chunk's rows then overwrite.
+  if (staged_pos < pos0)
+    launch_stage(kv, layer, m, pos0, tile_stride, (int)(staged_pos / kBT), (int)((pos0 + kBT - 1) / kBT),
+                 (char*)kv->staged[layer], s);
+  staged_pos = pos0 + rows;
+  sd->base = (char*)kv->staged[layer];
+  sd->tile_stride = tile_stride;
+  sd->mode = m;
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "prefill stage launch";
   return st;
 }
 

@@ -14,6 +14,7 @@
 // sin/cos in f64 and cast to f32, as rope.rs:35-39 does.
 #include "rv_device.hpp"
 #include "rv_internal.hpp"
+#include "rv_staged.hpp"
 
 #include <math.h>
 
@@ -38,6 +39,45 @@ __device__ __forceinline__ void store_elem<uint16_t>(uint16_t* p, float v) {
   *p = f32_to_f16_bits(v);
 }
 
+// Stores v as the cache's element type; returns what the cache now holds,
+// as f32 (what the prefill stage kernel would read back).
+template <typename T>
+__device__ __forceinline__ float store_cached(T* p, float v);
+template <>
+__device__ __forceinline__ float store_cached<float>(float* p, float v) {
+  *p = v;
+  return v;
+}
+template <>
+__device__ __forceinline__ float store_cached<uint16_t>(uint16_t* p, float v) {
+  const uint16_t b = f32_to_f16_bits(v);
+  *p = b;
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// The staged tiles a prefill chunk's prologue writes its k and v rows into
+// (positions row0 + r; rows [rows, grid rows) are the rest of the last tile).
+struct StagedRows {
+  char* base;
+  int tile_stride;
+  int rows;
+  long row0;
+};
+
+// Element d of kv head h's K (kind 0) or V (kind 1) row at position p, in
+// the staged layout of mode SM: hi, and lo in the split mode.
+template <int SM>
+__device__ __forceinline__ void stage_elem(const StagedRows& sr, int kind, int h, long p, int d, float x) {
+  typedef typename Op<SM>::E E;
+  constexpr int P = kPlanes<SM>;
+  const int t = (int)(p % kBT);
+  char* tile = sr.base + ((size_t)h * sr.tile_stride + (size_t)(p / kBT)) * (2 * P * kPlaneBytes);
+  char* dst = kind == 0 ? tile + k_off(t, d >> 3) + 2 * (d & 7) : tile + P * kPlaneBytes + vt_byte(d, t);
+  const E hi = (E)x;
+  *reinterpret_cast<E*>(dst) = hi;
+  if constexpr (Op<SM>::kSplit) *reinterpret_cast<E*>(dst + kPlaneBytes) = (E)(x - (float)hi);
+}
+
 // grid (rows, n_kv_heads), one wave each: K and V heads copied into the
 // cache, converted to the plane's element type (KvCache::append as is).
 template <typename T>
@@ -57,21 +97,42 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
 // (i, i + half) with i = l + 64 j, j < NP, for every head of its slots, so
 // the row's sin/cos (f64, cast to f32) are computed once per wave rather than
 // once per head, while the wave's head loads are in flight.
+// SM >= 0 (a prefill chunk, n_q = 0, head_dim 128): k and v rows, as the
+// cache holds them, are also written into the staged tiles in mode SM, and
+// the grid's rows past the chunk zero the rest of its last tile.
 constexpr int kSlots = 4;
 
-template <typename T, int NP>
+template <typename T, int NP, int SM>
 __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
                                                           int n_q, const float* __restrict__ k,
                                                           const float* __restrict__ v, T* __restrict__ kp,
                                                           T* __restrict__ vp, int n_kv, int hd,
                                                           const float* __restrict__ q_w,
                                                           const float* __restrict__ k_w, float eps, InvFreq inv,
-                                                          long pos0, float* __restrict__ tab) {
+                                                          long pos0, float* __restrict__ tab, StagedRows sr) {
 #pragma clang fp contract(off)
   const int r = blockIdx.x, lane = threadIdx.x;
   const int half = hd / 2;
   const int n_slots = n_q + 2 * n_kv;
   const int s0 = (int)blockIdx.y * kSlots;
+  if constexpr (SM >= 0) {
+    if (r >= sr.rows) {
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) {
+        const int s = s0 + j;
+        if (s < n_q || s >= n_slots) continue;
+        const int kind = s >= n_q + n_kv, h = s - n_q - kind * n_kv;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const int i = lane + 64 * p;
+          if (i >= half) continue;
+          stage_elem<SM>(sr, kind, h, sr.row0 + r, i, 0.f);
+          stage_elem<SM>(sr, kind, h, sr.row0 + r, i + half, 0.f);
+        }
+      }
+      return;
+    }
+  }
   // Source of slot s (q, k or v head of row r); its destination is below.
   auto src = [&](int s) -> const float* {
     if (s < n_q) return q + ((size_t)r * n_q + s) * hd;
@@ -150,8 +211,12 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
       for (int p = 0; p < NP; ++p) {
         const int i = lane + 64 * p;
         if (i < half) {
-          store_elem<T>(d + i, x0[j][p]);
-          store_elem<T>(d + i + half, x1[j][p]);
+          const float c0 = store_cached<T>(d + i, x0[j][p]);
+          const float c1 = store_cached<T>(d + i + half, x1[j][p]);
+          if constexpr (SM >= 0) {
+            stage_elem<SM>(sr, 1, s - n_q - n_kv, sr.row0 + r, i, c0);
+            stage_elem<SM>(sr, 1, s - n_q - n_kv, sr.row0 + r, i + half, c1);
+          }
         }
       }
       continue;
@@ -170,8 +235,12 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
         d[i + half] = yb;
       } else {
         T* d = kp + ((size_t)r * n_kv + (s - n_q)) * hd;
-        store_elem<T>(d + i, ya);
-        store_elem<T>(d + i + half, yb);
+        const float c0 = store_cached<T>(d + i, ya);
+        const float c1 = store_cached<T>(d + i + half, yb);
+        if constexpr (SM >= 0) {
+          stage_elem<SM>(sr, 0, s - n_q, sr.row0 + r, i, c0);
+          stage_elem<SM>(sr, 0, s - n_q, sr.row0 + r, i + half, c1);
+        }
       }
     }
   }
@@ -180,16 +249,23 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
 template <typename T>
 void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int n_q, const float* k, const float* v,
                            T* kp, T* vp, int n_kv, int hd, const float* q_w, const float* k_w, float eps,
-                           const InvFreq& inv, long pos0, float* tab, hipStream_t s) {
-  if (np == 1)
-    hipLaunchKernelGGL((row_prologue_kernel<T, 1>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0, tab);
+                           const InvFreq& inv, long pos0, float* tab, int sm, const StagedRows& sr, hipStream_t s) {
+#define RV_PROLOGUE(NP, SM)                                                                                      \
+  hipLaunchKernelGGL((row_prologue_kernel<T, NP, SM>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, \
+                     q_w, k_w, eps, inv, pos0, tab, sr)
+  if (sm == kF16)
+    RV_PROLOGUE(1, kF16);
+  else if (sm == kBF16)
+    RV_PROLOGUE(1, kBF16);
+  else if (sm == kExact)
+    RV_PROLOGUE(1, kExact);
+  else if (np == 1)
+    RV_PROLOGUE(1, -1);
   else if (np == 2)
-    hipLaunchKernelGGL((row_prologue_kernel<T, 2>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0, tab);
+    RV_PROLOGUE(2, -1);
   else
-    hipLaunchKernelGGL((row_prologue_kernel<T, 4>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, q_w,
-                       k_w, eps, inv, pos0, tab);
+    RV_PROLOGUE(4, -1);
+#undef RV_PROLOGUE
 }
 
 }  // namespace
@@ -215,7 +291,7 @@ HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float*
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
                               const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
-                              hipStream_t s) {
+                              const StageDst* sd, hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
   const int hd = (int)kv->head_dim, n_kv = (int)kv->n_kv_heads;
@@ -225,16 +301,28 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   if (n_q == 0) q_w = k_w;
   const int np = half <= 64 ? 1 : half <= 128 ? 2 : 4;
   const int n_slots = (int)n_q + 2 * n_kv;
-  const dim3 grid((unsigned)rows, (unsigned)((n_slots + kSlots - 1) / kSlots));
+  // Staging: k and v heads only, head_dim 128; the grid covers the chunk's
+  // last tile to its end.
+  const bool staging = sd && sd->base;
+  if (staging && (n_q != 0 || hd != 128)) {
+    st.e = hipErrorInvalidValue;
+    st.what = "staged prologue geometry";
+    return st;
+  }
+  const size_t end = cache_row + rows;
+  const size_t grid_rows = staging ? rows + (kBT - end % kBT) % kBT : rows;
+  const int sm = !staging ? -1 : sd->mode == RV_PREFILL_F16 ? kF16 : sd->mode == RV_PREFILL_BF16 ? kBF16 : kExact;
+  const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
+  const dim3 grid((unsigned)grid_rows, (unsigned)((n_slots + kSlots - 1) / kSlots));
   const size_t off = cache_row * kv->kv_dim;
   if (kv->elem == RV_ELEM_F32)
     launch_row_prologue_t<float>(grid, np, q, q_out, (int)n_q, k, v, (float*)kv->k_layer(layer) + off,
                                  (float*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0, rope_tab,
-                                 s);
+                                 sm, sr, s);
   else
     launch_row_prologue_t<uint16_t>(grid, np, q, q_out, (int)n_q, k, v, (uint16_t*)kv->k_layer(layer) + off,
                                     (uint16_t*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0,
-                                    rope_tab, s);
+                                    rope_tab, sm, sr, s);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prologue launch";
   return st;

@@ -1,0 +1,85 @@
+// rv_staged.hpp — the staged K/V tile layout that the prefill attention
+// kernels read, shared by the kernels that write it: the prefill stage
+// kernel (converting cache rows) and the row prologue (writing a prefill
+// chunk's own rows as it appends them).
+#pragma once
+
+#include "rv_device.hpp"
+
+namespace rv {
+
+constexpr int kBT = 64;             // positions per K/V tile
+constexpr int kPlaneBytes = 16384;  // one staged 64 x 128 plane of 2-byte elements
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// Arithmetic modes of the staged copy (RV_PREFILL_EXACT / F16 / BF16).
+enum Mode { kExact = 0, kF16 = 1, kBF16 = 2 };
+
+template <int MODE>
+struct Op;
+template <>
+struct Op<kExact> {
+  typedef _Float16 E;
+  typedef f16x8 V8;
+  typedef f16x4 V4;
+  static constexpr bool kSplit = true;
+  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+template <>
+struct Op<kF16> {
+  typedef _Float16 E;
+  typedef f16x8 V8;
+  typedef f16x4 V4;
+  static constexpr bool kSplit = false;
+  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+template <>
+struct Op<kBF16> {
+  typedef __bf16 E;
+  typedef bf16x8 V8;
+  typedef bf16x4 V4;
+  static constexpr bool kSplit = false;
+  __device__ static f32x4 mfma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+
+// Planes per K or V half of a staged tile: hi and lo in the split mode.
+template <int MODE>
+constexpr int kPlanes = Op<MODE>::kSplit ? 2 : 1;
+
+// hi = round(x); lo = round(x - hi), into element e of two vectors.
+template <typename E, typename V>
+__device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
+  const E h = (E)x;
+  hi[e] = h;
+  lo[e] = (E)(x - (float)h);
+}
+
+// ---- staged tile layout -------------------------------------------------------------
+// One tile = P planes of K, then P planes of V^T (P = 2 in the split mode:
+// hi, lo), each plane 16 KiB of 16-byte chunks (8 elements).
+//   K plane: row t (64) x chunk c (16): elements d = 8c .. 8c+7, stored at
+//     byte 256 t + 16 (c ^ (t & 15)).
+//   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot
+//     j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
+//     (j >= 4); stored at byte 8192 s2 + 64 d + 16 (k ^ ((d >> 2) & 3)), so
+//     each 32-position half of the tile (s2) is 8 KiB of its own.
+// The rows of K's first and second 32 positions are likewise contiguous
+// halves. The swizzles put the 16 lanes of one operand read on 16 distinct
+// 16-byte bank groups.
+__device__ __forceinline__ int k_off(int t, int c) { return 256 * t + 16 * (c ^ (t & 15)); }
+__device__ __forceinline__ int vt_off(int d, int c) {
+  return 8192 * (c >> 2) + 64 * d + 16 * ((c & 3) ^ ((d >> 2) & 3));
+}
+__device__ __forceinline__ int vt_pos(int c, int j) {
+  const int s2 = c >> 2, k = c & 3;
+  return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
+}
+// Byte of element (position t, dim d) in a V^T plane: the inverse of vt_pos
+// (t = 32 s2 + u: chunk 4 s2 + (u & 15) / 4, slot (u & 3) + 4 (u >= 16)).
+__device__ __forceinline__ int vt_byte(int d, int t) {
+  const int u = t & 31;
+  return vt_off(d, 4 * (t >> 5) + ((u & 15) >> 2)) + 2 * ((u & 3) + ((u >> 4) << 2));
+}
+
+}  // namespace rv

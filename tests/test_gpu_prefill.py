@@ -121,16 +121,19 @@ def test_prefill_chunk_matches_the_oracle_across_geometries(mode, elem, impl):
 
 @pytest.mark.parametrize("elem", ["f32", "f16"])
 def test_chunked_prefill_truncation_and_mode_changes_keep_the_staged_copy_current(elem):
-    """The prefill kernels keep a staged copy of each layer's K/V across calls
-    and restage only from the first tile at or past the current prefix. A
+    """The prefill kernels keep a staged copy of each layer's K/V across calls:
+    a chunk's row prologue writes its own rows into it, rows that reached the
+    cache otherwise are staged from the cache, and attention over existing
+    rows restages from the first tile at or past the current prefix. A
     sequence of chunks, a truncation (server prefix reuse), a change of
-    arithmetic mode, attention over a shorter prefix and a cleared cache must
-    each match the oracle running the same sequence."""
+    arithmetic mode, rows added by decode steps and plain appends, attention
+    over a shorter prefix and a cleared cache must each match the oracle
+    running the same sequence."""
     torch_cuda()
     rng = Rng(0x57A6E + (elem == "f16"))
     n_kv, n_q, hd = 2, 16, 128
-    kv = rv.KvCache(2, n_kv, hd, 400, elem)
-    ref = oracle.KvCache(2, n_kv, hd, 400, elem_code(elem))
+    kv = rv.KvCache(2, n_kv, hd, 448, elem)
+    ref = oracle.KvCache(2, n_kv, hd, 448, elem_code(elem))
     wq, wk = rng.vec_in(hd, 0.9, 1.1), rng.vec_in(hd, 0.9, 1.1)
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     loose = elem == "f16"
@@ -154,9 +157,28 @@ def test_chunked_prefill_truncation_and_mode_changes_keep_the_staged_copy_curren
     for layer in (0, 1):
         chunk(layer, 130, 90, "f16")    # rows 130.. rewritten: restage from tile 2
         chunk(layer, 220, 33, "exact")  # a mode change restages everything
+    # Rows that reach the cache outside a chunk (decode steps, plain appends)
+    # are staged from it before the next chunk writes its own rows; chunks
+    # ending on a tile boundary leave no tail to zero.
+    for layer in (0, 1):
+        pos = kv.len(layer)
+        for _ in range(3):
+            q1 = rng.vec_in(n_q * hd, -2.0, 2.0)
+            k1, v1 = rng.vec_in(n_kv * hd, -2.0, 2.0), rng.vec_in(n_kv * hd, -1.0, 1.0)
+            out = dev(np.full(q1.shape, np.nan))
+            rv.decode_step(kv, layer, dev(q1), dev(k1), dev(v1), dev(wq), dev(wk), 1e-6, 1e6, pos, scale, out)
+            ref.decode_step(layer, q1, k1, v1, wq, wk, 1e-6, 1e6, pos, scale, threads=THREADS)
+            pos += 1
+        assert pos == 256
+        chunk(layer, 256, 64, "exact")   # starts and ends on tile boundaries
+        k2, v2 = rng.vec_in(9 * n_kv * hd, -2.0, 2.0), rng.vec_in(9 * n_kv * hd, -1.0, 1.0)
+        kv.append_rows(layer, k2, v2)
+        ref.append_rows(layer, k2, v2)
+        chunk(layer, 329, 55, "bf16")    # a mode change after plain appends
+        chunk(layer, 384, 17, "bf16")
     # attention over a shorter prefix of the staged layer, then the full one
     q = rng.vec_in(20 * n_q * hd, -2.0, 2.0).reshape(20, -1)
-    for start in (40, 233):
+    for start in (40, 381):
         out = dev(np.full(q.shape, np.nan))
         rv.attention_at_rows(dev(q), kv, 1, start, scale, out, mode="f16")
         want = ref.scatter_attention(q, 1, start, scale, THREADS)
