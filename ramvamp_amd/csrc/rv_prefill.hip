@@ -848,39 +848,35 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
   }
 }
 
-// Log-sum-exp merge of the KV splits: one 256-thread workgroup per (kv head,
-// row block, 8 columns), thread -> (column, 4 consecutive d). Every split's
-// partial is loaded before any is folded (one memory round trip).
-__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int kv_splits, int n_rb,
-                                                            int n_cb, int qr, int rows, int group, int q_stride,
+// Log-sum-exp merge of the S KV splits: one 256-thread workgroup per (kv
+// head, row block, 8 columns), thread -> (column, 4 consecutive d). Every
+// split's partial is loaded before any is folded (one memory round trip).
+template <int S>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int n_rb, int n_cb,
+                                                            int qr, int rows, int group, int q_stride,
                                                             float* __restrict__ out) {
   const int cb = blockIdx.x % n_cb, rb = (blockIdx.x / n_cb) % n_rb, kvh = blockIdx.x / (n_cb * n_rb);
   const int m = 8 * cb + (threadIdx.x >> 5), d = 4 * (threadIdx.x & 31);
   const int head = m / qr, row = rb * qr + m % qr;
   if (head >= group || row >= rows) return;
-  const float* base = part + ((size_t)kvh * n_rb + rb) * kv_splits * kPartStride;
-  f32x4 o[kMaxKvSplits];
-  float2 ml[kMaxKvSplits];
+  const float* base = part + ((size_t)kvh * n_rb + rb) * S * kPartStride;
+  f32x4 o[S];
+  float2 ml[S];
 #pragma unroll
-  for (int sp = 0; sp < kMaxKvSplits; ++sp) {
-    if (sp < kv_splits) {
-      o[sp] = *reinterpret_cast<const f32x4*>(base + sp * kPartStride + (size_t)m * kD + d);
-      ml[sp] = *reinterpret_cast<const float2*>(base + sp * kPartStride + 128 * kD + 2 * m);
-    }
+  for (int sp = 0; sp < S; ++sp) {
+    o[sp] = *reinterpret_cast<const f32x4*>(base + sp * kPartStride + (size_t)m * kD + d);
+    ml[sp] = *reinterpret_cast<const float2*>(base + sp * kPartStride + 128 * kD + 2 * m);
   }
-  float M = kNegSentinel;
+  float M = ml[0].x;
 #pragma unroll
-  for (int sp = 0; sp < kMaxKvSplits; ++sp)
-    if (sp < kv_splits) M = fmaxf(M, ml[sp].x);
+  for (int sp = 1; sp < S; ++sp) M = fmaxf(M, ml[sp].x);
   float L = 0.f;
   f32x4 O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int sp = 0; sp < kMaxKvSplits; ++sp) {
-    if (sp < kv_splits) {
-      const float w = __builtin_amdgcn_exp2f(ml[sp].x - M);
-      L += ml[sp].y * w;
-      O += o[sp] * w;
-    }
+  for (int sp = 0; sp < S; ++sp) {
+    const float w = __builtin_amdgcn_exp2f(ml[sp].x - M);
+    L += ml[sp].y * w;
+    O += o[sp] * w;
   }
   // The caller's rows may be only 4-byte aligned: scalar stores.
   float* op = out + (size_t)row * q_stride + (size_t)(kvh * group + head) * kD + d;
@@ -1027,18 +1023,21 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const int n_kv = (int)kv->n_kv_heads;
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
   const int planes = planes_of(m);
+  const size_t positions = start + rows;
+  const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);  // tiles this call reads
   // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
   // 128-vector blocks would leave CUs idle (fewer than 256 workgroups) or the
-  // tuning asks for it.
+  // tuning asks for it. The split mode keeps 128 when the range is long
+  // enough for a KV split to fill the chip (at least 16 tiles): its
+  // one-group kernel gains more from 32 columns per wave than the split and
+  // its merge cost (config 4: 123 vs 134 us).
   int vectors = 128;
   if (kv->tune_prefill_rows > 0)
     vectors = kv->tune_prefill_rows * group <= 64 ? 64 : 128;
-  else if ((long)((rows * group + 127) / 128) * n_kv < 256)
+  else if ((long)((rows * group + 127) / 128) * n_kv < 256 && !(planes == 2 && n_stage_tiles >= 16))
     vectors = 64;
   const int qr = vectors / group;
   const int n_rb = (int)((rows + qr - 1) / qr);
-  const size_t positions = start + rows;
-  const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);  // tiles this call reads
   int kv_splits = (int)kv->tune_prefill_kv_split;
   if (kv_splits <= 0) {
     // Split the KV axis until about 256 workgroups are in flight, keeping at
@@ -1086,9 +1085,25 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   if (impl <= 0) impl = (n_stage_tiles + kv_splits - 1) / kv_splits <= 16 ? 2 : 1;
   launch_stage(kv, layer, m, positions, tile_stride, stage_lo, n_stage_tiles, stage, s);
   launch_attention(m, vectors, impl, a, s);
-  if (kv_splits > 1)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)(n_kv * n_rb * vectors / 8)), dim3(256), 0, s,
-                       (const float*)part, kv_splits, n_rb, vectors / 8, qr, (int)rows, group, (int)(n_q_heads * kD), out);
+  if (kv_splits > 1) {
+    const dim3 grid((unsigned)(n_kv * n_rb * vectors / 8));
+    const int n_cb = vectors / 8, q_stride = (int)(n_q_heads * kD);
+#define RV_MERGE(S)                                                                                               \
+  case S:                                                                                                         \
+    hipLaunchKernelGGL(prefill_merge_kernel<S>, grid, dim3(256), 0, s, (const float*)part, n_rb, n_cb, qr, (int)rows, \
+                       group, q_stride, out);                                                                    \
+    break
+    switch (kv_splits) {
+      RV_MERGE(2);
+      RV_MERGE(3);
+      RV_MERGE(4);
+      RV_MERGE(5);
+      RV_MERGE(6);
+      RV_MERGE(7);
+      default: RV_MERGE(8);
+    }
+#undef RV_MERGE
+  }
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
   return st;

@@ -260,9 +260,11 @@ def test_prefill_errors_and_first_row_semantics():
 
 @pytest.mark.parametrize("impl", [1, 2])
 @pytest.mark.parametrize("mode", ["exact", "f16"])
-@pytest.mark.parametrize("vectors_rows,splits", [(0, 0), (8, 1), (16, 1), (16, 2), (8, 3), (16, 8)])
+@pytest.mark.parametrize("vectors_rows,splits", [(0, 0), (8, 1), (16, 1), (16, 2), (8, 3), (8, 4), (16, 5), (8, 6),
+                                                 (16, 7), (16, 8)])
 def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits, impl):
-    """64 or 128 query vectors per workgroup and 1..8 KV splits (some empty),
+    """64 or 128 query vectors per workgroup and 1..8 KV splits (some empty;
+    each split count has its own merge kernel),
     over a chunk whose rows cross several 64-position tiles and end in a
     partial row block, for both f16/bf16 attention kernels."""
     torch_cuda()
