@@ -62,15 +62,14 @@ __device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
 //     byte 256 t + 16 (c ^ (t & 15)).
 //   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot
 //     j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
-//     (j >= 4); stored at byte 8192 s2 + 64 d + 16 (k ^ ((d >> 2) & 3)), so
-//     each 32-position half of the tile (s2) is 8 KiB of its own.
-// The rows of K's first and second 32 positions are likewise contiguous
-// halves. The swizzles put the 16 lanes of one operand read on 16 distinct
-// 16-byte bank groups.
+//     (j >= 4); stored at byte 128 d + 16 (c ^ ((d >> 1) & 7)).
+// The swizzles put the 16 lanes of one operand read on 16 distinct 16-byte
+// bank groups; the counters read no LDS bank conflicts for either plane
+// (an alternative V^T layout with each 32-position half contiguous,
+// 8192 s2 + 64 d + 16 (k ^ ((d >> 2) & 3)), read ~4 conflict cycles per
+// operand read).
 __device__ __forceinline__ int k_off(int t, int c) { return 256 * t + 16 * (c ^ (t & 15)); }
-__device__ __forceinline__ int vt_off(int d, int c) {
-  return 8192 * (c >> 2) + 64 * d + 16 * ((c & 3) ^ ((d >> 2) & 3));
-}
+__device__ __forceinline__ int vt_off(int d, int c) { return 128 * d + 16 * (c ^ ((d >> 1) & 7)); }
 __device__ __forceinline__ int vt_pos(int c, int j) {
   const int s2 = c >> 2, k = c & 3;
   return j < 4 ? 32 * s2 + 4 * k + j : 32 * s2 + 16 + 4 * k + (j - 4);
