@@ -78,6 +78,65 @@ __device__ __forceinline__ void stage_elem(const StagedRows& sr, int kind, int h
   if constexpr (Op<SM>::kSplit) *reinterpret_cast<E*>(dst + kPlaneBytes) = (E)(x - (float)hi);
 }
 
+// A staging prologue's V rows, four positions [p0, p0 + 4) of kv head h per
+// wave (p0 a multiple of 4 counted from row0's quad): the chunk's rows are
+// copied into the cache, and each lane's two V^T elements (dims lane and
+// lane + 64) of the four positions, which share one 8-byte piece of a V^T
+// chunk, are written with one store per plane. Positions past the chunk in
+// its last tile are staged as zeros; positions before row0 (already staged)
+// are left alone, so a quad holding some takes 2-byte stores.
+template <typename T, int SM>
+__device__ __forceinline__ void stage_v_quad(const float* __restrict__ v, T* __restrict__ vp, int n_kv, int h,
+                                             const StagedRows& sr, int g, int lane) {
+  typedef typename Op<SM>::E E;
+  typedef typename Op<SM>::V4 V4;
+  constexpr int P = kPlanes<SM>;
+  const long p0 = (sr.row0 & ~3L) + 4L * g;
+  const long tile_end = (sr.row0 + sr.rows + kBT - 1) / kBT * kBT;
+  if (p0 >= tile_end) return;
+  float x[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long r = p0 + i - sr.row0;
+    const bool live = r >= 0 && r < sr.rows;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const size_t at = ((size_t)(live ? r : 0) * n_kv + h) * 128 + lane + 64 * k;
+      x[i][k] = live ? v[at] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long r = p0 + i - sr.row0;
+    if (r < 0 || r >= sr.rows) continue;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) x[i][k] = store_cached<T>(vp + ((size_t)r * n_kv + h) * 128 + lane + 64 * k, x[i][k]);
+  }
+  char* plane = sr.base + ((size_t)h * sr.tile_stride + (size_t)(p0 / kBT)) * (2 * P * kPlaneBytes) + P * kPlaneBytes;
+  const int t = (int)(p0 % kBT);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    char* dst = plane + vt_byte(lane + 64 * k, t);  // positions t .. t + 3: 8 contiguous bytes
+    V4 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      hi[i] = (E)x[i][k];
+      lo[i] = (E)(x[i][k] - (float)hi[i]);
+    }
+    if (p0 >= sr.row0) {
+      *reinterpret_cast<V4*>(dst) = hi;
+      if constexpr (P == 2) *reinterpret_cast<V4*>(dst + kPlaneBytes) = lo;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (p0 + i < sr.row0) continue;
+        *reinterpret_cast<E*>(dst + 2 * i) = hi[i];
+        if constexpr (P == 2) *reinterpret_cast<E*>(dst + kPlaneBytes + 2 * i) = lo[i];
+      }
+    }
+  }
+}
+
 // grid (rows, n_kv_heads), one wave each: K and V heads copied into the
 // cache, converted to the plane's element type (KvCache::append as is).
 template <typename T>
@@ -99,7 +158,10 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
 // once per head, while the wave's head loads are in flight.
 // SM >= 0 (a prefill chunk, n_q = 0, head_dim 128): k and v rows, as the
 // cache holds them, are also written into the staged tiles in mode SM, and
-// the grid's rows past the chunk zero the rest of its last tile.
+// the rest of the chunk's last tile is zeroed. The slot list is then the k
+// heads only (grid rows past the chunk zero their K rows); v heads are
+// handled by the blocks y >= the k slot blocks, one per (quad of positions
+// x, head y - k slot blocks): stage_v_quad.
 constexpr int kSlots = 4;
 
 template <typename T, int NP, int SM>
@@ -113,9 +175,14 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
 #pragma clang fp contract(off)
   const int r = blockIdx.x, lane = threadIdx.x;
   const int half = hd / 2;
-  const int n_slots = n_q + 2 * n_kv;
+  const int n_slots = SM >= 0 ? n_q + n_kv : n_q + 2 * n_kv;
   const int s0 = (int)blockIdx.y * kSlots;
   if constexpr (SM >= 0) {
+    const int kb = (n_slots + kSlots - 1) / kSlots;
+    if ((int)blockIdx.y >= kb) {
+      stage_v_quad<T, SM>(v, vp, n_kv, (int)blockIdx.y - kb, sr, r, lane);
+      return;
+    }
     if (r >= sr.rows) {
 #pragma unroll
       for (int j = 0; j < kSlots; ++j) {
@@ -313,7 +380,10 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   const size_t grid_rows = staging ? rows + (kBT - end % kBT) % kBT : rows;
   const int sm = !staging ? -1 : sd->mode == RV_PREFILL_F16 ? kF16 : sd->mode == RV_PREFILL_BF16 ? kBF16 : kExact;
   const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
-  const dim3 grid((unsigned)grid_rows, (unsigned)((n_slots + kSlots - 1) / kSlots));
+  // Staging: k slot blocks, then one block row per v head (its quads of
+  // positions along x; grid_rows covers them).
+  const int slot_blocks = staging ? (n_kv + kSlots - 1) / kSlots + n_kv : (n_slots + kSlots - 1) / kSlots;
+  const dim3 grid((unsigned)grid_rows, (unsigned)slot_blocks);
   const size_t off = cache_row * kv->kv_dim;
   if (kv->elem == RV_ELEM_F32)
     launch_row_prologue_t<float>(grid, np, q, q_out, (int)n_q, k, v, (float*)kv->k_layer(layer) + off,
