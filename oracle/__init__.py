@@ -104,6 +104,18 @@ def lib():
         "rvo_prefill_chunk": (c_int32, [c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t,
                                         c_void_p, c_void_p, c_float, c_float, c_size_t, c_float, c_void_p, c_size_t,
                                         c_int, E]),
+        "rvo_quant_block_weights": (c_size_t, [c_uint32]),
+        "rvo_quant_block_bytes": (c_size_t, [c_uint32]),
+        "rvo_quant_row_bytes": (c_int32, [c_uint32, c_size_t, POINTER(c_size_t), E]),
+        "rvo_quantize_row_q8_0": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, E]),
+        "rvo_quantize_row_q8_k": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, E]),
+        "rvo_dequantize_row": (c_int32, [c_uint32, c_void_p, c_size_t, c_void_p, E]),
+        "rvo_vec_dot_q8_k": (c_int32, [c_uint32, c_void_p, c_size_t, c_void_p, c_size_t, fp, E]),
+        "rvo_vec_dot_q8_0": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, fp, E]),
+        "rvo_gemv_q8_k": (c_int32, [c_uint32, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_size_t, c_size_t,
+                                    c_size_t, c_size_t, c_void_p, c_size_t, E]),
+        "rvo_gemv_q8_0": (c_int32, [c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_size_t, c_size_t, c_size_t,
+                                    c_size_t, c_void_p, c_size_t, E]),
     }
     del fp
     for name, (res, args) in sig.items():
@@ -327,3 +339,86 @@ class KvCache:
                                        _ptr(wk), eps, theta, start, scale, _ptr(out), threads, int(force_scalar),
                                        byref(err)), err)
         return out
+
+
+# ---- quantized projections (rv_oracle_quant.c; kernels/quants, kernels/gemv.rs) ----
+
+RV_QF_Q4_K, RV_QF_Q5_K, RV_QF_Q6_K, RV_QF_Q8_0, RV_QF_Q8_K = 1, 2, 3, 4, 5
+# The ABI's activation blocks (include/ramvamp_gemv.h): ggml field order, no padding.
+BLOCK_Q8_K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+BLOCK_Q8_0 = np.dtype([("d", "<f4"), ("qs", "i1", (32,))])
+assert BLOCK_Q8_K.itemsize == 292 and BLOCK_Q8_0.itemsize == 36
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def quant_block_weights(fmt: int) -> int:
+    return int(lib().rvo_quant_block_weights(fmt))
+
+
+def quant_block_bytes(fmt: int) -> int:
+    return int(lib().rvo_quant_block_bytes(fmt))
+
+
+def quant_row_bytes(fmt: int, in_dim: int) -> int:
+    n, err = c_size_t(), RvError()
+    _check(lib().rvo_quant_row_bytes(fmt, in_dim, byref(n), byref(err)), err)
+    return int(n.value)
+
+
+def quantize_row_q8_0(x, n_blocks=None) -> np.ndarray:
+    x = _f32(x).ravel()
+    n = x.size // 32 if n_blocks is None else n_blocks
+    out = np.zeros(n, dtype=BLOCK_Q8_0)
+    err = RvError()
+    _check(lib().rvo_quantize_row_q8_0(_ptr(x), x.size, out.ctypes.data, n, byref(err)), err)
+    return out
+
+
+def quantize_row_q8_k(x, n_blocks=None) -> np.ndarray:
+    x = _f32(x).ravel()
+    n = x.size // 256 if n_blocks is None else n_blocks
+    out = np.zeros(n, dtype=BLOCK_Q8_K)
+    err = RvError()
+    _check(lib().rvo_quantize_row_q8_k(_ptr(x), x.size, out.ctypes.data, n, byref(err)), err)
+    return out
+
+
+def dequantize_row(fmt: int, row) -> np.ndarray:
+    row = _u8(row).ravel()
+    bb = max(1, quant_block_bytes(fmt))
+    out = np.zeros(row.size // bb * quant_block_weights(fmt), dtype=np.float32)
+    err = RvError()
+    _check(lib().rvo_dequantize_row(fmt, row.ctypes.data, row.size, _ptr(out), byref(err)), err)
+    return out
+
+
+def vec_dot(fmt: int, row, acts) -> float:
+    row = _u8(row).ravel()
+    r, err = c_float(), RvError()
+    if fmt == RV_QF_Q8_0:
+        _check(lib().rvo_vec_dot_q8_0(row.ctypes.data, row.size, acts.ctypes.data, acts.size, byref(r), byref(err)),
+               err)
+    else:
+        _check(lib().rvo_vec_dot_q8_k(fmt, row.ctypes.data, row.size, acts.ctypes.data, acts.size, byref(r),
+                                      byref(err)), err)
+    return float(np.float32(r.value))
+
+
+def gemv(fmt: int, weight, in_dim: int, out_dim: int, acts, n_acts: int = 1, rows=None) -> np.ndarray:
+    """gemv.rs: out[(r - lo) * n_acts + a] = weight_row(r) . act_row(a) for r in rows."""
+    weight = _u8(weight).ravel()
+    lo, hi = (0, out_dim) if rows is None else rows
+    out = np.full(max(0, hi - lo) * n_acts, np.nan, dtype=np.float32)
+    err = RvError()
+    if fmt == RV_QF_Q8_0:
+        rc = lib().rvo_gemv_q8_0(weight.ctypes.data, weight.size, in_dim, out_dim, acts.ctypes.data, acts.size, n_acts,
+                                 lo, hi, _ptr(out), out.size, byref(err))
+    else:
+        rc = lib().rvo_gemv_q8_k(fmt, weight.ctypes.data, weight.size, in_dim, out_dim, acts.ctypes.data, acts.size,
+                                 n_acts, lo, hi, _ptr(out), out.size, byref(err))
+    _check(rc, err)
+    return out
+

@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "../include/ramvamp_attn.h"
+#include "../include/ramvamp_gemv.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -118,6 +119,31 @@ int32_t rvo_prefill_chunk(rvo_kv* kv, size_t layer, float* q_rows, float* k_rows
 /* Per-row prologue alone (for tests): norm + rope of `n_heads` heads. */
 int32_t rvo_norm_rope_heads(float* x, size_t n_heads, size_t head_dim, const float* w,
                             float eps, float theta, uint32_t position);
+
+/* ---- quantized projections (rv_oracle_quant.c) ---- */
+/* QuantFormat geometry (kernels/quants/mod.rs:75-105). */
+size_t rvo_quant_block_weights(uint32_t format);
+size_t rvo_quant_block_bytes(uint32_t format);
+int32_t rvo_quant_row_bytes(uint32_t format, size_t in_dim, size_t* row_bytes, rv_error* err);
+/* quantize.rs:37-55 and :71-106. */
+int32_t rvo_quantize_row_q8_0(const float* x, size_t x_len, rv_block_q8_0* out, size_t n_blocks, rv_error* err);
+int32_t rvo_quantize_row_q8_k(const float* x, size_t x_len, rv_block_q8_k* out, size_t n_blocks, rv_error* err);
+/* dequant.rs: Q4_K, Q5_K, Q6_K and Q8_0 rows (len bytes) into out. */
+int32_t rvo_dequantize_row(uint32_t format, const uint8_t* bytes, size_t len, float* out, rv_error* err);
+/* dot.rs scalar dots: one weight row of `len` bytes against n_blocks
+ * activation blocks. */
+int32_t rvo_vec_dot_q8_k(uint32_t format, const uint8_t* row, size_t len, const rv_block_q8_k* acts,
+                         size_t n_blocks, float* out, rv_error* err);
+int32_t rvo_vec_dot_q8_0(const uint8_t* row, size_t len, const rv_block_q8_0* acts, size_t n_blocks, float* out,
+                         rv_error* err);
+/* gemv.rs row-range GEMVs against n_acts activation rows
+ * (out[i * n_acts + a]; n_acts = 1: gemv_*_rows). */
+int32_t rvo_gemv_q8_k(uint32_t format, const uint8_t* weight, size_t weight_len, size_t in_dim, size_t out_dim,
+                      const rv_block_q8_k* acts, size_t act_blocks, size_t n_acts, size_t row_lo, size_t row_hi,
+                      float* out, size_t out_len, rv_error* err);
+int32_t rvo_gemv_q8_0(const uint8_t* weight, size_t weight_len, size_t in_dim, size_t out_dim,
+                      const rv_block_q8_0* acts, size_t act_blocks, size_t n_acts, size_t row_lo, size_t row_hi,
+                      float* out, size_t out_len, rv_error* err);
 
 #ifdef __cplusplus
 }
