@@ -28,6 +28,12 @@ RV_TUNE_DECODE_HG = 5
 RV_TUNE_DECODE_IMPL = 6
 RV_TUNE_KERNEL_TIMING = 7
 RV_TUNE_PREFILL_IMPL = 8
+# include/ramvamp_gemv.h
+RV_QF_Q4_K = 1
+RV_QF_Q5_K = 2
+RV_QF_Q6_K = 3
+RV_QF_Q8_0 = 4
+RV_QF_Q8_K = 5
 
 
 class RvError(ctypes.Structure):
@@ -35,7 +41,7 @@ class RvError(ctypes.Structure):
                 ("what", c_char_p)]
 
 
-# Every symbol include/ramvamp_attn.h declares: name -> (restype, argtypes).
+# Every symbol include/*.h declares: name -> (restype, argtypes).
 _E = POINTER(RvError)
 _P = c_void_p
 SIGNATURES = {
@@ -79,6 +85,25 @@ SIGNATURES = {
                                    c_float, _P, c_uint32, _E]),
     "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
     "rv_kv_kernel_time": (c_int32, [_P, POINTER(c_double), POINTER(c_uint64), _E]),
+    # include/ramvamp_gemv.h
+    "rv_quant_block_weights": (c_size_t, [c_uint32]),
+    "rv_quant_block_bytes": (c_size_t, [c_uint32]),
+    "rv_quant_row_bytes": (c_int32, [c_uint32, c_size_t, POINTER(c_size_t), _E]),
+    "rv_quantize_row_q8_0": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_uint32, _E]),
+    "rv_quantize_row_q8_k": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_uint32, _E]),
+    "rv_gemv_q8_k_rows": (c_int32, [c_uint32, _P, c_size_t, c_size_t, c_size_t, _P, c_size_t, c_size_t, c_size_t, _P,
+                                    c_size_t, _P, c_uint32, _E]),
+    "rv_gemv_q8_k": (c_int32, [c_uint32, _P, c_size_t, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32,
+                               _E]),
+    "rv_gemv_q8_0_rows": (c_int32, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, c_size_t, c_size_t, _P, c_size_t,
+                                    _P, c_uint32, _E]),
+    "rv_gemv_q8_0": (c_int32, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32, _E]),
+    "rv_attn_in_proj_scratch_bytes": (c_size_t, [c_size_t]),
+    "rv_attn_in_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t,
+                                  c_uint32, _P, c_size_t, _P, _P, c_size_t, _P, c_uint32, _E]),
+    "rv_attn_out_proj_scratch_bytes": (c_size_t, [c_size_t]),
+    "rv_attn_out_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32,
+                                   _E]),
 }
 
 _lib = None

@@ -47,6 +47,11 @@ _VARIANTS = {
     33: ("DeviceError", "Unsupported", ("value",)),
     34: ("DeviceError", "Hip", ("hip_error",)),
     35: ("DeviceError", "BadElem", ("elem",)),
+    40: ("KernelError", "IndivisibleRow", ("format", "in_dim", "block_weights")),
+    41: ("KernelError", "RowBytesNotBlockMultiple", ("format", "len", "block_bytes")),
+    42: ("KernelError", "BlockCountMismatch", ("weight_blocks", "activation_blocks")),
+    43: ("KernelError", "QuantizeLenMismatch", ("format", "floats", "out_blocks")),
+    44: ("KernelError", "UnsupportedFormat", ("format",)),
 }
 
 
@@ -81,8 +86,13 @@ class DeviceError(RamvampError):
     """Failures of the device path itself (HIP errors, null arguments, unsupported shapes)."""
 
 
+class KernelError(RamvampError):
+    """kernels/error.rs: the quantized projections' geometry errors (LengthMismatch
+    arrives as PrimitiveError's LengthMismatch with its ``what``)."""
+
+
 _CLASSES = {"KvError": KvError, "AttentionError": AttentionError, "PrimitiveError": PrimitiveError,
-            "DeviceError": DeviceError}
+            "DeviceError": DeviceError, "KernelError": KernelError}
 
 
 def _check(rc: int, err: L.RvError):

@@ -13,6 +13,7 @@
 #include <new>
 
 #include "rv_internal.hpp"
+#include "../../include/ramvamp_gemv.h"
 
 namespace {
 
@@ -314,6 +315,11 @@ const char* rv_status_name(int32_t code) {
     case RV_ERR_UNSUPPORTED: return "RV_ERR_UNSUPPORTED";
     case RV_ERR_HIP: return "RV_ERR_HIP";
     case RV_ERR_BAD_ELEM: return "RV_ERR_BAD_ELEM";
+    case RV_QUANT_INDIVISIBLE_ROW: return "RV_QUANT_INDIVISIBLE_ROW";
+    case RV_QUANT_ROW_BYTES_NOT_BLOCK_MULTIPLE: return "RV_QUANT_ROW_BYTES_NOT_BLOCK_MULTIPLE";
+    case RV_QUANT_BLOCK_COUNT_MISMATCH: return "RV_QUANT_BLOCK_COUNT_MISMATCH";
+    case RV_QUANT_QUANTIZE_LEN_MISMATCH: return "RV_QUANT_QUANTIZE_LEN_MISMATCH";
+    case RV_QUANT_UNSUPPORTED_FORMAT: return "RV_QUANT_UNSUPPORTED_FORMAT";
     default: return "RV_UNKNOWN";
   }
 }

@@ -1,0 +1,401 @@
+// rv_quant.hip — the quantized projections either side of attention on gfx950:
+// Q8_K / Q8_0 activation quantizers and the k-quant / Q8_0 GEMVs.
+//
+// Replaces quantize_row_q8_k / quantize_row_q8_0
+// (crates/core/src/kernels/quants/quantize.rs:37-106) and the row-range GEMVs
+// gemv_q8_k_rows / gemv_q8_0_rows (kernels/gemv.rs:296-615) over the scalar
+// dots vec_dot_{q4_k,q5_k,q6_k}_q8_k / vec_dot_q8_0_q8_0 (quants/dot.rs),
+// as called at model/forward.rs:2574-2646.
+//
+// Results are bit-identical to the reference's scalar kernels:
+//  - quantizers: one wave per 256-value Q8_K block (the first value of
+//    largest magnitude found by a lane-ordered wave reduction, RNE rounding,
+//    the scalar code's f32 divisions) and 32 lanes per Q8_0 block;
+//  - GEMVs: one wave per output row. Lanes split each super-block's
+//    sub-blocks and form the integer sub-block sums with v_dot4_i32_i8
+//    (exact, in any order), a block's integer totals come from an exact
+//    8-lane reduction, the block's float contribution is the scalar dot's
+//    expression, and the row's sum adds the blocks in order.
+// The GEMVs stream each weight byte once (HBM-bound); activations are
+// re-read per row from L2.
+#include "rv_device.hpp"
+#include "rv_internal.hpp"
+#include "rv_quant.hpp"
+
+namespace rv {
+namespace {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+}
+
+// 32 bytes at a 2-byte-aligned address, as 8 little-endian dwords, reading
+// nothing outside [a, a + 32) except the two bytes before `a` (which the
+// callers' layouts guarantee belong to the same block).
+__device__ __forceinline__ void load32_a2(const uint8_t* a, uint32_t (&w)[8]) {
+  if (((uintptr_t)a & 2) == 0) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(a);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = p[k];
+    return;
+  }
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(a - 2);  // bytes a-2 .. a+1
+  uint32_t e[8];
+#pragma unroll
+  for (int k = 0; k < 7; ++k) e[k + 1] = p[k + 1];  // bytes a+2+4k .. a+5+4k
+  e[0] = p[0];
+  const uint32_t tail = *reinterpret_cast<const uint16_t*>(a + 30);
+#pragma unroll
+  for (int k = 0; k < 7; ++k) w[k] = __builtin_amdgcn_alignbyte(e[k + 1], e[k], 2);
+  w[7] = (e[7] >> 16) | (tail << 16);
+}
+
+// Sum over the 8 lanes of an aligned lane group (exact for integers).
+__device__ __forceinline__ int sum8_lanes(int v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  return v;
+}
+
+__device__ __forceinline__ int dot4(uint32_t w, int a, int acc) {
+  return __builtin_amdgcn_sdot4((int)w, a, acc, false);
+}
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// get_scale_min_k4 (quants/blocks.rs:158-167) from the 12 scale bytes as
+// three little-endian dwords.
+__device__ __forceinline__ void scale_min_k4(int j, const uint32_t (&s)[3], int& sc, int& m) {
+  auto byte = [&](int i) { return (int)((s[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+  if (j < 4) {
+    sc = byte(j) & 63;
+    m = byte(j + 4) & 63;
+  } else {
+    sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+    m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+  }
+}
+
+// One super-block's float contribution for the k-quants, computed by the 8
+// lanes of a group, lane j owning sub-block j (Q4_K/Q5_K: 32 weights) or
+// the two 16-weight sub-blocks 2j, 2j+1 (Q6_K); every lane of the group
+// returns the same value.
+template <int FMT>
+__device__ __forceinline__ float kq_block(const uint8_t* __restrict__ blk, const rv_block_q8_k* __restrict__ y,
+                                          int j);
+
+// k_quant_affine_block with the q4_K / q5_K expansions (dot.rs:56-143):
+// d*sumi - dmin*sumi_mins, d = f16(d)*y.d, dmin = f16(dmin)*y.d.
+template <int FMT>
+__device__ __forceinline__ float affine_block(const uint8_t* __restrict__ blk, const rv_block_q8_k* __restrict__ y,
+                                              int j) {
+#pragma clang fp contract(off)
+  constexpr bool kQ5 = FMT == RV_QF_Q5_K;
+  const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
+  const uint32_t* sp = reinterpret_cast<const uint32_t*>(blk + 4);
+  const uint32_t s[3] = {sp[0], sp[1], sp[2]};
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(blk + (kQ5 ? 48 : 16) + 32 * (j >> 1));
+  const int* a = reinterpret_cast<const int*>(y->qs + 32 * j);
+  uint32_t qh[8];
+  if constexpr (kQ5) {
+    const uint32_t* h = reinterpret_cast<const uint32_t*>(blk + 16);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qh[k] = h[k];
+  }
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint32_t w = (j & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
+    if constexpr (kQ5) w |= ((qh[k] >> j) & 0x01010101u) << 4;
+    acc = dot4(w, a[k], acc);
+  }
+  int sc, m;
+  scale_min_k4(j, s, sc, m);
+  const uint32_t bs = *reinterpret_cast<const uint32_t*>(y->bsums + 2 * j);
+  const int bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
+  const int sumi = sum8_lanes(sc * acc);
+  const int sumi_mins = sum8_lanes(m * bsum);
+  const float d = f16_bits_to_f32(dd) * y->d;
+  const float dmin = f16_bits_to_f32(dd >> 16) * y->d;
+  return d * (float)sumi - dmin * (float)sumi_mins;
+}
+
+template <>
+__device__ __forceinline__ float kq_block<RV_QF_Q4_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+  return affine_block<RV_QF_Q4_K>(blk, y, j);
+}
+template <>
+__device__ __forceinline__ float kq_block<RV_QF_Q5_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+  return affine_block<RV_QF_Q5_K>(blk, y, j);
+}
+
+// vec_dot_q6_k_q8_k (dot.rs:150-179): lane j = 4 half + group holds weights
+// 32j .. 32j+31: ql nibbles (byte l + 32 (group & 1) of the half, high
+// nibble for groups 2, 3) and two qh bits (2 group). The stored values are
+// q + 32 in 0..63; sum (q+32)a - 32 sum a, with sum a the activation bsums.
+template <>
+__device__ __forceinline__ float kq_block<RV_QF_Q6_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+#pragma clang fp contract(off)
+  const int half = j >> 2, grp = j & 3;
+  uint32_t ql[8], qh[8];
+  load32_a2(blk + 64 * half + 32 * (grp & 1), ql);
+  load32_a2(blk + 128 + 32 * half, qh);
+  const int* a = reinterpret_cast<const int*>(y->qs + 32 * j);
+  int lo = 0, hi = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t nib = (grp >> 1) ? (ql[k] >> 4) & 0x0F0F0F0Fu : ql[k] & 0x0F0F0F0Fu;
+    const uint32_t w = nib | (((qh[k] >> (2 * grp)) & 0x03030303u) << 4);
+    if (k < 4)
+      lo = dot4(w, a[k], lo);
+    else
+      hi = dot4(w, a[k], hi);
+  }
+  const uint32_t bs = *reinterpret_cast<const uint32_t*>(y->bsums + 2 * j);
+  lo -= 32 * (int)(int16_t)(bs & 0xFFFFu);
+  hi -= 32 * (int)(int16_t)(bs >> 16);
+  const uint32_t scp = *reinterpret_cast<const uint16_t*>(blk + 192 + 2 * j);
+  const int sc_lo = (int)(int8_t)(scp & 0xFF), sc_hi = (int)(int8_t)(scp >> 8);
+  const int sumi = sum8_lanes(sc_lo * lo + sc_hi * hi);
+  const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
+  return d * y->d * (float)sumi;
+}
+
+// One k-quant row against its activation blocks, every lane returning the
+// row's sum: 8 super-blocks per pass (lane group b), added in block order.
+template <int FMT>
+__device__ __forceinline__ float kq_row(const uint8_t* __restrict__ row, int nb, const rv_block_q8_k* __restrict__ acts,
+                                        int lane) {
+  constexpr int BB = FMT == RV_QF_Q4_K ? 144 : FMT == RV_QF_Q5_K ? 176 : 210;
+  const int bl = lane >> 3, j = lane & 7;
+  float sumf = 0.f;
+  for (int b0 = 0; b0 < nb; b0 += 8) {
+    const int b = min(b0 + bl, nb - 1);  // groups past the row recompute its last block (unused)
+    const float c = kq_block<FMT>(row + (size_t)b * BB, acts + b, j);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (b0 + k < nb) sumf += lane_f(c, 8 * k);
+  }
+  return sumf;
+}
+
+// vec_dot_q8_0_q8_0 (dot.rs:185-201): lane per 32-weight block, 64 blocks
+// per pass, sumf += sumi * (f16(d) * y.d) in block order.
+__device__ __forceinline__ float q80_row(const uint8_t* __restrict__ row, int nb, const rv_block_q8_0* __restrict__ acts,
+                                         int lane) {
+#pragma clang fp contract(off)
+  float sumf = 0.f;
+  for (int b0 = 0; b0 < nb; b0 += 64) {
+    const int b = min(b0 + lane, nb - 1);
+    const uint8_t* blk = row + (size_t)b * 34;
+    uint32_t w[8];
+    load32_a2(blk + 2, w);
+    const int* a = reinterpret_cast<const int*>(acts[b].qs);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s = dot4(w[k], a[k], s);
+    const float c = (float)s * (f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk)) * acts[b].d);
+    const int n = min(64, nb - b0);
+    for (int k = 0; k < n; ++k) sumf += lane_f(c, k);
+  }
+  return sumf;
+}
+
+__device__ __forceinline__ float row_dot(uint32_t fmt, const uint8_t* row, int nb, const void* acts, int lane) {
+  switch (fmt) {
+    case RV_QF_Q4_K: return kq_row<RV_QF_Q4_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    case RV_QF_Q5_K: return kq_row<RV_QF_Q5_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    case RV_QF_Q6_K: return kq_row<RV_QF_Q6_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    default: return q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
+  }
+}
+
+constexpr int kRowsPerWG = 4;
+
+// out[i] = row(row_lo + i) . acts for i < n_rows; one wave per row.
+template <int FMT>
+__global__ __launch_bounds__(64 * kRowsPerWG) void gemv_rows_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                                    int nb, const void* __restrict__ acts, long row_lo,
+                                                                    int n_rows, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int i = (int)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
+  if (i >= n_rows) return;  // wave-uniform
+  const uint8_t* row = w + (size_t)(row_lo + i) * row_bytes;
+  float v;
+  if constexpr (FMT == RV_QF_Q8_0)
+    v = q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
+  else
+    v = kq_row<FMT>(row, nb, (const rv_block_q8_k*)acts, lane);
+  if (lane == 0) out[i] = v;
+}
+
+// The attention-input projections as one row space: rows [0, n_q) of Wq,
+// then [0, n_kv) of Wk, then of Wv, each against its own activation row.
+__global__ __launch_bounds__(64 * kRowsPerWG) void in_proj_kernel(InProjArgs a) {
+  const int lane = threadIdx.x & 63;
+  int i = (int)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
+  int seg = 0;
+  if (i >= a.n_rows[0]) {
+    i -= a.n_rows[0];
+    seg = 1;
+    if (i >= a.n_rows[1]) {
+      i -= a.n_rows[1];
+      seg = 2;
+      if (i >= a.n_rows[2]) return;
+    }
+  }
+  const InProjSeg& s = a.seg[seg];
+  const float v = row_dot(s.fmt, s.w + (size_t)i * s.row_bytes, s.nb, s.acts, lane);
+  if (lane == 0) s.out[i] = v;
+}
+
+// quantize_row_q8_k (quantize.rs:71-106): one wave per block, lane l holds
+// values 4l .. 4l+3.
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x, rv_block_q8_k* __restrict__ out,
+                                                           int n_blocks) {
+  const int lane = threadIdx.x & 63;
+  const int b = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= n_blocks) return;
+  const float* xs = x + (size_t)b * 256 + 4 * lane;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = xs[e];
+  // First value of largest magnitude: per lane in order, then across lanes
+  // by (magnitude, lowest index). Magnitudes of 0 (and NaN) never win,
+  // as `av > amax` from amax = 0 never takes them.
+  float amax = 0.f, mx = 0.f;
+  int idx = 1 << 30;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float av = fabsf(v[e]);
+    if (av > amax) {
+      amax = av;
+      mx = v[e];
+      idx = 4 * lane + e;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float a2 = __shfl_xor(amax, off, 64), m2 = __shfl_xor(mx, off, 64);
+    const int i2 = __shfl_xor(idx, off, 64);
+    if (a2 > amax || (a2 == amax && i2 < idx)) {
+      amax = a2;
+      mx = m2;
+      idx = i2;
+    }
+  }
+  rv_block_q8_k* blk = out + b;
+  if (amax == 0.f) {
+    *reinterpret_cast<uint32_t*>(blk->qs + 4 * lane) = 0u;
+    if (lane < 16) blk->bsums[lane] = 0;
+    if (lane == 0) blk->d = 0.f;
+    return;
+  }
+  const float iscale = -127.f / mx;
+  uint32_t packed = 0;
+  int gsum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int n = min(max((int)__builtin_rintf(iscale * v[e]), -128), 127);
+    packed |= (uint32_t)(n & 0xFF) << (8 * e);
+    gsum += n;
+  }
+  *reinterpret_cast<uint32_t*>(blk->qs + 4 * lane) = packed;
+  // bsums[g]: the 16 values of lanes 4g .. 4g+3.
+  gsum += __shfl_xor(gsum, 1, 64);
+  gsum += __shfl_xor(gsum, 2, 64);
+  if ((lane & 3) == 0) blk->bsums[lane >> 2] = (int16_t)gsum;
+  if (lane == 0) blk->d = 1.f / iscale;
+}
+
+// quantize_row_q8_0 (quantize.rs:37-55): 32 lanes per block.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x, rv_block_q8_0* __restrict__ out,
+                                                           int n_blocks) {
+  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const int b = t >> 5, i = t & 31;
+  if (b >= n_blocks) return;  // whole 32-lane halves
+  const float v = x[(size_t)b * 32 + i];
+  float amax = fabsf(v);
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const float d = amax / 127.f;
+  const float id = d != 0.f ? 1.f / d : 0.f;
+  out[b].qs[i] = (int8_t)roundf(v * id);
+  if (i == 0) out[b].d = (float)(_Float16)d;
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = 0.f;
+}
+
+template <int FMT>
+void launch_rows_t(const uint8_t* w, size_t row_bytes, int nb, const void* acts, size_t row_lo, size_t n_rows,
+                   float* out, hipStream_t s) {
+  const unsigned grid = (unsigned)((n_rows + kRowsPerWG - 1) / kRowsPerWG);
+  hipLaunchKernelGGL((gemv_rows_kernel<FMT>), dim3(grid), dim3(64 * kRowsPerWG), 0, s, w, row_bytes, nb, acts,
+                     (long)row_lo, (int)n_rows, out);
+}
+
+}  // namespace
+
+HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s) {
+  HipStatus st;
+  if (n_blocks == 0) return st;
+  hipLaunchKernelGGL(quantize_q8_k_kernel, dim3((unsigned)((n_blocks + 3) / 4)), dim3(256), 0, s, x, out,
+                     (int)n_blocks);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "quantize_q8_k launch";
+  return st;
+}
+
+HipStatus launch_quantize_q8_0(const float* x, rv_block_q8_0* out, size_t n_blocks, hipStream_t s) {
+  HipStatus st;
+  if (n_blocks == 0) return st;
+  hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)((n_blocks * 32 + 255) / 256)), dim3(256), 0, s, x, out,
+                     (int)n_blocks);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "quantize_q8_0 launch";
+  return st;
+}
+
+HipStatus launch_gemv_rows(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
+                           size_t row_lo, size_t n_rows, float* out, hipStream_t s) {
+  HipStatus st;
+  if (n_rows == 0 || in_dim == 0) return st;
+  const int nb = (int)(in_dim / (fmt == RV_QF_Q8_0 ? 32 : 256));
+  switch (fmt) {
+    case RV_QF_Q4_K: launch_rows_t<RV_QF_Q4_K>(w, row_bytes, nb, acts, row_lo, n_rows, out, s); break;
+    case RV_QF_Q5_K: launch_rows_t<RV_QF_Q5_K>(w, row_bytes, nb, acts, row_lo, n_rows, out, s); break;
+    case RV_QF_Q6_K: launch_rows_t<RV_QF_Q6_K>(w, row_bytes, nb, acts, row_lo, n_rows, out, s); break;
+    default: launch_rows_t<RV_QF_Q8_0>(w, row_bytes, nb, acts, row_lo, n_rows, out, s);
+  }
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "gemv launch";
+  return st;
+}
+
+HipStatus launch_fill_zero(float* out, size_t n, hipStream_t s) {
+  HipStatus st;
+  if (n == 0) return st;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, (long)n);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "fill launch";
+  return st;
+}
+
+HipStatus launch_in_proj(const InProjArgs& a, hipStream_t s) {
+  HipStatus st;
+  const long rows = (long)a.n_rows[0] + a.n_rows[1] + a.n_rows[2];
+  if (rows == 0) return st;
+  hipLaunchKernelGGL(in_proj_kernel, dim3((unsigned)((rows + kRowsPerWG - 1) / kRowsPerWG)), dim3(64 * kRowsPerWG), 0,
+                     s, a);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "in_proj launch";
+  return st;
+}
+
+}  // namespace rv

@@ -13,13 +13,16 @@ from ramvamp_amd import _lib as L
 from ramvamp_amd import synth
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "ramvamp_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def header_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(rv_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(rv_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -46,8 +49,9 @@ def test_library_is_a_gfx950_hip_build():
 def test_version_and_status_names(lib):
     assert lib.rv_abi_version() == 1
     names = {c: lib.rv_status_name(c).decode() for c in (0, 1, 2, 3, 4, 5, 6, 7, 16, 17, 18, 19, 20, 21, 24, 25, 32,
-                                                            33, 34, 35)}
+                                                            33, 34, 35, 40, 41, 42, 43, 44)}
     assert names[0] == "RV_OK" and names[21] == "RV_ATTN_SCRATCH_TOO_SHORT"
+    assert names[44] == "RV_QUANT_UNSUPPORTED_FORMAT"
     assert len(set(names.values())) == len(names)
     assert lib.rv_status_name(999).decode() == "RV_UNKNOWN"
 
@@ -83,3 +87,26 @@ def test_synthetic_generator_is_deterministic_and_standard_normal():
     assert np.array_equal(synth.normal(123, 1001), synth.normal(123, 5000)[:1001])
     w = synth.norm_weight(1, synth.T_QN)
     assert w.shape == (128,) and abs(float(w.mean()) - 1.0) < 0.01
+
+
+def test_quant_geometry_matches_the_oracle(lib):
+    """QuantFormat geometry and row_bytes (quants/mod.rs:75-105) and the
+    projection scratch sizes, host-only entry points."""
+    for fmt in (1, 2, 3, 4, 5, 0, 6):
+        assert lib.rv_quant_block_weights(fmt) == (oracle.quant_block_weights(fmt) if fmt in range(1, 6) else 0)
+        assert lib.rv_quant_block_bytes(fmt) == oracle.quant_block_bytes(fmt)
+    for fmt in (1, 2, 3, 4, 5):
+        for in_dim in (0, 32, 100, 256, 768, 2048, 4096, 4097):
+            n, err = ctypes.c_size_t(), L.RvError()
+            rc = lib.rv_quant_row_bytes(fmt, in_dim, ctypes.byref(n), ctypes.byref(err))
+            try:
+                want = oracle.quant_row_bytes(fmt, in_dim)
+            except oracle.OracleError as e:
+                assert (rc, err.a, err.b, err.c) == e.payload()[:4]
+            else:
+                assert rc == 0 and n.value == want
+    n, err = ctypes.c_size_t(), L.RvError()
+    assert lib.rv_quant_row_bytes(9, 256, ctypes.byref(n), ctypes.byref(err)) == 44
+    assert lib.rv_attn_in_proj_scratch_bytes(2048) == 16 * ((8 * 292 + 15) // 16) + 64 * 36
+    assert lib.rv_attn_out_proj_scratch_bytes(4096) == 16 * 292
+
