@@ -227,6 +227,63 @@ def bench_config5(torch, rv, synth, iters=50, n_caches=5):
             "hbm_frac_kernel": round(byts / k_avg / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": byts}
 
 
+PROJ_SHAPES = {"hidden": 2048, "q_dim": 4096, "kv_dim": 512}
+PROJ_FORMATS = {"q": 1, "k": 4, "v": 3, "o": 2}  # Q4_K q, Q8_0 k, Q6_K v, Q5_K o (the audited model's)
+
+
+def synth_weight_rows(rng, fmt: int, rows: int, in_dim: int) -> np.ndarray:
+    """Random packed rows of `fmt` (every quant byte uniform, f16 scales in
+    [1e-3, 5e-2)): synthetic weights of the real geometry."""
+    bb = {1: 144, 2: 176, 3: 210, 4: 34}[fmt]
+    nb = in_dim // (32 if fmt == 4 else 256)
+    w = rng.integers(0, 256, size=(rows, nb, bb), dtype=np.uint8)
+    offs = {1: (0, 2), 2: (0, 2), 3: (208,), 4: (0,)}[fmt]
+    for off in offs:
+        bits = rng.uniform(1e-3, 5e-2, size=(rows, nb)).astype(np.float16).view(np.uint16)
+        w[:, :, off] = bits & 0xFF
+        w[:, :, off + 1] = bits >> 8
+    return w.reshape(rows, nb * bb)
+
+
+def bench_projections(torch, rv, iters=100, n_sets=24):
+    """The attention projections of one decode layer (model/forward.rs:2574-2646):
+    rv_attn_in_proj (quantize both ways, q/k/v GEMVs) and rv_attn_out_proj,
+    over n_sets distinct layers' weights (300 MB, past the 256 MB MALL), graph
+    replayed; per-layer time and the rate of the weight bytes streamed."""
+    from ramvamp_amd import projections as P
+    H, Q, KV = PROJ_SHAPES["hidden"], PROJ_SHAPES["q_dim"], PROJ_SHAPES["kv_dim"]
+    F = PROJ_FORMATS
+    rng = np.random.default_rng(0x9E0)
+    sets = []
+    for _ in range(n_sets):
+        sets.append({k: torch.from_numpy(synth_weight_rows(rng, F[k], rows, ind).ravel()).cuda()
+                     for k, rows, ind in (("q", Q, H), ("k", KV, H), ("v", KV, H), ("o", H, Q))})
+    wbytes = sum(t.numel() for t in sets[0].values())
+    x = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).cuda()
+    a = torch.from_numpy(rng.standard_normal(Q).astype(np.float32)).cuda()
+    q, k, v = (torch.empty(n, device="cuda") for n in (Q, KV, KV))
+    o = torch.empty(H, device="cuda")
+    s_in = torch.empty(P.attn_in_proj_scratch_bytes(H), dtype=torch.uint8, device="cuda")
+    s_out = torch.empty(P.attn_out_proj_scratch_bytes(Q), dtype=torch.uint8, device="cuda")
+
+    def once():
+        for w in sets:
+            P.attn_in_proj(x, F["q"], w["q"], q, w["k"], k, F["v"], w["v"], v, s_in)
+            P.attn_out_proj(a, F["o"], w["o"], o, s_out)
+
+    for _ in range(3):
+        once()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        once()
+    graph.replay()
+    per = timed(torch, graph.replay, iters) / (iters * n_sets)
+    return {"us_per_layer": round(per * 1e6, 3), "weight_bytes_per_layer": wbytes,
+            "gbs": round(wbytes / per / 1e9, 1), "hbm_frac": round(wbytes / per / 1e9 / HBM_PEAK_GBS, 4),
+            "formats": "q Q4_K 4096x2048, k Q8_0 512x2048, v Q6_K 512x2048, o Q5_K 2048x4096",
+            "launches_per_layer": 5, "distinct_layers": n_sets}
+
+
 def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
     """The oracle (C restatement of ramvamp's AVX2+F16C decode path with its
     kv-head fan-out over min(4, cores) threads, forward.rs:1914-2063) on the
@@ -269,6 +326,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the prefill legs (configs 3 and 4, every mode), log them and exit (for profiling)")
+    ap.add_argument("--projections-only", action="store_true",
+                    help="only run the attention-projection leg, log it and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -292,6 +351,10 @@ def main():
         torch.cuda.synchronize()
         log("copied 10 x 64 MiB")
         return
+    if args.projections_only:
+        rp = bench_projections(torch, rv)
+        log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
+        return
     if args.prefill_only:
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
             r = bench_prefill(torch, rv, synth, cfg, mode)
@@ -313,6 +376,9 @@ def main():
         r5 = bench_config5(torch, rv, synth)
         extra["config5_decode_f16_ctx32768"] = r5
         log(f"config 5: {r5['us_per_call']:.2f} us/call, kernel {r5['us_kernel']:.2f} us, {r5['gbs_kernel']:.0f} GB/s")
+        rp = bench_projections(torch, rv)
+        extra["projections_decode_layer"] = rp
+        log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")

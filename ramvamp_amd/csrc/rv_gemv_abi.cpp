@@ -228,20 +228,32 @@ int32_t rv_attn_in_proj(const float* normed, size_t hidden, uint32_t q_format, c
                              {scratch, "scratch"}})))
     return rc;
   const hipStream_t s = (hipStream_t)stream;
+  if (hidden / 256 <= (size_t)rv::kFusedMaxKBlocks) {
+    // One launch: each workgroup quantizes the normed row into LDS (both
+    // forms, bit-identical to quantize_row_q8_k / _q8_0) and runs its rows;
+    // the quantized row never goes through memory and `scratch` is left
+    // untouched.
+    rv::FusedProjArgs a{};
+    a.x = normed;
+    a.nbk = (int)(hidden / 256);
+    a.nb0 = (int)(hidden / 32);
+    a.n_seg = 3;
+    a.seg[0] = {q_format, wq, rb_q, q};
+    a.seg[1] = {RV_QF_Q8_0, wk, rb_k, k};
+    a.seg[2] = {v_format, wv, rb_v, v};
+    a.n_rows[0] = (int)q_dim;
+    a.n_rows[1] = (int)kv_dim;
+    a.n_rows[2] = (int)kv_dim;
+    return finish(s, flags, rv::launch_fused_proj(a, s), err);
+  }
+  // Wider rows: quantized into `scratch`, then the three GEMVs.
   auto* acts_k = reinterpret_cast<rv_block_q8_k*>(scratch);
   auto* acts_0 = reinterpret_cast<rv_block_q8_0*>((char*)scratch + align16(hidden / 256 * sizeof(rv_block_q8_k)));
   rv::HipStatus st = rv::launch_quantize_q8_k(normed, acts_k, hidden / 256, s);
   if (st.e == hipSuccess) st = rv::launch_quantize_q8_0(normed, acts_0, hidden / 32, s);
-  if (st.e == hipSuccess) {
-    rv::InProjArgs a{};
-    a.seg[0] = {q_format, wq, rb_q, (int)(hidden / 256), acts_k, q};
-    a.seg[1] = {RV_QF_Q8_0, wk, rb_k, (int)(hidden / 32), acts_0, k};
-    a.seg[2] = {v_format, wv, rb_v, (int)(hidden / 256), acts_k, v};
-    a.n_rows[0] = (int)q_dim;
-    a.n_rows[1] = (int)kv_dim;
-    a.n_rows[2] = (int)kv_dim;
-    st = rv::launch_in_proj(a, s);
-  }
+  if (st.e == hipSuccess) st = rv::launch_gemv_rows(q_format, wq, rb_q, hidden, acts_k, 0, q_dim, q, s);
+  if (st.e == hipSuccess) st = rv::launch_gemv_rows(RV_QF_Q8_0, wk, rb_k, hidden, acts_0, 0, kv_dim, k, s);
+  if (st.e == hipSuccess) st = rv::launch_gemv_rows(v_format, wv, rb_v, hidden, acts_k, 0, kv_dim, v, s);
   return finish(s, flags, st, err);
 }
 
@@ -264,6 +276,17 @@ int32_t rv_attn_out_proj(const float* attn_out, size_t q_dim, uint32_t o_format,
   if (q_dim == 0) return fail(err, RV_ERR_UNSUPPORTED, 0, 0, 0, "attn_out_proj with q_dim 0");
   if ((rc = check_ptrs(err, {{attn_out, "attn_out"}, {wo, "wo"}, {o, "o"}, {scratch, "scratch"}}))) return rc;
   const hipStream_t s = (hipStream_t)stream;
+  if (q_dim / 256 <= (size_t)rv::kFusedMaxKBlocks) {
+    // One launch, the activation quantized into LDS per workgroup (as above).
+    rv::FusedProjArgs a{};
+    a.x = attn_out;
+    a.nbk = (int)(q_dim / 256);
+    a.nb0 = (int)(q_dim / 32);
+    a.n_seg = 1;
+    a.seg[0] = {o_format, wo, rb, o};
+    a.n_rows[0] = (int)hidden;
+    return finish(s, flags, rv::launch_fused_proj(a, s), err);
+  }
   auto* acts = reinterpret_cast<rv_block_q8_k*>(scratch);
   rv::HipStatus st = rv::launch_quantize_q8_k(attn_out, acts, q_dim / 256, s);
   if (st.e == hipSuccess) st = rv::launch_gemv_rows(o_format, wo, rb, q_dim, acts, 0, hidden, o, s);

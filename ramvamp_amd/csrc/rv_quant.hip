@@ -79,56 +79,78 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint32_t (&s)[3], int&
   }
 }
 
+// 16 bytes at a 4-byte-aligned global address (global_load_dwordx4 needs
+// only dword alignment).
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+// Lane j's view of one Q8_K activation block: qs[32j .. 32j+31] packed 4
+// per int, the scale d, and bsums[2j], bsums[2j+1].
+struct ActK {
+  int a[8];
+  float d;
+  int bs_lo, bs_hi;
+};
+
+__device__ __forceinline__ ActK act_from_block(const rv_block_q8_k* __restrict__ y, int j) {
+  ActK r;
+  const int* q = reinterpret_cast<const int*>(y->qs + 32 * j);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) r.a[k] = q[k];
+  const uint32_t bs = *reinterpret_cast<const uint32_t*>(y->bsums + 2 * j);
+  r.bs_lo = (int)(int16_t)(bs & 0xFFFFu);
+  r.bs_hi = (int)(int16_t)(bs >> 16);
+  r.d = y->d;
+  return r;
+}
+
 // One super-block's float contribution for the k-quants, computed by the 8
 // lanes of a group, lane j owning sub-block j (Q4_K/Q5_K: 32 weights) or
 // the two 16-weight sub-blocks 2j, 2j+1 (Q6_K); every lane of the group
 // returns the same value.
 template <int FMT>
-__device__ __forceinline__ float kq_block(const uint8_t* __restrict__ blk, const rv_block_q8_k* __restrict__ y,
-                                          int j);
+__device__ __forceinline__ float kq_block(const uint8_t* __restrict__ blk, const ActK& y, int j);
 
 // k_quant_affine_block with the q4_K / q5_K expansions (dot.rs:56-143):
 // d*sumi - dmin*sumi_mins, d = f16(d)*y.d, dmin = f16(dmin)*y.d.
 template <int FMT>
-__device__ __forceinline__ float affine_block(const uint8_t* __restrict__ blk, const rv_block_q8_k* __restrict__ y,
-                                              int j) {
+__device__ __forceinline__ float affine_block(const uint8_t* __restrict__ blk, const ActK& y, int j) {
 #pragma clang fp contract(off)
   constexpr bool kQ5 = FMT == RV_QF_Q5_K;
   const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
   const uint32_t* sp = reinterpret_cast<const uint32_t*>(blk + 4);
   const uint32_t s[3] = {sp[0], sp[1], sp[2]};
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(blk + (kQ5 ? 48 : 16) + 32 * (j >> 1));
-  const int* a = reinterpret_cast<const int*>(y->qs + 32 * j);
+  const u32x4a* qp = reinterpret_cast<const u32x4a*>(blk + (kQ5 ? 48 : 16) + 32 * (j >> 1));
+  const u32x4a q0 = qp[0], q1 = qp[1];
+  const uint32_t q[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
   uint32_t qh[8];
   if constexpr (kQ5) {
-    const uint32_t* h = reinterpret_cast<const uint32_t*>(blk + 16);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) qh[k] = h[k];
+    const u32x4a* hp = reinterpret_cast<const u32x4a*>(blk + 16);
+    const u32x4a h0 = hp[0], h1 = hp[1];
+    qh[0] = h0[0], qh[1] = h0[1], qh[2] = h0[2], qh[3] = h0[3];
+    qh[4] = h1[0], qh[5] = h1[1], qh[6] = h1[2], qh[7] = h1[3];
   }
   int acc = 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     uint32_t w = (j & 1) ? (q[k] >> 4) & 0x0F0F0F0Fu : q[k] & 0x0F0F0F0Fu;
     if constexpr (kQ5) w |= ((qh[k] >> j) & 0x01010101u) << 4;
-    acc = dot4(w, a[k], acc);
+    acc = dot4(w, y.a[k], acc);
   }
   int sc, m;
   scale_min_k4(j, s, sc, m);
-  const uint32_t bs = *reinterpret_cast<const uint32_t*>(y->bsums + 2 * j);
-  const int bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
   const int sumi = sum8_lanes(sc * acc);
-  const int sumi_mins = sum8_lanes(m * bsum);
-  const float d = f16_bits_to_f32(dd) * y->d;
-  const float dmin = f16_bits_to_f32(dd >> 16) * y->d;
+  const int sumi_mins = sum8_lanes(m * (y.bs_lo + y.bs_hi));
+  const float d = f16_bits_to_f32(dd) * y.d;
+  const float dmin = f16_bits_to_f32(dd >> 16) * y.d;
   return d * (float)sumi - dmin * (float)sumi_mins;
 }
 
 template <>
-__device__ __forceinline__ float kq_block<RV_QF_Q4_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+__device__ __forceinline__ float kq_block<RV_QF_Q4_K>(const uint8_t* blk, const ActK& y, int j) {
   return affine_block<RV_QF_Q4_K>(blk, y, j);
 }
 template <>
-__device__ __forceinline__ float kq_block<RV_QF_Q5_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+__device__ __forceinline__ float kq_block<RV_QF_Q5_K>(const uint8_t* blk, const ActK& y, int j) {
   return affine_block<RV_QF_Q5_K>(blk, y, j);
 }
 
@@ -137,35 +159,34 @@ __device__ __forceinline__ float kq_block<RV_QF_Q5_K>(const uint8_t* blk, const 
 // nibble for groups 2, 3) and two qh bits (2 group). The stored values are
 // q + 32 in 0..63; sum (q+32)a - 32 sum a, with sum a the activation bsums.
 template <>
-__device__ __forceinline__ float kq_block<RV_QF_Q6_K>(const uint8_t* blk, const rv_block_q8_k* y, int j) {
+__device__ __forceinline__ float kq_block<RV_QF_Q6_K>(const uint8_t* blk, const ActK& y, int j) {
 #pragma clang fp contract(off)
   const int half = j >> 2, grp = j & 3;
   uint32_t ql[8], qh[8];
   load32_a2(blk + 64 * half + 32 * (grp & 1), ql);
   load32_a2(blk + 128 + 32 * half, qh);
-  const int* a = reinterpret_cast<const int*>(y->qs + 32 * j);
   int lo = 0, hi = 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t nib = (grp >> 1) ? (ql[k] >> 4) & 0x0F0F0F0Fu : ql[k] & 0x0F0F0F0Fu;
     const uint32_t w = nib | (((qh[k] >> (2 * grp)) & 0x03030303u) << 4);
     if (k < 4)
-      lo = dot4(w, a[k], lo);
+      lo = dot4(w, y.a[k], lo);
     else
-      hi = dot4(w, a[k], hi);
+      hi = dot4(w, y.a[k], hi);
   }
-  const uint32_t bs = *reinterpret_cast<const uint32_t*>(y->bsums + 2 * j);
-  lo -= 32 * (int)(int16_t)(bs & 0xFFFFu);
-  hi -= 32 * (int)(int16_t)(bs >> 16);
+  lo -= 32 * y.bs_lo;
+  hi -= 32 * y.bs_hi;
   const uint32_t scp = *reinterpret_cast<const uint16_t*>(blk + 192 + 2 * j);
   const int sc_lo = (int)(int8_t)(scp & 0xFF), sc_hi = (int)(int8_t)(scp >> 8);
   const int sumi = sum8_lanes(sc_lo * lo + sc_hi * hi);
   const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
-  return d * y->d * (float)sumi;
+  return d * y.d * (float)sumi;
 }
 
-// One k-quant row against its activation blocks, every lane returning the
-// row's sum: 8 super-blocks per pass (lane group b), added in block order.
+// One k-quant row against its Q8_K activation blocks (global memory or
+// LDS), every lane returning the row's sum: 8 super-blocks per pass (lane
+// group b), added in block order.
 template <int FMT>
 __device__ __forceinline__ float kq_row(const uint8_t* __restrict__ row, int nb, const rv_block_q8_k* __restrict__ acts,
                                         int lane) {
@@ -174,7 +195,7 @@ __device__ __forceinline__ float kq_row(const uint8_t* __restrict__ row, int nb,
   float sumf = 0.f;
   for (int b0 = 0; b0 < nb; b0 += 8) {
     const int b = min(b0 + bl, nb - 1);  // groups past the row recompute its last block (unused)
-    const float c = kq_block<FMT>(row + (size_t)b * BB, acts + b, j);
+    const float c = kq_block<FMT>(row + (size_t)b * BB, act_from_block(acts + b, j), j);
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (b0 + k < nb) sumf += lane_f(c, 8 * k);
@@ -204,68 +225,15 @@ __device__ __forceinline__ float q80_row(const uint8_t* __restrict__ row, int nb
   return sumf;
 }
 
-__device__ __forceinline__ float row_dot(uint32_t fmt, const uint8_t* row, int nb, const void* acts, int lane) {
-  switch (fmt) {
-    case RV_QF_Q4_K: return kq_row<RV_QF_Q4_K>(row, nb, (const rv_block_q8_k*)acts, lane);
-    case RV_QF_Q5_K: return kq_row<RV_QF_Q5_K>(row, nb, (const rv_block_q8_k*)acts, lane);
-    case RV_QF_Q6_K: return kq_row<RV_QF_Q6_K>(row, nb, (const rv_block_q8_k*)acts, lane);
-    default: return q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
-  }
-}
-
-constexpr int kRowsPerWG = 4;
-
-// out[i] = row(row_lo + i) . acts for i < n_rows; one wave per row.
-template <int FMT>
-__global__ __launch_bounds__(64 * kRowsPerWG) void gemv_rows_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
-                                                                    int nb, const void* __restrict__ acts, long row_lo,
-                                                                    int n_rows, float* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
-  const int i = (int)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
-  if (i >= n_rows) return;  // wave-uniform
-  const uint8_t* row = w + (size_t)(row_lo + i) * row_bytes;
-  float v;
-  if constexpr (FMT == RV_QF_Q8_0)
-    v = q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
-  else
-    v = kq_row<FMT>(row, nb, (const rv_block_q8_k*)acts, lane);
-  if (lane == 0) out[i] = v;
-}
-
-// The attention-input projections as one row space: rows [0, n_q) of Wq,
-// then [0, n_kv) of Wk, then of Wv, each against its own activation row.
-__global__ __launch_bounds__(64 * kRowsPerWG) void in_proj_kernel(InProjArgs a) {
-  const int lane = threadIdx.x & 63;
-  int i = (int)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
-  int seg = 0;
-  if (i >= a.n_rows[0]) {
-    i -= a.n_rows[0];
-    seg = 1;
-    if (i >= a.n_rows[1]) {
-      i -= a.n_rows[1];
-      seg = 2;
-      if (i >= a.n_rows[2]) return;
-    }
-  }
-  const InProjSeg& s = a.seg[seg];
-  const float v = row_dot(s.fmt, s.w + (size_t)i * s.row_bytes, s.nb, s.acts, lane);
-  if (lane == 0) s.out[i] = v;
-}
-
-// quantize_row_q8_k (quantize.rs:71-106): one wave per block, lane l holds
-// values 4l .. 4l+3.
-__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x, rv_block_q8_k* __restrict__ out,
-                                                           int n_blocks) {
-  const int lane = threadIdx.x & 63;
-  const int b = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (b >= n_blocks) return;
-  const float* xs = x + (size_t)b * 256 + 4 * lane;
+// quantize_row_q8_k (quantize.rs:71-106) of one block by one wave, lane l
+// holding values 4l .. 4l+3: the first value of largest magnitude (per lane
+// in order, then across lanes by magnitude and lowest index; magnitudes of
+// 0 and NaN never win, as `av > amax` from amax = 0 never takes them), RNE
+// rounding, the clamp, bsums, and the scalar code's f32 divisions.
+__device__ __forceinline__ void quantize_block_q8_k(const float* __restrict__ xs, rv_block_q8_k* blk, int lane) {
   float v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = xs[e];
-  // First value of largest magnitude: per lane in order, then across lanes
-  // by (magnitude, lowest index). Magnitudes of 0 (and NaN) never win,
-  // as `av > amax` from amax = 0 never takes them.
+  for (int e = 0; e < 4; ++e) v[e] = xs[4 * lane + e];
   float amax = 0.f, mx = 0.f;
   int idx = 1 << 30;
 #pragma unroll
@@ -287,8 +255,7 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restr
       idx = i2;
     }
   }
-  rv_block_q8_k* blk = out + b;
-  if (amax == 0.f) {
+  if (amax == 0.f) {  // wave-uniform
     *reinterpret_cast<uint32_t*>(blk->qs + 4 * lane) = 0u;
     if (lane < 16) blk->bsums[lane] = 0;
     if (lane == 0) blk->d = 0.f;
@@ -311,20 +278,111 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restr
   if (lane == 0) blk->d = 1.f / iscale;
 }
 
-// quantize_row_q8_0 (quantize.rs:37-55): 32 lanes per block.
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x, rv_block_q8_0* __restrict__ out,
-                                                           int n_blocks) {
-  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  const int b = t >> 5, i = t & 31;
-  if (b >= n_blocks) return;  // whole 32-lane halves
-  const float v = x[(size_t)b * 32 + i];
+// quantize_row_q8_0 (quantize.rs:37-55) of one block by the 32 lanes of a
+// half-wave, lane i holding value i: d = amax/127, q = round(v/d) half away
+// from zero, d stored f16-rounded.
+__device__ __forceinline__ void quantize_block_q8_0(const float* __restrict__ xs, rv_block_q8_0* blk, int i) {
+  const float v = xs[i];
   float amax = fabsf(v);
 #pragma unroll
   for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
   const float d = amax / 127.f;
   const float id = d != 0.f ? 1.f / d : 0.f;
-  out[b].qs[i] = (int8_t)roundf(v * id);
-  if (i == 0) out[b].d = (float)(_Float16)d;
+  blk->qs[i] = (int8_t)roundf(v * id);
+  if (i == 0) blk->d = (float)(_Float16)d;
+}
+
+__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* __restrict__ x, rv_block_q8_k* __restrict__ out,
+                                                           int n_blocks) {
+  const int b = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= n_blocks) return;  // wave-uniform
+  quantize_block_q8_k(x + (size_t)b * 256, out + b, threadIdx.x & 63);
+}
+
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x, rv_block_q8_0* __restrict__ out,
+                                                           int n_blocks) {
+  const int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const int b = t >> 5;
+  if (b >= n_blocks) return;  // whole 32-lane halves
+  quantize_block_q8_0(x + (size_t)b * 32, out + b, t & 31);
+}
+
+__device__ __forceinline__ float row_dot(uint32_t fmt, const uint8_t* row, int nb, const void* acts, int lane) {
+  switch (fmt) {
+    case RV_QF_Q4_K: return kq_row<RV_QF_Q4_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    case RV_QF_Q5_K: return kq_row<RV_QF_Q5_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    case RV_QF_Q6_K: return kq_row<RV_QF_Q6_K>(row, nb, (const rv_block_q8_k*)acts, lane);
+    default: return q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
+  }
+}
+
+constexpr int kRowsPerWG = 4;
+
+// out[i] = row(row_lo + i) . acts for i < n_rows, acts quantized blocks in
+// global memory; one wave per row.
+template <int FMT>
+__global__ __launch_bounds__(64 * kRowsPerWG) void gemv_rows_kernel(const uint8_t* __restrict__ w, size_t row_bytes,
+                                                                    int nb, const void* __restrict__ acts, long row_lo,
+                                                                    int n_rows, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int i = (int)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
+  if (i >= n_rows) return;  // wave-uniform
+  const uint8_t* row = w + (size_t)(row_lo + i) * row_bytes;
+  float v;
+  if constexpr (FMT == RV_QF_Q8_0)
+    v = q80_row(row, nb, (const rv_block_q8_0*)acts, lane);
+  else
+    v = kq_row<FMT>(row, nb, (const rv_block_q8_k*)acts, lane);
+  if (lane == 0) out[i] = v;
+}
+
+// The fused projections: one row per wave, 8 waves per workgroup, the f32
+// activation row quantized once per workgroup into LDS first (the same
+// per-block code as the quantizer kernels, so bit-identical), then every
+// wave's GEMV row reads its blocks from LDS. Segments (at most 3) are row
+// ranges of independent matrices, each against the Q8_K or the Q8_0 form.
+__global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjArgs a) {
+  __shared__ rv_block_q8_k lk[kFusedMaxKBlocks];
+  __shared__ rv_block_q8_0 l0[kFusedMax0Blocks];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int first = (int)blockIdx.x * kFusedWaves;
+  // The segments this workgroup's rows touch decide which forms it needs.
+  bool need_k = false, need_0 = false;
+  {
+    int lo = 0;
+    for (int sg = 0; sg < a.n_seg; ++sg) {
+      const int hi = lo + a.n_rows[sg];
+      if (first < hi && first + kFusedWaves > lo) (a.seg[sg].fmt == RV_QF_Q8_0 ? need_0 : need_k) = true;
+      lo = hi;
+    }
+  }
+  int i = first + wave, sg = 0;
+  while (sg < a.n_seg && i >= a.n_rows[sg]) i -= a.n_rows[sg++];
+  // This wave's weight row starts streaming now, while the workgroup
+  // quantizes: one dword from each of its 128-byte lines (lane l: byte
+  // 128 l, clamped to the row and aligned down; the matrix base is 4-byte
+  // aligned, so the address stays inside it). The value is consumed only
+  // after the barrier, so nothing waits for it here.
+  uint32_t touch = 0;
+  if (sg < a.n_seg) {
+    const FusedSeg& s = a.seg[sg];
+    const uint8_t* row = s.w + (size_t)i * s.row_bytes;
+    const size_t off = min((size_t)128 * lane, s.row_bytes - 4);
+    touch = *reinterpret_cast<const uint32_t*>((uintptr_t)(row + off) & ~(uintptr_t)3);
+  }
+  if (need_k)
+    for (int b = wave; b < a.nbk; b += kFusedWaves) quantize_block_q8_k(a.x + (size_t)b * 256, &lk[b], lane);
+  if (need_0)
+    for (int b = 2 * wave + (lane >> 5); b < a.nb0; b += 2 * kFusedWaves)
+      quantize_block_q8_0(a.x + (size_t)b * 32, &l0[b], lane & 31);
+  __syncthreads();
+  asm volatile("" ::"v"(touch));
+  if (sg >= a.n_seg) return;  // wave-uniform
+  const FusedSeg& s = a.seg[sg];
+  const bool q80 = s.fmt == RV_QF_Q8_0;
+  const float v = row_dot(s.fmt, s.w + (size_t)i * s.row_bytes, q80 ? a.nb0 : a.nbk,
+                          q80 ? (const void*)l0 : (const void*)lk, lane);
+  if (lane == 0) s.out[i] = v;
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out, long n) {
@@ -387,14 +445,15 @@ HipStatus launch_fill_zero(float* out, size_t n, hipStream_t s) {
   return st;
 }
 
-HipStatus launch_in_proj(const InProjArgs& a, hipStream_t s) {
+HipStatus launch_fused_proj(const FusedProjArgs& a, hipStream_t s) {
   HipStatus st;
-  const long rows = (long)a.n_rows[0] + a.n_rows[1] + a.n_rows[2];
+  long rows = 0;
+  for (int i = 0; i < a.n_seg; ++i) rows += a.n_rows[i];
   if (rows == 0) return st;
-  hipLaunchKernelGGL(in_proj_kernel, dim3((unsigned)((rows + kRowsPerWG - 1) / kRowsPerWG)), dim3(64 * kRowsPerWG), 0,
-                     s, a);
+  hipLaunchKernelGGL(fused_proj_kernel, dim3((unsigned)((rows + kFusedWaves - 1) / kFusedWaves)),
+                     dim3(64 * kFusedWaves), 0, s, a);
   st.e = hipGetLastError();
-  if (st.e != hipSuccess) st.what = "in_proj launch";
+  if (st.e != hipSuccess) st.what = "fused projection launch";
   return st;
 }
 

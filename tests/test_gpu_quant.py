@@ -214,3 +214,35 @@ def test_gemv_errors_match_the_oracle_and_write_nothing():
     with pytest.raises(rv.KernelError) as e:
         P.quantize_row_q8_k(torch.zeros(100, device="cuda"), P.q8_k_buffer(1))
     assert e.value.variant == "QuantizeLenMismatch" and e.value.fields["floats"] == 100
+
+
+def test_projections_quantize_in_the_wave_like_the_quantizers():
+    """The fused projections quantize each activation block inside the GEMV
+    wave; on rows built to stress the quantizers (a zero block, magnitude
+    ties of both signs in different lanes, one huge value, exact halves) the
+    outputs stay bit-identical to the oracle's quantize-then-GEMV."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(0xF0)
+    hidden, q_dim, kv_dim = 1024, 256, 64
+    x = rng.standard_normal(hidden).astype(F32)
+    x[0:256] = 0.0                      # a zero Q8_K block (and eight zero Q8_0 blocks)
+    x[256 + 3], x[256 + 200] = -2.5, 2.5  # tie across lanes: the first (negative) one anchors
+    x[256 + 100] = 2.5
+    x[512:768] = np.round(x[512:768] * 2) / 2  # exact halves
+    x[800] = 3e4
+    wq = random_weight_rows(oracle.RV_QF_Q4_K, q_dim, hidden, rng)
+    wk = random_weight_rows(oracle.RV_QF_Q8_0, kv_dim, hidden, rng)
+    wv = random_weight_rows(oracle.RV_QF_Q6_K, kv_dim, hidden, rng)
+    wo = random_weight_rows(oracle.RV_QF_Q5_K, kv_dim, hidden, rng)
+    acts_k, acts_0 = oracle.quantize_row_q8_k(x), oracle.quantize_row_q8_0(x)
+    q = torch.empty(q_dim, device="cuda")
+    k = torch.empty(kv_dim, device="cuda")
+    v = torch.empty(kv_dim, device="cuda")
+    P.attn_in_proj(f32(torch, x), oracle.RV_QF_Q4_K, u8(torch, wq), q, u8(torch, wk), k, oracle.RV_QF_Q6_K,
+                   u8(torch, wv), v)
+    assert q.cpu().numpy().tobytes() == oracle.gemv(oracle.RV_QF_Q4_K, wq, hidden, q_dim, acts_k).tobytes()
+    assert k.cpu().numpy().tobytes() == oracle.gemv(oracle.RV_QF_Q8_0, wk, hidden, kv_dim, acts_0).tobytes()
+    assert v.cpu().numpy().tobytes() == oracle.gemv(oracle.RV_QF_Q6_K, wv, hidden, kv_dim, acts_k).tobytes()
+    o = torch.empty(kv_dim, device="cuda")
+    P.attn_out_proj(f32(torch, x), oracle.RV_QF_Q5_K, u8(torch, wo), o)
+    assert o.cpu().numpy().tobytes() == oracle.gemv(oracle.RV_QF_Q5_K, wo, hidden, kv_dim, acts_k).tobytes()
