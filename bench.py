@@ -317,6 +317,35 @@ def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
     }
 
 
+def cpu_projections(budget_s=4.0):
+    """The oracle's scalar projections (quantize both ways, the q/k/v GEMVs,
+    quantize, the o GEMV; kernels/quants/dot.rs, one thread) at the bench
+    shapes, timed on this host for a bounded number of layers."""
+    import oracle
+    H, Q, KV = PROJ_SHAPES["hidden"], PROJ_SHAPES["q_dim"], PROJ_SHAPES["kv_dim"]
+    F = PROJ_FORMATS
+    rng = np.random.default_rng(0x9E0)
+    w = {k: synth_weight_rows(rng, F[k], rows, ind) for k, rows, ind in (("q", Q, H), ("k", KV, H), ("v", KV, H),
+                                                                          ("o", H, Q))}
+    wbytes = sum(a.size for a in w.values())
+    x = rng.standard_normal(H).astype(np.float32)
+    a = rng.standard_normal(Q).astype(np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        ak, a0 = oracle.quantize_row_q8_k(x), oracle.quantize_row_q8_0(x)
+        oracle.gemv(F["q"], w["q"], H, Q, ak)
+        oracle.gemv(F["k"], w["k"], H, KV, a0)
+        oracle.gemv(F["v"], w["v"], H, KV, ak)
+        oracle.gemv(F["o"], w["o"], Q, H, oracle.quantize_row_q8_k(a))
+        times.append(time.perf_counter() - t0)
+    per = float(np.median(times))
+    return {"value": round(wbytes / per / 1e9, 3), "unit": "GB/s of weights", "cores": 1, "kind": "port",
+            "us_per_layer": round(per * 1e6, 1),
+            "sample": f"{len(times)} layers' projections (one weight set), median; oracle scalar dots, one thread"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -383,6 +412,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         cpu = cpu_baseline(synth)
+        if "projections_decode_layer" in extra:
+            extra["projections_decode_layer"]["cpu_baseline"] = cpu_projections()
     traffic = traffic_from_profile(DECODE_PROFILE)
     line = {
         "metric": "decode attn µs/layer + HBM GB/s at ctx 4096; prefill attn TFLOP/s (512 tok)",
