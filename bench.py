@@ -281,7 +281,53 @@ def bench_projections(torch, rv, iters=100, n_sets=24):
     return {"us_per_layer": round(per * 1e6, 3), "weight_bytes_per_layer": wbytes,
             "gbs": round(wbytes / per / 1e9, 1), "hbm_frac": round(wbytes / per / 1e9 / HBM_PEAK_GBS, 4),
             "formats": "q Q4_K 4096x2048, k Q8_0 512x2048, v Q6_K 512x2048, o Q5_K 2048x4096",
-            "launches_per_layer": 5, "distinct_layers": n_sets}
+            "launches_per_layer": 2, "distinct_layers": n_sets}
+
+
+def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
+    """One token's attention blocks over config 2's 48 layers (ctx 4096, fp32
+    KV): rv_attn_block_decode per layer (model/forward.rs:2570-2650: RMSNorm,
+    q/k/v projections, QK norm + RoPE, append, attention, output projection,
+    residual add), n_sets distinct layers' weights, one captured graph per
+    token replayed (each replay re-appends the token at the captured cursor
+    and attends 4096 + 3 positions)."""
+    from ramvamp_amd import block as B
+    H, Q, KV = PROJ_SHAPES["hidden"], PROJ_SHAPES["q_dim"], PROJ_SHAPES["kv_dim"]
+    F = PROJ_FORMATS
+    rng = np.random.default_rng(0xB10C)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    sets = []
+    for _ in range(n_sets):
+        sets.append(B.AttnBlockWeights(
+            d((1 + 0.02 * rng.standard_normal(H)).astype(np.float32)), F["q"], d(synth_weight_rows(rng, F["q"], Q, H)),
+            d(synth_weight_rows(rng, F["k"], KV, H)), F["v"], d(synth_weight_rows(rng, F["v"], KV, H)),
+            d(synth.norm_weight(2, synth.T_QN)), d(synth.norm_weight(2, synth.T_KN)), F["o"],
+            d(synth_weight_rows(rng, F["o"], H, Q))))
+    kv = rv.KvCache(n_layers, 4, 128, 4096 + 8, "f32")
+    for layer in range(n_layers):
+        K, V = synth.cached_kv(2, layer, 4096)
+        kv.append_rows(layer, K, V)
+    residual = d(rng.standard_normal(H).astype(np.float32))
+    scratch = torch.empty(B.scratch_bytes(H, Q, KV), dtype=torch.uint8, device="cuda")
+    scale = float(synth.SCALE)
+
+    def token():
+        for layer in range(n_layers):
+            B.attn_block_decode(kv, layer, residual, Q, sets[layer % n_sets], synth.EPS, synth.THETA,
+                                kv.len(layer), scale, scratch=scratch)
+
+    for _ in range(2):
+        token()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        token()
+    graph.replay()
+    per = timed(torch, graph.replay, iters) / (iters * n_layers)
+    wbytes = sum(t.numel() for t in (sets[0].wq, sets[0].wk, sets[0].wv, sets[0].wo))
+    kv_bytes = 2 * 4099 * 512 * 4
+    return {"us_per_layer": round(per * 1e6, 3), "ms_per_token_48_layers": round(per * n_layers * 1e3, 3),
+            "bytes_per_layer": wbytes + kv_bytes, "gbs": round((wbytes + kv_bytes) / per / 1e9, 1),
+            "launches_per_layer": 5, "distinct_weight_sets": n_sets, "context": 4099}
 
 
 def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
@@ -357,6 +403,8 @@ def main():
                     help="only run the prefill legs (configs 3 and 4, every mode), log them and exit (for profiling)")
     ap.add_argument("--projections-only", action="store_true",
                     help="only run the attention-projection leg, log it and exit (for profiling)")
+    ap.add_argument("--block-only", action="store_true",
+                    help="only run the attention-block leg (48 layers, ctx 4096), log it and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -384,6 +432,10 @@ def main():
         rp = bench_projections(torch, rv)
         log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
         return
+    if args.block_only:
+        rb = bench_attn_block(torch, rv, synth)
+        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        return
     if args.prefill_only:
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
             r = bench_prefill(torch, rv, synth, cfg, mode)
@@ -408,6 +460,9 @@ def main():
         rp = bench_projections(torch, rv)
         extra["projections_decode_layer"] = rp
         log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
+        rb = bench_attn_block(torch, rv, synth)
+        extra["attn_block_decode_layer"] = rb
+        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")

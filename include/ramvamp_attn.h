@@ -57,6 +57,7 @@ extern "C" {
 /* Primitive errors of the fused prologue (kernels/primitives/error.rs). */
 #define RV_PRIM_INVALID_HEAD_DIM 24   /* a head_dim (rope needs it even, nonzero) */
 #define RV_PRIM_LENGTH_MISMATCH 25    /* what, a left, b right */
+#define RV_PRIM_EMPTY 26              /* what (an empty row to normalize) */
 /* Errors of this library with no reference counterpart. */
 #define RV_ERR_NULL_ARG 32            /* what argument */
 #define RV_ERR_UNSUPPORTED 33         /* what, a value */

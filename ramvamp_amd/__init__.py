@@ -1,10 +1,11 @@
 """ramvamp_amd — MI355X-native (gfx950) GQA attention hot path of ramvamp.
 
 The product is ``libramvamp_attn.so`` (hand-written HIP kernels behind the C
-ABI in include/ramvamp_attn.h and include/ramvamp_gemv.h). This package
+ABI in include/ramvamp_attn.h, ramvamp_gemv.h and ramvamp_block.h). This package
 builds it (``build``), loads it (``_lib``), mirrors the reference's Rust
 attention API (``attention``) and quantized projections (``projections``)
-over it, and makes seeded synthetic inputs (``synth``).
+over it, one layer's attention block as a single device call (``block``),
+and makes seeded synthetic inputs (``synth``).
 """
 from .attention import (  # noqa: F401
     AttentionError,
@@ -36,4 +37,4 @@ from ._lib import (  # noqa: F401  (knobs of KvCache.set_tuning)
     RV_TUNE_PREFILL_KV_SPLIT,
     RV_TUNE_PREFILL_ROWS,
 )
-from . import projections  # noqa: F401,E402
+from . import block, projections  # noqa: F401,E402

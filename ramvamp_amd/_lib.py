@@ -41,6 +41,14 @@ class RvError(ctypes.Structure):
                 ("what", c_char_p)]
 
 
+class RvAttnBlockWeights(ctypes.Structure):
+    """rv_attn_block_weights (include/ramvamp_block.h)."""
+    _fields_ = [("attn_norm", c_void_p), ("q_format", c_uint32), ("wq", c_void_p), ("wq_len", c_size_t),
+                ("wk", c_void_p), ("wk_len", c_size_t), ("v_format", c_uint32), ("wv", c_void_p),
+                ("wv_len", c_size_t), ("q_norm", c_void_p), ("k_norm", c_void_p), ("o_format", c_uint32),
+                ("wo", c_void_p), ("wo_len", c_size_t)]
+
+
 # Every symbol include/*.h declares: name -> (restype, argtypes).
 _E = POINTER(RvError)
 _P = c_void_p
@@ -104,6 +112,9 @@ SIGNATURES = {
     "rv_attn_out_proj_scratch_bytes": (c_size_t, [c_size_t]),
     "rv_attn_out_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32,
                                    _E]),
+    "rv_attn_block_scratch_bytes": (c_size_t, [c_size_t, c_size_t, c_size_t]),
+    "rv_attn_block_decode": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, POINTER(RvAttnBlockWeights), c_float,
+                                       c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
 }
 
 _lib = None

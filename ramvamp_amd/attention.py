@@ -43,6 +43,7 @@ _VARIANTS = {
     21: ("AttentionError", "ScratchTooShort", ("len", "need")),
     24: ("PrimitiveError", "InvalidHeadDim", ("head_dim",)),
     25: ("PrimitiveError", "LengthMismatch", ("left", "right")),
+    26: ("PrimitiveError", "Empty", ()),
     32: ("DeviceError", "NullArgument", ()),
     33: ("DeviceError", "Unsupported", ("value",)),
     34: ("DeviceError", "Hip", ("hip_error",)),

@@ -212,6 +212,21 @@ int32_t check_rope_dim(const rv_kv* kv, rv_error* err) {
 
 namespace rv {
 
+int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err) {
+  // rv_decode_step's checks, in its order, for k, v and out of the sizes the
+  // cache and q imply (the composite callers own those buffers).
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  int32_t rc = check_rope_dim(kv, err);
+  if (rc) return rc;
+  const size_t hd = kv->head_dim;
+  if (q_len == 0 || q_len % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_len, hd);
+  if ((q_len / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_len / hd, kv->n_kv_heads);
+  if ((rc = check_layer(kv, layer, err))) return rc;
+  if (kv->lens[layer] == kv->capacity) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
+  if (position > 0xFFFFFFFFull) return fail(err, RV_ERR_UNSUPPORTED, position, 0, 0, 0, "position past u32");
+  return RV_OK;
+}
+
 constexpr size_t kMaxTimedPairs = 4096;  // pairs held before they are folded
 
 bool capturing(hipStream_t s) {
@@ -311,6 +326,7 @@ const char* rv_status_name(int32_t code) {
     case RV_ATTN_SCRATCH_TOO_SHORT: return "RV_ATTN_SCRATCH_TOO_SHORT";
     case RV_PRIM_INVALID_HEAD_DIM: return "RV_PRIM_INVALID_HEAD_DIM";
     case RV_PRIM_LENGTH_MISMATCH: return "RV_PRIM_LENGTH_MISMATCH";
+    case RV_PRIM_EMPTY: return "RV_PRIM_EMPTY";
     case RV_ERR_NULL_ARG: return "RV_ERR_NULL_ARG";
     case RV_ERR_UNSUPPORTED: return "RV_ERR_UNSUPPORTED";
     case RV_ERR_HIP: return "RV_ERR_HIP";

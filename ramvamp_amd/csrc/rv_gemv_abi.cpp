@@ -196,30 +196,15 @@ int32_t rv_gemv_q8_0(const uint8_t* weight, size_t weight_len, size_t in_dim, si
                            flags, err);
 }
 
-size_t rv_attn_in_proj_scratch_bytes(size_t hidden) {
-  return align16(hidden / 256 * sizeof(rv_block_q8_k)) + hidden / 32 * sizeof(rv_block_q8_0);
-}
+size_t rv_attn_in_proj_scratch_bytes(size_t hidden) { return rv::in_proj_scratch_bytes(hidden, false); }
 
 int32_t rv_attn_in_proj(const float* normed, size_t hidden, uint32_t q_format, const uint8_t* wq, size_t wq_len,
                         float* q, size_t q_dim, const uint8_t* wk, size_t wk_len, float* k, size_t kv_dim,
                         uint32_t v_format, const uint8_t* wv, size_t wv_len, float* v, void* scratch,
                         size_t scratch_len, void* stream, uint32_t flags, rv_error* err) {
-  // forward.rs:2576-2612 in order: both quantizations, then q, k, v.
+  rv::InProj p{normed, nullptr, 0.f, hidden, q_format, wq, 0, q, q_dim, wk, 0, k, kv_dim, v_format, wv, 0, v, scratch};
   int32_t rc;
-  if ((rc = check_quantize(RV_QF_Q8_K, hidden, hidden / 256, err))) return rc;
-  if ((rc = check_quantize(RV_QF_Q8_0, hidden, hidden / 32, err))) return rc;
-  if (!k_quant(q_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, q_format, 0, 0, "attn_in_proj q");
-  size_t rb_q, rb_k, rb_v;
-  if ((rc = check_gemv("attn_in_proj q: weight bytes vs rows / out vs range", q_format, wq_len, hidden, q_dim,
-                       hidden / 256, 0, q_dim, q_dim, &rb_q, err)))
-    return rc;
-  if ((rc = check_gemv("attn_in_proj k: weight bytes vs rows / out vs range", RV_QF_Q8_0, wk_len, hidden, kv_dim,
-                       hidden / 32, 0, kv_dim, kv_dim, &rb_k, err)))
-    return rc;
-  if (!k_quant(v_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, v_format, 0, 0, "attn_in_proj v");
-  if ((rc = check_gemv("attn_in_proj v: weight bytes vs rows / out vs range", v_format, wv_len, hidden, kv_dim,
-                       hidden / 256, 0, kv_dim, kv_dim, &rb_v, err)))
-    return rc;
+  if ((rc = rv::in_proj_check(p, wq_len, wk_len, wv_len, err))) return rc;
   const size_t need = rv_attn_in_proj_scratch_bytes(hidden);
   if (scratch_len < need) return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, 0, "attn_in_proj scratch");
   if ((rc = check_flags(flags, err))) return rc;
@@ -228,69 +213,126 @@ int32_t rv_attn_in_proj(const float* normed, size_t hidden, uint32_t q_format, c
                              {scratch, "scratch"}})))
     return rc;
   const hipStream_t s = (hipStream_t)stream;
-  if (hidden / 256 <= (size_t)rv::kFusedMaxKBlocks) {
-    // One launch: each workgroup quantizes the normed row into LDS (both
-    // forms, bit-identical to quantize_row_q8_k / _q8_0) and runs its rows;
-    // the quantized row never goes through memory and `scratch` is left
-    // untouched.
-    rv::FusedProjArgs a{};
-    a.x = normed;
-    a.nbk = (int)(hidden / 256);
-    a.nb0 = (int)(hidden / 32);
-    a.n_seg = 3;
-    a.seg[0] = {q_format, wq, rb_q, q};
-    a.seg[1] = {RV_QF_Q8_0, wk, rb_k, k};
-    a.seg[2] = {v_format, wv, rb_v, v};
-    a.n_rows[0] = (int)q_dim;
-    a.n_rows[1] = (int)kv_dim;
-    a.n_rows[2] = (int)kv_dim;
-    return finish(s, flags, rv::launch_fused_proj(a, s), err);
-  }
-  // Wider rows: quantized into `scratch`, then the three GEMVs.
-  auto* acts_k = reinterpret_cast<rv_block_q8_k*>(scratch);
-  auto* acts_0 = reinterpret_cast<rv_block_q8_0*>((char*)scratch + align16(hidden / 256 * sizeof(rv_block_q8_k)));
-  rv::HipStatus st = rv::launch_quantize_q8_k(normed, acts_k, hidden / 256, s);
-  if (st.e == hipSuccess) st = rv::launch_quantize_q8_0(normed, acts_0, hidden / 32, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_rows(q_format, wq, rb_q, hidden, acts_k, 0, q_dim, q, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_rows(RV_QF_Q8_0, wk, rb_k, hidden, acts_0, 0, kv_dim, k, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_rows(v_format, wv, rb_v, hidden, acts_k, 0, kv_dim, v, s);
-  return finish(s, flags, st, err);
+  return finish(s, flags, rv::in_proj_launch(p, s), err);
 }
 
-size_t rv_attn_out_proj_scratch_bytes(size_t q_dim) { return q_dim / 256 * sizeof(rv_block_q8_k); }
+size_t rv_attn_out_proj_scratch_bytes(size_t q_dim) { return rv::out_proj_scratch_bytes(q_dim, 0, false); }
 
 int32_t rv_attn_out_proj(const float* attn_out, size_t q_dim, uint32_t o_format, const uint8_t* wo, size_t wo_len,
                          float* o, size_t hidden, void* scratch, size_t scratch_len, void* stream, uint32_t flags,
                          rv_error* err) {
-  // forward.rs:2630-2646: quantize_row_q8_k(attn_out), then the o_proj GEMV.
+  rv::OutProj p{attn_out, q_dim, o_format, wo, 0, o, hidden, false, scratch};
   int32_t rc;
-  if ((rc = check_quantize(RV_QF_Q8_K, q_dim, q_dim / 256, err))) return rc;
-  if (!k_quant(o_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, o_format, 0, 0, "attn_out_proj");
-  size_t rb;
-  if ((rc = check_gemv("attn_out_proj: weight bytes vs rows / out vs range", o_format, wo_len, q_dim, hidden,
-                       q_dim / 256, 0, hidden, hidden, &rb, err)))
-    return rc;
+  if ((rc = rv::out_proj_check(p, wo_len, err))) return rc;
   const size_t need = rv_attn_out_proj_scratch_bytes(q_dim);
   if (scratch_len < need) return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, 0, "attn_out_proj scratch");
   if ((rc = check_flags(flags, err))) return rc;
   if (q_dim == 0) return fail(err, RV_ERR_UNSUPPORTED, 0, 0, 0, "attn_out_proj with q_dim 0");
   if ((rc = check_ptrs(err, {{attn_out, "attn_out"}, {wo, "wo"}, {o, "o"}, {scratch, "scratch"}}))) return rc;
   const hipStream_t s = (hipStream_t)stream;
-  if (q_dim / 256 <= (size_t)rv::kFusedMaxKBlocks) {
-    // One launch, the activation quantized into LDS per workgroup (as above).
-    rv::FusedProjArgs a{};
-    a.x = attn_out;
-    a.nbk = (int)(q_dim / 256);
-    a.nb0 = (int)(q_dim / 32);
-    a.n_seg = 1;
-    a.seg[0] = {o_format, wo, rb, o};
-    a.n_rows[0] = (int)hidden;
-    return finish(s, flags, rv::launch_fused_proj(a, s), err);
-  }
-  auto* acts = reinterpret_cast<rv_block_q8_k*>(scratch);
-  rv::HipStatus st = rv::launch_quantize_q8_k(attn_out, acts, q_dim / 256, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_rows(o_format, wo, rb, q_dim, acts, 0, hidden, o, s);
-  return finish(s, flags, st, err);
+  return finish(s, flags, rv::out_proj_launch(p, s), err);
 }
 
 }  // extern "C"
+
+namespace rv {
+
+size_t in_proj_scratch_bytes(size_t hidden, bool norm) {
+  // Rows past the fused limit: the Q8_K and Q8_0 forms of the row (and, with
+  // the norm, the normalized row before them).
+  const size_t acts = align16(hidden / 256 * sizeof(rv_block_q8_k)) + align16(hidden / 32 * sizeof(rv_block_q8_0));
+  return acts + (norm ? hidden * sizeof(float) : 0);
+}
+
+size_t out_proj_scratch_bytes(size_t q_dim, size_t hidden, bool add) {
+  return align16(q_dim / 256 * sizeof(rv_block_q8_k)) + (add ? hidden * sizeof(float) : 0);
+}
+
+int32_t in_proj_check(InProj& p, size_t wq_len, size_t wk_len, size_t wv_len, rv_error* err) {
+  // forward.rs:2576-2612 in order: both quantizations, then q, k, v.
+  int32_t rc;
+  if ((rc = check_quantize(RV_QF_Q8_K, p.hidden, p.hidden / 256, err))) return rc;
+  if ((rc = check_quantize(RV_QF_Q8_0, p.hidden, p.hidden / 32, err))) return rc;
+  if (!k_quant(p.q_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.q_format, 0, 0, "attn_in_proj q");
+  if ((rc = check_gemv("attn_in_proj q: weight bytes vs rows / out vs range", p.q_format, wq_len, p.hidden, p.q_dim,
+                       p.hidden / 256, 0, p.q_dim, p.q_dim, &p.rb_q, err)))
+    return rc;
+  if ((rc = check_gemv("attn_in_proj k: weight bytes vs rows / out vs range", RV_QF_Q8_0, wk_len, p.hidden, p.kv_dim,
+                       p.hidden / 32, 0, p.kv_dim, p.kv_dim, &p.rb_k, err)))
+    return rc;
+  if (!k_quant(p.v_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.v_format, 0, 0, "attn_in_proj v");
+  return check_gemv("attn_in_proj v: weight bytes vs rows / out vs range", p.v_format, wv_len, p.hidden, p.kv_dim,
+                    p.hidden / 256, 0, p.kv_dim, p.kv_dim, &p.rb_v, err);
+}
+
+int32_t out_proj_check(OutProj& p, size_t wo_len, rv_error* err) {
+  // forward.rs:2630-2646: quantize_row_q8_k(attn_out), then the o_proj GEMV.
+  int32_t rc;
+  if ((rc = check_quantize(RV_QF_Q8_K, p.q_dim, p.q_dim / 256, err))) return rc;
+  if (!k_quant(p.o_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.o_format, 0, 0, "attn_out_proj");
+  return check_gemv("attn_out_proj: weight bytes vs rows / out vs range", p.o_format, wo_len, p.q_dim, p.hidden,
+                    p.q_dim / 256, 0, p.hidden, p.hidden, &p.rb, err);
+}
+
+HipStatus in_proj_launch(const InProj& p, hipStream_t s) {
+  if (p.hidden / 256 <= (size_t)kFusedMaxKBlocks) {
+    // One launch: each workgroup (normalizes and) quantizes the row into LDS
+    // (both forms, bit-identical to quantize_row_q8_k / _q8_0) and runs its
+    // rows; the quantized row never goes through memory and `scratch` is
+    // left untouched.
+    FusedProjArgs a{};
+    a.x = p.x;
+    a.nbk = (int)(p.hidden / 256);
+    a.nb0 = (int)(p.hidden / 32);
+    a.n_seg = 3;
+    a.seg[0] = {p.q_format, p.wq, p.rb_q, p.q, nullptr};
+    a.seg[1] = {RV_QF_Q8_0, p.wk, p.rb_k, p.k, nullptr};
+    a.seg[2] = {p.v_format, p.wv, p.rb_v, p.v, nullptr};
+    a.n_rows[0] = (int)p.q_dim;
+    a.n_rows[1] = (int)p.kv_dim;
+    a.n_rows[2] = (int)p.kv_dim;
+    a.norm_w = p.norm_w;
+    a.eps = p.eps;
+    return launch_fused_proj(a, s);
+  }
+  // Wider rows: (normalized and) quantized into `scratch`, then the GEMVs.
+  auto* acts_k = reinterpret_cast<rv_block_q8_k*>(p.scratch);
+  char* next = (char*)p.scratch + align16(p.hidden / 256 * sizeof(rv_block_q8_k));
+  auto* acts_0 = reinterpret_cast<rv_block_q8_0*>(next);
+  next += align16(p.hidden / 32 * sizeof(rv_block_q8_0));
+  HipStatus st;
+  const float* x = p.x;
+  if (p.norm_w) {
+    float* normed = reinterpret_cast<float*>(next);
+    st = launch_rmsnorm(p.x, p.norm_w, p.eps, p.hidden, normed, s);
+    x = normed;
+  }
+  if (st.e == hipSuccess) st = launch_quantize_q8_k(x, acts_k, p.hidden / 256, s);
+  if (st.e == hipSuccess) st = launch_quantize_q8_0(x, acts_0, p.hidden / 32, s);
+  if (st.e == hipSuccess) st = launch_gemv_rows(p.q_format, p.wq, p.rb_q, p.hidden, acts_k, 0, p.q_dim, p.q, s);
+  if (st.e == hipSuccess) st = launch_gemv_rows(RV_QF_Q8_0, p.wk, p.rb_k, p.hidden, acts_0, 0, p.kv_dim, p.k, s);
+  if (st.e == hipSuccess) st = launch_gemv_rows(p.v_format, p.wv, p.rb_v, p.hidden, acts_k, 0, p.kv_dim, p.v, s);
+  return st;
+}
+
+HipStatus out_proj_launch(const OutProj& p, hipStream_t s) {
+  if (p.q_dim / 256 <= (size_t)kFusedMaxKBlocks) {
+    FusedProjArgs a{};
+    a.x = p.x;
+    a.nbk = (int)(p.q_dim / 256);
+    a.nb0 = (int)(p.q_dim / 32);
+    a.n_seg = 1;
+    a.seg[0] = {p.o_format, p.wo, p.rb, p.o, p.add ? p.o : nullptr};
+    a.n_rows[0] = (int)p.hidden;
+    return launch_fused_proj(a, s);
+  }
+  auto* acts = reinterpret_cast<rv_block_q8_k*>(p.scratch);
+  float* dst = p.add ? reinterpret_cast<float*>((char*)p.scratch + align16(p.q_dim / 256 * sizeof(rv_block_q8_k)))
+                     : p.o;
+  HipStatus st = launch_quantize_q8_k(p.x, acts, p.q_dim / 256, s);
+  if (st.e == hipSuccess) st = launch_gemv_rows(p.o_format, p.wo, p.rb, p.q_dim, acts, 0, p.hidden, dst, s);
+  if (st.e == hipSuccess && p.add) st = launch_vec_add(p.o, dst, p.hidden, s);
+  return st;
+}
+
+}  // namespace rv

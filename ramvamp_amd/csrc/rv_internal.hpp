@@ -158,4 +158,8 @@ HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t row
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
                          size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s);
 
+// rv_decode_step's validation alone (no launch), for callers that validate
+// a whole composite call before launching any of it.
+int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err);
+
 }  // namespace rv

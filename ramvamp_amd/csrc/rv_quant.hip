@@ -341,6 +341,28 @@ __global__ __launch_bounds__(64 * kRowsPerWG) void gemv_rows_kernel(const uint8_
 // per-block code as the quantizer kernels, so bit-identical), then every
 // wave's GEMV row reads its blocks from LDS. Segments (at most 3) are row
 // ranges of independent matrices, each against the Q8_K or the Q8_0 form.
+// 1 / sqrt(mean(x^2) + eps) of n values, as norm.rs:18-26 computes it: the
+// squares summed in f64 (here per thread, then over lanes and waves in a
+// fixed order, so every thread of the workgroup gets the same value), sqrt
+// and reciprocal in f64, rounded once to f32. `red` holds NT / 64 doubles.
+template <int NT>
+__device__ __forceinline__ float block_inv_rms(const float* __restrict__ x, int n, float eps, double* red) {
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const double v = (double)x[i];
+    ss += v * v;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) tot += red[w];
+  return (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+}
+
+template <bool NORM>
 __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjArgs a) {
   __shared__ rv_block_q8_k lk[kFusedMaxKBlocks];
   __shared__ rv_block_q8_0 l0[kFusedMax0Blocks];
@@ -370,11 +392,26 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
     const size_t off = min((size_t)128 * lane, s.row_bytes - 4);
     touch = *reinterpret_cast<const uint32_t*>((uintptr_t)(row + off) & ~(uintptr_t)3);
   }
+  const float* x = a.x;
+  if constexpr (NORM) {
+    // The normalized row, x * inv * w left to right in f32 (norm.rs:55-57),
+    // staged in LDS for the quantizers.
+    __shared__ float xs[kFusedMaxKBlocks * 256];
+    __shared__ double red[kFusedWaves];
+    const int n = a.nbk * 256;
+    const float inv = block_inv_rms<64 * kFusedWaves>(a.x, n, a.eps, red);
+    for (int j = threadIdx.x; j < n; j += 64 * kFusedWaves) {
+#pragma clang fp contract(off)
+      xs[j] = a.x[j] * inv * a.norm_w[j];
+    }
+    __syncthreads();
+    x = xs;
+  }
   if (need_k)
-    for (int b = wave; b < a.nbk; b += kFusedWaves) quantize_block_q8_k(a.x + (size_t)b * 256, &lk[b], lane);
+    for (int b = wave; b < a.nbk; b += kFusedWaves) quantize_block_q8_k(x + (size_t)b * 256, &lk[b], lane);
   if (need_0)
     for (int b = 2 * wave + (lane >> 5); b < a.nb0; b += 2 * kFusedWaves)
-      quantize_block_q8_0(a.x + (size_t)b * 32, &l0[b], lane & 31);
+      quantize_block_q8_0(x + (size_t)b * 32, &l0[b], lane & 31);
   __syncthreads();
   asm volatile("" ::"v"(touch));
   if (sg >= a.n_seg) return;  // wave-uniform
@@ -382,7 +419,22 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
   const bool q80 = s.fmt == RV_QF_Q8_0;
   const float v = row_dot(s.fmt, s.w + (size_t)i * s.row_bytes, q80 ? a.nb0 : a.nbk,
                           q80 ? (const void*)l0 : (const void*)lk, lane);
-  if (lane == 0) s.out[i] = v;
+  if (lane == 0) s.out[i] = s.add ? s.add[i] + v : v;
+}
+
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       float eps, int n, float* __restrict__ out) {
+  __shared__ double red[16];
+  const float inv = block_inv_rms<1024>(x, n, eps, red);
+  for (int j = threadIdx.x; j < n; j += 1024) {
+#pragma clang fp contract(off)
+    out[j] = x[j] * inv * w[j];
+  }
+}
+
+__global__ __launch_bounds__(256) void vec_add_kernel(float* __restrict__ a, const float* __restrict__ b, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) a[i] += b[i];
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ out, long n) {
@@ -450,10 +502,30 @@ HipStatus launch_fused_proj(const FusedProjArgs& a, hipStream_t s) {
   long rows = 0;
   for (int i = 0; i < a.n_seg; ++i) rows += a.n_rows[i];
   if (rows == 0) return st;
-  hipLaunchKernelGGL(fused_proj_kernel, dim3((unsigned)((rows + kFusedWaves - 1) / kFusedWaves)),
-                     dim3(64 * kFusedWaves), 0, s, a);
+  const dim3 grid((unsigned)((rows + kFusedWaves - 1) / kFusedWaves));
+  if (a.norm_w)
+    hipLaunchKernelGGL(fused_proj_kernel<true>, grid, dim3(64 * kFusedWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL(fused_proj_kernel<false>, grid, dim3(64 * kFusedWaves), 0, s, a);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "fused projection launch";
+  return st;
+}
+
+HipStatus launch_rmsnorm(const float* x, const float* w, float eps, size_t n, float* out, hipStream_t s) {
+  HipStatus st;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, s, x, w, eps, (int)n, out);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "rmsnorm launch";
+  return st;
+}
+
+HipStatus launch_vec_add(float* a, const float* b, size_t n, hipStream_t s) {
+  HipStatus st;
+  if (n == 0) return st;
+  hipLaunchKernelGGL(vec_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, (long)n);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "vec_add launch";
   return st;
 }
 

@@ -16,11 +16,16 @@ namespace rv {
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxKBlocks = 32;
 constexpr int kFusedMax0Blocks = kFusedMaxKBlocks * 8;
+// With norm_w set, x is first RMS-normalized (norm.rs:18-58: f64 mean of
+// squares, x * inv * w in f32) in LDS, and the normalized row is what gets
+// quantized. With a segment's `add` set, its rows store add[i] + dot
+// (vec.rs:10-22; add may alias out).
 struct FusedSeg {
   uint32_t fmt;
   const uint8_t* w;
   size_t row_bytes;
   float* out;
+  const float* add;
 };
 struct FusedProjArgs {
   const float* x;
@@ -28,7 +33,51 @@ struct FusedProjArgs {
   int n_seg;
   FusedSeg seg[3];
   int n_rows[3];
+  const float* norm_w;
+  float eps;
 };
+
+// The attention projections of one token (forward.rs:2574-2646) as the C
+// ABI and the fused attention block use them: validation (check, fills the
+// row sizes) apart from the launches, so a composite call can validate
+// everything before it launches anything.
+struct InProj {
+  const float* x;       // the normed row, or with norm_w the row to normalize
+  const float* norm_w;  // optional: RMSNorm weight [hidden], applied first
+  float eps;
+  size_t hidden;
+  uint32_t q_format;
+  const uint8_t* wq;
+  size_t rb_q;
+  float* q;
+  size_t q_dim;
+  const uint8_t* wk;
+  size_t rb_k;
+  float* k;
+  size_t kv_dim;
+  uint32_t v_format;
+  const uint8_t* wv;
+  size_t rb_v;
+  float* v;
+  void* scratch;     // in_proj_scratch_bytes(hidden, norm_w != nullptr) bytes
+};
+struct OutProj {
+  const float* x;    // attn_out [q_dim]
+  size_t q_dim;
+  uint32_t o_format;
+  const uint8_t* wo;
+  size_t rb;
+  float* o;          // [hidden]
+  size_t hidden;
+  bool add;          // o[i] += dot (the residual add) instead of o[i] = dot
+  void* scratch;     // out_proj_scratch_bytes(q_dim, hidden, add) bytes
+};
+size_t in_proj_scratch_bytes(size_t hidden, bool norm);
+size_t out_proj_scratch_bytes(size_t q_dim, size_t hidden, bool add);
+int32_t in_proj_check(InProj& p, size_t wq_len, size_t wk_len, size_t wv_len, rv_error* err);
+int32_t out_proj_check(OutProj& p, size_t wo_len, rv_error* err);
+HipStatus in_proj_launch(const InProj& p, hipStream_t s);
+HipStatus out_proj_launch(const OutProj& p, hipStream_t s);
 
 HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s);
 HipStatus launch_quantize_q8_0(const float* x, rv_block_q8_0* out, size_t n_blocks, hipStream_t s);
@@ -37,6 +86,10 @@ HipStatus launch_quantize_q8_0(const float* x, rv_block_q8_0* out, size_t n_bloc
 HipStatus launch_gemv_rows(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
                            size_t row_lo, size_t n_rows, float* out, hipStream_t s);
 HipStatus launch_fused_proj(const FusedProjArgs& a, hipStream_t s);
+// out = rmsnorm(x, w, eps) over n values (one workgroup; norm.rs:38-58).
+HipStatus launch_rmsnorm(const float* x, const float* w, float eps, size_t n, float* out, hipStream_t s);
+// a[i] += b[i], i < n (vec.rs:10-22).
+HipStatus launch_vec_add(float* a, const float* b, size_t n, hipStream_t s);
 // out[0 .. n) = 0 (a kernel, so the call can be captured into a graph).
 HipStatus launch_fill_zero(float* out, size_t n, hipStream_t s);
 
