@@ -392,17 +392,42 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
     const size_t off = min((size_t)128 * lane, s.row_bytes - 4);
     touch = *reinterpret_cast<const uint32_t*>((uintptr_t)(row + off) & ~(uintptr_t)3);
   }
+  // The residual an output row is added to is read now, under the rest.
+  float addv = 0.f;
+  if (sg < a.n_seg && a.seg[sg].add && lane == 0) addv = a.seg[sg].add[i];
   const float* x = a.x;
   if constexpr (NORM) {
+#pragma clang fp contract(off)
     // The normalized row, x * inv * w left to right in f32 (norm.rs:55-57),
-    // staged in LDS for the quantizers.
+    // staged in LDS for the quantizers. Each thread loads its values of x
+    // and w once (x <= 8192 values: at most 16 per thread), so the sum of
+    // squares and the scaling cost one memory round trip between them.
+    constexpr int NT = 64 * kFusedWaves, PER = kFusedMaxKBlocks * 256 / NT;
     __shared__ float xs[kFusedMaxKBlocks * 256];
     __shared__ double red[kFusedWaves];
     const int n = a.nbk * 256;
-    const float inv = block_inv_rms<64 * kFusedWaves>(a.x, n, a.eps, red);
-    for (int j = threadIdx.x; j < n; j += 64 * kFusedWaves) {
-#pragma clang fp contract(off)
-      xs[j] = a.x[j] * inv * a.norm_w[j];
+    float xr[PER], wr[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int j = threadIdx.x + r * NT;
+      xr[r] = j < n ? a.x[j] : 0.f;
+      wr[r] = j < n ? a.norm_w[j] : 0.f;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) ss += (double)xr[r] * (double)xr[r];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < kFusedWaves; ++w) tot += red[w];
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)a.eps));
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int j = threadIdx.x + r * NT;
+      if (j < n) xs[j] = xr[r] * inv * wr[r];
     }
     __syncthreads();
     x = xs;
@@ -419,7 +444,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
   const bool q80 = s.fmt == RV_QF_Q8_0;
   const float v = row_dot(s.fmt, s.w + (size_t)i * s.row_bytes, q80 ? a.nb0 : a.nbk,
                           q80 ? (const void*)l0 : (const void*)lk, lane);
-  if (lane == 0) s.out[i] = s.add ? s.add[i] + v : v;
+  if (lane == 0) s.out[i] = s.add ? addv + v : v;
 }
 
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
