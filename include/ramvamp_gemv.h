@@ -95,6 +95,23 @@ int32_t rv_gemv_q8_0(const uint8_t* weight, size_t weight_len, size_t in_dim, si
                      const rv_block_q8_0* acts, size_t act_blocks, float* out, size_t out_len, void* stream,
                      uint32_t flags, rv_error* err);
 
+/* gemv.rs:444-478 `gemv_q8_k_batched` and :616-651 `gemv_q8_0_batched`:
+ * out[i * n_acts + a] = row(row_lo + i) . act_row(a) for i < row_hi - row_lo
+ * and a < n_acts, where `acts` holds n_acts rows of in_dim / 256 Q8_K (or
+ * in_dim / 32 Q8_0) blocks, act_blocks in all. Validation as the single-row
+ * forms with out_len = (row_hi - row_lo) * n_acts and act_blocks =
+ * n_acts * in_dim / block_weights (saturating). Every output is
+ * bit-identical to the single-row GEMV of that activation row: the integer
+ * sums run on int8 MFMA tiles (exact), the float operations are the scalar
+ * dot's in block order. */
+int32_t rv_gemv_q8_k_batched(uint32_t format, const uint8_t* weight, size_t weight_len, size_t in_dim,
+                             size_t out_dim, const rv_block_q8_k* acts, size_t act_blocks, size_t n_acts,
+                             size_t row_lo, size_t row_hi, float* out, size_t out_len, void* stream, uint32_t flags,
+                             rv_error* err);
+int32_t rv_gemv_q8_0_batched(const uint8_t* weight, size_t weight_len, size_t in_dim, size_t out_dim,
+                             const rv_block_q8_0* acts, size_t act_blocks, size_t n_acts, size_t row_lo,
+                             size_t row_hi, float* out, size_t out_len, void* stream, uint32_t flags, rv_error* err);
+
 /* One layer's attention-input projections (forward.rs:2574-2612): the
  * normed hidden row is quantized to Q8_K and Q8_0 into `scratch`, then
  * q = Wq . x (q_format k-quant, q_dim rows), k = Wk . x (Q8_0, kv_dim rows)

@@ -61,9 +61,11 @@ int32_t check_quantize(uint32_t format, size_t floats, size_t out_blocks, rv_err
   return RV_OK;
 }
 
-// gemv.rs `validate` (:212-266), n_acts = 1; returns row_bytes.
+// gemv.rs `validate` (:212-266); returns row_bytes. The products with
+// n_acts saturate, so an absurd n_acts falls out as a mismatch.
 int32_t check_gemv(const char* what, uint32_t format, size_t weight_len, size_t in_dim, size_t out_dim,
-                   size_t act_blocks, size_t row_lo, size_t row_hi, size_t out_len, size_t* row_bytes, rv_error* err) {
+                   size_t act_blocks, size_t row_lo, size_t row_hi, size_t out_len, size_t* row_bytes, rv_error* err,
+                   size_t n_acts = 1) {
   const int32_t rc = rv_quant_row_bytes(format, in_dim, row_bytes, err);
   if (rc) return rc;
   const size_t expected = sat_mul(*row_bytes, out_dim);
@@ -72,8 +74,9 @@ int32_t check_gemv(const char* what, uint32_t format, size_t weight_len, size_t 
     return fail(err, RV_PRIM_LENGTH_MISMATCH, row_lo, row_hi, 0, "gemv rows: row range start vs end");
   if (row_hi > out_dim)
     return fail(err, RV_PRIM_LENGTH_MISMATCH, row_hi, out_dim, 0, "gemv rows: row range end vs out_dim");
-  if (out_len != row_hi - row_lo) return fail(err, RV_PRIM_LENGTH_MISMATCH, out_len, row_hi - row_lo, 0, what);
-  const size_t wb = in_dim / rv_quant_block_weights(format);
+  const size_t wanted = sat_mul(row_hi - row_lo, n_acts);
+  if (out_len != wanted) return fail(err, RV_PRIM_LENGTH_MISMATCH, out_len, wanted, 0, what);
+  const size_t wb = sat_mul(in_dim / rv_quant_block_weights(format), n_acts);
   if (wb != act_blocks) return fail(err, RV_QUANT_BLOCK_COUNT_MISMATCH, wb, act_blocks, 0, "gemv");
   return RV_OK;
 }
@@ -194,6 +197,40 @@ int32_t rv_gemv_q8_0(const uint8_t* weight, size_t weight_len, size_t in_dim, si
                      uint32_t flags, rv_error* err) {
   return rv_gemv_q8_0_rows(weight, weight_len, in_dim, out_dim, acts, act_blocks, 0, out_dim, out, out_len, stream,
                            flags, err);
+}
+
+int32_t rv_gemv_q8_k_batched(uint32_t format, const uint8_t* weight, size_t weight_len, size_t in_dim,
+                             size_t out_dim, const rv_block_q8_k* acts, size_t act_blocks, size_t n_acts,
+                             size_t row_lo, size_t row_hi, float* out, size_t out_len, void* stream, uint32_t flags,
+                             rv_error* err) {
+  if (!k_quant(format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, format, 0, 0, "gemv_q8_k_batched");
+  size_t row_bytes;
+  int32_t rc = check_gemv("gemv_q8_k_batched: weight bytes vs rows / out vs range x n_acts", format, weight_len,
+                          in_dim, out_dim, act_blocks, row_lo, row_hi, out_len, &row_bytes, err, n_acts);
+  if (rc || (rc = check_flags(flags, err))) return rc;
+  if (out_len == 0 || in_dim == 0) return empty_rows(out, out_len, stream, flags, err);
+  if ((rc = check_ptrs(err, {{weight, "weight"}, {acts, "acts"}, {out, "out"}}))) return rc;
+  const hipStream_t s = (hipStream_t)stream;
+  return finish(s, flags,
+                rv::launch_gemv_batched(format, weight, row_bytes, in_dim, acts, n_acts, row_lo, row_hi - row_lo, out,
+                                        n_acts, false, s),
+                err);
+}
+
+int32_t rv_gemv_q8_0_batched(const uint8_t* weight, size_t weight_len, size_t in_dim, size_t out_dim,
+                             const rv_block_q8_0* acts, size_t act_blocks, size_t n_acts, size_t row_lo,
+                             size_t row_hi, float* out, size_t out_len, void* stream, uint32_t flags, rv_error* err) {
+  size_t row_bytes;
+  int32_t rc = check_gemv("gemv_q8_0_batched: weight bytes vs rows / out vs range x n_acts", RV_QF_Q8_0, weight_len,
+                          in_dim, out_dim, act_blocks, row_lo, row_hi, out_len, &row_bytes, err, n_acts);
+  if (rc || (rc = check_flags(flags, err))) return rc;
+  if (out_len == 0 || in_dim == 0) return empty_rows(out, out_len, stream, flags, err);
+  if ((rc = check_ptrs(err, {{weight, "weight"}, {acts, "acts"}, {out, "out"}}))) return rc;
+  const hipStream_t s = (hipStream_t)stream;
+  return finish(s, flags,
+                rv::launch_gemv_batched(RV_QF_Q8_0, weight, row_bytes, in_dim, acts, n_acts, row_lo,
+                                        row_hi - row_lo, out, n_acts, false, s),
+                err);
 }
 
 size_t rv_attn_in_proj_scratch_bytes(size_t hidden) { return rv::in_proj_scratch_bytes(hidden, false); }

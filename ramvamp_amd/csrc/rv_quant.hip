@@ -475,6 +475,232 @@ void launch_rows_t(const uint8_t* w, size_t row_bytes, int nb, const void* acts,
                      (long)row_lo, (int)n_rows, out);
 }
 
+
+// ---- batched GEMV on int8 MFMA (gemv.rs:444-543, :616-651) ------------------
+//
+// out[i][a] = row(row_lo + i) . act_row(a) for a tile of 32 weight rows x
+// 32 * kBWaves * TPW activation rows per workgroup. Every output is the
+// scalar dot's f32 value bit for bit: the integer sums are exact (int8
+// products, int32 accumulation) and the per-block float expression and the
+// block order are the scalar kernel's.
+//
+// The k-quant integer sums go through v_mfma_i32_32x32x32_i8 with the
+// sub-block scales folded into the weights (the A operand, weight rows =
+// the MFMA's rows; the activations' int8 values are B, one column per
+// activation row). sc * q does not fit in int8, so it is split exactly:
+//   Q4_K/Q5_K: sc*q = 32 hi + lo (lo < 32), planes hi, lo and the mins m
+//     broadcast over their sub-block: sumi = 32 H + L, sumi_mins = M (the
+//     Q8_K bsums are exactly the sub-block sums of the activation values);
+//   Q6_K: sc*(q+32) = 64 hi + lo (lo < 64; sc signed), planes hi, lo and sc:
+//     sumi = 64 H + L - 32 S (dot.rs:150-179's -32 * bsum correction);
+//   Q8_0: the weight bytes themselves, one MFMA per 32-weight block.
+// The planes of one block (eight Q8_0 blocks) of the workgroup's 32 rows
+// are built once in LDS, one thread per (row, 32-weight sub-block), and
+// used by every activation tile of the workgroup.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBRows = 32;
+constexpr int kBWaves = 4;
+constexpr int kPlaneRow = 272;  // 256 bytes + 16: 16-byte LDS reads of 32 rows spread over the banks
+
+struct BatchedArgs {
+  const uint8_t* w;
+  size_t row_bytes;
+  int nb;            // weight blocks per row (k-quant: 256 weights, Q8_0: 32)
+  const void* acts;  // n_acts rows of nb Q8_K (k-quants) or Q8_0 blocks
+  int n_acts;
+  long row_lo;
+  int n_rows;
+  float* out;
+  long ldo;
+  int transposed;    // 0: out[i * ldo + a] (the reference's layout); 1: out[a * ldo + i]
+};
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+// Thread (r, j) writes the 32 plane bytes of its row's sub-block j (weights
+// 32j .. 32j+31 of the block) and, for j == 0, the row's block scalars.
+template <int FMT>
+__device__ __forceinline__ void build_planes(const uint8_t* __restrict__ blk, int j, int8_t (*pl)[kBRows][kPlaneRow],
+                                             int r, float (*sd)[8]) {
+  uint32_t q[8], aux[8];
+  int sc[2], m = 0;
+  if constexpr (FMT == RV_QF_Q4_K || FMT == RV_QF_Q5_K) {
+    constexpr bool kQ5 = FMT == RV_QF_Q5_K;
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(blk + 4);
+    const uint32_t s3[3] = {sp[0], sp[1], sp[2]};
+    scale_min_k4(j, s3, sc[0], m);
+    sc[1] = sc[0];
+    const u32x4a* qp = reinterpret_cast<const u32x4a*>(blk + (kQ5 ? 48 : 16) + 32 * (j >> 1));
+    const u32x4a q0 = qp[0], q1 = qp[1];
+    const uint32_t raw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+    if constexpr (kQ5) {
+      const u32x4a* hp = reinterpret_cast<const u32x4a*>(blk + 16);
+      const u32x4a h0 = hp[0], h1 = hp[1];
+      const uint32_t hr[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) aux[k] = hr[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      q[k] = (j & 1) ? (raw[k] >> 4) & 0x0F0F0F0Fu : raw[k] & 0x0F0F0F0Fu;
+      if constexpr (kQ5) q[k] |= ((aux[k] >> j) & 0x01010101u) << 4;
+    }
+    if (j == 0) {
+      const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
+      sd[r][0] = f16_bits_to_f32(dd);
+      sd[r][1] = f16_bits_to_f32(dd >> 16);
+    }
+  } else if constexpr (FMT == RV_QF_Q6_K) {
+    const int half = j >> 2, grp = j & 3;
+    uint32_t ql[8];
+    load32_a2(blk + 64 * half + 32 * (grp & 1), ql);
+    load32_a2(blk + 128 + 32 * half, aux);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nib = (grp >> 1) ? (ql[k] >> 4) & 0x0F0F0F0Fu : ql[k] & 0x0F0F0F0Fu;
+      q[k] = nib | (((aux[k] >> (2 * grp)) & 0x03030303u) << 4);
+    }
+    const uint32_t scp = *reinterpret_cast<const uint16_t*>(blk + 192 + 2 * j);
+    sc[0] = (int)(int8_t)(scp & 0xFF);
+    sc[1] = (int)(int8_t)(scp >> 8);
+    if (j == 0) sd[r][0] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
+  } else {  // Q8_0: blk is block j of the group of eight
+    load32_a2(blk + 2, q);
+    sd[r][j] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
+  }
+  uint32_t* d0 = reinterpret_cast<uint32_t*>(&pl[0][r][32 * j]);
+  if constexpr (FMT == RV_QF_Q8_0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) d0[k] = q[k];
+    return;
+  } else {
+    constexpr int kShift = FMT == RV_QF_Q6_K ? 6 : 5;
+    uint32_t* d1 = reinterpret_cast<uint32_t*>(&pl[1][r][32 * j]);
+    uint32_t* d2 = reinterpret_cast<uint32_t*>(&pl[2][r][32 * j]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int s = sc[k >> 2];  // Q6_K: the first 16 weights take sc[0], the rest sc[1]
+      int hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = s * (int)((q[k] >> (8 * e)) & 0xFF);
+        hi[e] = v >> kShift;  // arithmetic shift: floor, so lo = v - (hi << kShift) is in [0, 2^kShift)
+        lo[e] = v & ((1 << kShift) - 1);
+      }
+      d0[k] = pack4(hi[0], hi[1], hi[2], hi[3]);
+      d1[k] = pack4(lo[0], lo[1], lo[2], lo[3]);
+      d2[k] = FMT == RV_QF_Q6_K ? pack4(s, s, s, s) : pack4(m, m, m, m);
+    }
+  }
+}
+
+template <int FMT, int TPW>
+__global__ __launch_bounds__(64 * kBWaves) void gemv_batched_kernel(BatchedArgs a) {
+#pragma clang fp contract(off)
+  constexpr bool kQ80 = FMT == RV_QF_Q8_0;
+  constexpr int kPlanes = kQ80 ? 1 : 3;
+  constexpr int BB = FMT == RV_QF_Q4_K ? 144 : FMT == RV_QF_Q5_K ? 176 : FMT == RV_QF_Q6_K ? 210 : 34;
+  __shared__ __attribute__((aligned(16))) int8_t pl[kPlanes][kBRows][kPlaneRow];
+  __shared__ float sd[kBRows][8];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, kh = lane >> 5;
+  const int row0 = blockIdx.x * kBRows;
+  const int act0 = blockIdx.y * (32 * kBWaves * TPW);
+  // Builder role: thread -> (row br, sub-block bj); rows past the range
+  // re-read the last row (their outputs are not stored).
+  const int br = tid >> 3, bj = tid & 7;
+  const uint8_t* wrow = a.w + (size_t)(a.row_lo + min(row0 + br, a.n_rows - 1)) * a.row_bytes;
+  float sumf[TPW][16];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sumf[t][r] = 0.f;
+  const int n_steps = kQ80 ? (a.nb + 7) / 8 : a.nb;
+  for (int step = 0; step < n_steps; ++step) {
+    if constexpr (kQ80)
+      build_planes<FMT>(wrow + (size_t)min(8 * step + bj, a.nb - 1) * BB, bj, pl, br, sd);
+    else
+      build_planes<FMT>(wrow + (size_t)step * BB, bj, pl, br, sd);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int act = min(act0 + 32 * (wave * TPW + t) + li, a.n_acts - 1);
+      i32x4 bq[8];
+      float da[8];
+      if constexpr (kQ80) {
+        const rv_block_q8_0* y = reinterpret_cast<const rv_block_q8_0*>(a.acts) + (size_t)act * a.nb;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const rv_block_q8_0* yb = y + min(8 * step + c, a.nb - 1);
+          const u32x4a v = *reinterpret_cast<const u32x4a*>(yb->qs + 16 * kh);
+          bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+          da[c] = yb->d;
+        }
+      } else {
+        const rv_block_q8_k* y = reinterpret_cast<const rv_block_q8_k*>(a.acts) + (size_t)act * a.nb + step;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const u32x4a v = *reinterpret_cast<const u32x4a*>(y->qs + 32 * c + 16 * kh);
+          bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+        }
+        da[0] = y->d;
+      }
+      if constexpr (kQ80) {
+        const int nblk = min(8, a.nb - 8 * step);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const i32x4 wa = *reinterpret_cast<const i32x4*>(&pl[0][li][32 * c + 16 * kh]);
+          i32x16 acc = {};
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, bq[c], acc, 0, 0, 0);
+          if (c < nblk) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+              sumf[t][r] += (float)acc[r] * (sd[i][c] * da[c]);
+            }
+          }
+        }
+      } else {
+        i32x16 H = {}, L = {}, M = {};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const i32x4 w0 = *reinterpret_cast<const i32x4*>(&pl[0][li][32 * c + 16 * kh]);
+          const i32x4 w1 = *reinterpret_cast<const i32x4*>(&pl[1][li][32 * c + 16 * kh]);
+          const i32x4 w2 = *reinterpret_cast<const i32x4*>(&pl[2][li][32 * c + 16 * kh]);
+          H = __builtin_amdgcn_mfma_i32_32x32x32_i8(w0, bq[c], H, 0, 0, 0);
+          L = __builtin_amdgcn_mfma_i32_32x32x32_i8(w1, bq[c], L, 0, 0, 0);
+          M = __builtin_amdgcn_mfma_i32_32x32x32_i8(w2, bq[c], M, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+          if constexpr (FMT == RV_QF_Q6_K) {
+            const int sumi = 64 * H[r] + L[r] - 32 * M[r];
+            sumf[t][r] += sd[i][0] * da[0] * (float)sumi;
+          } else {
+            const float d = sd[i][0] * da[0], dmin = sd[i][1] * da[0];
+            sumf[t][r] += d * (float)(32 * H[r] + L[r]) - dmin * (float)M[r];
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next step's planes overwrite these
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int act = act0 + 32 * (wave * TPW + t) + li;
+    if (act >= a.n_acts) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = row0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+      if (i < a.n_rows) a.out[a.transposed ? (size_t)act * a.ldo + i : (size_t)i * a.ldo + act] = sumf[t][r];
+    }
+  }
+}
+
 }  // namespace
 
 HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s) {
@@ -551,6 +777,41 @@ HipStatus launch_vec_add(float* a, const float* b, size_t n, hipStream_t s) {
   hipLaunchKernelGGL(vec_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, (long)n);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "vec_add launch";
+  return st;
+}
+
+template <int FMT, int TPW>
+void launch_batched_t(const BatchedArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.n_rows + kBRows - 1) / kBRows),
+                  (unsigned)((a.n_acts + 32 * kBWaves * TPW - 1) / (32 * kBWaves * TPW)));
+  hipLaunchKernelGGL((gemv_batched_kernel<FMT, TPW>), grid, dim3(64 * kBWaves), 0, s, a);
+}
+
+template <int FMT>
+void launch_batched_f(const BatchedArgs& a, hipStream_t s) {
+  // Two activation tiles per wave once that still leaves a workgroup per CU.
+  const long tiles2 = (long)((a.n_rows + kBRows - 1) / kBRows) * ((a.n_acts + 255) / 256);
+  if (tiles2 >= 256)
+    launch_batched_t<FMT, 2>(a, s);
+  else
+    launch_batched_t<FMT, 1>(a, s);
+}
+
+HipStatus launch_gemv_batched(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
+                              size_t n_acts, size_t row_lo, size_t n_rows, float* out, size_t ldo, bool transposed,
+                              hipStream_t s) {
+  HipStatus st;
+  if (n_rows == 0 || n_acts == 0) return st;
+  BatchedArgs a{w, row_bytes, (int)(in_dim / (fmt == RV_QF_Q8_0 ? 32 : 256)), acts, (int)n_acts, (long)row_lo,
+                (int)n_rows, out, (long)ldo, transposed ? 1 : 0};
+  switch (fmt) {
+    case RV_QF_Q4_K: launch_batched_f<RV_QF_Q4_K>(a, s); break;
+    case RV_QF_Q5_K: launch_batched_f<RV_QF_Q5_K>(a, s); break;
+    case RV_QF_Q6_K: launch_batched_f<RV_QF_Q6_K>(a, s); break;
+    default: launch_batched_f<RV_QF_Q8_0>(a, s);
+  }
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "batched gemv launch";
   return st;
 }
 

@@ -128,6 +128,26 @@ def gemv_q8_0(weight, in_dim: int, out_dim: int, acts, out):
     return out
 
 
+def gemv_q8_k_batched(fmt: int, weight, in_dim: int, out_dim: int, acts, n_acts: int, rows, out):
+    """gemv.rs:444-478: out[i * n_acts + a] = weight_row(rows[0] + i) . act_row(a)."""
+    lo, hi = rows
+    err = L.RvError()
+    _check(_lib().rv_gemv_q8_k_batched(fmt, _dev(weight, "weight"), weight.numel(), in_dim, out_dim,
+                                       _dev(acts, "acts"), _blocks(acts, Q8_K_BLOCK_BYTES, "acts"), n_acts, lo, hi,
+                                       _dev(out, "out"), out.numel(), _stream(), 0, byref(err)), err)
+    return out
+
+
+def gemv_q8_0_batched(weight, in_dim: int, out_dim: int, acts, n_acts: int, rows, out):
+    """gemv.rs:616-651, the Q8_0 sibling."""
+    lo, hi = rows
+    err = L.RvError()
+    _check(_lib().rv_gemv_q8_0_batched(_dev(weight, "weight"), weight.numel(), in_dim, out_dim, _dev(acts, "acts"),
+                                       _blocks(acts, Q8_0_BLOCK_BYTES, "acts"), n_acts, lo, hi, _dev(out, "out"),
+                                       out.numel(), _stream(), 0, byref(err)), err)
+    return out
+
+
 def attn_in_proj_scratch_bytes(hidden: int) -> int:
     return int(_lib().rv_attn_in_proj_scratch_bytes(hidden))
 
