@@ -284,6 +284,47 @@ def bench_projections(torch, rv, iters=100, n_sets=24):
             "launches_per_layer": 2, "distinct_layers": n_sets}
 
 
+def bench_prefill_projections(torch, rv, iters=20, n_rows=512, n_sets=24):
+    """A 512-row prefill chunk's attention projections per layer
+    (prefill.rs:1985-2053, :2113-2154): rv_attn_in_proj_rows (both
+    quantizations, batched q/k/v on int8 MFMA, row-major outputs) and
+    rv_attn_out_proj_rows (quantization, batched o, residual add), over
+    n_sets distinct layers' weights, graph replayed."""
+    from ramvamp_amd import projections as P
+    H, Q, KV = PROJ_SHAPES["hidden"], PROJ_SHAPES["q_dim"], PROJ_SHAPES["kv_dim"]
+    F = PROJ_FORMATS
+    rng = np.random.default_rng(0x9E1)
+    sets = []
+    for _ in range(n_sets):
+        sets.append({k: torch.from_numpy(synth_weight_rows(rng, F[k], rows, ind).ravel()).cuda()
+                     for k, rows, ind in (("q", Q, H), ("k", KV, H), ("v", KV, H), ("o", H, Q))})
+    wbytes = sum(t.numel() for t in sets[0].values())
+    x = torch.from_numpy(rng.standard_normal((n_rows, H)).astype(np.float32)).cuda()
+    attn = torch.from_numpy(rng.standard_normal((n_rows, Q)).astype(np.float32)).cuda()
+    res = torch.zeros(n_rows, H, device="cuda")
+    q, k, v = (torch.empty(n_rows, m, device="cuda") for m in (Q, KV, KV))
+    lib = rv._lib.load()
+    s_in = torch.empty(int(lib.rv_attn_in_proj_rows_scratch_bytes(n_rows, H)), dtype=torch.uint8, device="cuda")
+    s_out = torch.empty(int(lib.rv_attn_out_proj_rows_scratch_bytes(n_rows, Q)), dtype=torch.uint8, device="cuda")
+
+    def once():
+        for w in sets:
+            P.attn_in_proj_rows(x, F["q"], w["q"], q, w["k"], k, F["v"], w["v"], v, s_in)
+            P.attn_out_proj_rows(attn, F["o"], w["o"], res, s_out)
+
+    for _ in range(2):
+        once()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        once()
+    graph.replay()
+    per = timed(torch, graph.replay, iters) / (iters * n_sets)
+    ops = 2 * n_rows * (H * (Q + 2 * KV) + Q * H)  # int8 multiply-adds of the exact dots, x2
+    return {"us_per_layer": round(per * 1e6, 3), "rows": n_rows, "int8_tops": round(ops / per / 1e12, 2),
+            "weight_bytes_per_layer": wbytes, "weight_gbs": round(wbytes / per / 1e9, 1),
+            "launches_per_layer": 7, "distinct_layers": n_sets}
+
+
 def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
     """One token's attention blocks over config 2's 48 layers (ctx 4096, fp32
     KV): rv_attn_block_decode per layer (model/forward.rs:2570-2650: RMSNorm,
@@ -403,6 +444,8 @@ def main():
                     help="only run the prefill legs (configs 3 and 4, every mode), log them and exit (for profiling)")
     ap.add_argument("--projections-only", action="store_true",
                     help="only run the attention-projection leg, log it and exit (for profiling)")
+    ap.add_argument("--prefill-proj-only", action="store_true",
+                    help="only run the prefill-chunk projection leg (512 rows), log it and exit (for profiling)")
     ap.add_argument("--block-only", action="store_true",
                     help="only run the attention-block leg (48 layers, ctx 4096), log it and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -432,6 +475,11 @@ def main():
         rp = bench_projections(torch, rv)
         log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
         return
+    if args.prefill_proj_only:
+        rpp = bench_prefill_projections(torch, rv)
+        log(f"prefill projections: {rpp['us_per_layer']:.2f} us/layer for {rpp['rows']} rows, "
+            f"{rpp['int8_tops']:.1f} int8 TOP/s")
+        return
     if args.block_only:
         rb = bench_attn_block(torch, rv, synth)
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
@@ -460,6 +508,10 @@ def main():
         rp = bench_projections(torch, rv)
         extra["projections_decode_layer"] = rp
         log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
+        rpp = bench_prefill_projections(torch, rv)
+        extra["prefill_projections_512_rows"] = rpp
+        log(f"prefill projections: {rpp['us_per_layer']:.2f} us/layer for {rpp['rows']} rows, "
+            f"{rpp['int8_tops']:.1f} int8 TOP/s")
         rb = bench_attn_block(torch, rv, synth)
         extra["attn_block_decode_layer"] = rb
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")

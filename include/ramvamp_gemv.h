@@ -112,6 +112,25 @@ int32_t rv_gemv_q8_0_batched(const uint8_t* weight, size_t weight_len, size_t in
                              const rv_block_q8_0* acts, size_t act_blocks, size_t n_acts, size_t row_lo,
                              size_t row_hi, float* out, size_t out_len, void* stream, uint32_t flags, rv_error* err);
 
+/* A prefill chunk's attention projections (model/prefill.rs:1985-2053 and
+ * :2113-2154), rows row-major. rv_attn_in_proj_rows quantizes each normed
+ * row [n_rows][hidden] to Q8_K and Q8_0 (into scratch), then writes
+ * q_rows[n_rows][q_dim], k_rows[n_rows][kv_dim] and v_rows[n_rows][kv_dim]
+ * with the batched GEMVs (the reference's transposes are the store layout);
+ * rv_attn_out_proj_rows quantizes attn_rows[n_rows][q_dim] to Q8_K and adds
+ * Wo . row into residual_rows[n_rows][hidden] (residual + o, one f32 add per
+ * element). Each projected value equals the single-row GEMV of its row. */
+size_t rv_attn_in_proj_rows_scratch_bytes(size_t n_rows, size_t hidden);
+int32_t rv_attn_in_proj_rows(const float* normed_rows, size_t n_rows, size_t hidden, uint32_t q_format,
+                             const uint8_t* wq, size_t wq_len, float* q_rows, size_t q_dim, const uint8_t* wk,
+                             size_t wk_len, float* k_rows, size_t kv_dim, uint32_t v_format, const uint8_t* wv,
+                             size_t wv_len, float* v_rows, void* scratch, size_t scratch_len, void* stream,
+                             uint32_t flags, rv_error* err);
+size_t rv_attn_out_proj_rows_scratch_bytes(size_t n_rows, size_t q_dim);
+int32_t rv_attn_out_proj_rows(const float* attn_rows, size_t n_rows, size_t q_dim, uint32_t o_format,
+                              const uint8_t* wo, size_t wo_len, float* residual_rows, size_t hidden, void* scratch,
+                              size_t scratch_len, void* stream, uint32_t flags, rv_error* err);
+
 /* One layer's attention-input projections (forward.rs:2574-2612): the
  * normed hidden row is quantized to Q8_K and Q8_0 into `scratch`, then
  * q = Wq . x (q_format k-quant, q_dim rows), k = Wk . x (Q8_0, kv_dim rows)

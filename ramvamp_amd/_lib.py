@@ -110,6 +110,12 @@ SIGNATURES = {
                                        c_size_t, _P, c_size_t, _P, c_uint32, _E]),
     "rv_gemv_q8_0_batched": (c_int32, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, c_size_t, c_size_t, c_size_t,
                                        _P, c_size_t, _P, c_uint32, _E]),
+    "rv_attn_in_proj_rows_scratch_bytes": (c_size_t, [c_size_t, c_size_t]),
+    "rv_attn_in_proj_rows": (c_int32, [_P, c_size_t, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t,
+                                       _P, c_size_t, c_uint32, _P, c_size_t, _P, _P, c_size_t, _P, c_uint32, _E]),
+    "rv_attn_out_proj_rows_scratch_bytes": (c_size_t, [c_size_t, c_size_t]),
+    "rv_attn_out_proj_rows": (c_int32, [_P, c_size_t, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t,
+                                        _P, c_uint32, _E]),
     "rv_attn_in_proj_scratch_bytes": (c_size_t, [c_size_t]),
     "rv_attn_in_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t,
                                   c_uint32, _P, c_size_t, _P, _P, c_size_t, _P, c_uint32, _E]),

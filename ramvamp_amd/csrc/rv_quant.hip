@@ -515,6 +515,7 @@ struct BatchedArgs {
   float* out;
   long ldo;
   int transposed;    // 0: out[i * ldo + a] (the reference's layout); 1: out[a * ldo + i]
+  int accumulate;    // out += dot (one f32 add, as the prefill's residual add)
 };
 
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
@@ -696,7 +697,10 @@ __global__ __launch_bounds__(64 * kBWaves) void gemv_batched_kernel(BatchedArgs 
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = row0 + 8 * (r >> 2) + 4 * kh + (r & 3);
-      if (i < a.n_rows) a.out[a.transposed ? (size_t)act * a.ldo + i : (size_t)i * a.ldo + act] = sumf[t][r];
+      if (i < a.n_rows) {
+        float* o = a.out + (a.transposed ? (size_t)act * a.ldo + i : (size_t)i * a.ldo + act);
+        *o = a.accumulate ? *o + sumf[t][r] : sumf[t][r];
+      }
     }
   }
 }
@@ -799,11 +803,11 @@ void launch_batched_f(const BatchedArgs& a, hipStream_t s) {
 
 HipStatus launch_gemv_batched(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
                               size_t n_acts, size_t row_lo, size_t n_rows, float* out, size_t ldo, bool transposed,
-                              hipStream_t s) {
+                              hipStream_t s, bool accumulate) {
   HipStatus st;
   if (n_rows == 0 || n_acts == 0) return st;
   BatchedArgs a{w, row_bytes, (int)(in_dim / (fmt == RV_QF_Q8_0 ? 32 : 256)), acts, (int)n_acts, (long)row_lo,
-                (int)n_rows, out, (long)ldo, transposed ? 1 : 0};
+                (int)n_rows, out, (long)ldo, transposed ? 1 : 0, accumulate ? 1 : 0};
   switch (fmt) {
     case RV_QF_Q4_K: launch_batched_f<RV_QF_Q4_K>(a, s); break;
     case RV_QF_Q5_K: launch_batched_f<RV_QF_Q5_K>(a, s); break;

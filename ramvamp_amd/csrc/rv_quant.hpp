@@ -89,10 +89,10 @@ HipStatus launch_fused_proj(const FusedProjArgs& a, hipStream_t s);
 // Batched GEMV (int8 MFMA): out[i * ldo + a] (or, transposed, out[a * ldo + i])
 // = row(row_lo + i) . act_row(a), i < n_rows, a < n_acts; acts holds n_acts
 // rows of in_dim / 256 Q8_K (or in_dim / 32 Q8_0 for RV_QF_Q8_0) blocks.
-// in_dim > 0.
+// in_dim > 0. With accumulate, out += the dot instead.
 HipStatus launch_gemv_batched(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
                               size_t n_acts, size_t row_lo, size_t n_rows, float* out, size_t ldo, bool transposed,
-                              hipStream_t s);
+                              hipStream_t s, bool accumulate = false);
 // out = rmsnorm(x, w, eps) over n values (one workgroup; norm.rs:38-58).
 HipStatus launch_rmsnorm(const float* x, const float* w, float eps, size_t n, float* out, hipStream_t s);
 // a[i] += b[i], i < n (vec.rs:10-22).

@@ -182,3 +182,34 @@ def attn_out_proj(attn_out, o_format: int, wo, o, scratch=None):
                                    _dev(o, "o"), o.numel(), _dev(scratch, "scratch"), scratch.numel(), _stream(), 0,
                                    byref(err)), err)
     return o
+
+
+def attn_in_proj_rows(normed_rows, q_format: int, wq, q_rows, wk, k_rows, v_format: int, wv, v_rows, scratch=None):
+    """prefill.rs:1985-2053: q/k/v rows [n][dim] of a chunk's normed rows [n][hidden]."""
+    import torch
+    n, hidden = normed_rows.shape
+    if scratch is None:
+        scratch = torch.empty(max(16, int(_lib().rv_attn_in_proj_rows_scratch_bytes(n, hidden))), dtype=torch.uint8,
+                              device=normed_rows.device)
+    err = L.RvError()
+    _check(_lib().rv_attn_in_proj_rows(_dev(normed_rows, "normed_rows"), n, hidden, q_format, _dev(wq, "wq"),
+                                       wq.numel(), _dev(q_rows, "q_rows"), q_rows.shape[1], _dev(wk, "wk"), wk.numel(),
+                                       _dev(k_rows, "k_rows"), k_rows.shape[1], v_format, _dev(wv, "wv"), wv.numel(),
+                                       _dev(v_rows, "v_rows"), _dev(scratch, "scratch"), scratch.numel(), _stream(),
+                                       0, byref(err)), err)
+    return q_rows, k_rows, v_rows
+
+
+def attn_out_proj_rows(attn_rows, o_format: int, wo, residual_rows, scratch=None):
+    """prefill.rs:2113-2154: residual_rows[n][hidden] += Wo . quantize_q8_k(attn_rows[n][q_dim])."""
+    import torch
+    n, q_dim = attn_rows.shape
+    if scratch is None:
+        scratch = torch.empty(max(16, int(_lib().rv_attn_out_proj_rows_scratch_bytes(n, q_dim))), dtype=torch.uint8,
+                              device=attn_rows.device)
+    err = L.RvError()
+    _check(_lib().rv_attn_out_proj_rows(_dev(attn_rows, "attn_rows"), n, q_dim, o_format, _dev(wo, "wo"), wo.numel(),
+                                        _dev(residual_rows, "residual_rows"), residual_rows.shape[1],
+                                        _dev(scratch, "scratch"), scratch.numel(), _stream(), 0, byref(err)), err)
+    return residual_rows
+

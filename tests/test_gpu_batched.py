@@ -144,3 +144,37 @@ def test_batched_gemv_validation_order():
     P.gemv_q8_k_batched(oracle.RV_QF_Q4_K, w, 256, 8, acts[:0], 0, (0, 8), empty)
     P.gemv_q8_k_batched(oracle.RV_QF_Q4_K, w, 256, 8, acts, 3, (4, 4), empty)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n", [1, 37, 130])
+def test_prefill_chunk_projections_match_the_single_row_gemvs(n):
+    """prefill.rs:1985-2053 and :2113-2154 at the model's shapes: each row of
+    q/k/v equals the single-row GEMV of that row's quantized normed input,
+    and each residual row gains exactly its o row (one f32 add)."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(0xC4 + n)
+    hidden, q_dim, kv_dim = 2048, 4096, 512
+    Q = oracle
+    wq = random_weight_rows(Q.RV_QF_Q4_K, q_dim, hidden, rng)
+    wk = random_weight_rows(Q.RV_QF_Q8_0, kv_dim, hidden, rng)
+    wv = random_weight_rows(Q.RV_QF_Q6_K, kv_dim, hidden, rng)
+    wo = random_weight_rows(Q.RV_QF_Q5_K, hidden, q_dim, rng)
+    x = rng.standard_normal((n, hidden)).astype(F32)
+    attn = rng.standard_normal((n, q_dim)).astype(F32)
+    res = rng.standard_normal((n, hidden)).astype(F32)
+    say(f"case prefill chunk projections n={n}")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    q, k, v = (torch.full((n, m), float("nan"), device="cuda") for m in (q_dim, kv_dim, kv_dim))
+    P.attn_in_proj_rows(d(x), Q.RV_QF_Q4_K, dev_u8(torch, wq), q, dev_u8(torch, wk), k, Q.RV_QF_Q6_K,
+                        dev_u8(torch, wv), v)
+    r_dev = d(res)
+    P.attn_out_proj_rows(d(attn), Q.RV_QF_Q5_K, dev_u8(torch, wo), r_dev)
+    torch.cuda.synchronize()
+    q, k, v, r_got = (t.cpu().numpy() for t in (q, k, v, r_dev))
+    for r in range(n):
+        ak, a0 = oracle.quantize_row_q8_k(x[r]), oracle.quantize_row_q8_0(x[r])
+        assert q[r].tobytes() == oracle.gemv(Q.RV_QF_Q4_K, wq, hidden, q_dim, ak).tobytes(), f"q row {r}"
+        assert k[r].tobytes() == oracle.gemv(Q.RV_QF_Q8_0, wk, hidden, kv_dim, a0).tobytes(), f"k row {r}"
+        assert v[r].tobytes() == oracle.gemv(Q.RV_QF_Q6_K, wv, hidden, kv_dim, ak).tobytes(), f"v row {r}"
+        o = oracle.gemv(Q.RV_QF_Q5_K, wo, q_dim, hidden, oracle.quantize_row_q8_k(attn[r]))
+        assert r_got[r].tobytes() == (res[r] + o).astype(F32).tobytes(), f"residual row {r}"
