@@ -479,7 +479,7 @@ void launch_rows_t(const uint8_t* w, size_t row_bytes, int nb, const void* acts,
 // ---- batched GEMV on int8 MFMA (gemv.rs:444-543, :616-651) ------------------
 //
 // out[i][a] = row(row_lo + i) . act_row(a) for a tile of 32 weight rows x
-// 32 * kBWaves * TPW activation rows per workgroup. Every output is the
+// 32 * W activation rows (one 32-row tile per wave) per workgroup. Every output is the
 // scalar dot's f32 value bit for bit: the integer sums are exact (int8
 // products, int32 accumulation) and the per-block float expression and the
 // block order are the scalar kernel's.
@@ -487,12 +487,16 @@ void launch_rows_t(const uint8_t* w, size_t row_bytes, int nb, const void* acts,
 // The k-quant integer sums go through v_mfma_i32_32x32x32_i8 with the
 // sub-block scales folded into the weights (the A operand, weight rows =
 // the MFMA's rows; the activations' int8 values are B, one column per
-// activation row). sc * q does not fit in int8, so it is split exactly:
-//   Q4_K/Q5_K: sc*q = 32 hi + lo (lo < 32), planes hi, lo and the mins m
-//     broadcast over their sub-block: sumi = 32 H + L, sumi_mins = M (the
-//     Q8_K bsums are exactly the sub-block sums of the activation values);
-//   Q6_K: sc*(q+32) = 64 hi + lo (lo < 64; sc signed), planes hi, lo and sc:
-//     sumi = 64 H + L - 32 S (dot.rs:150-179's -32 * bsum correction);
+// activation row). sc * q does not fit in int8; the scale is split instead,
+// so that each plane is a packed product with no carries between bytes:
+//   Q4_K: sc = 8 sh + sl (sh, sl <= 7), q <= 15: planes sh*q, sl*q (<= 105)
+//     and the mins m broadcast over their sub-block: sumi = 8 H + L,
+//     sumi_mins = M (the Q8_K bsums are exactly the sub-block sums of the
+//     activation values);
+//   Q5_K: the same on q - 16 (sh*(q-16) in [-112, 105]) plus the scales
+//     broadcast: sumi = 8 H + L + 16 S, sumi_mins = M;
+//   Q6_K: sum_s sc_s (sum q a - 32 bsum_s) (dot.rs:150-179) is exactly
+//     sum sc (q - 32) a; sc (q - 32) = 64 hi + lo (lo < 64): sumi = 64 H + L;
 //   Q8_0: the weight bytes themselves, one MFMA per 32-weight block.
 // The planes of one block (eight Q8_0 blocks) of the workgroup's 32 rows
 // are built once in LDS, one thread per (row, 32-weight sub-block), and
@@ -501,7 +505,6 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBRows = 32;
-constexpr int kBWaves = 4;
 constexpr int kPlaneRow = 272;  // 256 bytes + 16: 16-byte LDS reads of 32 rows spread over the banks
 
 struct BatchedArgs {
@@ -522,189 +525,313 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
 }
 
-// Thread (r, j) writes the 32 plane bytes of its row's sub-block j (weights
-// 32j .. 32j+31 of the block) and, for j == 0, the row's block scalars.
+// 32 bytes at a 2-byte-aligned address as raw dwords (aligned-down reads
+// plus a 2-byte tail, as load32_a2), with the realignment left to
+// fix32_a2, so the loads can be issued one step ahead of their use.
+struct Raw32 {
+  uint32_t e[8];
+  uint32_t tail;
+  bool odd;
+};
+__device__ __forceinline__ Raw32 raw32_a2(const uint8_t* a) {
+  Raw32 r;
+  r.odd = ((uintptr_t)a & 2) != 0;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(a - (r.odd ? 2 : 0));
+#pragma unroll
+  for (int k = 0; k < 8; ++k) r.e[k] = p[k];
+  r.tail = r.odd ? *reinterpret_cast<const uint16_t*>(a + 30) : 0u;
+  return r;
+}
+__device__ __forceinline__ void fix32_a2(const Raw32& r, uint32_t (&w)[8]) {
+#pragma unroll
+  for (int k = 0; k < 7; ++k) w[k] = r.odd ? __builtin_amdgcn_alignbyte(r.e[k + 1], r.e[k], 2) : r.e[k];
+  w[7] = r.odd ? (r.e[7] >> 16) | (r.tail << 16) : r.e[7];
+}
+
+// The bytes thread (r, j) needs to build its row's sub-block j of one block
+// (or block j of a group of eight Q8_0 blocks), loaded one step ahead.
 template <int FMT>
-__device__ __forceinline__ void build_planes(const uint8_t* __restrict__ blk, int j, int8_t (*pl)[kBRows][kPlaneRow],
-                                             int r, float (*sd)[8]) {
-  uint32_t q[8], aux[8];
-  int sc[2], m = 0;
+struct WRaw {
+  uint32_t hdr[4];  // k-quants: d/dmin dword and the 12 scale bytes; Q6_K: scale pair, d
+  uint32_t q[8];    // Q4_K/Q5_K quants
+  uint32_t h[8];    // Q5_K high bits
+  Raw32 a, b;       // Q6_K ql / qh; Q8_0 qs (a) and d (hdr[0])
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_wraw(const uint8_t* __restrict__ blk, int j, WRaw<FMT>& w) {
   if constexpr (FMT == RV_QF_Q4_K || FMT == RV_QF_Q5_K) {
     constexpr bool kQ5 = FMT == RV_QF_Q5_K;
-    const uint32_t* sp = reinterpret_cast<const uint32_t*>(blk + 4);
-    const uint32_t s3[3] = {sp[0], sp[1], sp[2]};
-    scale_min_k4(j, s3, sc[0], m);
-    sc[1] = sc[0];
+    const uint32_t* hp = reinterpret_cast<const uint32_t*>(blk);
+    w.hdr[0] = hp[0], w.hdr[1] = hp[1], w.hdr[2] = hp[2], w.hdr[3] = hp[3];
     const u32x4a* qp = reinterpret_cast<const u32x4a*>(blk + (kQ5 ? 48 : 16) + 32 * (j >> 1));
     const u32x4a q0 = qp[0], q1 = qp[1];
-    const uint32_t raw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+    w.q[0] = q0[0], w.q[1] = q0[1], w.q[2] = q0[2], w.q[3] = q0[3];
+    w.q[4] = q1[0], w.q[5] = q1[1], w.q[6] = q1[2], w.q[7] = q1[3];
     if constexpr (kQ5) {
-      const u32x4a* hp = reinterpret_cast<const u32x4a*>(blk + 16);
-      const u32x4a h0 = hp[0], h1 = hp[1];
-      const uint32_t hr[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-#pragma unroll
-      for (int k = 0; k < 8; ++k) aux[k] = hr[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      q[k] = (j & 1) ? (raw[k] >> 4) & 0x0F0F0F0Fu : raw[k] & 0x0F0F0F0Fu;
-      if constexpr (kQ5) q[k] |= ((aux[k] >> j) & 0x01010101u) << 4;
-    }
-    if (j == 0) {
-      const uint32_t dd = *reinterpret_cast<const uint32_t*>(blk);
-      sd[r][0] = f16_bits_to_f32(dd);
-      sd[r][1] = f16_bits_to_f32(dd >> 16);
+      const u32x4a* qh = reinterpret_cast<const u32x4a*>(blk + 16);
+      const u32x4a h0 = qh[0], h1 = qh[1];
+      w.h[0] = h0[0], w.h[1] = h0[1], w.h[2] = h0[2], w.h[3] = h0[3];
+      w.h[4] = h1[0], w.h[5] = h1[1], w.h[6] = h1[2], w.h[7] = h1[3];
     }
   } else if constexpr (FMT == RV_QF_Q6_K) {
     const int half = j >> 2, grp = j & 3;
-    uint32_t ql[8];
-    load32_a2(blk + 64 * half + 32 * (grp & 1), ql);
-    load32_a2(blk + 128 + 32 * half, aux);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t nib = (grp >> 1) ? (ql[k] >> 4) & 0x0F0F0F0Fu : ql[k] & 0x0F0F0F0Fu;
-      q[k] = nib | (((aux[k] >> (2 * grp)) & 0x03030303u) << 4);
-    }
-    const uint32_t scp = *reinterpret_cast<const uint16_t*>(blk + 192 + 2 * j);
-    sc[0] = (int)(int8_t)(scp & 0xFF);
-    sc[1] = (int)(int8_t)(scp >> 8);
-    if (j == 0) sd[r][0] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
-  } else {  // Q8_0: blk is block j of the group of eight
-    load32_a2(blk + 2, q);
-    sd[r][j] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
-  }
-  uint32_t* d0 = reinterpret_cast<uint32_t*>(&pl[0][r][32 * j]);
-  if constexpr (FMT == RV_QF_Q8_0) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) d0[k] = q[k];
-    return;
+    w.a = raw32_a2(blk + 64 * half + 32 * (grp & 1));
+    w.b = raw32_a2(blk + 128 + 32 * half);
+    w.hdr[0] = *reinterpret_cast<const uint16_t*>(blk + 192 + 2 * j);
+    w.hdr[1] = *reinterpret_cast<const uint16_t*>(blk + 208);
   } else {
-    constexpr int kShift = FMT == RV_QF_Q6_K ? 6 : 5;
-    uint32_t* d1 = reinterpret_cast<uint32_t*>(&pl[1][r][32 * j]);
-    uint32_t* d2 = reinterpret_cast<uint32_t*>(&pl[2][r][32 * j]);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int s = sc[k >> 2];  // Q6_K: the first 16 weights take sc[0], the rest sc[1]
-      int hi[4], lo[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int v = s * (int)((q[k] >> (8 * e)) & 0xFF);
-        hi[e] = v >> kShift;  // arithmetic shift: floor, so lo = v - (hi << kShift) is in [0, 2^kShift)
-        lo[e] = v & ((1 << kShift) - 1);
-      }
-      d0[k] = pack4(hi[0], hi[1], hi[2], hi[3]);
-      d1[k] = pack4(lo[0], lo[1], lo[2], lo[3]);
-      d2[k] = FMT == RV_QF_Q6_K ? pack4(s, s, s, s) : pack4(m, m, m, m);
-    }
+    w.a = raw32_a2(blk + 2);
+    w.hdr[0] = *reinterpret_cast<const uint16_t*>(blk);
   }
 }
 
-template <int FMT, int TPW>
-__global__ __launch_bounds__(64 * kBWaves) void gemv_batched_kernel(BatchedArgs a) {
+// Thread (r, j) writes the 32 plane bytes of its row's sub-block j
+// (weights 32j .. 32j+31 of the block) and, for j == 0, the row's block
+// scalars (Q8_0: block j's d).
+template <int FMT>
+__device__ __forceinline__ void build_planes(const WRaw<FMT>& wr, int j, int8_t (*pl)[kBRows][kPlaneRow], int r,
+                                             float (*sd)[kBRows]) {
+  uint32_t q[8];
+  int sc[2], m = 0;
+  if constexpr (FMT == RV_QF_Q4_K || FMT == RV_QF_Q5_K) {
+    const uint32_t s3[3] = {wr.hdr[1], wr.hdr[2], wr.hdr[3]};
+    scale_min_k4(j, s3, sc[0], m);
+    sc[1] = sc[0];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      q[k] = (j & 1) ? (wr.q[k] >> 4) & 0x0F0F0F0Fu : wr.q[k] & 0x0F0F0F0Fu;
+      if constexpr (FMT == RV_QF_Q5_K) q[k] |= ((wr.h[k] >> j) & 0x01010101u) << 4;
+    }
+    if (j == 0) {
+      sd[0][r] = f16_bits_to_f32(wr.hdr[0]);
+      sd[1][r] = f16_bits_to_f32(wr.hdr[0] >> 16);
+    }
+  } else if constexpr (FMT == RV_QF_Q6_K) {
+    const int grp = j & 3;
+    uint32_t ql[8], qh[8];
+    fix32_a2(wr.a, ql);
+    fix32_a2(wr.b, qh);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t nib = (grp >> 1) ? (ql[k] >> 4) & 0x0F0F0F0Fu : ql[k] & 0x0F0F0F0Fu;
+      q[k] = nib | (((qh[k] >> (2 * grp)) & 0x03030303u) << 4);
+    }
+    sc[0] = (int)(int8_t)(wr.hdr[0] & 0xFF);
+    sc[1] = (int)(int8_t)(wr.hdr[0] >> 8);
+    if (j == 0) sd[0][r] = f16_bits_to_f32(wr.hdr[1]);
+  } else {
+    fix32_a2(wr.a, q);
+    sd[j][r] = f16_bits_to_f32(wr.hdr[0]);
+  }
+  auto plane = [&](int p) { return reinterpret_cast<u32x4a*>(&pl[p][r][32 * j]); };
+  auto put = [&](int p, const uint32_t (&v)[8]) {
+    plane(p)[0] = u32x4a{v[0], v[1], v[2], v[3]};
+    plane(p)[1] = u32x4a{v[4], v[5], v[6], v[7]};
+  };
+  if constexpr (FMT == RV_QF_Q8_0) {
+    put(0, q);
+  } else if constexpr (FMT == RV_QF_Q4_K || FMT == RV_QF_Q5_K) {
+    // q bytes times a 3-bit scale part: four exact byte products per dword.
+    const uint32_t sh = (uint32_t)sc[0] >> 3, sl = (uint32_t)sc[0] & 7;
+    uint32_t h[8], l[8], mm[8], ss[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if constexpr (FMT == RV_QF_Q4_K) {
+        h[k] = q[k] * sh;
+        l[k] = q[k] * sl;
+      } else {
+        // bytes s*q + (128 - 16 s) in [16, 233] (no carries), then the top
+        // bit flipped: the signed bytes s*(q - 16).
+        h[k] = (q[k] * sh + (128u - 16u * sh) * 0x01010101u) ^ 0x80808080u;
+        l[k] = (q[k] * sl + (128u - 16u * sl) * 0x01010101u) ^ 0x80808080u;
+        ss[k] = (uint32_t)sc[0] * 0x01010101u;
+      }
+      mm[k] = (uint32_t)m * 0x01010101u;
+    }
+    put(0, h);
+    put(1, l);
+    put(2, mm);
+    if constexpr (FMT == RV_QF_Q5_K) put(3, ss);
+  } else {
+    uint32_t h[8], l[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int s2 = sc[k >> 2];  // the first 16 weights take sc[0], the rest sc[1]
+      int hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = s2 * ((int)((q[k] >> (8 * e)) & 0xFF) - 32);
+        hi[e] = v >> 6;  // arithmetic shift: floor, so lo = v - 64 hi is in [0, 64)
+        lo[e] = v & 63;
+      }
+      h[k] = pack4(hi[0], hi[1], hi[2], hi[3]);
+      l[k] = pack4(lo[0], lo[1], lo[2], lo[3]);
+    }
+    put(0, h);
+    put(1, l);
+  }
+}
+
+// The activation operands of one step for one tile: lane (li, kh) holds
+// activation row li's bytes 16 kh .. 16 kh + 15 of each 32-value chunk.
+template <bool Q80>
+__device__ __forceinline__ void load_acts(const void* __restrict__ acts, int act, int nb, int step, i32x4 (&bq)[8],
+                                          float (&da)[8], int kh) {
+  if constexpr (Q80) {
+    const rv_block_q8_0* y = reinterpret_cast<const rv_block_q8_0*>(acts) + (size_t)act * nb;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const rv_block_q8_0* yb = y + min(8 * step + c, nb - 1);
+      const u32x4a v = *reinterpret_cast<const u32x4a*>(yb->qs + 16 * kh);
+      bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+      da[c] = yb->d;
+    }
+  } else {
+    const rv_block_q8_k* y = reinterpret_cast<const rv_block_q8_k*>(acts) + (size_t)act * nb + step;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const u32x4a v = *reinterpret_cast<const u32x4a*>(y->qs + 32 * c + 16 * kh);
+      bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+    }
+    da[0] = y->d;
+  }
+}
+
+template <int FMT, int W>
+__global__ __launch_bounds__(64 * W) void gemv_batched_kernel(BatchedArgs a) {
 #pragma clang fp contract(off)
   constexpr bool kQ80 = FMT == RV_QF_Q8_0;
-  constexpr int kPlanes = kQ80 ? 1 : 3;
+  constexpr int kPlanes = kQ80 ? 1 : FMT == RV_QF_Q6_K ? 2 : FMT == RV_QF_Q5_K ? 4 : 3;
   constexpr int BB = FMT == RV_QF_Q4_K ? 144 : FMT == RV_QF_Q5_K ? 176 : FMT == RV_QF_Q6_K ? 210 : 34;
+  constexpr int NB = 4 / W;  // (row, sub-block) build tasks per thread: 256 per step
   __shared__ __attribute__((aligned(16))) int8_t pl[kPlanes][kBRows][kPlaneRow];
-  __shared__ float sd[kBRows][8];
+  // Per-row block scalars, row-minor so a lane's four consecutive output
+  // rows come in one 16-byte read: k-quants [0] d and [1] dmin; Q8_0 [c]
+  // the d of block c of the group.
+  __shared__ __attribute__((aligned(16))) float sd[8][kBRows];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, kh = lane >> 5;
   const int row0 = blockIdx.x * kBRows;
-  const int act0 = blockIdx.y * (32 * kBWaves * TPW);
-  // Builder role: thread -> (row br, sub-block bj); rows past the range
-  // re-read the last row (their outputs are not stored).
-  const int br = tid >> 3, bj = tid & 7;
-  const uint8_t* wrow = a.w + (size_t)(a.row_lo + min(row0 + br, a.n_rows - 1)) * a.row_bytes;
-  float sumf[TPW][16];
+  // Builder role: task u = tid + 64 W n -> (row u >> 3, sub-block u & 7);
+  // rows past the range re-read the last row (their outputs are not stored).
+  const uint8_t* wrow[NB];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+  for (int n = 0; n < NB; ++n)
+    wrow[n] = a.w + (size_t)(a.row_lo + min(row0 + ((tid + 64 * W * n) >> 3), a.n_rows - 1)) * a.row_bytes;
+  const int bj = tid & 7;  // the same for every task of the thread (64 W is a multiple of 8)
+  auto wblk = [&](int n, int step) {
+    return kQ80 ? wrow[n] + (size_t)min(8 * step + bj, a.nb - 1) * BB : wrow[n] + (size_t)step * BB;
+  };
+  const int act = min((int)blockIdx.y * 32 * W + 32 * wave + li, a.n_acts - 1);
+  float sumf[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sumf[t][r] = 0.f;
+  for (int r = 0; r < 16; ++r) sumf[r] = 0.f;
   const int n_steps = kQ80 ? (a.nb + 7) / 8 : a.nb;
-  for (int step = 0; step < n_steps; ++step) {
-    if constexpr (kQ80)
-      build_planes<FMT>(wrow + (size_t)min(8 * step + bj, a.nb - 1) * BB, bj, pl, br, sd);
-    else
-      build_planes<FMT>(wrow + (size_t)step * BB, bj, pl, br, sd);
+  // Software pipeline: the weight bytes of steps + 1 .. + 2 and the
+  // activation operands of step + 1 are in flight while step's planes are
+  // built and its MFMAs run (a weight block's memory round trip is longer
+  // than one step). The register rings are indexed by the unrolled u. Every
+  // load is issued unconditionally (steps past the end re-read the last
+  // one): a conditional load would make the compiler merge the old and new
+  // registers after the branch and wait for the load right there.
+  constexpr int DW = 3, DA = 2;
+  const int last = n_steps - 1;
+  WRaw<FMT> wr[DW][NB];
+#pragma unroll
+  for (int u = 0; u < DW; ++u)
+#pragma unroll
+    for (int n = 0; n < NB; ++n) load_wraw<FMT>(wblk(n, min(u, last)), bj, wr[u][n]);
+  i32x4 bq[DA][8];
+  float da[DA][8];
+#pragma unroll
+  for (int u = 0; u < DA; ++u) load_acts<kQ80>(a.acts, act, a.nb, min(u, last), bq[u], da[u], kh);
+  for (int s0 = 0; s0 < n_steps; s0 += DW * DA) {
+#pragma unroll
+  for (int u = 0; u < DW * DA; ++u) {
+    const int step = s0 + u;
+    if (step >= n_steps) break;
+    const int uw = u % DW, ua = u % DA;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) build_planes<FMT>(wr[uw][n], bj, pl, (tid + 64 * W * n) >> 3, sd);
     __syncthreads();
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int act = min(act0 + 32 * (wave * TPW + t) + li, a.n_acts - 1);
-      i32x4 bq[8];
-      float da[8];
-      if constexpr (kQ80) {
-        const rv_block_q8_0* y = reinterpret_cast<const rv_block_q8_0*>(a.acts) + (size_t)act * a.nb;
+    for (int n = 0; n < NB; ++n) load_wraw<FMT>(wblk(n, min(step + DW, last)), bj, wr[uw][n]);
+    i32x4 cur[8];
+    float dcur[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const rv_block_q8_0* yb = y + min(8 * step + c, a.nb - 1);
-          const u32x4a v = *reinterpret_cast<const u32x4a*>(yb->qs + 16 * kh);
-          bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
-          da[c] = yb->d;
-        }
-      } else {
-        const rv_block_q8_k* y = reinterpret_cast<const rv_block_q8_k*>(a.acts) + (size_t)act * a.nb + step;
+    for (int c = 0; c < 8; ++c) cur[c] = bq[ua][c], dcur[c] = da[ua][c];
+    load_acts<kQ80>(a.acts, act, a.nb, min(step + DA, last), bq[ua], da[ua], kh);
+    // Lane (li, kh) owns output rows 8 g + 4 kh + e (e < 4) of the tile, g < 4.
+    auto rows4 = [&](int k, int g) { return *reinterpret_cast<const f32x4*>(&sd[k][8 * g + 4 * kh]); };
+    auto aop = [&](int p, int c) { return *reinterpret_cast<const i32x4*>(&pl[p][li][32 * c + 16 * kh]); };
+    if constexpr (kQ80) {
+      const int nblk = min(8, a.nb - 8 * step);
+      i32x4 wa = aop(0, 0);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const u32x4a v = *reinterpret_cast<const u32x4a*>(y->qs + 32 * c + 16 * kh);
-          bq[c] = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+      for (int c = 0; c < 8; ++c) {
+        i32x16 acc = {};
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, cur[c], acc, 0, 0, 0);
+        if (c + 1 < 8) wa = aop(0, c + 1);  // in flight under this MFMA
+        f32x4 dw[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) dw[g] = rows4(c, g);
+        if (c < nblk) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sumf[r] += (float)acc[r] * (dw[r >> 2][r & 3] * dcur[c]);
         }
-        da[0] = y->d;
       }
-      if constexpr (kQ80) {
-        const int nblk = min(8, a.nb - 8 * step);
+    } else {
+      f32x4 dw[4], dm[4];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const i32x4 wa = *reinterpret_cast<const i32x4*>(&pl[0][li][32 * c + 16 * kh]);
-          i32x16 acc = {};
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, bq[c], acc, 0, 0, 0);
-          if (c < nblk) {
+      for (int g = 0; g < 4; ++g) {
+        dw[g] = rows4(0, g);
+        if constexpr (FMT != RV_QF_Q6_K) dm[g] = rows4(1, g);
+      }
+      i32x16 acc[kPlanes];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
-              sumf[t][r] += (float)acc[r] * (sd[i][c] * da[c]);
-            }
-          }
-        }
-      } else {
-        i32x16 H = {}, L = {}, M = {};
+      for (int p = 0; p < kPlanes; ++p) acc[p] = i32x16{};
+      i32x4 wa[kPlanes], wn[kPlanes];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const i32x4 w0 = *reinterpret_cast<const i32x4*>(&pl[0][li][32 * c + 16 * kh]);
-          const i32x4 w1 = *reinterpret_cast<const i32x4*>(&pl[1][li][32 * c + 16 * kh]);
-          const i32x4 w2 = *reinterpret_cast<const i32x4*>(&pl[2][li][32 * c + 16 * kh]);
-          H = __builtin_amdgcn_mfma_i32_32x32x32_i8(w0, bq[c], H, 0, 0, 0);
-          L = __builtin_amdgcn_mfma_i32_32x32x32_i8(w1, bq[c], L, 0, 0, 0);
-          M = __builtin_amdgcn_mfma_i32_32x32x32_i8(w2, bq[c], M, 0, 0, 0);
+      for (int p = 0; p < kPlanes; ++p) wa[p] = aop(p, 0);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if (c + 1 < 8) {
+#pragma unroll
+          for (int p = 0; p < kPlanes; ++p) wn[p] = aop(p, c + 1);  // in flight under chunk c's MFMAs
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
-          if constexpr (FMT == RV_QF_Q6_K) {
-            const int sumi = 64 * H[r] + L[r] - 32 * M[r];
-            sumf[t][r] += sd[i][0] * da[0] * (float)sumi;
-          } else {
-            const float d = sd[i][0] * da[0], dmin = sd[i][1] * da[0];
-            sumf[t][r] += d * (float)(32 * H[r] + L[r]) - dmin * (float)M[r];
-          }
+        for (int p = 0; p < kPlanes; ++p) acc[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[p], cur[c], acc[p], 0, 0, 0);
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p) wa[p] = wn[p];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float dr = dw[r >> 2][r & 3];
+        if constexpr (FMT == RV_QF_Q6_K) {
+          const int sumi = 64 * acc[0][r] + acc[1][r];
+          sumf[r] += dr * dcur[0] * (float)sumi;
+        } else {
+          int sumi = 8 * acc[0][r] + acc[1][r];
+          if constexpr (FMT == RV_QF_Q5_K) sumi += 16 * acc[3][r];
+          const float d = dr * dcur[0], dmin = dm[r >> 2][r & 3] * dcur[0];
+          sumf[r] += d * (float)sumi - dmin * (float)acc[2][r];
         }
       }
     }
     __syncthreads();  // the next step's planes overwrite these
   }
+  }
+  const int act_out = (int)blockIdx.y * 32 * W + 32 * wave + li;
+  if (act_out >= a.n_acts) return;
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const int act = act0 + 32 * (wave * TPW + t) + li;
-    if (act >= a.n_acts) continue;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = row0 + 8 * (r >> 2) + 4 * kh + (r & 3);
-      if (i < a.n_rows) {
-        float* o = a.out + (a.transposed ? (size_t)act * a.ldo + i : (size_t)i * a.ldo + act);
-        *o = a.accumulate ? *o + sumf[t][r] : sumf[t][r];
-      }
+  for (int r = 0; r < 16; ++r) {
+    const int i = row0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+    if (i < a.n_rows) {
+      float* o = a.out + (a.transposed ? (size_t)act_out * a.ldo + i : (size_t)i * a.ldo + act_out);
+      *o = a.accumulate ? *o + sumf[r] : sumf[r];
     }
   }
 }
-
 }  // namespace
 
 HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s) {
@@ -784,21 +911,22 @@ HipStatus launch_vec_add(float* a, const float* b, size_t n, hipStream_t s) {
   return st;
 }
 
-template <int FMT, int TPW>
+template <int FMT, int W>
 void launch_batched_t(const BatchedArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.n_rows + kBRows - 1) / kBRows),
-                  (unsigned)((a.n_acts + 32 * kBWaves * TPW - 1) / (32 * kBWaves * TPW)));
-  hipLaunchKernelGGL((gemv_batched_kernel<FMT, TPW>), grid, dim3(64 * kBWaves), 0, s, a);
+  const dim3 grid((unsigned)((a.n_rows + kBRows - 1) / kBRows), (unsigned)((a.n_acts + 32 * W - 1) / (32 * W)));
+  hipLaunchKernelGGL((gemv_batched_kernel<FMT, W>), grid, dim3(64 * W), 0, s, a);
 }
 
 template <int FMT>
 void launch_batched_f(const BatchedArgs& a, hipStream_t s) {
-  // Two activation tiles per wave once that still leaves a workgroup per CU.
-  const long tiles2 = (long)((a.n_rows + kBRows - 1) / kBRows) * ((a.n_acts + 255) / 256);
-  if (tiles2 >= 256)
-    launch_batched_t<FMT, 2>(a, s);
-  else
+  // Four 32-activation tiles per workgroup share its planes; Q8_0 matrices
+  // with few row tiles (the k projection: 16) take one tile per workgroup
+  // instead, four times the workgroups (its plane build is a copy).
+  const long row_tiles = (a.n_rows + kBRows - 1) / kBRows;
+  if (FMT == RV_QF_Q8_0 && row_tiles * ((a.n_acts + 127) / 128) < 256)
     launch_batched_t<FMT, 1>(a, s);
+  else
+    launch_batched_t<FMT, 4>(a, s);
 }
 
 HipStatus launch_gemv_batched(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
