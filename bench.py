@@ -325,6 +325,40 @@ def bench_prefill_projections(torch, rv, iters=20, n_rows=512, n_sets=24):
             "launches_per_layer": 7, "distinct_layers": n_sets}
 
 
+def bench_attn_block_prefill(torch, rv, synth, mode="f16", iters=20):
+    """One layer's attention block for a 512-row prefill chunk at config 4
+    (3449 cached rows, fp32 KV): rv_attn_block_prefill (row RMSNorm, batched
+    q/k/v, QK norm + RoPE + append + causal attention in `mode`, batched o +
+    residual add), back to back (the cache truncated to 3449 between calls)."""
+    from ramvamp_amd import block as B
+    H, Q, KV = PROJ_SHAPES["hidden"], PROJ_SHAPES["q_dim"], PROJ_SHAPES["kv_dim"]
+    F = PROJ_FORMATS
+    c = synth.CONFIGS[4]
+    start, rows = c.context, c.rows
+    rng = np.random.default_rng(0xB10D)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    w = B.AttnBlockWeights(d((1 + 0.02 * rng.standard_normal(H)).astype(np.float32)), F["q"],
+                           d(synth_weight_rows(rng, F["q"], Q, H)), d(synth_weight_rows(rng, F["k"], KV, H)), F["v"],
+                           d(synth_weight_rows(rng, F["v"], KV, H)), d(synth.norm_weight(4, synth.T_QN)),
+                           d(synth.norm_weight(4, synth.T_KN)), F["o"], d(synth_weight_rows(rng, F["o"], H, Q)))
+    kv = rv.KvCache(1, 4, 128, start + rows, "f32")
+    K, V = synth.cached_kv(4, 0, start)
+    kv.append_rows(0, K, V)
+    residual = d(rng.standard_normal((rows, H)).astype(np.float32))
+    scratch = torch.empty(B.prefill_scratch_bytes(rows, H, Q, KV), dtype=torch.uint8, device="cuda")
+
+    def once():
+        kv.truncate(start)
+        B.attn_block_prefill(kv, 0, residual, Q, w, synth.EPS, synth.THETA, start, float(synth.SCALE), mode=mode,
+                             scratch=scratch)
+
+    for _ in range(3):
+        once()
+    per = timed(torch, once, iters) / iters
+    return {"mode": mode, "rows": rows, "start": start, "us_per_layer": round(per * 1e6, 2),
+            "us_per_token": round(per * 1e6 / rows, 4)}
+
+
 def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
     """One token's attention blocks over config 2's 48 layers (ctx 4096, fp32
     KV): rv_attn_block_decode per layer (model/forward.rs:2570-2650: RMSNorm,
@@ -483,6 +517,9 @@ def main():
     if args.block_only:
         rb = bench_attn_block(torch, rv, synth)
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        for mode in ("f16", "exact"):
+            rbp = bench_attn_block_prefill(torch, rv, synth, mode)
+            log(f"attention block prefill {mode}: {rbp['us_per_layer']:.1f} us/layer for {rbp['rows']} rows")
         return
     if args.prefill_only:
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
@@ -515,6 +552,10 @@ def main():
         rb = bench_attn_block(torch, rv, synth)
         extra["attn_block_decode_layer"] = rb
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        for mode in ("f16", "exact"):
+            rbp = bench_attn_block_prefill(torch, rv, synth, mode)
+            extra[f"attn_block_prefill_config4_{mode}"] = rbp
+            log(f"attention block prefill {mode}: {rbp['us_per_layer']:.1f} us/layer for {rbp['rows']} rows")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")

@@ -71,6 +71,21 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
                              const rv_attn_block_weights* w, float eps, float theta, size_t position,
                              float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err);
 
+/* The same block for a prefill chunk of n_rows tokens at positions start ..
+ * start + n_rows - 1 (model/prefill.rs:1975-2154, the attention half of a
+ * layer): each residual row normalized (rmsnorm_rows), quantized both ways,
+ * the batched q/k/v projections (rv_attn_in_proj_rows), the chunk's QK norm,
+ * RoPE, append and causal attention (rv_prefill_chunk; flags carries its
+ * RV_PREFILL_* mode), and the batched output projection added into each
+ * residual row (rv_attn_out_proj_rows). residual_rows[n_rows][hidden] is
+ * updated in place; start must equal the layer's length. Launches: the row
+ * norm, two quantizers, three batched GEMVs, the prefill chunk's, one
+ * quantizer and one batched GEMV. */
+size_t rv_attn_block_prefill_scratch_bytes(size_t n_rows, size_t hidden, size_t q_dim, size_t kv_dim);
+int32_t rv_attn_block_prefill(rv_kv* kv, size_t layer, float* residual_rows, size_t n_rows, size_t hidden,
+                              size_t q_dim, const rv_attn_block_weights* w, float eps, float theta, size_t start,
+                              float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err);
+
 #ifdef __cplusplus
 }
 #endif

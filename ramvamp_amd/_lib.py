@@ -123,6 +123,9 @@ SIGNATURES = {
     "rv_attn_out_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32,
                                    _E]),
     "rv_attn_block_scratch_bytes": (c_size_t, [c_size_t, c_size_t, c_size_t]),
+    "rv_attn_block_prefill_scratch_bytes": (c_size_t, [c_size_t, c_size_t, c_size_t, c_size_t]),
+    "rv_attn_block_prefill": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, c_size_t, POINTER(RvAttnBlockWeights),
+                                        c_float, c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_attn_block_decode": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, POINTER(RvAttnBlockWeights), c_float,
                                        c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
 }

@@ -66,3 +66,31 @@ def attn_block_decode(cache: KvCache, layer: int, residual, q_dim: int, w: AttnB
                                          eps, theta, position, scale, c_void_p(scratch.data_ptr()), scratch.numel(),
                                          0, byref(err)), err)
     return residual
+
+
+_MODES = {"exact": L.RV_PREFILL_EXACT, "f16": L.RV_PREFILL_F16, "bf16": L.RV_PREFILL_BF16}
+
+
+def prefill_scratch_bytes(n_rows: int, hidden: int, q_dim: int, kv_dim: int) -> int:
+    return int(L.load().rv_attn_block_prefill_scratch_bytes(n_rows, hidden, q_dim, kv_dim))
+
+
+def attn_block_prefill(cache: KvCache, layer: int, residual_rows, q_dim: int, w: AttnBlockWeights, eps: float,
+                       theta: float, start: int, scale: float, mode: str = "exact", scratch=None):
+    """prefill.rs:1975-2154 (the attention half of a layer) for a chunk:
+    residual_rows (float32 [n][hidden], device) is updated in place."""
+    import torch
+    if not (hasattr(residual_rows, "is_cuda") and residual_rows.is_cuda and residual_rows.is_contiguous()):
+        raise TypeError("residual_rows must be a contiguous torch tensor on the GPU")
+    n, hidden = residual_rows.shape
+    if scratch is None:
+        scratch = torch.empty(max(256, prefill_scratch_bytes(n, hidden, q_dim, cache.kv_dim())), dtype=torch.uint8,
+                              device=residual_rows.device)
+    cache._bind_stream()
+    err = L.RvError()
+    cw = w._c()
+    _check(L.load().rv_attn_block_prefill(cache.handle, layer, c_void_p(residual_rows.data_ptr()), n, hidden, q_dim,
+                                          byref(cw), eps, theta, start, scale, c_void_p(scratch.data_ptr()),
+                                          scratch.numel(), _MODES[mode], byref(err)), err)
+    return residual_rows
+

@@ -212,6 +212,22 @@ int32_t check_rope_dim(const rv_kv* kv, rv_error* err) {
 
 namespace rv {
 
+int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start, rv_error* err) {
+  // rv_prefill_chunk's checks, in its order, before its pointer checks.
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  int32_t rc = check_rope_dim(kv, err);
+  if (rc) return rc;
+  const size_t hd = kv->head_dim;
+  if (q_dim == 0 || q_dim % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_dim, hd);
+  if ((q_dim / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_dim / hd, kv->n_kv_heads);
+  if ((rc = check_layer(kv, layer, err))) return rc;
+  const size_t len = kv->lens[layer];
+  if (start != len) return fail(err, RV_KV_POSITION_OUT_OF_RANGE, layer, start, len, 0, "start != len(layer)");
+  if (rows > kv->capacity - len) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
+  if (start + rows > 0x100000000ull) return fail(err, RV_ERR_UNSUPPORTED, start + rows, 0, 0, 0, "position past u32");
+  return RV_OK;
+}
+
 int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err) {
   // rv_decode_step's checks, in its order, for k, v and out of the sizes the
   // cache and q imply (the composite callers own those buffers).

@@ -29,7 +29,7 @@ struct Carve {
   void* proj;
 };
 
-Carve carve(void* scratch, size_t hidden, size_t q_dim, size_t kv_dim) {
+Carve carve(void* scratch, size_t q_dim, size_t kv_dim) {
   char* p = (char*)scratch;
   Carve c;
   c.q = (float*)p;
@@ -41,7 +41,6 @@ Carve carve(void* scratch, size_t hidden, size_t q_dim, size_t kv_dim) {
   c.attn = (float*)p;
   p += align256(q_dim * sizeof(float));
   c.proj = p;
-  (void)hidden;
   return c;
 }
 
@@ -62,7 +61,7 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
   // forward.rs:2572 rmsnorm (norm.rs:38-40): an empty row has no mean.
   if (hidden == 0) return fail(err, RV_PRIM_EMPTY, 0, 0, "rmsnorm");
   const size_t kv_dim = kv->kv_dim;
-  const Carve c = carve(scratch, hidden, q_dim, kv_dim);
+  const Carve c = carve(scratch, q_dim, kv_dim);
   rv::InProj in{residual, w->attn_norm, eps,     hidden, w->q_format, w->wq, 0,   c.q,   q_dim,
                 w->wk,    0,            c.k,     kv_dim, w->v_format, w->wv, 0,   c.v,   c.proj};
   int32_t rc;
@@ -93,6 +92,79 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
                         scale, c.attn, q_dim, 0, err);
   if (!rc) {
     st = rv::out_proj_launch(out, s);
+    if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
+  }
+  if (!rc && (flags & RV_SYNC)) {
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)e, 0, "hipStreamSynchronize");
+  }
+  if (prev >= 0 && prev != kv->device) (void)hipSetDevice(prev);
+  if (!rc && err) *err = rv_error{RV_OK, 0, 0, 0, 0, nullptr};
+  return rc;
+}
+
+// The prefill chunk's scratch: normalized rows, q/k/v rows, attention rows,
+// then the projections' quantized rows.
+size_t rv_attn_block_prefill_scratch_bytes(size_t n_rows, size_t hidden, size_t q_dim, size_t kv_dim) {
+  const size_t proj = std::max(rv::in_proj_rows_scratch_bytes(n_rows, hidden), rv::out_proj_rows_scratch_bytes(n_rows, q_dim));
+  return align256(n_rows * hidden * 4) + 2 * align256(n_rows * q_dim * 4) + 2 * align256(n_rows * kv_dim * 4) +
+         align256(proj);
+}
+
+int32_t rv_attn_block_prefill(rv_kv* kv, size_t layer, float* residual_rows, size_t n_rows, size_t hidden,
+                              size_t q_dim, const rv_attn_block_weights* w, float eps, float theta, size_t start,
+                              float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, "kv");
+  if (!w) return fail(err, RV_ERR_NULL_ARG, 0, 0, "weights");
+  // prefill.rs:1975-1993 (a): each row's rmsnorm; an empty row has no mean.
+  if (hidden == 0) return fail(err, RV_PRIM_EMPTY, 0, 0, "rmsnorm");
+  const size_t kv_dim = kv->kv_dim, n = n_rows;
+  char* p = (char*)scratch;
+  float* normed = (float*)p;
+  p += align256(n * hidden * 4);
+  float* q = (float*)p;
+  p += align256(n * q_dim * 4);
+  float* k = (float*)p;
+  p += align256(n * kv_dim * 4);
+  float* v = (float*)p;
+  p += align256(n * kv_dim * 4);
+  float* attn = (float*)p;
+  p += align256(n * q_dim * 4);
+  rv::InProj in{normed, nullptr, 0.f, hidden, w->q_format, w->wq, 0, q, q_dim, w->wk, 0, k, kv_dim,
+                w->v_format, w->wv, 0, v, p};
+  int32_t rc;
+  if ((rc = rv::in_proj_rows_check(in, n, w->wq_len, w->wk_len, w->wv_len, err))) return rc;
+  if ((rc = rv::prefill_chunk_check(kv, layer, n, q_dim, start, err))) return rc;
+  rv::OutProj out{attn, q_dim, w->o_format, w->wo, 0, residual_rows, hidden, true, p};
+  if ((rc = rv::out_proj_rows_check(out, n, w->wo_len, err))) return rc;
+  const size_t need = rv_attn_block_prefill_scratch_bytes(n, hidden, q_dim, kv_dim);
+  if (scratch_len < need) return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, "attn_block_prefill scratch");
+  if (flags & RV_HOST_PTRS) return fail(err, RV_ERR_UNSUPPORTED, flags, 0, "RV_HOST_PTRS (device pointers only)");
+  if (n == 0) {
+    if (err) *err = rv_error{RV_OK, 0, 0, 0, 0, nullptr};
+    return RV_OK;
+  }
+  const struct {
+    const void* p;
+    const char* what;
+  } ptrs[] = {{residual_rows, "residual_rows"}, {w->attn_norm, "attn_norm"}, {w->wq, "wq"},   {w->wk, "wk"},
+              {w->wv, "wv"},                    {w->q_norm, "q_norm"},       {w->k_norm, "k_norm"}, {w->wo, "wo"},
+              {scratch, "scratch"}};
+  for (const auto& ptr : ptrs)
+    if (bad_ptr(ptr.p)) return fail(err, ptr.p ? RV_ERR_UNSUPPORTED : RV_ERR_NULL_ARG, (uintptr_t)ptr.p, 0, ptr.what);
+
+  int prev = -1;
+  if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+  if (prev != kv->device) (void)hipSetDevice(kv->device);
+  const hipStream_t s = kv->stream;
+  rv::HipStatus st = rv::launch_rmsnorm_rows(residual_rows, w->attn_norm, eps, n, hidden, normed, s);
+  if (st.e == hipSuccess) st = rv::in_proj_rows_launch(in, n, s);
+  if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
+  if (!rc)
+    rc = rv_prefill_chunk(kv, layer, q, k, v, n, q_dim, w->q_norm, w->k_norm, eps, theta, start, scale, attn,
+                          flags & RV_PREFILL_MODE_MASK, err);
+  if (!rc) {
+    st = rv::out_proj_rows_launch(out, n, s);
     if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
   }
   if (!rc && (flags & RV_SYNC)) {

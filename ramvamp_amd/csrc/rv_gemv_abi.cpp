@@ -234,8 +234,7 @@ int32_t rv_gemv_q8_0_batched(const uint8_t* weight, size_t weight_len, size_t in
 }
 
 size_t rv_attn_in_proj_rows_scratch_bytes(size_t n_rows, size_t hidden) {
-  return align16(sat_mul(n_rows, hidden / 256 * sizeof(rv_block_q8_k))) +
-         sat_mul(n_rows, hidden / 32 * sizeof(rv_block_q8_0));
+  return rv::in_proj_rows_scratch_bytes(n_rows, hidden);
 }
 
 int32_t rv_attn_in_proj_rows(const float* normed_rows, size_t n_rows, size_t hidden, uint32_t q_format,
@@ -243,77 +242,43 @@ int32_t rv_attn_in_proj_rows(const float* normed_rows, size_t n_rows, size_t hid
                              size_t wk_len, float* k_rows, size_t kv_dim, uint32_t v_format, const uint8_t* wv,
                              size_t wv_len, float* v_rows, void* scratch, size_t scratch_len, void* stream,
                              uint32_t flags, rv_error* err) {
-  // prefill.rs:1985-2053 in order: each row quantized both ways, then the
-  // batched q, k and v projections (their transposes are the store layout).
+  rv::InProj p{normed_rows, nullptr, 0.f, hidden, q_format, wq, 0, q_rows, q_dim, wk, 0, k_rows, kv_dim,
+               v_format, wv, 0, v_rows, scratch};
   int32_t rc;
-  if ((rc = check_quantize(RV_QF_Q8_K, hidden, hidden / 256, err))) return rc;
-  if ((rc = check_quantize(RV_QF_Q8_0, hidden, hidden / 32, err))) return rc;
-  const size_t n = n_rows;
-  if (!k_quant(q_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, q_format, 0, 0, "gemv_q8_k_batched");
-  size_t rb_q, rb_k, rb_v;
-  if ((rc = check_gemv("attn_in_proj_rows q: weight bytes vs rows / out vs range x n_acts", q_format, wq_len, hidden,
-                       q_dim, sat_mul(n, hidden / 256), 0, q_dim, sat_mul(q_dim, n), &rb_q, err, n)))
-    return rc;
-  if ((rc = check_gemv("attn_in_proj_rows k: weight bytes vs rows / out vs range x n_acts", RV_QF_Q8_0, wk_len, hidden,
-                       kv_dim, sat_mul(n, hidden / 32), 0, kv_dim, sat_mul(kv_dim, n), &rb_k, err, n)))
-    return rc;
-  if (!k_quant(v_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, v_format, 0, 0, "gemv_q8_k_batched");
-  if ((rc = check_gemv("attn_in_proj_rows v: weight bytes vs rows / out vs range x n_acts", v_format, wv_len, hidden,
-                       kv_dim, sat_mul(n, hidden / 256), 0, kv_dim, sat_mul(kv_dim, n), &rb_v, err, n)))
-    return rc;
-  const size_t need = rv_attn_in_proj_rows_scratch_bytes(n, hidden);
+  if ((rc = rv::in_proj_rows_check(p, n_rows, wq_len, wk_len, wv_len, err))) return rc;
+  const size_t need = rv_attn_in_proj_rows_scratch_bytes(n_rows, hidden);
   if (scratch_len < need) return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, 0, "attn_in_proj_rows scratch");
   if ((rc = check_flags(flags, err))) return rc;
-  if (n == 0) return finish((hipStream_t)stream, flags, rv::HipStatus{}, err);
+  if (n_rows == 0) return finish((hipStream_t)stream, flags, rv::HipStatus{}, err);
   if (hidden == 0) return fail(err, RV_ERR_UNSUPPORTED, 0, 0, 0, "attn_in_proj_rows with hidden 0");
   if ((rc = check_ptrs(err, {{normed_rows, "normed_rows"}, {wq, "wq"}, {q_rows, "q_rows"}, {wk, "wk"},
                              {k_rows, "k_rows"}, {wv, "wv"}, {v_rows, "v_rows"}, {scratch, "scratch"}})))
     return rc;
   const hipStream_t s = (hipStream_t)stream;
-  auto* acts_k = reinterpret_cast<rv_block_q8_k*>(scratch);
-  auto* acts_0 = reinterpret_cast<rv_block_q8_0*>((char*)scratch + align16(n * (hidden / 256) * sizeof(rv_block_q8_k)));
-  // A row of hidden values is a whole number of blocks of both forms, so the
-  // rows quantized one after another are one quantization of their concatenation.
-  rv::HipStatus st = rv::launch_quantize_q8_k(normed_rows, acts_k, n * (hidden / 256), s);
-  if (st.e == hipSuccess) st = rv::launch_quantize_q8_0(normed_rows, acts_0, n * (hidden / 32), s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_batched(q_format, wq, rb_q, hidden, acts_k, n, 0, q_dim, q_rows, q_dim, true, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_batched(RV_QF_Q8_0, wk, rb_k, hidden, acts_0, n, 0, kv_dim, k_rows, kv_dim, true, s);
-  if (st.e == hipSuccess) st = rv::launch_gemv_batched(v_format, wv, rb_v, hidden, acts_k, n, 0, kv_dim, v_rows, kv_dim, true, s);
-  return finish(s, flags, st, err);
+  return finish(s, flags, rv::in_proj_rows_launch(p, n_rows, s), err);
 }
 
 size_t rv_attn_out_proj_rows_scratch_bytes(size_t n_rows, size_t q_dim) {
-  return sat_mul(n_rows, q_dim / 256 * sizeof(rv_block_q8_k));
+  return rv::out_proj_rows_scratch_bytes(n_rows, q_dim);
 }
 
 int32_t rv_attn_out_proj_rows(const float* attn_rows, size_t n_rows, size_t q_dim, uint32_t o_format,
                               const uint8_t* wo, size_t wo_len, float* residual_rows, size_t hidden, void* scratch,
                               size_t scratch_len, void* stream, uint32_t flags, rv_error* err) {
-  // prefill.rs:2113-2154 (g): each attention row quantized to Q8_K, the
-  // batched o projection, and residual[r][h] += o[h][r] (one f32 add each).
+  rv::OutProj p{attn_rows, q_dim, o_format, wo, 0, residual_rows, hidden, true, scratch};
   int32_t rc;
-  if ((rc = check_quantize(RV_QF_Q8_K, q_dim, q_dim / 256, err))) return rc;
-  const size_t n = n_rows;
-  if (!k_quant(o_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, o_format, 0, 0, "gemv_q8_k_batched");
-  size_t rb;
-  if ((rc = check_gemv("attn_out_proj_rows: weight bytes vs rows / out vs range x n_acts", o_format, wo_len, q_dim,
-                       hidden, sat_mul(n, q_dim / 256), 0, hidden, sat_mul(hidden, n), &rb, err, n)))
-    return rc;
-  const size_t need = rv_attn_out_proj_rows_scratch_bytes(n, q_dim);
+  if ((rc = rv::out_proj_rows_check(p, n_rows, wo_len, err))) return rc;
+  const size_t need = rv_attn_out_proj_rows_scratch_bytes(n_rows, q_dim);
   if (scratch_len < need)
     return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, 0, "attn_out_proj_rows scratch");
   if ((rc = check_flags(flags, err))) return rc;
-  if (n == 0 || hidden == 0) return finish((hipStream_t)stream, flags, rv::HipStatus{}, err);
+  if (n_rows == 0 || hidden == 0) return finish((hipStream_t)stream, flags, rv::HipStatus{}, err);
   if (q_dim == 0) return fail(err, RV_ERR_UNSUPPORTED, 0, 0, 0, "attn_out_proj_rows with q_dim 0");
   if ((rc = check_ptrs(err, {{attn_rows, "attn_rows"}, {wo, "wo"}, {residual_rows, "residual_rows"},
                              {scratch, "scratch"}})))
     return rc;
   const hipStream_t s = (hipStream_t)stream;
-  auto* acts = reinterpret_cast<rv_block_q8_k*>(scratch);
-  rv::HipStatus st = rv::launch_quantize_q8_k(attn_rows, acts, n * (q_dim / 256), s);
-  if (st.e == hipSuccess)
-    st = rv::launch_gemv_batched(o_format, wo, rb, q_dim, acts, n, 0, hidden, residual_rows, hidden, true, s, true);
-  return finish(s, flags, st, err);
+  return finish(s, flags, rv::out_proj_rows_launch(p, n_rows, s), err);
 }
 
 size_t rv_attn_in_proj_scratch_bytes(size_t hidden) { return rv::in_proj_scratch_bytes(hidden, false); }
@@ -455,4 +420,69 @@ HipStatus out_proj_launch(const OutProj& p, hipStream_t s) {
   return st;
 }
 
+size_t in_proj_rows_scratch_bytes(size_t n_rows, size_t hidden) {
+  return align16(sat_mul(n_rows, hidden / 256 * sizeof(rv_block_q8_k))) +
+         sat_mul(n_rows, hidden / 32 * sizeof(rv_block_q8_0));
+}
+
+size_t out_proj_rows_scratch_bytes(size_t n_rows, size_t q_dim) {
+  return sat_mul(n_rows, q_dim / 256 * sizeof(rv_block_q8_k));
+}
+
+int32_t in_proj_rows_check(InProj& p, size_t n, size_t wq_len, size_t wk_len, size_t wv_len, rv_error* err) {
+  // prefill.rs:1985-2053 in order: each row quantized both ways, then the
+  // batched q, k and v projections (their transposes are the store layout).
+  int32_t rc;
+  if ((rc = check_quantize(RV_QF_Q8_K, p.hidden, p.hidden / 256, err))) return rc;
+  if ((rc = check_quantize(RV_QF_Q8_0, p.hidden, p.hidden / 32, err))) return rc;
+  if (!k_quant(p.q_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.q_format, 0, 0, "gemv_q8_k_batched");
+  if ((rc = check_gemv("attn_in_proj_rows q: weight bytes vs rows / out vs range x n_acts", p.q_format, wq_len,
+                       p.hidden, p.q_dim, sat_mul(n, p.hidden / 256), 0, p.q_dim, sat_mul(p.q_dim, n), &p.rb_q, err,
+                       n)))
+    return rc;
+  if ((rc = check_gemv("attn_in_proj_rows k: weight bytes vs rows / out vs range x n_acts", RV_QF_Q8_0, wk_len,
+                       p.hidden, p.kv_dim, sat_mul(n, p.hidden / 32), 0, p.kv_dim, sat_mul(p.kv_dim, n), &p.rb_k, err,
+                       n)))
+    return rc;
+  if (!k_quant(p.v_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.v_format, 0, 0, "gemv_q8_k_batched");
+  return check_gemv("attn_in_proj_rows v: weight bytes vs rows / out vs range x n_acts", p.v_format, wv_len, p.hidden,
+                    p.kv_dim, sat_mul(n, p.hidden / 256), 0, p.kv_dim, sat_mul(p.kv_dim, n), &p.rb_v, err, n);
+}
+
+int32_t out_proj_rows_check(OutProj& p, size_t n, size_t wo_len, rv_error* err) {
+  // prefill.rs:2113-2154 (g): each attention row quantized to Q8_K, the
+  // batched o projection, and residual[r][h] += o[h][r] (one f32 add each).
+  int32_t rc;
+  if ((rc = check_quantize(RV_QF_Q8_K, p.q_dim, p.q_dim / 256, err))) return rc;
+  if (!k_quant(p.o_format)) return fail(err, RV_QUANT_UNSUPPORTED_FORMAT, p.o_format, 0, 0, "gemv_q8_k_batched");
+  return check_gemv("attn_out_proj_rows: weight bytes vs rows / out vs range x n_acts", p.o_format, wo_len, p.q_dim,
+                    p.hidden, sat_mul(n, p.q_dim / 256), 0, p.hidden, sat_mul(p.hidden, n), &p.rb, err, n);
+}
+
+HipStatus in_proj_rows_launch(const InProj& p, size_t n, hipStream_t s) {
+  auto* acts_k = reinterpret_cast<rv_block_q8_k*>(p.scratch);
+  auto* acts_0 =
+      reinterpret_cast<rv_block_q8_0*>((char*)p.scratch + align16(n * (p.hidden / 256) * sizeof(rv_block_q8_k)));
+  // A row of hidden values is a whole number of blocks of both forms, so the
+  // rows quantized one after another are one quantization of their concatenation.
+  HipStatus st = launch_quantize_q8_k(p.x, acts_k, n * (p.hidden / 256), s);
+  if (st.e == hipSuccess) st = launch_quantize_q8_0(p.x, acts_0, n * (p.hidden / 32), s);
+  if (st.e == hipSuccess)
+    st = launch_gemv_batched(p.q_format, p.wq, p.rb_q, p.hidden, acts_k, n, 0, p.q_dim, p.q, p.q_dim, true, s);
+  if (st.e == hipSuccess)
+    st = launch_gemv_batched(RV_QF_Q8_0, p.wk, p.rb_k, p.hidden, acts_0, n, 0, p.kv_dim, p.k, p.kv_dim, true, s);
+  if (st.e == hipSuccess)
+    st = launch_gemv_batched(p.v_format, p.wv, p.rb_v, p.hidden, acts_k, n, 0, p.kv_dim, p.v, p.kv_dim, true, s);
+  return st;
+}
+
+HipStatus out_proj_rows_launch(const OutProj& p, size_t n, hipStream_t s) {
+  auto* acts = reinterpret_cast<rv_block_q8_k*>(p.scratch);
+  HipStatus st = launch_quantize_q8_k(p.x, acts, n * (p.q_dim / 256), s);
+  if (st.e == hipSuccess)
+    st = launch_gemv_batched(p.o_format, p.wo, p.rb, p.q_dim, acts, n, 0, p.hidden, p.o, p.hidden, true, s, true);
+  return st;
+}
+
 }  // namespace rv
+

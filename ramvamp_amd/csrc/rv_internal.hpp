@@ -161,5 +161,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
 // rv_decode_step's validation alone (no launch), for callers that validate
 // a whole composite call before launching any of it.
 int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err);
+// rv_prefill_chunk's validation alone.
+int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start, rv_error* err);
 
 }  // namespace rv

@@ -457,6 +457,19 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
   }
 }
 
+// One workgroup per row: out[r] = rmsnorm(x[r], w, eps) over n values.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float eps, int n, float* __restrict__ out) {
+  __shared__ double red[4];
+  const float* xr = x + (size_t)blockIdx.x * n;
+  float* orow = out + (size_t)blockIdx.x * n;
+  const float inv = block_inv_rms<256>(xr, n, eps, red);
+  for (int j = threadIdx.x; j < n; j += 256) {
+#pragma clang fp contract(off)
+    orow[j] = xr[j] * inv * w[j];
+  }
+}
+
 __global__ __launch_bounds__(256) void vec_add_kernel(float* __restrict__ a, const float* __restrict__ b, long n) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i < n) a[i] += b[i];
@@ -944,6 +957,16 @@ HipStatus launch_gemv_batched(uint32_t fmt, const uint8_t* w, size_t row_bytes, 
   }
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "batched gemv launch";
+  return st;
+}
+
+HipStatus launch_rmsnorm_rows(const float* x, const float* w, float eps, size_t n_rows, size_t n, float* out,
+                              hipStream_t s) {
+  HipStatus st;
+  if (n_rows == 0) return st;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)n_rows), dim3(256), 0, s, x, w, eps, (int)n, out);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "rmsnorm rows launch";
   return st;
 }
 

@@ -78,6 +78,18 @@ int32_t in_proj_check(InProj& p, size_t wq_len, size_t wk_len, size_t wv_len, rv
 int32_t out_proj_check(OutProj& p, size_t wo_len, rv_error* err);
 HipStatus in_proj_launch(const InProj& p, hipStream_t s);
 HipStatus out_proj_launch(const OutProj& p, hipStream_t s);
+// The same for n_rows rows of a prefill chunk (prefill.rs:1985-2053,
+// :2113-2154): x and the outputs row-major; the out form adds into o (the
+// residual rows). p.scratch holds the rows' quantized blocks.
+size_t in_proj_rows_scratch_bytes(size_t n_rows, size_t hidden);
+size_t out_proj_rows_scratch_bytes(size_t n_rows, size_t q_dim);
+int32_t in_proj_rows_check(InProj& p, size_t n_rows, size_t wq_len, size_t wk_len, size_t wv_len, rv_error* err);
+int32_t out_proj_rows_check(OutProj& p, size_t n_rows, size_t wo_len, rv_error* err);
+HipStatus in_proj_rows_launch(const InProj& p, size_t n_rows, hipStream_t s);
+HipStatus out_proj_rows_launch(const OutProj& p, size_t n_rows, hipStream_t s);
+// out[r] = rmsnorm(x[r], w, eps), n_rows rows of n values.
+HipStatus launch_rmsnorm_rows(const float* x, const float* w, float eps, size_t n_rows, size_t n, float* out,
+                              hipStream_t s);
 
 HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s);
 HipStatus launch_quantize_q8_0(const float* x, rv_block_q8_0* out, size_t n_blocks, hipStream_t s);

@@ -188,3 +188,45 @@ def test_attn_block_errors_leave_residual_and_cache_untouched():
         B.attn_block_decode(kv, 1, res, q_dim, w, EPS, THETA, 5, 0.1)
     assert ei.value.variant == "CapacityExceeded"
     assert np.array_equal(res.cpu().numpy(), before) and kv.len(1) == 5
+
+
+@pytest.mark.parametrize("mode,tol", [("exact", 2e-3), ("f16", 1e-2)])
+def test_attn_block_prefill_matches_the_oracle_composition(mode, tol):
+    """prefill.rs:1975-2154 for a 37-row chunk after 40 cached rows, then a
+    second chunk: per-row rmsnorm, quantizations, batched q/k/v (bit-identical
+    to the oracle's GEMVs on the oracle's normalized rows), the chunk's
+    attention (EXACT: fp32-equivalent; F16: f16 MFMA inputs) and the batched
+    o projection added into the residual rows. The residual is held to tol of
+    max|o| (one quantum of a quantized attention value moves o by one step)."""
+    torch = torch_cuda()
+    Q = oracle
+    rng = np.random.default_rng(0xB10F)
+    hidden, n_heads, n_kv, hd = 2048, 32, 4, 128
+    q_dim, kv_dim = n_heads * hd, n_kv * hd
+    lay = Layer(torch, rng, hidden, q_dim, kv_dim, hd, Q.RV_QF_Q4_K, Q.RV_QF_Q6_K, Q.RV_QF_Q5_K)
+    n_pos, n = 40, 37
+    kv, ref = twin(Rng(0xB1), 2, n_kv, hd, n_pos, n_pos + 2 * n, "f32")
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    start = n_pos
+    for chunk in range(2):
+        say(f"case prefill block mode={mode} chunk {chunk} start {start}")
+        res = (1.5 * rng.standard_normal((n, hidden))).astype(np.float32)
+        res_dev = torch.from_numpy(res.copy()).cuda()
+        B.attn_block_prefill(kv, 1, res_dev, q_dim, lay.dev, EPS, THETA, start, scale, mode=mode)
+        torch.cuda.synchronize()
+        got = res_dev.cpu().numpy()
+        normed = [oracle.rmsnorm(res[r], lay.attn_norm, EPS) for r in range(n)]
+        ak = [oracle.quantize_row_q8_k(x) for x in normed]
+        a0 = [oracle.quantize_row_q8_0(x) for x in normed]
+        q = np.stack([oracle.gemv(lay.q_fmt, lay.wq, hidden, q_dim, a) for a in ak])
+        k = np.stack([oracle.gemv(Q.RV_QF_Q8_0, lay.wk, hidden, kv_dim, a) for a in a0])
+        v = np.stack([oracle.gemv(lay.v_fmt, lay.wv, hidden, kv_dim, a) for a in ak])
+        attn = ref.prefill_chunk(1, q, k, v, lay.q_norm, lay.k_norm, EPS, THETA, start, scale)
+        o = np.stack([oracle.gemv(lay.o_fmt, lay.wo, q_dim, hidden, oracle.quantize_row_q8_k(attn[r]))
+                      for r in range(n)])
+        want = (res + o).astype(np.float32)
+        err = np.max(np.abs(got.astype(np.float64) - want)) / np.max(np.abs(o))
+        say(f"prefill block {mode} chunk {chunk}: residual max|err|/max|o| {err:.2e}")
+        assert err <= tol, f"{mode} chunk {chunk}"
+        assert kv.len(1) == start + n and kv.len(0) == n_pos
+        start += n
