@@ -392,8 +392,7 @@ HipStatus in_proj_launch(const InProj& p, hipStream_t s) {
     st = launch_rmsnorm(p.x, p.norm_w, p.eps, p.hidden, normed, s);
     x = normed;
   }
-  if (st.e == hipSuccess) st = launch_quantize_q8_k(x, acts_k, p.hidden / 256, s);
-  if (st.e == hipSuccess) st = launch_quantize_q8_0(x, acts_0, p.hidden / 32, s);
+  if (st.e == hipSuccess) st = launch_quantize_both(x, acts_k, acts_0, p.hidden / 256, s);
   if (st.e == hipSuccess) st = launch_gemv_rows(p.q_format, p.wq, p.rb_q, p.hidden, acts_k, 0, p.q_dim, p.q, s);
   if (st.e == hipSuccess) st = launch_gemv_rows(RV_QF_Q8_0, p.wk, p.rb_k, p.hidden, acts_0, 0, p.kv_dim, p.k, s);
   if (st.e == hipSuccess) st = launch_gemv_rows(p.v_format, p.wv, p.rb_v, p.hidden, acts_k, 0, p.kv_dim, p.v, s);
@@ -465,8 +464,7 @@ HipStatus in_proj_rows_launch(const InProj& p, size_t n, hipStream_t s) {
       reinterpret_cast<rv_block_q8_0*>((char*)p.scratch + align16(n * (p.hidden / 256) * sizeof(rv_block_q8_k)));
   // A row of hidden values is a whole number of blocks of both forms, so the
   // rows quantized one after another are one quantization of their concatenation.
-  HipStatus st = launch_quantize_q8_k(p.x, acts_k, n * (p.hidden / 256), s);
-  if (st.e == hipSuccess) st = launch_quantize_q8_0(p.x, acts_0, n * (p.hidden / 32), s);
+  HipStatus st = launch_quantize_both(p.x, acts_k, acts_0, n * (p.hidden / 256), s);
   if (st.e == hipSuccess)
     st = launch_gemv_batched(p.q_format, p.wq, p.rb_q, p.hidden, acts_k, n, 0, p.q_dim, p.q, p.q_dim, true, s);
   if (st.e == hipSuccess)

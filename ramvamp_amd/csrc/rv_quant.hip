@@ -307,6 +307,23 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
   quantize_block_q8_0(x + (size_t)b * 32, out + b, t & 31);
 }
 
+// Both forms in one launch: wave b quantizes 256-value block b to Q8_K and
+// its eight 32-value blocks to Q8_0 (each half-wave four of them), with the
+// same per-block code as the two kernels above, so the same bytes.
+__global__ __launch_bounds__(256) void quantize_both_kernel(const float* __restrict__ x, rv_block_q8_k* __restrict__ ok,
+                                                            rv_block_q8_0* __restrict__ o0, int n_blocks) {
+  const int b = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= n_blocks) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const float* xb = x + (size_t)b * 256;
+  quantize_block_q8_k(xb, ok + b, lane);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sb = 2 * i + (lane >> 5);
+    quantize_block_q8_0(xb + 32 * sb, o0 + (size_t)b * 8 + sb, lane & 31);
+  }
+}
+
 __device__ __forceinline__ float row_dot(uint32_t fmt, const uint8_t* row, int nb, const void* acts, int lane) {
   switch (fmt) {
     case RV_QF_Q4_K: return kq_row<RV_QF_Q4_K>(row, nb, (const rv_block_q8_k*)acts, lane);
@@ -970,4 +987,16 @@ HipStatus launch_rmsnorm_rows(const float* x, const float* w, float eps, size_t 
   return st;
 }
 
+HipStatus launch_quantize_both(const float* x, rv_block_q8_k* ok, rv_block_q8_0* o0, size_t n_k_blocks,
+                               hipStream_t s) {
+  HipStatus st;
+  if (n_k_blocks == 0) return st;
+  hipLaunchKernelGGL(quantize_both_kernel, dim3((unsigned)((n_k_blocks + 3) / 4)), dim3(256), 0, s, x, ok, o0,
+                     (int)n_k_blocks);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "quantize launch";
+  return st;
+}
+
 }  // namespace rv
+

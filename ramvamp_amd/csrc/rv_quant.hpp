@@ -93,6 +93,10 @@ HipStatus launch_rmsnorm_rows(const float* x, const float* w, float eps, size_t 
 
 HipStatus launch_quantize_q8_k(const float* x, rv_block_q8_k* out, size_t n_blocks, hipStream_t s);
 HipStatus launch_quantize_q8_0(const float* x, rv_block_q8_0* out, size_t n_blocks, hipStream_t s);
+// Both forms of n_k_blocks * 256 values in one launch (Q8_K blocks to ok,
+// 8 n_k_blocks Q8_0 blocks to o0).
+HipStatus launch_quantize_both(const float* x, rv_block_q8_k* ok, rv_block_q8_0* o0, size_t n_k_blocks,
+                               hipStream_t s);
 // out[i] = row(row_lo + i) . acts, i < n_rows; acts quantized blocks
 // (Q8_K, or Q8_0 for RV_QF_Q8_0) in global memory.
 HipStatus launch_gemv_rows(uint32_t fmt, const uint8_t* w, size_t row_bytes, size_t in_dim, const void* acts,
