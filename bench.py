@@ -359,6 +359,25 @@ def bench_attn_block_prefill(torch, rv, synth, mode="f16", iters=20):
             "us_per_token": round(per * 1e6 / rows, 4)}
 
 
+def bench_router(torch, rv, iters=50, n_experts=128, hidden=2048, top_k=8):
+    """The router decision (forward.rs:2658-2705) for one decode row and for
+    a 512-row prefill chunk, 128 experts over a 2048-wide row, top 8 with
+    renormalization, host-timed back to back."""
+    from ramvamp_amd import router as R
+    rng = np.random.default_rng(0x40)
+    w = torch.from_numpy((rng.standard_normal((n_experts, hidden)) * 0.03).astype(np.float32)).cuda()
+    out = {}
+    for rows in (1, 512):
+        x = torch.from_numpy(rng.standard_normal((rows, hidden)).astype(np.float32)).cuda()
+        ex = torch.empty(rows, top_k, dtype=torch.int32, device="cuda")
+        wt = torch.empty(rows, top_k, device="cuda")
+        fn = lambda: R.router_topk(x, w, top_k, True, ex, wt)
+        for _ in range(3):
+            fn()
+        out[f"us_{rows}_rows"] = round(timed(torch, fn, iters) / iters * 1e6, 2)
+    return out
+
+
 def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
     """One token's attention blocks over config 2's 48 layers (ctx 4096, fp32
     KV): rv_attn_block_decode per layer (model/forward.rs:2570-2650: RMSNorm,
@@ -515,6 +534,8 @@ def main():
             f"{rpp['int8_tops']:.1f} int8 TOP/s")
         return
     if args.block_only:
+        rr = bench_router(torch, rv)
+        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")
         rb = bench_attn_block(torch, rv, synth)
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
         for mode in ("f16", "exact"):
@@ -552,6 +573,9 @@ def main():
         rb = bench_attn_block(torch, rv, synth)
         extra["attn_block_decode_layer"] = rb
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        rr = bench_router(torch, rv)
+        extra["router_128x2048_top8"] = rr
+        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")
         for mode in ("f16", "exact"):
             rbp = bench_attn_block_prefill(torch, rv, synth, mode)
             extra[f"attn_block_prefill_config4_{mode}"] = rbp

@@ -114,6 +114,8 @@ def lib():
         "rvo_vec_dot_q8_0": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, fp, E]),
         "rvo_gemv_q8_k": (c_int32, [c_uint32, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_size_t, c_size_t,
                                     c_size_t, c_size_t, c_void_p, c_size_t, E]),
+        "rvo_router_topk": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t, c_int, c_void_p, c_void_p,
+                                      c_void_p]),
         "rvo_gemv_q8_0": (c_int32, [c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_size_t, c_size_t, c_size_t,
                                     c_size_t, c_void_p, c_size_t, E]),
     }
@@ -421,4 +423,21 @@ def gemv(fmt: int, weight, in_dim: int, out_dim: int, acts, n_acts: int = 1, row
                                  n_acts, lo, hi, _ptr(out), out.size, byref(err))
     _check(rc, err)
     return out
+
+
+RV_FWD_INVALID_TOP_K = 48
+RV_PRIM_EMPTY = 26
+
+
+def router_topk(x, router, n_experts: int, top_k: int, norm: bool):
+    """forward.rs:2658-2705 for one row: (experts uint32 [top_k], weights float32 [top_k])."""
+    x, router = _f32(x).ravel(), _f32(router).ravel()
+    probs = np.zeros(max(1, n_experts), np.float32)
+    experts = np.zeros(max(1, top_k), np.uint32)
+    weights = np.zeros(max(1, top_k), np.float32)
+    rc = lib().rvo_router_topk(_ptr(x), x.size, _ptr(router), n_experts, top_k, int(bool(norm)), _ptr(probs),
+                               experts.ctypes.data, _ptr(weights))
+    if rc:
+        raise OracleError(rc)
+    return experts[:top_k], weights[:top_k]
 

@@ -825,3 +825,42 @@ int32_t rvo_prefill_chunk(rvo_kv* kv, size_t layer, float* q_rows, float* k_rows
   return rvo_scatter_attention(kv, layer, start, rows, q_dim, scale, q_rows, out, threads,
                                force_scalar, err);
 }
+
+/* model/forward.rs:2658-2705, one row: logits by dot_f32 (forward.rs:
+ * 1231-1238, serial f32, each product rounded), softmax (softmax.rs:18-40),
+ * top_k scans (strict >: the first index wins ties; the winner set to -inf),
+ * then with norm the f32 sum of the selection in order and one division
+ * each. probs is scratch of n_experts floats. */
+int32_t rvo_router_topk(const float* x, size_t hidden, const float* router, size_t n_experts, size_t top_k,
+                        int norm, float* probs, uint32_t* experts, float* weights) {
+  if (top_k == 0 || top_k > n_experts) return RV_FWD_INVALID_TOP_K;
+  if (hidden == 0) return RV_PRIM_EMPTY;
+  for (size_t e = 0; e < n_experts; ++e) {
+    const float* w = router + e * hidden;
+    float acc = 0.0f;
+    for (size_t i = 0; i < hidden; ++i) {
+      const float p = w[i] * x[i];
+      acc += p;
+    }
+    probs[e] = acc;
+  }
+  rvo_softmax(probs, n_experts);
+  for (size_t k = 0; k < top_k; ++k) {
+    size_t best_e = 0;
+    float best_p = -INFINITY;
+    for (size_t e = 0; e < n_experts; ++e)
+      if (probs[e] > best_p) {
+        best_p = probs[e];
+        best_e = e;
+      }
+    experts[k] = (uint32_t)best_e;
+    weights[k] = best_p;
+    probs[best_e] = -INFINITY;
+  }
+  if (norm) {
+    float s = 0.0f;
+    for (size_t k = 0; k < top_k; ++k) s += weights[k];
+    for (size_t k = 0; k < top_k; ++k) weights[k] = weights[k] / s;
+  }
+  return RV_OK;
+}

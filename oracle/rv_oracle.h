@@ -21,6 +21,7 @@
 
 #include "../include/ramvamp_attn.h"
 #include "../include/ramvamp_gemv.h"
+#include "../include/ramvamp_router.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -144,6 +145,10 @@ int32_t rvo_gemv_q8_k(uint32_t format, const uint8_t* weight, size_t weight_len,
 int32_t rvo_gemv_q8_0(const uint8_t* weight, size_t weight_len, size_t in_dim, size_t out_dim,
                       const rv_block_q8_0* acts, size_t act_blocks, size_t n_acts, size_t row_lo, size_t row_hi,
                       float* out, size_t out_len, rv_error* err);
+
+/* model/forward.rs:2658-2705: one row's router decision (probs: n_experts floats of scratch). */
+int32_t rvo_router_topk(const float* x, size_t hidden, const float* router, size_t n_experts, size_t top_k,
+                        int norm, float* probs, uint32_t* experts, float* weights);
 
 #ifdef __cplusplus
 }

@@ -37,4 +37,4 @@ from ._lib import (  # noqa: F401  (knobs of KvCache.set_tuning)
     RV_TUNE_PREFILL_KV_SPLIT,
     RV_TUNE_PREFILL_ROWS,
 )
-from . import block, projections  # noqa: F401,E402
+from . import block, projections, router  # noqa: F401,E402

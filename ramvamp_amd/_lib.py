@@ -122,6 +122,8 @@ SIGNATURES = {
     "rv_attn_out_proj_scratch_bytes": (c_size_t, [c_size_t]),
     "rv_attn_out_proj": (c_int32, [_P, c_size_t, c_uint32, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_uint32,
                                    _E]),
+    "rv_router_topk": (c_int32, [_P, c_size_t, c_size_t, _P, c_size_t, c_size_t, c_size_t, c_int, _P, _P, _P,
+                                 c_uint32, _E]),
     "rv_attn_block_scratch_bytes": (c_size_t, [c_size_t, c_size_t, c_size_t]),
     "rv_attn_block_prefill_scratch_bytes": (c_size_t, [c_size_t, c_size_t, c_size_t, c_size_t]),
     "rv_attn_block_prefill": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, c_size_t, POINTER(RvAttnBlockWeights),

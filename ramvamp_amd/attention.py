@@ -53,6 +53,7 @@ _VARIANTS = {
     42: ("KernelError", "BlockCountMismatch", ("weight_blocks", "activation_blocks")),
     43: ("KernelError", "QuantizeLenMismatch", ("format", "floats", "out_blocks")),
     44: ("KernelError", "UnsupportedFormat", ("format",)),
+    48: ("ForwardError", "InvalidTopK", ("top_k", "n_experts")),
 }
 
 

@@ -14,6 +14,7 @@
 
 #include "rv_internal.hpp"
 #include "../../include/ramvamp_gemv.h"
+#include "../../include/ramvamp_router.h"
 
 namespace {
 
@@ -343,6 +344,7 @@ const char* rv_status_name(int32_t code) {
     case RV_PRIM_INVALID_HEAD_DIM: return "RV_PRIM_INVALID_HEAD_DIM";
     case RV_PRIM_LENGTH_MISMATCH: return "RV_PRIM_LENGTH_MISMATCH";
     case RV_PRIM_EMPTY: return "RV_PRIM_EMPTY";
+    case RV_FWD_INVALID_TOP_K: return "RV_FWD_INVALID_TOP_K";
     case RV_ERR_NULL_ARG: return "RV_ERR_NULL_ARG";
     case RV_ERR_UNSUPPORTED: return "RV_ERR_UNSUPPORTED";
     case RV_ERR_HIP: return "RV_ERR_HIP";
