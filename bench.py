@@ -184,6 +184,33 @@ def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
             "mfma_frac_kernel": round(flops / k_avg / 1e12 / MFMA_F16_PEAK_TFLOPS, 4), "flops": flops}
 
 
+def bench_config1(torch, rv, synth, iters=50):
+    """Config 1: the fused decode step (q/k RMSNorm + RoPE, append, attention)
+    at position 512 after 512 cached rows, fp32 KV; the cache truncated back
+    to 512 between calls. Bytes: the K and V head slices of 513 positions
+    read once, q and out."""
+    start = 512
+    kv = rv.KvCache(1, 4, 128, start + 1, "f32")
+    K, V = synth.cached_kv(1, 0, start)
+    kv.append_rows(0, K, V)
+    q, k, v = (torch.from_numpy(a[0].copy()).cuda() for a in synth.new_rows(1, 1))
+    wq, wk = (torch.from_numpy(synth.norm_weight(1, t)).cuda() for t in (synth.T_QN, synth.T_KN))
+    out = torch.zeros_like(q)
+
+    def once():
+        kv.truncate(start)
+        rv.decode_step(kv, 0, q, k, v, wq, wk, synth.EPS, synth.THETA, start, synth.SCALE, out)
+
+    for _ in range(3):
+        once()
+    wall = timed(torch, once, iters) / iters
+    k_avg, _ = kernel_avg(torch, kv, once, iters, lead_cycles=400_000)
+    nbytes = 2 * (start + 1) * 512 * 4 + 2 * 4096 * 4
+    return {"us_per_call": round(wall * 1e6, 2), "us_attention_kernel": round(k_avg * 1e6, 2),
+            "gbs_kernel": round(nbytes / k_avg / 1e9, 1), "hbm_frac_kernel": round(nbytes / k_avg / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_call": nbytes}
+
+
 def bench_config5(torch, rv, synth, iters=50, n_caches=5):
     """ctx 32,768 f16 KV, rotating 5 distinct caches (335 MB) past the 256 MB MALL."""
     n = 32768
@@ -457,6 +484,64 @@ def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
     }
 
 
+def cpu_configs(synth, threads):
+    """The oracle (the reference's CPU path restated, its kv-head fan-out over
+    `threads`) on bounded samples of configs 1, 3, 4 and 5, on this host.
+    Prefill samples the chunk's first rows and scales by the causal work
+    (row r attends start + r + 1 positions); decode times whole calls."""
+    import oracle
+    res = {}
+    # Config 1: the fused decode step after 512 cached rows.
+    ref = oracle.KvCache(1, 4, 128, 513, oracle.RV_ELEM_F32)
+    K, V = synth.cached_kv(1, 0, 512)
+    ref.append_rows(0, K, V)
+    q, k, v = (a[0] for a in synth.new_rows(1, 1))
+    wq, wk = synth.norm_weight(1, synth.T_QN), synth.norm_weight(1, synth.T_KN)
+    times = []
+    for i in range(21):  # the first call warms up (not timed)
+        ref.truncate(512)
+        t0 = time.perf_counter()
+        ref.decode_step(0, q, k, v, wq, wk, synth.EPS, synth.THETA, 512, synth.SCALE, threads=threads)
+        if i:
+            times.append(time.perf_counter() - t0)
+    res["config1"] = {"us_per_call": round(float(np.median(times)) * 1e6, 1), "cores": threads, "kind": "port",
+                      "sample": "20 decode steps, median"}
+    # Configs 3 and 4: the first rows of the chunk, scaled to 512 rows.
+    for cfg, sample in ((3, 64), (4, 16)):
+        c = synth.CONFIGS[cfg]
+        start = c.context
+        ref = oracle.KvCache(1, 4, 128, start + sample, oracle.RV_ELEM_F32)
+        if start:
+            K, V = synth.cached_kv(cfg, 0, start)
+            ref.append_rows(0, K, V)
+        q, k, v = synth.new_rows(cfg, sample)
+        wq, wk = synth.norm_weight(cfg, synth.T_QN), synth.norm_weight(cfg, synth.T_KN)
+        t0 = time.perf_counter()
+        ref.prefill_chunk(0, q, k, v, wq, wk, synth.EPS, synth.THETA, start, synth.SCALE, threads=threads)
+        dt = time.perf_counter() - t0
+        work = lambda rows: rows * start + rows * (rows + 1) // 2
+        est = dt * work(c.rows) / work(sample)
+        flops = prefill_flops(c.rows, start)
+        res[f"config{cfg}"] = {"us_per_call": round(est * 1e6, 1), "tflops": round(flops / est / 1e12, 5),
+                               "cores": threads, "kind": "port",
+                               "sample": f"first {sample} of {c.rows} rows, scaled by causal work"}
+    # Config 5: decode over 32768 f16 positions.
+    ref = oracle.KvCache(1, 4, 128, 32768, oracle.RV_ELEM_F16)
+    K, V = synth.cached_kv(5, 0, 32768)
+    ref.append_rows(0, K, V)
+    q5 = synth.normal(synth.seed(5, synth.T_Q), synth.Q_DIM)
+    ref.pool_decode_attention(q5, 0, float(synth.SCALE), threads)  # warm-up
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        ref.pool_decode_attention(q5, 0, float(synth.SCALE), threads)
+        times.append(time.perf_counter() - t0)
+    per = float(np.median(times))
+    res["config5"] = {"us_per_call": round(per * 1e6, 1), "gbs": round(67141632 / per / 1e9, 3), "cores": threads,
+                      "kind": "port", "sample": "5 decode calls, median"}
+    return res
+
+
 def cpu_projections(budget_s=4.0):
     """The oracle's scalar projections (quantize both ways, the q/k/v GEMVs,
     quantize, the o GEMV; kernels/quants/dot.rs, one thread) at the bench
@@ -560,6 +645,9 @@ def main():
             extra[f"config{cfg}_prefill_{mode}"] = r
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")
+        r1 = bench_config1(torch, rv, synth)
+        extra["config1_decode_step_ctx512"] = r1
+        log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us")
         r5 = bench_config5(torch, rv, synth)
         extra["config5_decode_f16_ctx32768"] = r5
         log(f"config 5: {r5['us_per_call']:.2f} us/call, kernel {r5['us_kernel']:.2f} us, {r5['gbs_kernel']:.0f} GB/s")
@@ -586,6 +674,11 @@ def main():
         cpu = cpu_baseline(synth)
         if "projections_decode_layer" in extra:
             extra["projections_decode_layer"]["cpu_baseline"] = cpu_projections()
+            threads = max(1, min(4, os.cpu_count() or 1))
+            for name, r in cpu_configs(synth, threads).items():
+                for key in extra:
+                    if key.startswith(name + "_"):
+                        extra[key]["cpu_baseline"] = r
     traffic = traffic_from_profile(DECODE_PROFILE)
     line = {
         "metric": "decode attn µs/layer + HBM GB/s at ctx 4096; prefill attn TFLOP/s (512 tok)",
