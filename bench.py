@@ -448,7 +448,7 @@ def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
     kv_bytes = 2 * 4099 * 512 * 4
     return {"us_per_layer": round(per * 1e6, 3), "ms_per_token_48_layers": round(per * n_layers * 1e3, 3),
             "bytes_per_layer": wbytes + kv_bytes, "gbs": round((wbytes + kv_bytes) / per / 1e9, 1),
-            "launches_per_layer": 5, "distinct_weight_sets": n_sets, "context": 4099}
+            "launches_per_layer": 4, "distinct_weight_sets": n_sets, "context": 4099}
 
 
 def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):

@@ -9,11 +9,12 @@
  *   residual += Wo . quantize_q8_k(attn_out)              (:2636-2650)
  *
  * It replaces that sequence of host calls (and the host round trips of q, k,
- * v and attn_out between them) with five launches on the cache's stream:
+ * v and attn_out between them) with four launches on the cache's stream:
  * the input projections with the RMSNorm fused into each workgroup's
- * activation quantization, the row prologue (norm, RoPE, append), the
- * attention and its split merge, and the output projection with the residual
- * add fused into its stores. Captured into one graph per token, the 48
+ * activation quantization, the attention (its query heads normalized and
+ * rotated as they load, the token's k and v rows normalized, rotated and
+ * appended by the workgroup of the last split) and its split merge, and the
+ * output projection with the residual add fused into its stores. Captured into one graph per token, the 48
  * layers' blocks replay with no host work between them.
  *
  * Conventions are those of ramvamp_attn.h and ramvamp_gemv.h: device

@@ -688,11 +688,30 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
     dout = st.carve(q_len);
     if (st.e != hipSuccess) return hip_fail(err, st.e, "hipMemcpyAsync H2D");
   }
-  rv::HipStatus hs = rv::ensure_qbuf(kv, q_len * sizeof(float));
-  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   rv::InvFreq inv;
   rv::fill_inv_freq(inv, hd, theta);
   const size_t n_q = q_len / hd;
+  if (rv::decode_pro_supported(kv, n_q)) {
+    // One launch (plus the split merge): the prologue runs in the tile
+    // kernel; (cos, sin) of the position in f64, as rope.rs:35-39.
+    rv::DecodePro pro{dk, dv, dwq, dwk, eps, {}, {}};
+    const double pos = (double)position;
+    for (size_t i = 0; i < hd / 2; ++i) {
+      double sd, cd;
+      sincos(pos * inv.f[i], &sd, &cd);
+      pro.cs[i] = (float)cd;
+      pro.sn[i] = (float)sd;
+    }
+    kv->lens[layer] = len + 1;
+    rv::HipStatus hs = rv::launch_decode_pro(kv, dq, n_q, layer, len + 1, scale, pro, dout, kv->stream);
+    if (hs.e != hipSuccess) {
+      kv->lens[layer] = len;
+      return hip_fail(err, hs.e, hs.what);
+    }
+    return finish(kv, flags, dout, out, q_len, err);
+  }
+  rv::HipStatus hs = rv::ensure_qbuf(kv, q_len * sizeof(float));
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   // q and k rotate at `position` (forward.rs:2628-2629); the row lands at
   // the layer's cursor.
   hs = rv::launch_row_prologue(kv, layer, len, dq, kv->qbuf, n_q, dk, dv, 1, dwq, dwk, eps, inv, position, nullptr,

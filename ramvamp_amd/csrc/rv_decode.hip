@@ -30,6 +30,7 @@
 #include "rv_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace rv {
 namespace {
@@ -248,6 +249,19 @@ __global__ __launch_bounds__(W * 64) void decode_split_kernel(const float* __res
   }
 }
 
+// A plane element as the cache holds it: f32, or f16 bits with the
+// reference's round-to-nearest-even (kv/mod.rs append).
+template <typename T>
+__device__ __forceinline__ void store_plane(T* p, float v);
+template <>
+__device__ __forceinline__ void store_plane<float>(float* p, float v) {
+  *p = v;
+}
+template <>
+__device__ __forceinline__ void store_plane<_Float16>(_Float16* p, float v) {
+  *reinterpret_cast<uint16_t*>(p) = f32_to_f16_bits(v);
+}
+
 // ---- MFMA path ----------------------------------------------------------------------
 
 // 16-byte vector of plane elements: 4 fp32 or 8 f16.
@@ -285,12 +299,21 @@ struct Chunk<_Float16> {
 // tile's after the current one is computed. The waves merge through LDS; the
 // workgroup writes `out` (one split) or its partial (o, max, sum) row for
 // decode_merge_kernel.
-template <typename T, int W>
-__global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __restrict__ q, const T* __restrict__ kl,
-                                                             const T* __restrict__ vl, int kv_dim, int positions,
+// With PRO the decode step's prologue runs here too (DecodePro): the planes
+// are then written (the token's row) as well as read, so they are not
+// declared __restrict__ (a restrict-qualified read-only plane would let the
+// compiler treat its loads as unclobbered by the row's store).
+struct NoPro {};
+template <bool PRO, typename T>
+using PlanePtr = std::conditional_t<PRO, const T*, const T* __restrict__>;
+
+template <typename T, int W, bool PRO = false>
+__global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __restrict__ q, PlanePtr<PRO, T> kl,
+                                                             PlanePtr<PRO, T> vl, int kv_dim, int positions,
                                                              int split_len, int n_splits, int group, int kv_lo,
                                                              float qscale, float* __restrict__ part,
-                                                             float* __restrict__ out) {
+                                                             float* __restrict__ out,
+                                                             std::conditional_t<PRO, DecodePro, NoPro> pro = {}) {
   typedef typename Chunk<T>::type CT;
   constexpr int E = Chunk<T>::n;
   constexpr int NKC = 32 / E;  // K chunks per lane per tile
@@ -308,6 +331,32 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   const size_t col = (size_t)kvh * kD;
   const bool col_ok = li < group;
 
+  if constexpr (PRO) {
+    // The token's row (position positions - 1) lives in the last split:
+    // wave 0 writes this kv head's k (RMSNorm, then the rotation of pairs
+    // (i, i + 64), as norm.rs:18-26 and rope.rs:31-45, contraction off) and
+    // v into the cache row; the barrier makes them visible to the tiles.
+    if (split == n_splits - 1) {
+      if (wave == 0) {
+#pragma clang fp contract(off)
+        const float* kr = pro.k + col;
+        const float* vr = pro.v + col;
+        const float k0 = kr[lane], k1 = kr[lane + 64];
+        const double ss = wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1);
+        const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)pro.eps));
+        const float a0 = k0 * inv * pro.k_w[lane], a1 = k1 * inv * pro.k_w[lane + 64];
+        const float c = pro.cs[lane], sn = pro.sn[lane];
+        T* krow = const_cast<T*>(kl) + (size_t)(positions - 1) * kv_dim + col;
+        T* vrow = const_cast<T*>(vl) + (size_t)(positions - 1) * kv_dim + col;
+        store_plane<T>(krow + lane, a0 * c - a1 * sn);
+        store_plane<T>(krow + lane + 64, a0 * sn + a1 * c);
+        store_plane<T>(vrow + lane, vr[lane]);
+        store_plane<T>(vrow + lane + 64, vr[lane + 64]);
+      }
+      __threadfence_block();
+      __syncthreads();
+    }
+  }
   float qv[32];
   {
     // q may be only 4-byte aligned: scalar loads (once per workgroup).
@@ -335,6 +384,28 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   // then complete under theirs).
   const float qsc = col_ok ? qscale : 0.f;
   auto scale_q = [&]() {
+    if constexpr (PRO) {
+#pragma clang fp contract(off)
+      // RMSNorm of head li over its 128 values (this lane holds 32, the
+      // lanes 16 and 32 apart the rest), then the rotation of pairs
+      // (d, d + 64): chunks c and c + NKC / 2 of the same lane.
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ss += (double)qv[i] * (double)qv[i];
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)pro.eps));
+#pragma unroll
+      for (int c = 0; c < NKC / 2; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int d = E * (lk + 4 * c) + e;  // < 64
+          const float a0 = qv[c * E + e] * inv * pro.q_w[d];
+          const float a1 = qv[(c + NKC / 2) * E + e] * inv * pro.q_w[d + 64];
+          qv[c * E + e] = a0 * pro.cs[d] - a1 * pro.sn[d];
+          qv[(c + NKC / 2) * E + e] = a0 * pro.sn[d] + a1 * pro.cs[d];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 32; ++i) qv[i] *= qsc;
   };
@@ -675,10 +746,57 @@ static void launch_tile(const TimedPair& tp, int waves, dim3 grid, hipStream_t s
                         float qscale, float* part, float* out) {
   if (waves == 8)
     launch_timed(tp, decode_tile_kernel<T, 8>, grid, dim3(512), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
-                 split_len, n_splits, group, kv_lo, qscale, part, out);
+                 split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
   else
     launch_timed(tp, decode_tile_kernel<T, 4>, grid, dim3(256), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
-                 split_len, n_splits, group, kv_lo, qscale, part, out);
+                 split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
+}
+
+bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads) {
+  return kv->head_dim == kD && n_q_heads % kv->n_kv_heads == 0 && n_q_heads / kv->n_kv_heads <= 16 &&
+         kv->tune_decode_impl != 1;
+}
+
+HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, size_t layer, size_t positions,
+                            float scale, const DecodePro& pro, float* out, hipStream_t s) {
+  HipStatus st;
+  const int n_heads = (int)kv->n_kv_heads;
+  const int group = (int)(n_q_heads / kv->n_kv_heads);
+  // The launch shape of launch_decode's MFMA path.
+  const long want = ((long)positions * n_heads + 511) / 512;
+  const int waves = kv->tune_decode_waves == 8 || kv->tune_decode_waves == 4 ? (int)kv->tune_decode_waves
+                                                                             : (want >= 256 ? 8 : 4);
+  const int step = waves * 16;
+  long len = kv->tune_decode_split_len;
+  if (len <= 0) len = want;
+  len = std::max<long>(len, step);
+  const int split_len = (int)((len + step - 1) / step * step);
+  const int n_splits = (int)((positions + split_len - 1) / split_len);
+  st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float));
+  if (st.e != hipSuccess) return st;
+  float* part = (float*)kv->ws;
+  const dim3 grid((unsigned)(n_heads * n_splits));
+  const TimedPair tp = timing_pair(kv, s);
+  const float qscale = scale * kLog2e;
+  auto go = [&](auto* tag) {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    const T* kl = (const T*)kv->k_layer(layer);
+    const T* vl = (const T*)kv->v_layer(layer);
+    if (waves == 8)
+      launch_timed(tp, decode_tile_kernel<T, 8, true>, grid, dim3(512), s, q_raw, kl, vl, (int)kv->kv_dim,
+                   (int)positions, split_len, n_splits, group, 0, qscale, part, out, pro);
+    else
+      launch_timed(tp, decode_tile_kernel<T, 4, true>, grid, dim3(256), s, q_raw, kl, vl, (int)kv->kv_dim,
+                   (int)positions, split_len, n_splits, group, 0, qscale, part, out, pro);
+  };
+  if (kv->elem == RV_ELEM_F32)
+    go((float*)nullptr);
+  else
+    go((_Float16*)nullptr);
+  if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "decode launch";
+  return st;
 }
 
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,

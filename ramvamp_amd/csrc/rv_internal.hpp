@@ -135,6 +135,27 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
                         float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s);
 
+// The decode step's prologue carried into the tile kernel (forward.rs:
+// 2617-2633): q pre-norm (each workgroup normalizes and rotates its group's
+// heads as it loads them), and the token's pre-norm k and v rows, which the
+// workgroup of the last split writes into the cache row positions - 1
+// (k normalized and rotated) before its tiles read it. (cos, sin) of the
+// token's position for pair i, computed on the host in f64.
+struct DecodePro {
+  const float* k;
+  const float* v;
+  const float* q_w;
+  const float* k_w;
+  float eps;
+  float cs[64], sn[64];
+};
+// True when launch_decode_pro covers the geometry (head_dim 128, group <= 16:
+// the MFMA tile kernel); the caller then skips the row prologue.
+bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads);
+// The whole decode step over positions (the token's row is positions - 1).
+HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, size_t layer, size_t positions,
+                            float scale, const DecodePro& pro, float* out, hipStream_t s);
+
 // ---- prefill (rv_prefill.hip) -------------------------------------------------
 // The q prologue fused into the prefill kernels' query loads: RMSNorm with
 // w and eps, rotation with the rows' (cos, sin) table from
