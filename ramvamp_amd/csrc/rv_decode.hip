@@ -307,7 +307,16 @@ struct NoPro {};
 template <bool PRO, typename T>
 using PlanePtr = std::conditional_t<PRO, const T*, const T* __restrict__>;
 
-template <typename T, int W, bool PRO = false>
+// H16 (f16 planes, no PRO): f16 MFMA operands (v_mfma_f32_16x16x16_f16)
+// with fp32-equivalent products. K and V are exact in f16. Each head's q
+// (scaled by a power of two so that its largest value is at most 2^14) is
+// split into f16 hi + lo halves, and the scores scaled back exactly. The
+// probabilities, scaled by 2^14 so that their low halves stay normal, are
+// split the same way, and the output rescaled by 2^-14 at the end. Each MFMA
+// takes 4 of the 8 values of a 16-byte K chunk (K·q: the same d slots from q)
+// or element b of a lane's four V rows (P·V: the S^T accumulator is already
+// the B layout), so the loads and the output layout are the fp32 path's.
+template <typename T, int W, bool PRO = false, bool H16 = false>
 __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __restrict__ q, PlanePtr<PRO, T> kl,
                                                              PlanePtr<PRO, T> vl, int kv_dim, int positions,
                                                              int split_len, int n_splits, int group, int kv_lo,
@@ -383,6 +392,8 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   // q is scaled once the first tile's loads are in flight (its own loads
   // then complete under theirs).
   const float qsc = col_ok ? qscale : 0.f;
+  f16x4 qh[H16 ? 8 : 1], ql[H16 ? 8 : 1];
+  float q_up = 1.f;
   auto scale_q = [&]() {
     if constexpr (PRO) {
 #pragma clang fp contract(off)
@@ -408,6 +419,27 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
     }
 #pragma unroll
     for (int i = 0; i < 32; ++i) qv[i] *= qsc;
+    if constexpr (H16) {
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(qv[i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+      int ex = 0;
+      (void)frexpf(amax, &ex);  // amax < 2^ex
+      const int k = ex > 14 ? ex - 14 : 0;
+      const float down = ldexpf(1.f, -k);
+      q_up = ldexpf(1.f, k);
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const float v = qv[(m >> 1) * 8 + 4 * (m & 1) + kk] * down;
+          const _Float16 h = (_Float16)v;
+          qh[m][kk] = h;
+          ql[m][kk] = (_Float16)(v - (float)h);
+        }
+    }
   };
 
   f32x4 o[8];
@@ -417,10 +449,22 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   auto compute = [&](int j, const CT (&kb)[NKC], const CT (&vb)[NVC]) {
     const int t0 = t_begin + (wave + j * W) * 16;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (H16) {
 #pragma unroll
-    for (int c = 0; c < NKC; ++c)
+      for (int m = 0; m < 8; ++m) {
+        const f16x4 k4 = {(_Float16)kb[m >> 1][4 * (m & 1)], (_Float16)kb[m >> 1][4 * (m & 1) + 1],
+                          (_Float16)kb[m >> 1][4 * (m & 1) + 2], (_Float16)kb[m >> 1][4 * (m & 1) + 3]};
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k4, qh[m], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k4, ql[m], acc, 0, 0, 0);
+      }
+      acc *= q_up;
+    } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kb[c][e], qv[c * E + e], acc, 0, 0, 0);
+      for (int c = 0; c < NKC; ++c)
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kb[c][e], qv[c * E + e], acc, 0, 0, 0);
+    }
     float x[4], mx = kNegSentinel;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -438,12 +482,30 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - mn);
     l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    if constexpr (H16) {
+      f16x4 ph, pl;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      o[b] *= alpha;
+      for (int r = 0; r < 4; ++r) {
+        const float pp = p[r] * 16384.f;
+        const _Float16 h = (_Float16)pp;
+        ph[r] = h;
+        pl[r] = (_Float16)(pp - (float)h);
+      }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vb[(r * 8 + b) / E][(r * 8 + b) % E], p[r], o[b], 0, 0, 0);
+      for (int b = 0; b < 8; ++b) {
+        o[b] *= alpha;
+        const f16x4 v4 = {(_Float16)vb[0][b], (_Float16)vb[1][b], (_Float16)vb[2][b], (_Float16)vb[3][b]};
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph, o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl, o[b], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        o[b] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vb[(r * 8 + b) / E][(r * 8 + b) % E], p[r], o[b], 0, 0, 0);
+      }
     }
   };
   // Every load of a tile is issued unconditionally before the tile is used
@@ -473,6 +535,10 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
+  if constexpr (H16) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[b] *= 1.f / 16384.f;  // the probabilities' 2^14, exactly
+  }
   // o[b][r] = O^T[d = 8*(4*lk + r) + b][m = li]. Merge the W waves in LDS.
   __shared__ __attribute__((aligned(16))) float sm_o[W][16][kD + 4];
   __shared__ float sm_ml[W][16][2];
@@ -740,16 +806,16 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
                      part_stride_of(G), G, group, n_hg, out);
 }
 
-template <typename T>
+template <typename T, bool H16 = false>
 static void launch_tile(const TimedPair& tp, int waves, dim3 grid, hipStream_t s, const float* q, const void* kl,
                         const void* vl, int kv_dim, int positions, int split_len, int n_splits, int group, int kv_lo,
                         float qscale, float* part, float* out) {
   if (waves == 8)
-    launch_timed(tp, decode_tile_kernel<T, 8>, grid, dim3(512), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
-                 split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
+    launch_timed(tp, decode_tile_kernel<T, 8, false, H16>, grid, dim3(512), s, q, (const T*)kl, (const T*)vl, kv_dim,
+                 positions, split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
   else
-    launch_timed(tp, decode_tile_kernel<T, 4>, grid, dim3(256), s, q, (const T*)kl, (const T*)vl, kv_dim, positions,
-                 split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
+    launch_timed(tp, decode_tile_kernel<T, 4, false, H16>, grid, dim3(256), s, q, (const T*)kl, (const T*)vl, kv_dim,
+                 positions, split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
 }
 
 bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads) {
@@ -830,9 +896,12 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     if (kv->elem == RV_ELEM_F32)
       launch_tile<float>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
                          (int)kv_lo, qscale, part, out);
-    else
+    else if (kv->tune_decode_impl == 2)  // fp32 MFMA operands for f16 planes (the reference form)
       launch_tile<_Float16>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
                             (int)kv_lo, qscale, part, out);
+    else
+      launch_tile<_Float16, true>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits,
+                                  group, (int)kv_lo, qscale, part, out);
     if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
   } else if (kv->head_dim == kD) {
     const DecodeShape d = pick_shape(kv, (int)positions, n_heads, group);
