@@ -371,3 +371,19 @@ def test_outputs_are_convex_combinations_of_v_rows():
     rv.decode_attention(q, kv2, 0, synth.SCALE, None, out)
     assert np.allclose(host(out), 0.375, rtol=1e-6, atol=0)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("q_scale", [3e4, 1e6, 1e-4])
+def test_f16_decode_keeps_fp32_products_at_extreme_q(q_scale):
+    # The f16-operand decode splits each head's q into f16 halves after a
+    # power-of-two scaling: q far outside f16's range (or deep in its
+    # subnormals) must still give the fp32 result on the same f16 cache.
+    torch_cuda()
+    say(f"case f16 decode q_scale={q_scale}")
+    rng = Rng(0xF16)
+    kv, ref = twin_caches(rng, 1, 4, 128, 300, "f16")
+    q = rng.vec_in(32 * 128, -1.0, 1.0) * np.float32(q_scale)
+    scale = 0.0883883 / max(q_scale, 1.0)  # keep the scores in a sane range
+    out = np.zeros(q.size, np.float32)
+    rv.decode_attention(q, kv, 0, scale, None, out)
+    gate(out, ref.attention(q, 0, scale), what=f"f16 decode q x {q_scale}")
