@@ -107,6 +107,31 @@ def _lib():
     return L.load()
 
 
+_F32 = None
+_RAW_STREAM = None
+
+
+def _torch_f32():
+    global _F32
+    if _F32 is None:
+        import torch
+
+        _F32 = torch.float32
+    return _F32
+
+
+def _raw_stream(device: int) -> int:
+    """The current HIP stream of `device` as an address: torch's raw-stream
+    query (one call, no Stream object) when this torch build has it."""
+    global _RAW_STREAM
+    if _RAW_STREAM is None:
+        import torch
+
+        _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+            lambda d: torch.cuda.current_stream(d).cuda_stream)
+    return _RAW_STREAM(device)
+
+
 class _Arg:
     """One tensor argument: device (torch) or host (numpy) pointer plus length."""
 
@@ -116,15 +141,15 @@ class _Arg:
         if x is None:
             self.ptr, self.n, self.host, self.keep = None, 0, None, None
             return
-        mod = type(x).__module__
-        if mod.startswith("torch"):
-            import torch
-
-            if x.dtype != torch.float32 or not x.is_contiguous():
+        if type(x).__module__.startswith("torch"):
+            # The per-call cost matters here (a decode step marshals six of
+            # these): cached dtype, is_cuda instead of a device object, and
+            # the raw address handed to ctypes as an int.
+            if x.dtype is not _torch_f32() or not x.is_contiguous():
                 raise TypeError("device tensors must be contiguous torch.float32")
-            if x.device.type != "cuda":
+            if not x.is_cuda:
                 raise TypeError("torch tensors must live on the GPU; pass numpy arrays for host memory")
-            self.ptr, self.n, self.host, self.keep = c_void_p(x.data_ptr()), x.numel(), False, x
+            self.ptr, self.n, self.host, self.keep = x.data_ptr(), x.numel(), False, x
         else:
             a = x if isinstance(x, np.ndarray) else np.asarray(x, dtype=dtype)
             if a.dtype != dtype or not a.flags["C_CONTIGUOUS"]:
@@ -185,9 +210,7 @@ class KvCache:
         return self._h
 
     def _bind_stream(self):
-        import torch
-
-        s = torch.cuda.current_stream(self.device).cuda_stream
+        s = _raw_stream(self.device)
         if s != self._stream:
             err = L.RvError()
             _check(_lib().rv_kv_set_stream(self._h, c_void_p(s), byref(err)), err)
