@@ -15,7 +15,7 @@ from __future__ import annotations
 from ctypes import byref, c_size_t, c_void_p
 
 from . import _lib as L
-from .attention import _check
+from .attention import _check, _raw_stream
 
 Q4_K, Q5_K, Q6_K, Q8_0, Q8_K = L.RV_QF_Q4_K, L.RV_QF_Q5_K, L.RV_QF_Q6_K, L.RV_QF_Q8_0, L.RV_QF_Q8_K
 Q8_K_BLOCK_BYTES = 292  # sizeof(rv_block_q8_k)
@@ -28,7 +28,7 @@ def _lib():
 
 def _stream():
     import torch
-    return c_void_p(torch.cuda.current_stream().cuda_stream)
+    return c_void_p(_raw_stream(torch.cuda.current_device()))
 
 
 def _dev(t, what):

@@ -11,7 +11,7 @@ from __future__ import annotations
 from ctypes import byref, c_void_p
 
 from . import _lib as L
-from .attention import _check
+from .attention import _check, _raw_stream
 
 
 def router_topk(x, router, top_k: int, norm_topk_prob: bool, experts=None, weights=None):
@@ -32,5 +32,5 @@ def router_topk(x, router, top_k: int, norm_topk_prob: bool, experts=None, weigh
     _check(L.load().rv_router_topk(c_void_p(rows.data_ptr()), n_rows, hidden, c_void_p(router.data_ptr()),
                                    router.numel(), n_experts, top_k, int(bool(norm_topk_prob)),
                                    c_void_p(experts.data_ptr()), c_void_p(weights.data_ptr()),
-                                   c_void_p(torch.cuda.current_stream().cuda_stream), 0, byref(err)), err)
+                                   c_void_p(_raw_stream(torch.cuda.current_device())), 0, byref(err)), err)
     return experts, weights
