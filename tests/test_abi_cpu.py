@@ -110,3 +110,24 @@ def test_quant_geometry_matches_the_oracle(lib):
     assert lib.rv_attn_in_proj_scratch_bytes(2048) == 16 * ((8 * 292 + 15) // 16) + 64 * 36
     assert lib.rv_attn_out_proj_scratch_bytes(4096) == 16 * 292
 
+
+
+def test_mirror_argument_checks_reject_bad_device_tensors():
+    # The Python mirror's per-call marshalling: device tensors must be
+    # contiguous float32 on the GPU; host arrays go through numpy.
+    import numpy as np
+    import torch
+    from ramvamp_amd import attention as A
+
+    with pytest.raises(TypeError, match="on the GPU"):
+        A._Arg(torch.zeros(8, dtype=torch.float32))
+    with pytest.raises(TypeError, match="float32"):
+        A._Arg(torch.zeros(8, dtype=torch.float64))
+    with pytest.raises(TypeError, match="float32"):
+        A._Arg(torch.zeros(4, 4, dtype=torch.float32).t())
+    a = A._Arg(np.arange(6, dtype=np.float64))  # converted to a float32 copy
+    assert a.host and a.n == 6 and a.keep.dtype == np.float32
+    with pytest.raises(TypeError, match="read-only"):
+        ro = np.zeros(4, np.float32)
+        ro.flags.writeable = False
+        A._Arg(ro, writable=True)
