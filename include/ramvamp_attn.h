@@ -211,34 +211,42 @@ int32_t rv_attention_at_rows(const rv_kv* kv, const float* q_rows, size_t rows, 
  * [head_dim] weights and `eps` (primitives/norm.rs:18-90), NeoX RoPE of both
  * at `position` with base `theta` (primitives/rope.rs:31-105), KvCache::append
  * of (k, v), then decode attention over every position of the layer.
- * q/k/v are pre-norm; q_len = n_q_heads*head_dim, k_len = v_len = kv_dim. */
+ * q/k/v are pre-norm; q_len = n_q_heads*head_dim, k_len = v_len = kv_dim.
+ * A norm weight whose length is not head_dim is RV_PRIM_LENGTH_MISMATCH
+ * (a = head_dim, b = its length), as rmsnorm_in_place reports it
+ * (primitives/norm.rs:72-83): q's weight first, then k's. */
 int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, const float* k,
                        size_t k_len, const float* v, size_t v_len, const float* q_norm_w,
-                       const float* k_norm_w, float eps, float theta, size_t position,
-                       float scale, float* out, size_t out_len, uint32_t flags,
-                       rv_error* err);
+                       size_t q_norm_len, const float* k_norm_w, size_t k_norm_len, float eps,
+                       float theta, size_t position, float scale, float* out, size_t out_len,
+                       uint32_t flags, rv_error* err);
 
 /* model/prefill.rs:2055-2111 steps (d)-(f) for one layer of a chunk: the
  * same prologue per row at absolute position start+r, the whole chunk's
  * K/V appended, then causal attention where row r sees start+r+1 positions.
- * `start` must equal len(layer) (the chunk continues the cache). */
+ * `start` must equal len(layer) (the chunk continues the cache). The norm
+ * weights' lengths are checked as rv_decode_step's (when rows > 0). */
 int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const float* k_rows,
                          const float* v_rows, size_t rows, size_t q_dim, const float* q_norm_w,
-                         const float* k_norm_w, float eps, float theta, size_t start,
-                         float scale, float* out, uint32_t flags, rv_error* err);
+                         size_t q_norm_len, const float* k_norm_w, size_t k_norm_len, float eps,
+                         float theta, size_t start, float scale, float* out, uint32_t flags,
+                         rv_error* err);
 
 /* Tuning knobs of the decode/prefill launches (0 = built-in heuristic).
  * Exposed for benchmarking sweeps; results never depend on them beyond
  * floating-point reassociation within the stated tolerance. */
 #define RV_TUNE_DECODE_SPLIT_LEN 1 /* positions per decode split (rounded to the workgroup step) */
 #define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill row tile (1..8) */
-#define RV_TUNE_DECODE_WAVES 3     /* waves per decode workgroup: 4 or 8 */
+#define RV_TUNE_DECODE_WAVES 3     /* waves per MFMA decode workgroup: 4 (default) or 8; VALU path: 4 or 8 (default) */
 #define RV_TUNE_PREFILL_ROWS 4     /* query rows per prefill tile: 8 or 16 */
 #define RV_TUNE_DECODE_HG 5        /* query heads per VALU decode workgroup: 1, 2, 4 or 8 */
 #define RV_TUNE_DECODE_IMPL 6      /* decode kernel: 0 auto (MFMA tiles when head_dim 128 and group <= 16; f16 planes on f16
                                       MFMA operands split hi/lo), 1 VALU subgroups, 2 MFMA tiles with fp32 operands */
 #define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
 #define RV_TUNE_PREFILL_IMPL 8     /* prefill attention kernel: 0 auto, 1 two wave groups, 2 software-pipelined */
+#define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1, 2 or 4 (f16 planes) */
+#define RV_TUNE_DECODE_FAN 10      /* decode splits folded per level-1 merge group (the rest in a second level) */
+#define RV_TUNE_DECODE_MERGE 11    /* 0: decode splits merged by a second kernel, 1: inside the tile launch (ticket) */
 int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
 
 /* No reference counterpart: benchmark instrumentation. With

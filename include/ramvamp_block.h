@@ -55,6 +55,8 @@ typedef struct rv_attn_block_weights {
   uint32_t o_format;       /* RV_QF_Q4_K / Q5_K / Q6_K */
   const uint8_t* wo;       /* hidden rows of `q_dim` weights */
   size_t wo_len;
+  size_t q_norm_len;       /* head_dim, checked as rv_decode_step checks it */
+  size_t k_norm_len;
 } rv_attn_block_weights;
 
 /* Bytes of device scratch rv_attn_block_decode needs: q, k, v and attn_out,

@@ -99,11 +99,12 @@ def lib():
                                                 c_size_t, c_int, E]),
         "rvo_scatter_attention": (c_int32, [c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p,
                                             c_void_p, c_size_t, c_int, E]),
-        "rvo_decode_step": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_void_p,
-                                      c_float, c_float, c_uint32, c_float, c_void_p, c_size_t, c_int, E]),
+        "rvo_decode_step": (c_int32, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t,
+                                      c_void_p, c_size_t, c_float, c_float, c_uint32, c_float, c_void_p, c_size_t,
+                                      c_int, E]),
         "rvo_prefill_chunk": (c_int32, [c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t,
-                                        c_void_p, c_void_p, c_float, c_float, c_size_t, c_float, c_void_p, c_size_t,
-                                        c_int, E]),
+                                        c_void_p, c_size_t, c_void_p, c_size_t, c_float, c_float, c_size_t, c_float,
+                                        c_void_p, c_size_t, c_int, E]),
         "rvo_quant_block_weights": (c_size_t, [c_uint32]),
         "rvo_quant_block_bytes": (c_size_t, [c_uint32]),
         "rvo_quant_row_bytes": (c_int32, [c_uint32, c_size_t, POINTER(c_size_t), E]),
@@ -326,8 +327,9 @@ class KvCache:
         wq, wk = _f32(q_norm_w), _f32(k_norm_w)
         out = np.full(q.size, np.nan, dtype=np.float32)
         err = RvError()
-        _check(lib().rvo_decode_step(self._h, layer, _ptr(q), q.size, _ptr(k), _ptr(v), _ptr(wq), _ptr(wk), eps, theta,
-                                     position, scale, _ptr(out), threads, int(force_scalar), byref(err)), err)
+        _check(lib().rvo_decode_step(self._h, layer, _ptr(q), q.size, _ptr(k), _ptr(v), _ptr(wq), wq.size, _ptr(wk),
+                                     wk.size, eps, theta, position, scale, _ptr(out), threads, int(force_scalar),
+                                     byref(err)), err)
         return out
 
     def prefill_chunk(self, layer, q_rows, k_rows, v_rows, q_norm_w, k_norm_w, eps, theta, start, scale, threads=1,
@@ -338,8 +340,8 @@ class KvCache:
         out = np.full(q_rows.shape, np.nan, dtype=np.float32)
         err = RvError()
         _check(lib().rvo_prefill_chunk(self._h, layer, _ptr(q_rows), _ptr(k_rows), _ptr(v_rows), rows, q_dim, _ptr(wq),
-                                       _ptr(wk), eps, theta, start, scale, _ptr(out), threads, int(force_scalar),
-                                       byref(err)), err)
+                                       wq.size, _ptr(wk), wk.size, eps, theta, start, scale, _ptr(out), threads,
+                                       int(force_scalar), byref(err)), err)
         return out
 
 
@@ -426,6 +428,7 @@ def gemv(fmt: int, weight, in_dim: int, out_dim: int, acts, n_acts: int = 1, row
 
 
 RV_FWD_INVALID_TOP_K = 48
+RV_PRIM_LENGTH_MISMATCH = 25
 RV_PRIM_EMPTY = 26
 
 

@@ -781,14 +781,27 @@ int32_t rvo_scatter_attention(const rvo_kv* kv, size_t layer, size_t start, size
 /* ---- layer steps ---------------------------------------------------------- */
 
 /* model/forward.rs:2622-2633. */
+/* primitives/norm.rs:72-83: a head of `hd` values against a weight of
+ * `w_len`. */
+static int32_t check_norm_weight(size_t hd, size_t w_len, rv_error* err) {
+  if (w_len != hd)
+    return set_err(err, RV_PRIM_LENGTH_MISMATCH, hd, w_len, 0, 0, "rmsnorm_in_place: x vs weight");
+  return RV_OK;
+}
+
 int32_t rvo_decode_step(rvo_kv* kv, size_t layer, float* q, size_t q_len, float* k,
-                        const float* v, const float* q_norm_w, const float* k_norm_w,
-                        float eps, float theta, uint32_t position, float scale, float* out,
-                        size_t threads, int force_scalar, rv_error* err) {
+                        const float* v, const float* q_norm_w, size_t q_norm_len,
+                        const float* k_norm_w, size_t k_norm_len, float eps, float theta,
+                        uint32_t position, float scale, float* out, size_t threads,
+                        int force_scalar, rv_error* err) {
   size_t hd = kv->head_dim;
+  int32_t rc;
+  /* forward.rs:2622-2627: every q head, then every k head. */
+  if (q_len >= hd && (rc = check_norm_weight(hd, q_norm_len, err))) return rc;
   for (size_t h = 0; h + hd <= q_len; h += hd) rvo_rmsnorm_in_place(q + h, q_norm_w, hd, eps);
+  if ((rc = check_norm_weight(hd, k_norm_len, err))) return rc;
   for (size_t h = 0; h + hd <= kv->kv_dim; h += hd) rvo_rmsnorm_in_place(k + h, k_norm_w, hd, eps);
-  int32_t rc = rvo_rope_neox_heads(q, q_len, q_len / hd, hd, position, theta);
+  rc = rvo_rope_neox_heads(q, q_len, q_len / hd, hd, position, theta);
   if (rc) return set_err(err, rc, hd, 0, 0, 0, "rope q");
   rc = rvo_rope_neox_heads(k, kv->kv_dim, kv->n_kv_heads, hd, position, theta);
   if (rc) return set_err(err, rc, hd, 0, 0, 0, "rope k");
@@ -802,17 +815,21 @@ int32_t rvo_decode_step(rvo_kv* kv, size_t layer, float* q, size_t q_len, float*
  * every row, (f) scatter_attention. */
 int32_t rvo_prefill_chunk(rvo_kv* kv, size_t layer, float* q_rows, float* k_rows,
                           const float* v_rows, size_t rows, size_t q_dim,
-                          const float* q_norm_w, const float* k_norm_w, float eps,
-                          float theta, size_t start, float scale, float* out, size_t threads,
-                          int force_scalar, rv_error* err) {
+                          const float* q_norm_w, size_t q_norm_len, const float* k_norm_w,
+                          size_t k_norm_len, float eps, float theta, size_t start, float scale,
+                          float* out, size_t threads, int force_scalar, rv_error* err) {
   size_t hd = kv->head_dim, kv_dim = kv->kv_dim;
   for (size_t r = 0; r < rows; ++r) {
     uint32_t pos = (uint32_t)(start + r);
     float* q = q_rows + r * q_dim;
     float* k = k_rows + r * kv_dim;
+    /* prefill.rs:2057-2076: q heads normed and rotated, then k heads. */
+    int32_t rc;
+    if (q_dim >= hd && (rc = check_norm_weight(hd, q_norm_len, err))) return rc;
     for (size_t h = 0; h + hd <= q_dim; h += hd) rvo_rmsnorm_in_place(q + h, q_norm_w, hd, eps);
-    int32_t rc = rvo_rope_neox_heads(q, q_dim, q_dim / hd, hd, pos, theta);
+    rc = rvo_rope_neox_heads(q, q_dim, q_dim / hd, hd, pos, theta);
     if (rc) return set_err(err, rc, hd, 0, 0, 0, "rope q");
+    if ((rc = check_norm_weight(hd, k_norm_len, err))) return rc;
     for (size_t h = 0; h + hd <= kv_dim; h += hd) rvo_rmsnorm_in_place(k + h, k_norm_w, hd, eps);
     rc = rvo_rope_neox_heads(k, kv_dim, kv->n_kv_heads, hd, pos, theta);
     if (rc) return set_err(err, rc, hd, 0, 0, 0, "rope k");

@@ -107,15 +107,16 @@ int32_t rvo_scatter_attention(const rvo_kv* kv, size_t layer, size_t start, size
 /* model/forward.rs:2622-2633: q/k per-head RMSNorm, RoPE, append, attention.
  * q (q_len) and k (kv_dim) are modified in place, as in the reference. */
 int32_t rvo_decode_step(rvo_kv* kv, size_t layer, float* q, size_t q_len, float* k,
-                        const float* v, const float* q_norm_w, const float* k_norm_w,
-                        float eps, float theta, uint32_t position, float scale, float* out,
-                        size_t threads, int force_scalar, rv_error* err);
+                        const float* v, const float* q_norm_w, size_t q_norm_len,
+                        const float* k_norm_w, size_t k_norm_len, float eps, float theta,
+                        uint32_t position, float scale, float* out, size_t threads,
+                        int force_scalar, rv_error* err);
 /* model/prefill.rs:2055-2111 steps (d)-(f); q_rows/k_rows modified in place. */
 int32_t rvo_prefill_chunk(rvo_kv* kv, size_t layer, float* q_rows, float* k_rows,
                           const float* v_rows, size_t rows, size_t q_dim,
-                          const float* q_norm_w, const float* k_norm_w, float eps,
-                          float theta, size_t start, float scale, float* out, size_t threads,
-                          int force_scalar, rv_error* err);
+                          const float* q_norm_w, size_t q_norm_len, const float* k_norm_w,
+                          size_t k_norm_len, float eps, float theta, size_t start, float scale,
+                          float* out, size_t threads, int force_scalar, rv_error* err);
 
 /* Per-row prologue alone (for tests): norm + rope of `n_heads` heads. */
 int32_t rvo_norm_rope_heads(float* x, size_t n_heads, size_t head_dim, const float* w,

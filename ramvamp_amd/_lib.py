@@ -46,7 +46,7 @@ class RvAttnBlockWeights(ctypes.Structure):
     _fields_ = [("attn_norm", c_void_p), ("q_format", c_uint32), ("wq", c_void_p), ("wq_len", c_size_t),
                 ("wk", c_void_p), ("wk_len", c_size_t), ("v_format", c_uint32), ("wv", c_void_p),
                 ("wv_len", c_size_t), ("q_norm", c_void_p), ("k_norm", c_void_p), ("o_format", c_uint32),
-                ("wo", c_void_p), ("wo_len", c_size_t)]
+                ("wo", c_void_p), ("wo_len", c_size_t), ("q_norm_len", c_size_t), ("k_norm_len", c_size_t)]
 
 
 # Every symbol include/*.h declares: name -> (restype, argtypes).
@@ -87,10 +87,10 @@ SIGNATURES = {
     "rv_attention_at_kv_range_in": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_float, c_size_t, c_size_t,
                                               c_size_t, _P, c_size_t, c_uint32, _E]),
     "rv_attention_at_rows": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_size_t, c_float, _P, c_uint32, _E]),
-    "rv_decode_step": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, _P, c_float, c_float,
-                                 c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
-    "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, _P, c_float, c_float, c_size_t,
-                                   c_float, _P, c_uint32, _E]),
+    "rv_decode_step": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t,
+                                 c_float, c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, c_float,
+                                   c_float, c_size_t, c_float, _P, c_uint32, _E]),
     "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
     "rv_kv_kernel_time": (c_int32, [_P, POINTER(c_double), POINTER(c_uint64), _E]),
     # include/ramvamp_gemv.h

@@ -275,6 +275,7 @@ class KvCache:
         _check(_lib().rv_kv_truncate(self._h, new_len, byref(err)), err)
 
     def _row(self, plane_v: int, layer: int, pos: int) -> np.ndarray:
+        self._bind_stream()  # the copy is ordered after work queued on torch's current stream
         out = np.empty(self.kv_dim(), dtype=np.uint16 if self.elem == "f16" else np.float32)
         err = L.RvError()
         _check(_lib().rv_kv_read_row(self._h, plane_v, layer, pos, out.ctypes.data_as(c_void_p), byref(err)), err)
@@ -303,12 +304,14 @@ class KvCache:
         _check(_lib().rv_kv_set_tuning(self._h, knob, value, byref(err)), err)
 
     def synchronize(self):
+        self._bind_stream()
         err = L.RvError()
         _check(_lib().rv_kv_synchronize(self._h, byref(err)), err)
 
     def kernel_time(self):
         """(total milliseconds, launches) of the dominant kernels timed since
         the last read (RV_TUNE_KERNEL_TIMING on); resets the tally."""
+        self._bind_stream()
         ms, n, err = c_double(), c_uint64(), L.RvError()
         _check(_lib().rv_kv_kernel_time(self._h, byref(ms), byref(n), byref(err)), err)
         return ms.value, n.value
@@ -410,8 +413,8 @@ def decode_step(cache: KvCache, layer: int, q, k, v, q_norm_w, k_norm_w, eps: fl
     qa, ka, va, wq, wk, oa = _Arg(q), _Arg(k), _Arg(v), _Arg(q_norm_w), _Arg(k_norm_w), _Arg(out, writable=True)
     err = L.RvError()
     flags = _flags(cache, (qa, ka, va, wq, wk, oa))
-    _check(_lib().rv_decode_step(cache.handle, layer, qa.ptr, qa.n, ka.ptr, ka.n, va.ptr, va.n, wq.ptr, wk.ptr, eps,
-                                 theta, position, scale, oa.ptr, oa.n, flags, byref(err)), err)
+    _check(_lib().rv_decode_step(cache.handle, layer, qa.ptr, qa.n, ka.ptr, ka.n, va.ptr, va.n, wq.ptr, wq.n, wk.ptr,
+                                 wk.n, eps, theta, position, scale, oa.ptr, oa.n, flags, byref(err)), err)
     return out
 
 
@@ -426,6 +429,6 @@ def prefill_chunk(cache: KvCache, layer: int, q_rows, k_rows, v_rows, q_norm_w, 
         raise ValueError("q_rows/out are rows x q_dim, k_rows/v_rows rows x kv_dim")
     err = L.RvError()
     flags = _flags(cache, (qa, ka, va, wq, wk, oa)) | _MODES[mode]
-    _check(_lib().rv_prefill_chunk(cache.handle, layer, qa.ptr, ka.ptr, va.ptr, rows, q_dim, wq.ptr, wk.ptr, eps,
-                                   theta, start, scale, oa.ptr, flags, byref(err)), err)
+    _check(_lib().rv_prefill_chunk(cache.handle, layer, qa.ptr, ka.ptr, va.ptr, rows, q_dim, wq.ptr, wq.n, wk.ptr,
+                                   wk.n, eps, theta, start, scale, oa.ptr, flags, byref(err)), err)
     return out

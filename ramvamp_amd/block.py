@@ -41,7 +41,8 @@ class AttnBlockWeights:
             return t.data_ptr()
         return L.RvAttnBlockWeights(p(self.attn_norm), self.q_format, p(self.wq), self.wq.numel(), p(self.wk),
                                     self.wk.numel(), self.v_format, p(self.wv), self.wv.numel(), p(self.q_norm),
-                                    p(self.k_norm), self.o_format, p(self.wo), self.wo.numel())
+                                    p(self.k_norm), self.o_format, p(self.wo), self.wo.numel(), self.q_norm.numel(),
+                                    self.k_norm.numel())
 
 
 def scratch_bytes(hidden: int, q_dim: int, kv_dim: int) -> int:

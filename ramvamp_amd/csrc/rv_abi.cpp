@@ -33,8 +33,10 @@ int32_t fail(rv_error* err, int32_t code, uint64_t a = 0, uint64_t b = 0, uint64
 
 int32_t ok(rv_error* err) { return fail(err, RV_OK); }
 
+// A HIP failure; a call that would have to allocate under graph capture is
+// RV_ERR_UNSUPPORTED instead.
 int32_t hip_fail(rv_error* err, hipError_t e, const char* what) {
-  return fail(err, RV_ERR_HIP, (uint64_t)e, 0, 0, 0, what);
+  return fail(err, rv::status_code(e), (uint64_t)e, 0, 0, 0, what);
 }
 
 // Makes the cache's device current for the scope of one call.
@@ -82,6 +84,17 @@ int32_t check_layer(const rv_kv* kv, size_t layer, rv_error* err) {
   return RV_OK;
 }
 
+// primitives/norm.rs:72-83 `rmsnorm_in_place` on a head_dim head: q's
+// weight first (its heads are normalised first, forward.rs:2622-2627), then
+// k's.
+int32_t check_norm_weights(size_t hd, size_t q_norm_len, size_t k_norm_len, rv_error* err) {
+  if (q_norm_len != hd)
+    return fail(err, RV_PRIM_LENGTH_MISMATCH, hd, q_norm_len, 0, 0, "rmsnorm_in_place: x vs weight");
+  if (k_norm_len != hd)
+    return fail(err, RV_PRIM_LENGTH_MISMATCH, hd, k_norm_len, 0, 0, "rmsnorm_in_place: x vs weight");
+  return RV_OK;
+}
+
 struct Plan {
   size_t n_q_heads, group, positions;
 };
@@ -120,17 +133,15 @@ struct Stager {
   explicit Stager(rv_kv* k) : kv(k), s(k->stream) {}
   bool reserve(size_t bytes) {
     if (bytes <= kv->stage_bytes) return true;
-    if (kv->stage) {
-      (void)hipStreamSynchronize(s);
-      (void)hipFree(kv->stage);
-      kv->stage = nullptr;
-      kv->stage_bytes = 0;
-    }
-    e = hipMalloc(&kv->stage, bytes);
-    if (e != hipSuccess) {
-      kv->stage = nullptr;
+    if (rv::capturing(s)) {
+      e = hipErrorStreamCaptureUnsupported;
       return false;
     }
+    void* p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return false;
+    if (kv->stage) kv->retired.push_back(kv->stage);
+    kv->stage = p;
     kv->stage_bytes = bytes;
     return true;
   }
@@ -213,7 +224,8 @@ int32_t check_rope_dim(const rv_kv* kv, rv_error* err) {
 
 namespace rv {
 
-int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start, rv_error* err) {
+int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start,
+                            size_t q_norm_len, size_t k_norm_len, rv_error* err) {
   // rv_prefill_chunk's checks, in its order, before its pointer checks.
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
   int32_t rc = check_rope_dim(kv, err);
@@ -221,6 +233,7 @@ int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q
   const size_t hd = kv->head_dim;
   if (q_dim == 0 || q_dim % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_dim, hd);
   if ((q_dim / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_dim / hd, kv->n_kv_heads);
+  if (rows > 0 && (rc = check_norm_weights(hd, q_norm_len, k_norm_len, err))) return rc;
   if ((rc = check_layer(kv, layer, err))) return rc;
   const size_t len = kv->lens[layer];
   if (start != len) return fail(err, RV_KV_POSITION_OUT_OF_RANGE, layer, start, len, 0, "start != len(layer)");
@@ -229,7 +242,8 @@ int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q
   return RV_OK;
 }
 
-int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err) {
+int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, size_t q_norm_len,
+                          size_t k_norm_len, rv_error* err) {
   // rv_decode_step's checks, in its order, for k, v and out of the sizes the
   // cache and q imply (the composite callers own those buffers).
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
@@ -238,6 +252,7 @@ int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t po
   const size_t hd = kv->head_dim;
   if (q_len == 0 || q_len % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_len, hd);
   if ((q_len / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_len / hd, kv->n_kv_heads);
+  if ((rc = check_norm_weights(hd, q_norm_len, k_norm_len, err))) return rc;
   if ((rc = check_layer(kv, layer, err))) return rc;
   if (kv->lens[layer] == kv->capacity) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
   if (position > 0xFFFFFFFFull) return fail(err, RV_ERR_UNSUPPORTED, position, 0, 0, 0, "position past u32");
@@ -279,42 +294,43 @@ TimedPair timing_pair(rv_kv* kv, hipStream_t s) {
   return tp;
 }
 
-HipStatus ensure_workspace(rv_kv* kv, size_t bytes) {
+HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t bound) {
   HipStatus st;
-  if (bytes > kv->ws_bytes) {
-    if (kv->ws) {
-      (void)hipStreamSynchronize(kv->stream);
-      (void)hipFree(kv->ws);
-      kv->ws = nullptr;
-      kv->ws_bytes = 0;
-    }
-    const size_t want = std::max<size_t>(bytes, 1 << 20);
-    st.e = hipMalloc(&kv->ws, want);
-    if (st.e != hipSuccess) {
-      kv->ws = nullptr;
-      st.what = "hipMalloc workspace";
-      return st;
-    }
-    kv->ws_bytes = want;
+  if (bytes <= kv->ws_bytes) return st;
+  if (capturing(kv->stream)) {
+    st.e = hipErrorStreamCaptureUnsupported;
+    st.what = "workspace growth under graph capture (run a call of this shape uncaptured first)";
+    return st;
   }
+  const size_t want = std::max<size_t>(std::max(bytes, bound), (size_t)1 << 20);
+  void* p = nullptr;
+  st.e = hipMalloc(&p, want);
+  if (st.e != hipSuccess) {
+    st.what = "hipMalloc workspace";
+    return st;
+  }
+  if (kv->ws) kv->retired.push_back(kv->ws);
+  kv->ws = p;
+  kv->ws_bytes = want;
   return st;
 }
 
 HipStatus ensure_qbuf(rv_kv* kv, size_t bytes) {
   HipStatus st;
   if (bytes <= kv->qbuf_bytes) return st;
-  if (kv->qbuf) {
-    (void)hipStreamSynchronize(kv->stream);
-    (void)hipFree(kv->qbuf);
-    kv->qbuf = nullptr;
-    kv->qbuf_bytes = 0;
+  if (capturing(kv->stream)) {
+    st.e = hipErrorStreamCaptureUnsupported;
+    st.what = "q buffer growth under graph capture (run a call of this shape uncaptured first)";
+    return st;
   }
-  st.e = hipMalloc(&kv->qbuf, bytes);
+  void* p = nullptr;
+  st.e = hipMalloc(&p, bytes);
   if (st.e != hipSuccess) {
-    kv->qbuf = nullptr;
     st.what = "hipMalloc qbuf";
     return st;
   }
+  if (kv->qbuf) kv->retired.push_back(kv->qbuf);
+  kv->qbuf = (float*)p;
   kv->qbuf_bytes = bytes;
   return st;
 }
@@ -404,6 +420,14 @@ int32_t rv_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t ca
   if (e == hipSuccess) e = hipMalloc(&kv->v, plane_bytes);
   if (e == hipSuccess) e = hipMemset(kv->k, 0, plane_bytes);
   if (e == hipSuccess) e = hipMemset(kv->v, 0, plane_bytes);
+  const size_t ticket_bytes = n_kv_heads * (rv::kMaxMergeGroups + 1) * sizeof(unsigned);
+  if (e == hipSuccess) e = hipMalloc(&kv->tickets, ticket_bytes);
+  if (e == hipSuccess) e = hipMemset(kv->tickets, 0, ticket_bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) {
+    const rv::HipStatus st = rv::ensure_workspace(kv, rv::decode_ws_bound(kv));
+    e = st.e;
+  }
   if (e != hipSuccess) {
     rv_kv_free(kv);
     return hip_fail(err, e, "hipMalloc planes");
@@ -418,18 +442,41 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets})
       if (p) (void)hipFree(p);
     for (void* p : kv->staged)
       if (p) (void)hipFree(p);
+    for (void* p : kv->retired) (void)hipFree(p);
     for (hipEvent_t e : kv->ev) (void)hipEventDestroy(e);
+    if (kv->order_ev) (void)hipEventDestroy(kv->order_ev);
   }
   delete kv;
 }
 
+// The cache's planes, workspace and staged copies are shared by every call,
+// so work queued on the new stream is ordered after what the old one holds.
+// Not across a graph capture: an event recorded outside a capture cannot
+// order work inside it (a capture's work runs when the graph is launched).
 int32_t rv_kv_set_stream(rv_kv* kv, void* hip_stream, rv_error* err) {
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
-  kv->stream = (hipStream_t)hip_stream;
+  const hipStream_t next = (hipStream_t)hip_stream;
+  if (next == kv->stream) return ok(err);
+  DeviceGuard dg(kv->device);
+  if (rv::capturing(next) || rv::capturing(kv->stream)) {
+    kv->stream = next;
+    return ok(err);
+  }
+  if (!kv->order_ev) {
+    const hipError_t e = hipEventCreateWithFlags(&kv->order_ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      kv->order_ev = nullptr;
+      return hip_fail(err, e, "hipEventCreate (stream hand-over)");
+    }
+  }
+  hipError_t e = hipEventRecord(kv->order_ev, kv->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(next, kv->order_ev, 0);
+  if (e != hipSuccess) return hip_fail(err, e, "stream hand-over");
+  kv->stream = next;
   return ok(err);
 }
 
@@ -656,15 +703,16 @@ int32_t rv_attention_at_rows(const rv_kv* ckv, const float* q_rows, size_t rows,
 
 // model/forward.rs:2622-2633.
 int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, const float* k, size_t k_len,
-                       const float* v, size_t v_len, const float* q_norm_w, const float* k_norm_w, float eps,
-                       float theta, size_t position, float scale, float* out, size_t out_len, uint32_t flags,
-                       rv_error* err) {
+                       const float* v, size_t v_len, const float* q_norm_w, size_t q_norm_len,
+                       const float* k_norm_w, size_t k_norm_len, float eps, float theta, size_t position,
+                       float scale, float* out, size_t out_len, uint32_t flags, rv_error* err) {
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
   int32_t rc = check_rope_dim(kv, err);
   if (rc) return rc;
   const size_t hd = kv->head_dim;
   if (q_len == 0 || q_len % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_len, hd);
   if ((q_len / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_len / hd, kv->n_kv_heads);
+  if ((rc = check_norm_weights(hd, q_norm_len, k_norm_len, err))) return rc;
   if ((rc = check_layer(kv, layer, err))) return rc;
   if (k_len != kv->kv_dim) return fail(err, RV_KV_ROW_LEN_MISMATCH, k_len, kv->kv_dim, 0, 0, "k");
   if (v_len != kv->kv_dim) return fail(err, RV_KV_ROW_LEN_MISMATCH, v_len, kv->kv_dim, 0, 0, "v");
@@ -725,14 +773,16 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
 
 // model/prefill.rs:2055-2111 steps (d)-(f).
 int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const float* k_rows, const float* v_rows,
-                         size_t rows, size_t q_dim, const float* q_norm_w, const float* k_norm_w, float eps,
-                         float theta, size_t start, float scale, float* out, uint32_t flags, rv_error* err) {
+                         size_t rows, size_t q_dim, const float* q_norm_w, size_t q_norm_len, const float* k_norm_w,
+                         size_t k_norm_len, float eps, float theta, size_t start, float scale, float* out,
+                         uint32_t flags, rv_error* err) {
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
   int32_t rc = check_rope_dim(kv, err);
   if (rc) return rc;
   const size_t hd = kv->head_dim;
   if (q_dim == 0 || q_dim % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_dim, hd);
   if ((q_dim / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_dim / hd, kv->n_kv_heads);
+  if (rows > 0 && (rc = check_norm_weights(hd, q_norm_len, k_norm_len, err))) return rc;
   if ((rc = check_layer(kv, layer, err))) return rc;
   const size_t len = kv->lens[layer];
   if (start != len) return fail(err, RV_KV_POSITION_OUT_OF_RANGE, layer, start, len, 0, "start != len(layer)");
@@ -800,6 +850,9 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_DECODE_IMPL: kv->tune_decode_impl = value; break;
     case RV_TUNE_PREFILL_IMPL: kv->tune_prefill_impl = value; break;
     case RV_TUNE_KERNEL_TIMING: kv->timing = value != 0; break;
+    case RV_TUNE_DECODE_DEPTH: kv->tune_decode_depth = value; break;
+    case RV_TUNE_DECODE_FAN: kv->tune_decode_fan = value; break;
+    case RV_TUNE_DECODE_MERGE: kv->tune_decode_merge = value; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }
   return ok(err);

@@ -66,7 +66,7 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
                 w->wk,    0,            c.k,     kv_dim, w->v_format, w->wv, 0,   c.v,   c.proj};
   int32_t rc;
   if ((rc = rv::in_proj_check(in, w->wq_len, w->wk_len, w->wv_len, err))) return rc;
-  if ((rc = rv::decode_step_check(kv, layer, q_dim, position, err))) return rc;
+  if ((rc = rv::decode_step_check(kv, layer, q_dim, position, w->q_norm_len, w->k_norm_len, err))) return rc;
   rv::OutProj out{c.attn, q_dim, w->o_format, w->wo, 0, residual, hidden, true, c.proj};
   if ((rc = rv::out_proj_check(out, w->wo_len, err))) return rc;
   const size_t need = rv_attn_block_scratch_bytes(hidden, q_dim, kv_dim);
@@ -88,7 +88,7 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
   rv::HipStatus st = rv::in_proj_launch(in, s);
   if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
   if (!rc)
-    rc = rv_decode_step(kv, layer, c.q, q_dim, c.k, kv_dim, c.v, kv_dim, w->q_norm, w->k_norm, eps, theta, position,
+    rc = rv_decode_step(kv, layer, c.q, q_dim, c.k, kv_dim, c.v, kv_dim, w->q_norm, w->q_norm_len, w->k_norm, w->k_norm_len, eps, theta, position,
                         scale, c.attn, q_dim, 0, err);
   if (!rc) {
     st = rv::out_proj_launch(out, s);
@@ -134,7 +134,7 @@ int32_t rv_attn_block_prefill(rv_kv* kv, size_t layer, float* residual_rows, siz
                 w->v_format, w->wv, 0, v, p};
   int32_t rc;
   if ((rc = rv::in_proj_rows_check(in, n, w->wq_len, w->wk_len, w->wv_len, err))) return rc;
-  if ((rc = rv::prefill_chunk_check(kv, layer, n, q_dim, start, err))) return rc;
+  if ((rc = rv::prefill_chunk_check(kv, layer, n, q_dim, start, w->q_norm_len, w->k_norm_len, err))) return rc;
   rv::OutProj out{attn, q_dim, w->o_format, w->wo, 0, residual_rows, hidden, true, p};
   if ((rc = rv::out_proj_rows_check(out, n, w->wo_len, err))) return rc;
   const size_t need = rv_attn_block_prefill_scratch_bytes(n, hidden, q_dim, kv_dim);
@@ -161,7 +161,7 @@ int32_t rv_attn_block_prefill(rv_kv* kv, size_t layer, float* residual_rows, siz
   if (st.e == hipSuccess) st = rv::in_proj_rows_launch(in, n, s);
   if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
   if (!rc)
-    rc = rv_prefill_chunk(kv, layer, q, k, v, n, q_dim, w->q_norm, w->k_norm, eps, theta, start, scale, attn,
+    rc = rv_prefill_chunk(kv, layer, q, k, v, n, q_dim, w->q_norm, w->q_norm_len, w->k_norm, w->k_norm_len, eps, theta, start, scale, attn,
                           flags & RV_PREFILL_MODE_MASK, err);
   if (!rc) {
     st = rv::out_proj_rows_launch(out, n, s);

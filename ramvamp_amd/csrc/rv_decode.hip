@@ -10,11 +10,13 @@
 // loaded straight into registers in the MFMA operand layouts; softmax is
 // online (running max and sum per query head, exp2 with log2(e) folded into
 // q). The splits of one kv head are merged by a second kernel with an fp32
-// log-sum-exp combine. The kernel boundary is what makes the partials
-// visible: the workgroups of one kv head run on different XCDs, whose L2s are
-// not coherent, and an in-kernel hand-off would need agent-scope release and
-// acquire fences (an L2 write-back and invalidate each), measured dearer
-// than the second launch.
+// log-sum-exp combine (decode_merge_kernel). The workgroups of one kv head
+// run on different XCDs, whose L2s are not coherent; an in-launch merge (the
+// last workgroup of a group of splits folds them, the hand-off made with
+// device-scope partial stores and loads and a relaxed agent-scope ticket,
+// no L2 write-back) is built as a tuning option and measured slower: its
+// chain of acknowledged stores, a memory-side atomic and L2-missing loads
+// costs more than the second launch.
 //
 // VALU path (head_dim 128, any group; groups over 16 use it by default):
 // decode_split_kernel, one workgroup per (kv head, subgroup of G query heads,
@@ -39,6 +41,11 @@ constexpr int kD = 128;                     // head_dim of the fast path
 constexpr int kLPR = 16;                    // lanes per K/V row (8 elements each)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegSentinel = -1.0e30f;    // finite "no position yet" max
+// Decode softmax: scores (log2 units) may exceed the running maximum by up to
+// kSlack before it moves, so probabilities are at most 2^kSlack; the f16 path
+// splits p * kPScale (<= 2^14, inside f16's range) into hi + lo halves.
+constexpr float kSlack = 8.f;
+constexpr float kPScale = 64.f;
 
 // Partial layout per (kv head, split): o[G][kD] then (m, l)[G], padded to a
 // 16-byte multiple so every partial row starts 16-byte aligned.
@@ -294,11 +301,15 @@ struct Chunk<_Float16> {
 //   O^T[d][m] += sum_t V[t][d] P^T[t][m]: 8 x 4 MFMAs; the accumulator layout
 //     of S^T is exactly the B layout P^T needs (step r takes rows 4k + r), and
 //     lane (i, k) holds V[4k + r][8i .. 8i+7], so output block b is d = 8i + b.
-// The first tile's loads are issued before anything waits (a scheduling
-// barrier keeps the compiler from sinking them to their uses), the next
-// tile's after the current one is computed. The waves merge through LDS; the
-// workgroup writes `out` (one split) or its partial (o, max, sum) row for
-// decode_merge_kernel.
+// Each wave keeps D tiles in flight in a register ring: the first D tiles'
+// loads are issued before anything waits, and the loads of tile j + D are
+// issued as soon as tile j has been computed (scheduling barriers keep the
+// compiler from sinking them to their first use). The kernel is held to 256
+// registers so that two waves fit per SIMD and a grid of ~2048 waves is
+// resident at once. The waves merge through LDS; the workgroup then writes
+// `out` (one split) or its partial (o, max, sum) row; the splits of a kv head
+// are folded by decode_merge_kernel or, with MergeArgs::fused, inside the
+// same launch (the in-launch split merge below).
 // With PRO the decode step's prologue runs here too (DecodePro): the planes
 // are then written (the token's row) as well as read, so they are not
 // declared __restrict__ (a restrict-qualified read-only plane would let the
@@ -307,22 +318,131 @@ struct NoPro {};
 template <bool PRO, typename T>
 using PlanePtr = std::conditional_t<PRO, const T*, const T* __restrict__>;
 
-// H16 (f16 planes, no PRO): f16 MFMA operands (v_mfma_f32_16x16x16_f16)
-// with fp32-equivalent products. K and V are exact in f16. Each head's q
-// (scaled by a power of two so that its largest value is at most 2^14) is
-// split into f16 hi + lo halves, and the scores scaled back exactly. The
-// probabilities, scaled by 2^14 so that their low halves stay normal, are
-// split the same way, and the output rescaled by 2^-14 at the end. Each MFMA
-// takes 4 of the 8 values of a 16-byte K chunk (K·q: the same d slots from q)
-// or element b of a lane's four V rows (P·V: the S^T accumulator is already
-// the B layout), so the loads and the output layout are the fp32 path's.
-template <typename T, int W, bool PRO = false, bool H16 = false>
-__global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __restrict__ q, PlanePtr<PRO, T> kl,
-                                                             PlanePtr<PRO, T> vl, int kv_dim, int positions,
-                                                             int split_len, int n_splits, int group, int kv_lo,
-                                                             float qscale, float* __restrict__ part,
-                                                             float* __restrict__ out,
-                                                             std::conditional_t<PRO, DecodePro, NoPro> pro = {}) {
+// ---- in-launch split merge ------------------------------------------------------------
+// The workgroups of one kv head run on different XCDs, whose L2 caches are not
+// kept coherent with each other for ordinary stores. The partial rows are
+// therefore written and read with device-scope (sc1) buffer accesses, which
+// the L2 writes through and does not serve from a possibly stale line: the
+// cache-policy form of a relaxed agent-scope atomic store / load. A
+// workgroup's partial stores are complete (vmcnt 0) before its ticket is
+// taken with a relaxed agent-scope atomic add, so the workgroup that draws
+// the last ticket of a group of splits sees every partial of the group; no
+// L2 write-back or invalidate is needed. That workgroup folds the group in
+// split order and resets the ticket to 0 for the next call. Splits are
+// folded in groups of `fan` (level 1); with more than one group, each
+// group's result is a level-2 partial row and the last group to finish
+// folds those, again in order. The tree depends only on n_splits and fan,
+// so every kv head's result is the same whichever workgroup merges it.
+constexpr int kPolicyDevice = 16;  // the sc1 bit of the buffer instructions' cache policy
+
+struct MergeArgs {
+  float* part;         // [n_heads][n_splits][stride]
+  float* part2;        // [n_heads][n_grp][stride]
+  unsigned* tickets;   // [n_heads][n_grp] level 1, then [n_heads] level 2; zero between calls
+  uint32_t ws_bytes;   // bytes addressable from `part` (the buffer accesses' bound)
+  int fan, n_grp;
+  bool fused;          // false: partials only, decode_merge_kernel folds them
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(float* base, uint32_t bytes) {
+  // Raw buffer over the workspace: stride 0, num_records in bytes (accesses
+  // past it read 0 and drop their writes), the gfx9 data-format word.
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Folds `cnt` partial rows (o[group][kD], then (max, sum) per head),
+// starting `row0` rows into the buffer, in row order: thread -> (head g, 4
+// consecutive d). Writes a partial row at dst_row (when out is null) or the
+// normalised output out[g * kD + d].
+template <int NT>
+__device__ void fold_rows(__amdgpu_buffer_rsrc_t rs, uint32_t row0, int cnt, int stride, int group, uint32_t dst_row,
+                          float* out, int tid) {
+  constexpr int kChunk = 8;
+  for (int j = tid; j < group * (kD / 4); j += NT) {
+    const int g = j / (kD / 4), d = (j % (kD / 4)) * 4;
+    float M = kNegSentinel, L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < cnt; b0 += kChunk) {
+      f32x4 ov[kChunk];
+      float mv[kChunk], lv[kChunk];
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        const uint32_t row = (row0 + (uint32_t)min(b0 + i, cnt - 1)) * (uint32_t)stride * 4u;
+        ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, row + (uint32_t)(g * kD + d) * 4u, 0, kPolicyDevice);
+        mv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rs, row + (uint32_t)(group * kD + 2 * g) * 4u, 0, kPolicyDevice));
+        lv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rs, row + (uint32_t)(group * kD + 2 * g + 1) * 4u, 0, kPolicyDevice));
+      }
+      float mc = M;
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i)
+        if (b0 + i < cnt) mc = fmaxf(mc, mv[i]);
+      const float a = __builtin_amdgcn_exp2f(M - mc);
+      L *= a;
+      O *= a;
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i)
+        if (b0 + i < cnt) {
+          const float c = __builtin_amdgcn_exp2f(mv[i] - mc);
+          L += lv[i] * c;
+          O += ov[i] * c;
+        }
+      M = mc;
+    }
+    if (out) {
+      const f32x4 r = O / L;  // out may be only 4-byte aligned
+      float* op = out + (size_t)g * kD + d;
+      op[0] = r[0];
+      op[1] = r[1];
+      op[2] = r[2];
+      op[3] = r[3];
+    } else {
+      const uint32_t row = dst_row * (uint32_t)stride * 4u;
+      __builtin_amdgcn_raw_buffer_store_b128(O, rs, row + (uint32_t)(g * kD + d) * 4u, 0, kPolicyDevice);
+      if (d == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, M), rs, row + (uint32_t)(group * kD + 2 * g) * 4u,
+                                              0, kPolicyDevice);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, L), rs,
+                                              row + (uint32_t)(group * kD + 2 * g + 1) * 4u, 0, kPolicyDevice);
+      }
+    }
+  }
+}
+
+// Takes this workgroup's ticket on `t` once all its threads' partial stores
+// are complete; true for the workgroup that drew the last of `n` tickets,
+// which also resets the counter for the next call.
+__device__ __forceinline__ bool last_of(unsigned* t, unsigned n, int tid) {
+  __shared__ unsigned sm_ticket;
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned got = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (got == n - 1) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_ticket = got;
+  }
+  __syncthreads();
+  return sm_ticket == n - 1;
+}
+
+// H16 (f16 planes, no PRO): f16 MFMA operands with fp32-equivalent
+// products. K and V are exact in f16. Each head's q (scaled by a power of
+// two so that its largest value is at most 2^14) is split into f16 hi + lo
+// halves, and the scores scaled back exactly; K·q runs on
+// v_mfma_f32_16x16x32_f16, whose A operand is a lane's loaded 16-byte K
+// chunk as is (the same d slots of q as B). The probabilities, scaled by
+// kPScale, are split the same way for P·V (v_mfma_f32_16x16x16_f16 on
+// element b of a lane's four V rows: the S^T accumulator is already the B
+// layout), and the output scaled back at the end; so the loads and the
+// output layout are the fp32 path's.
+template <typename T, int W, int D, bool PRO = false, bool H16 = false>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void decode_tile_kernel(
+    const float* __restrict__ q, PlanePtr<PRO, T> kl, PlanePtr<PRO, T> vl, int kv_dim, int positions, int split_len,
+    int n_splits, int group, int kv_lo, float qscale, MergeArgs mg, float* __restrict__ out,
+    std::conditional_t<PRO, DecodePro, NoPro> pro = {}) {
   typedef typename Chunk<T>::type CT;
   constexpr int E = Chunk<T>::n;
   constexpr int NKC = 32 / E;  // K chunks per lane per tile
@@ -368,7 +488,9 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   }
   float qv[32];
   {
-    // q may be only 4-byte aligned: scalar loads (once per workgroup).
+    // q may be only 4-byte aligned: scalar loads (once per workgroup). (Staging
+    // the group's rows through LDS with coalesced loads measured slower: its
+    // barrier costs more than the gather.)
     const float* qp = q + (size_t)(kvh * group + (col_ok ? li : 0)) * kD;
 #pragma unroll
     for (int c = 0; c < NKC; ++c)
@@ -376,7 +498,8 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       for (int e = 0; e < E; ++e) qv[c * E + e] = qp[E * (lk + 4 * c) + e];
   }
   // Rows past the split re-read its last row (in bounds, branch-free); their
-  // scores are masked below.
+  // scores are masked below, and tiles past the wave's share are loaded that
+  // way but never computed.
   auto load_tile = [&](int j, CT (&kb)[NKC], CT (&vb)[NVC]) {
     const int t0 = t_begin + (wave + j * W) * 16;
     const T* kp = kl + (size_t)min(t0 + li, t_end - 1) * kv_dim + col + E * lk;
@@ -389,10 +512,10 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       for (int h = 0; h < 8 / E; ++h) vb[r * (8 / E) + h] = *reinterpret_cast<const CT*>(vp + E * h);
     }
   };
-  // q is scaled once the first tile's loads are in flight (its own loads
+  // q is scaled once the first tiles' loads are in flight (its own loads
   // then complete under theirs).
   const float qsc = col_ok ? qscale : 0.f;
-  f16x4 qh[H16 ? 8 : 1], ql[H16 ? 8 : 1];
+  f16x8 qh[H16 ? 4 : 1], ql[H16 ? 4 : 1];
   float q_up = 1.f;
   auto scale_q = [&]() {
     if constexpr (PRO) {
@@ -403,8 +526,8 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       double ss = 0.0;
 #pragma unroll
       for (int i = 0; i < 32; ++i) ss += (double)qv[i] * (double)qv[i];
-      ss += __shfl_xor(ss, 16, 64);
-      ss += __shfl_xor(ss, 32, 64);
+      ss = swap_sum_f64<16>(ss);
+      ss = swap_sum_f64<32>(ss);
       const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)pro.eps));
 #pragma unroll
       for (int c = 0; c < NKC / 2; ++c)
@@ -423,21 +546,21 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       float amax = 0.f;
 #pragma unroll
       for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(qv[i]));
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+      amax = swap_max<16>(amax);
+      amax = swap_max<32>(amax);
       int ex = 0;
       (void)frexpf(amax, &ex);  // amax < 2^ex
       const int k = ex > 14 ? ex - 14 : 0;
       const float down = ldexpf(1.f, -k);
       q_up = ldexpf(1.f, k);
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const float v = qv[(m >> 1) * 8 + 4 * (m & 1) + kk] * down;
+        for (int e = 0; e < 8; ++e) {
+          const float v = qv[c * 8 + e] * down;
           const _Float16 h = (_Float16)v;
-          qh[m][kk] = h;
-          ql[m][kk] = (_Float16)(v - (float)h);
+          qh[c][e] = h;
+          ql[c][e] = (_Float16)(v - (float)h);
         }
     }
   };
@@ -448,22 +571,33 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   float m_run = kNegSentinel, l_run = 0.f;
   auto compute = [&](int j, const CT (&kb)[NKC], const CT (&vb)[NVC]) {
     const int t0 = t_begin + (wave + j * W) * 16;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // Independent accumulator chains: a dependent MFMA waits for its
+    // predecessor's result (~50 cycles on gfx950) where independent ones
+    // issue every 16-32.
+    f32x4 acc;
     if constexpr (H16) {
+      // v_mfma_f32_16x16x32_f16: lane (t, k) supplies K[t][32c + 8k .. +7],
+      // i.e. its loaded chunk c as is, and q the same slots; hi and lo
+      // products in separate chains.
+      f32x4 a4[4];
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const f16x4 k4 = {(_Float16)kb[m >> 1][4 * (m & 1)], (_Float16)kb[m >> 1][4 * (m & 1) + 1],
-                          (_Float16)kb[m >> 1][4 * (m & 1) + 2], (_Float16)kb[m >> 1][4 * (m & 1) + 3]};
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k4, qh[m], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(k4, ql[m], acc, 0, 0, 0);
+      for (int i = 0; i < 4; ++i) a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        a4[2 * (c & 1)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[c], qh[c], a4[2 * (c & 1)], 0, 0, 0);
+        a4[2 * (c & 1) + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[c], ql[c], a4[2 * (c & 1) + 1], 0, 0, 0);
       }
-      acc *= q_up;
+      acc = ((a4[0] + a4[2]) + (a4[1] + a4[3])) * q_up;
     } else {
+      f32x4 a4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NKC; ++c)
 #pragma unroll
         for (int e = 0; e < E; ++e)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kb[c][e], qv[c * E + e], acc, 0, 0, 0);
+          a4[e & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kb[c][e], qv[c * E + e], a4[e & 3], 0, 0, 0);
+      acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
     }
     float x[4], mx = kNegSentinel;
 #pragma unroll
@@ -471,73 +605,83 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       x[r] = (t0 + 4 * lk + r < t_end) ? acc[r] : -INFINITY;
       mx = fmaxf(mx, x[r]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m_run, mx);
-    // v_exp_f32 directly: results below 2^-126 flush to zero, which only
-    // drops weights that are negligible next to the running maximum's 1.
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-    m_run = mn;
+    mx = swap_max<16>(mx);
+    mx = swap_max<32>(mx);
+    // Lazy rescaling: the running maximum (per query head) moves only when
+    // a tile's scores exceed it by more than 2^kSlack, so the probabilities
+    // stay within 2^kSlack and the accumulators are rescaled only then (a
+    // wave-uniform branch, rare after a wave's first tile) instead of on
+    // every tile, where the multiplies also stalled the PV MFMA chains.
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {
+      const float mn = fmaxf(m_run, mx);
+      // v_exp_f32 directly: results below 2^-126 flush to zero, which only
+      // drops weights negligible next to the running maximum's.
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+      m_run = mn;
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) o[b] *= alpha;
+    }
     float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - mn);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - m_run);
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+    // PV with consecutive MFMAs on different accumulators (a dependent MFMA
+    // waits ~50 cycles for its predecessor).
     if constexpr (H16) {
       f16x4 ph, pl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pp = p[r] * 16384.f;
+        const float pp = p[r] * kPScale;
         const _Float16 h = (_Float16)pp;
         ph[r] = h;
         pl[r] = (_Float16)(pp - (float)h);
       }
+      f16x4 v4[8];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        o[b] *= alpha;
-        const f16x4 v4 = {(_Float16)vb[0][b], (_Float16)vb[1][b], (_Float16)vb[2][b], (_Float16)vb[3][b]};
-        o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph, o[b], 0, 0, 0);
-        o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl, o[b], 0, 0, 0);
-      }
+      for (int b = 0; b < 8; ++b) v4[b] = f16x4{(_Float16)vb[0][b], (_Float16)vb[1][b], (_Float16)vb[2][b], (_Float16)vb[3][b]};
+#pragma unroll
+      for (int b = 0; b < 8; ++b) o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4[b], ph, o[b], 0, 0, 0);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4[b], pl, o[b], 0, 0, 0);
     } else {
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        o[b] *= alpha;
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int b = 0; b < 8; ++b)
           o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vb[(r * 8 + b) / E][(r * 8 + b) % E], p[r], o[b], 0, 0, 0);
-      }
     }
   };
-  // Every load of a tile is issued unconditionally before the tile is used
-  // (exact wait counts: its first MFMAs start as its first chunks land); the
-  // sched_barrier keeps the compiler from sinking them to their first use.
-  // 4-wave workgroups take tiles in pairs (two in flight per wave); 8-wave
-  // ones one at a time, keeping their registers within four waves per SIMD.
-  CT ka[NKC], va[NVC];
-  int j = 0;
-  if constexpr (W == 4) {
-    CT kb2[NKC], vb2[NVC];
-    for (; j + 1 < my_tiles; j += 2) {
-      load_tile(j, ka, va);
-      load_tile(j + 1, kb2, vb2);
+  // The ring: every load of a tile is issued unconditionally (exact wait
+  // counts: a tile's first MFMAs start as its first chunks land), D tiles
+  // ahead of their use; the last round computes what is left and loads
+  // nothing.
+  CT kr[D][NKC], vr[D][NVC];
+#pragma unroll
+  for (int i = 0; i < D; ++i) load_tile(i, kr[i], vr[i]);
+  __builtin_amdgcn_sched_barrier(0);
+  scale_q();
+  const int n_rounds = (my_tiles + D - 1) / D;
+  for (int rr = 0; rr + 1 < n_rounds; ++rr) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      compute(rr * D + i, kr[i], vr[i]);
+      load_tile((rr + 1) * D + i, kr[i], vr[i]);
       __builtin_amdgcn_sched_barrier(0);
-      if (j == 0) scale_q();
-      compute(j, ka, va);
-      compute(j + 1, kb2, vb2);
     }
   }
-  for (; j < my_tiles; ++j) {
-    load_tile(j, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
-    if (j == 0) scale_q();
-    compute(j, ka, va);
+  if (n_rounds > 0) {
+    const int j0 = (n_rounds - 1) * D;
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if (j0 + i < my_tiles) compute(j0 + i, kr[i], vr[i]);
   }
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = swap_sum<16>(l_run);
+  l_run = swap_sum<32>(l_run);
 
   if constexpr (H16) {
 #pragma unroll
-    for (int b = 0; b < 8; ++b) o[b] *= 1.f / 16384.f;  // the probabilities' 2^14, exactly
+    for (int b = 0; b < 8; ++b) o[b] *= 1.f / kPScale;  // the probabilities' scale, exactly
   }
   // o[b][r] = O^T[d = 8*(4*lk + r) + b][m = li]. Merge the W waves in LDS.
   __shared__ __attribute__((aligned(16))) float sm_o[W][16][kD + 4];
@@ -554,7 +698,8 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
   }
   __syncthreads();
   const int stride = part_stride_of(group);
-  float* mine = part + ((size_t)hidx * n_splits + split) * stride;
+  const __amdgpu_buffer_rsrc_t rs = ws_rsrc(mg.part, mg.ws_bytes);
+  const uint32_t my_row = (uint32_t)(hidx * n_splits + split);
   for (int j = tid; j < group * (kD / 4); j += NT) {
     const int g = j / (kD / 4), d = (j % (kD / 4)) * 4;
     float M = sm_ml[0][g][0];
@@ -576,77 +721,116 @@ __global__ __launch_bounds__(W * 64) void decode_tile_kernel(const float* __rest
       op[2] = r[2];
       op[3] = r[3];
     } else {
-      *reinterpret_cast<f32x4*>(&mine[g * kD + d]) = O;
-      if (d == 0) {
-        mine[group * kD + 2 * g] = M;
-        mine[group * kD + 2 * g + 1] = L;
+      if (mg.fused) {  // device-scope stores for the in-launch hand-off
+        const uint32_t row = my_row * (uint32_t)stride * 4u;
+        __builtin_amdgcn_raw_buffer_store_b128(O, rs, row + (uint32_t)(g * kD + d) * 4u, 0, kPolicyDevice);
+        if (d == 0) {
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, M), rs,
+                                                row + (uint32_t)(group * kD + 2 * g) * 4u, 0, kPolicyDevice);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, L), rs,
+                                                row + (uint32_t)(group * kD + 2 * g + 1) * 4u, 0, kPolicyDevice);
+        }
+      } else {
+        float* mine = mg.part + (size_t)my_row * stride;
+        *reinterpret_cast<f32x4*>(mine + g * kD + d) = O;
+        if (d == 0) {
+          mine[group * kD + 2 * g] = M;
+          mine[group * kD + 2 * g + 1] = L;
+        }
       }
     }
   }
+  if (n_splits == 1 || !mg.fused) return;
+
+  // Level 1: the last workgroup of this split's group folds the group.
+  const int grp = split / mg.fan;
+  const int g_lo = grp * mg.fan, g_n = min(mg.fan, n_splits - g_lo);
+  if (!last_of(mg.tickets + hidx * mg.n_grp + grp, (unsigned)g_n, tid)) return;
+  float* const head_out = out + (size_t)hidx * group * kD;
+  if (mg.n_grp == 1) {
+    fold_rows<NT>(rs, (uint32_t)(hidx * n_splits), n_splits, stride, group, 0, head_out, tid);
+    return;
+  }
+  // part2 lies in the same buffer, n_heads * n_splits rows after part.
+  const uint32_t l2_row0 = (uint32_t)(gridDim.x + hidx * mg.n_grp);
+  fold_rows<NT>(rs, (uint32_t)(hidx * n_splits + g_lo), g_n, stride, group, l2_row0 + (uint32_t)grp, nullptr, tid);
+  // Level 2: the last group of this kv head folds the groups' rows.
+  if (!last_of(mg.tickets + (gridDim.x / n_splits) * mg.n_grp + hidx, (unsigned)mg.n_grp, tid)) return;
+  fold_rows<NT>(rs, l2_row0, mg.n_grp, stride, group, 0, head_out, tid);
 }
 
 // fp32 log-sum-exp merge of the splits of every (kv head, subgroup of G
-// heads) partial row set: one 256-thread workgroup per (query head, block of
-// kMergeCols output columns), its threads a grid of 256/kMergeCols split
-// lanes x kMergeCols columns. Each thread loads a chunk of kMergeChunk splits
-// (o, max, sum) before it folds any of them, so a chunk costs one memory
-// round trip; the split lanes then merge through LDS.
-constexpr int kMergeCols = 32;
-constexpr int kMergeChunk = 8;
+// heads) partial row set: one 256-thread workgroup per (query head of the
+// range, block of 16 output columns). Thread t takes columns 4*(t % 4) .. +3
+// of the block and the splits t/4, t/4 + 64, ...; it issues all of a round's
+// loads (kMergePer splits, 16-byte o loads) before folding any, in split
+// order, so up to 256 splits cost one memory round trip. The 64 split lanes
+// then merge in a fixed tree through LDS (lane i with lane i + w, w = 32 ..
+// 1). The order is fixed by n_splits alone. Measured against one workgroup
+// per query head (8 split lanes, 3-level tree) and one wave per 4 columns
+// (a 64-lane butterfly), this spread was the fastest: the merge's bytes
+// come from other XCDs' writes, and a CU's share of them bounds its time.
+constexpr int kMergeLanes = 64;
+constexpr int kMergeBlock = 16;  // output columns per workgroup
+template <int MP>  // splits per lane per round: 1, 2 or 4 (up to 64, 128, 256 splits in one round)
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, int n_splits, int stride,
                                                            int G, int group, int n_hg, float* __restrict__ out) {
-  constexpr int NS = 256 / kMergeCols;
-  constexpr int NB = kD / kMergeCols;
-  const int blk = blockIdx.x % NB, jg = blockIdx.x / NB;
-  const int g = jg % G, job = jg / G;
-  const int hidx = job / n_hg, hg = job % n_hg;
-  const int h = hidx * group + hg * G + g;  // q head within the range
-  const int tid = threadIdx.x, ci = tid % kMergeCols, sl = tid / kMergeCols;
-  const int d = blk * kMergeCols + ci;
+  constexpr int kMergePer = MP;
+  const int blk = blockIdx.x % (kD / kMergeBlock), h = blockIdx.x / (kD / kMergeBlock);  // h: q head in the range
+  const int hidx = h / group, hh = h % group;
+  const int g = hh % G, job = hidx * n_hg + hh / G;
+  const int tid = threadIdx.x, k = tid & 3, sl = tid >> 2;
+  const int d = blk * kMergeBlock + 4 * k;
   const float* base = part + (size_t)job * n_splits * stride;
-  float M = kNegSentinel, L = 0.f, O = 0.f;
-  for (int b0 = 0; b0 < n_splits; b0 += NS * kMergeChunk) {
-    float ov[kMergeChunk], mv[kMergeChunk], lv[kMergeChunk];
+  float M = kNegSentinel, L = 0.f;
+  f32x4 O = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < n_splits; s0 += kMergeLanes * kMergePer) {
+    f32x4 ov[kMergePer];
+    float mv[kMergePer], lv[kMergePer];
 #pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i) {
-      const float* ps = base + (size_t)min(b0 + NS * i + sl, n_splits - 1) * stride;
-      ov[i] = ps[g * kD + d];
+    for (int i = 0; i < kMergePer; ++i) {
+      const float* ps = base + (size_t)min(s0 + sl + i * kMergeLanes, n_splits - 1) * stride;
+      ov[i] = *reinterpret_cast<const f32x4*>(ps + g * kD + d);
       mv[i] = ps[G * kD + 2 * g];
       lv[i] = ps[G * kD + 2 * g + 1];
     }
-    float mc = M;
 #pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i)
-      if (b0 + NS * i + sl < n_splits) mc = fmaxf(mc, mv[i]);
-    const float a = __builtin_amdgcn_exp2f(M - mc);
-    L *= a;
-    O *= a;
-#pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i)
-      if (b0 + NS * i + sl < n_splits) {
-        const float c = __builtin_amdgcn_exp2f(mv[i] - mc);
-        L += lv[i] * c;
-        O += ov[i] * c;
+    for (int i = 0; i < kMergePer; ++i)
+      if (s0 + sl + i * kMergeLanes < n_splits) {
+        const float mn = fmaxf(M, mv[i]);
+        const float a = __builtin_amdgcn_exp2f(M - mn), c = __builtin_amdgcn_exp2f(mv[i] - mn);
+        L = L * a + lv[i] * c;
+        O = O * a + ov[i] * c;
+        M = mn;
       }
-    M = mc;
   }
-  __shared__ float sm[3][NS][kMergeCols + 1];
-  sm[0][sl][ci] = M;
-  sm[1][sl][ci] = L;
-  sm[2][sl][ci] = O;
-  __syncthreads();
-  if (tid < kMergeCols) {
-    float Mt = sm[0][0][tid];
-#pragma unroll
-    for (int i = 1; i < NS; ++i) Mt = fmaxf(Mt, sm[0][i][tid]);
-    float Lt = 0.f, Ot = 0.f;
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-      const float a = __builtin_amdgcn_exp2f(sm[0][i][tid] - Mt);
-      Lt += sm[1][i][tid] * a;
-      Ot += sm[2][i][tid] * a;
+  __shared__ float sm_m[kMergeLanes][4], sm_l[kMergeLanes][4];
+  __shared__ f32x4 sm_o[kMergeLanes][4];
+  sm_m[sl][k] = M;
+  sm_l[sl][k] = L;
+  sm_o[sl][k] = O;
+  for (int w = kMergeLanes / 2; w >= 1; w >>= 1) {
+    __syncthreads();
+    if (sl < w) {
+      const float m2 = sm_m[sl + w][k], l2 = sm_l[sl + w][k];
+      const f32x4 o2 = sm_o[sl + w][k];
+      const float mn = fmaxf(M, m2);
+      const float a = __builtin_amdgcn_exp2f(M - mn), c = __builtin_amdgcn_exp2f(m2 - mn);
+      L = L * a + l2 * c;
+      O = O * a + o2 * c;
+      M = mn;
+      sm_m[sl][k] = M;
+      sm_l[sl][k] = L;
+      sm_o[sl][k] = O;
     }
-    out[(size_t)h * kD + blk * kMergeCols + tid] = Ot / Lt;
+  }
+  if (sl == 0) {
+    const f32x4 r = O / L;  // out may be only 4-byte aligned
+    float* op = out + (size_t)h * kD + d;
+    op[0] = r[0];
+    op[1] = r[1];
+    op[2] = r[2];
+    op[3] = r[3];
   }
 }
 
@@ -802,20 +986,144 @@ static DecodeShape pick_shape(const rv_kv* kv, int positions, int n_heads, int g
 
 static void launch_merge(const float* part, int n_splits, int G, int group, int n_hg, int n_q, float* out,
                          hipStream_t s) {
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(n_q * (kD / kMergeCols))), dim3(256), 0, s, part, n_splits,
-                     part_stride_of(G), G, group, n_hg, out);
+  const dim3 grid((unsigned)(n_q * (kD / kMergeBlock)));
+  if (n_splits <= kMergeLanes)
+    hipLaunchKernelGGL(decode_merge_kernel<1>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+                       n_hg, out);
+  else if (n_splits <= 2 * kMergeLanes)
+    hipLaunchKernelGGL(decode_merge_kernel<2>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+                       n_hg, out);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+                       n_hg, out);
 }
 
-template <typename T, bool H16 = false>
-static void launch_tile(const TimedPair& tp, int waves, dim3 grid, hipStream_t s, const float* q, const void* kl,
-                        const void* vl, int kv_dim, int positions, int split_len, int n_splits, int group, int kv_lo,
-                        float qscale, float* part, float* out) {
-  if (waves == 8)
-    launch_timed(tp, decode_tile_kernel<T, 8, false, H16>, grid, dim3(512), s, q, (const T*)kl, (const T*)vl, kv_dim,
-                 positions, split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
+// Launch shape of the MFMA tile kernel. Default, from sweeps on MI355X:
+// 4-wave workgroups, each wave holding its share of the split's 16-position
+// tiles in a register ring `depth` deep, with the split long enough for
+// about kTileWaves waves in all (two per SIMD, all resident at once: the
+// kernel is capped at 256 registers) and every tile in flight when the ring
+// allows it (f16 planes: 4 tiles per wave, fp32: 2). The splits of a kv head
+// are folded by decode_merge_kernel; the in-launch ticket merge (fused) is a
+// tuning option: its hand-off (device-scope stores acknowledged, a
+// memory-side atomic, loads that miss L2) costs more than the second launch.
+// With fused, groups of up to kFanOne splits fold in one level, more in
+// groups of about sqrt(n_splits). Every field but split_len derives from
+// split_len and positions alone, so a kv-head range takes the same reduction
+// tree as the whole call.
+constexpr int kTileWaves = 2048;
+constexpr int kFanOne = 16;
+struct TilePlan {
+  int waves, depth, split_len, n_splits, fan, n_grp;
+  bool fused;
+};
+
+static int tile_depth(const rv_kv* kv, int waves, int split_len) {
+  const int tpw = (split_len / 16 + waves - 1) / waves;  // tiles per wave
+  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : tpw;
+  const int dmax = kv->elem == RV_ELEM_F32 ? 2 : 4;  // register ring: 64 (f32) or 32 (f16) VGPRs per tile
+  d = std::min(d, dmax);
+  return d >= 4 ? 4 : d >= 2 ? 2 : 1;
+}
+
+static TilePlan plan_tile(const rv_kv* kv, long positions, int n_heads) {
+  TilePlan p;
+  p.waves = kv->tune_decode_waves == 8 ? 8 : 4;
+  const int step = p.waves * 16;
+  long len = kv->tune_decode_split_len;
+  if (len <= 0) {
+    const long tiles = (positions + 15) / 16 * n_heads;
+    const long tpw = (tiles + kTileWaves - 1) / kTileWaves;  // tiles per wave for ~kTileWaves waves
+    len = tpw * step;
+  }
+  len = std::max<long>(len, step);
+  p.split_len = (int)((len + step - 1) / step * step);
+  p.n_splits = (int)((positions + p.split_len - 1) / p.split_len);
+  p.depth = tile_depth(kv, p.waves, p.split_len);
+  p.fused = kv->tune_decode_merge == 1;
+  int fan = (int)kv->tune_decode_fan;
+  if (fan <= 0) {
+    fan = p.n_splits;
+    if (p.n_splits > kFanOne) {
+      fan = 1;
+      while (fan * fan < p.n_splits) ++fan;
+    }
+  }
+  fan = std::max(fan, (p.n_splits + kMaxMergeGroups - 1) / kMaxMergeGroups);
+  p.fan = std::min(fan, p.n_splits);
+  p.n_grp = (p.n_splits + p.fan - 1) / p.fan;
+  return p;
+}
+
+// Workspace floats of a plan: level-1 rows, then level-2 rows.
+static size_t tile_ws_floats(const TilePlan& p, int n_heads, int group) {
+  const size_t rows = (size_t)n_heads * (p.n_splits + (p.n_grp > 1 ? p.n_grp : 0));
+  return rows * part_stride_of(group);
+}
+
+// The largest workspace any tile plan of this cache can ask for at up to
+// `capacity` positions: the default length keeps n_splits * n_heads at most
+// about kTileWaves / 4 + n_heads (split_len >= 64 * tiles-per-wave), a pinned
+// length gives capacity / split_len splits; n_grp <= n_splits.
+static size_t tile_ws_bound(const rv_kv* kv, int n_heads, int group) {
+  const long cap = (long)kv->capacity;
+  long splits = (cap + 63) / 64;
+  if (kv->tune_decode_split_len > 0)
+    splits = (cap + kv->tune_decode_split_len - 1) / kv->tune_decode_split_len;
   else
-    launch_timed(tp, decode_tile_kernel<T, 4, false, H16>, grid, dim3(256), s, q, (const T*)kl, (const T*)vl, kv_dim,
-                 positions, split_len, n_splits, group, kv_lo, qscale, part, out, NoPro{});
+    splits = std::min<long>(splits, kTileWaves / 4 / n_heads + 2);
+  splits = std::max<long>(splits, 1);
+  return (size_t)n_heads * 2 * (size_t)splits * part_stride_of(group);
+}
+
+template <typename T, int W, int D, bool PRO, bool H16, typename Pro>
+static void launch_tile_wd(const TimedPair& tp, dim3 grid, hipStream_t s, const float* q, const void* kl,
+                           const void* vl, int kv_dim, int positions, int split_len, int n_splits, int group,
+                           int kv_lo, float qscale, const MergeArgs& mg, float* out, const Pro& pro) {
+  launch_timed(tp, decode_tile_kernel<T, W, D, PRO, H16>, grid, dim3(W * 64), s, q, (PlanePtr<PRO, T>)kl,
+               (PlanePtr<PRO, T>)vl, kv_dim, positions, split_len, n_splits, group, kv_lo, qscale, mg, out, pro);
+}
+
+template <typename T, bool PRO, bool H16, typename Pro>
+static void launch_tile(const TilePlan& p, const TimedPair& tp, hipStream_t s, int n_heads, const float* q,
+                        const void* kl, const void* vl, int kv_dim, int positions, int group, int kv_lo, float qscale,
+                        const MergeArgs& mg, float* out, const Pro& pro) {
+  const dim3 grid((unsigned)(n_heads * p.n_splits));
+#define RV_TILE(W, D)                                                                                              \
+  launch_tile_wd<T, W, D, PRO, H16>(tp, grid, s, q, kl, vl, kv_dim, positions, p.split_len, p.n_splits, group, kv_lo, \
+                                    qscale, mg, out, pro)
+  // Depth 4 only for f16 planes (fp32 tiles would spill).
+  constexpr int D4 = std::is_same<T, float>::value ? 2 : 4;
+  if (p.waves == 8) {
+    if (p.depth == 1) RV_TILE(8, 1);
+    else if (p.depth == 2) RV_TILE(8, 2);
+    else RV_TILE(8, D4);
+  } else {
+    if (p.depth == 1) RV_TILE(4, 1);
+    else if (p.depth == 2) RV_TILE(4, 2);
+    else RV_TILE(4, D4);
+  }
+#undef RV_TILE
+}
+
+// Workspace and merge arguments of a tile plan; grows the workspace (sized
+// for the cache's capacity) on first need.
+static HipStatus tile_merge_args(rv_kv* kv, const TilePlan& p, int n_heads, int group, MergeArgs* mg) {
+  const size_t need = tile_ws_floats(p, n_heads, group) * sizeof(float);
+  HipStatus st = ensure_workspace(kv, need, tile_ws_bound(kv, n_heads, group) * sizeof(float));
+  if (st.e != hipSuccess) return st;
+  mg->part = (float*)kv->ws;
+  mg->tickets = kv->tickets;
+  mg->ws_bytes = (uint32_t)std::min<size_t>(kv->ws_bytes, 0xFFFFFFF0u);
+  mg->fan = p.fan;
+  mg->n_grp = p.n_grp;
+  mg->fused = p.fused;
+  return st;
+}
+
+size_t decode_ws_bound(const rv_kv* kv) {
+  if (kv->head_dim != kD) return 0;
+  return tile_ws_bound(kv, (int)kv->n_kv_heads, 16) * sizeof(float);
 }
 
 bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads) {
@@ -825,41 +1133,23 @@ bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads) {
 
 HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, size_t layer, size_t positions,
                             float scale, const DecodePro& pro, float* out, hipStream_t s) {
-  HipStatus st;
   const int n_heads = (int)kv->n_kv_heads;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
-  // The launch shape of launch_decode's MFMA path.
-  const long want = ((long)positions * n_heads + 511) / 512;
-  const int waves = kv->tune_decode_waves == 8 || kv->tune_decode_waves == 4 ? (int)kv->tune_decode_waves
-                                                                             : (want >= 256 ? 8 : 4);
-  const int step = waves * 16;
-  long len = kv->tune_decode_split_len;
-  if (len <= 0) len = want;
-  len = std::max<long>(len, step);
-  const int split_len = (int)((len + step - 1) / step * step);
-  const int n_splits = (int)((positions + split_len - 1) / split_len);
-  st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float));
+  const TilePlan p = plan_tile(kv, (long)positions, n_heads);
+  MergeArgs mg;
+  HipStatus st = tile_merge_args(kv, p, n_heads, group, &mg);
   if (st.e != hipSuccess) return st;
-  float* part = (float*)kv->ws;
-  const dim3 grid((unsigned)(n_heads * n_splits));
   const TimedPair tp = timing_pair(kv, s);
   const float qscale = scale * kLog2e;
-  auto go = [&](auto* tag) {
-    using T = std::remove_pointer_t<decltype(tag)>;
-    const T* kl = (const T*)kv->k_layer(layer);
-    const T* vl = (const T*)kv->v_layer(layer);
-    if (waves == 8)
-      launch_timed(tp, decode_tile_kernel<T, 8, true>, grid, dim3(512), s, q_raw, kl, vl, (int)kv->kv_dim,
-                   (int)positions, split_len, n_splits, group, 0, qscale, part, out, pro);
-    else
-      launch_timed(tp, decode_tile_kernel<T, 4, true>, grid, dim3(256), s, q_raw, kl, vl, (int)kv->kv_dim,
-                   (int)positions, split_len, n_splits, group, 0, qscale, part, out, pro);
-  };
+  const void* kl = kv->k_layer(layer);
+  const void* vl = kv->v_layer(layer);
   if (kv->elem == RV_ELEM_F32)
-    go((float*)nullptr);
+    launch_tile<float, true, false>(p, tp, s, n_heads, q_raw, kl, vl, (int)kv->kv_dim, (int)positions, group, 0,
+                                    qscale, mg, out, pro);
   else
-    go((_Float16*)nullptr);
-  if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
+    launch_tile<_Float16, true, false>(p, tp, s, n_heads, q_raw, kl, vl, (int)kv->kv_dim, (int)positions, group, 0,
+                                       qscale, mg, out, pro);
+  if (p.n_splits > 1 && !p.fused) launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "decode launch";
   return st;
@@ -875,41 +1165,30 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   const void* vl = kv->v_layer(layer);
   const float qscale = scale * kLog2e;
   if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1) {
-    // MFMA tile kernel. Default shape, from sweeps on MI355X: about 512
-    // workgroups in all, 4 waves (one tile each, 64 positions at ctx 4096)
-    // while splits stay short, 8 waves from 256 positions per split (ctx
-    // 32768: two tiles per wave); never less than one tile per wave.
-    const long want = ((long)positions * n_heads + 511) / 512;
-    const int waves = kv->tune_decode_waves == 8 || kv->tune_decode_waves == 4 ? (int)kv->tune_decode_waves
-                                                                               : (want >= 256 ? 8 : 4);
-    const int step = waves * 16;
-    long len = kv->tune_decode_split_len;
-    if (len <= 0) len = want;
-    len = std::max<long>(len, step);
-    const int split_len = (int)((len + step - 1) / step * step);
-    const int n_splits = (int)((positions + split_len - 1) / split_len);
-    st = ensure_workspace(kv, (size_t)n_heads * n_splits * part_stride_of(group) * sizeof(float));
+    const TilePlan p = plan_tile(kv, (long)positions, n_heads);
+    MergeArgs mg;
+    st = tile_merge_args(kv, p, n_heads, group, &mg);
     if (st.e != hipSuccess) return st;
-    float* part = (float*)kv->ws;
-    const dim3 grid((unsigned)(n_heads * n_splits));
     const TimedPair tp = timing_pair(kv, s);
+    const int kvd = (int)kv->kv_dim;
     if (kv->elem == RV_ELEM_F32)
-      launch_tile<float>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
-                         (int)kv_lo, qscale, part, out);
+      launch_tile<float, false, false>(p, tp, s, n_heads, q, kl, vl, kvd, (int)positions, group, (int)kv_lo, qscale,
+                                       mg, out, NoPro{});
     else if (kv->tune_decode_impl == 2)  // fp32 MFMA operands for f16 planes (the reference form)
-      launch_tile<_Float16>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits, group,
-                            (int)kv_lo, qscale, part, out);
+      launch_tile<_Float16, false, false>(p, tp, s, n_heads, q, kl, vl, kvd, (int)positions, group, (int)kv_lo,
+                                          qscale, mg, out, NoPro{});
     else
-      launch_tile<_Float16, true>(tp, waves, grid, s, q, kl, vl, (int)kv->kv_dim, (int)positions, split_len, n_splits,
-                                  group, (int)kv_lo, qscale, part, out);
-    if (n_splits > 1) launch_merge(part, n_splits, group, group, 1, n_heads * group, out, s);
+      launch_tile<_Float16, false, true>(p, tp, s, n_heads, q, kl, vl, kvd, (int)positions, group, (int)kv_lo, qscale,
+                                         mg, out, NoPro{});
+    if (p.n_splits > 1 && !p.fused) launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
   } else if (kv->head_dim == kD) {
     const DecodeShape d = pick_shape(kv, (int)positions, n_heads, group);
     const int n_hg = group / d.hg_size;
     const int n_splits = (int)((positions + d.split_len - 1) / d.split_len);
     const int n_jobs = n_heads * n_hg;
     const size_t part_bytes = (size_t)n_jobs * n_splits * part_stride_of(d.hg_size) * sizeof(float);
-    st = ensure_workspace(kv, part_bytes);
+    const size_t bound_splits = std::max<size_t>(1, (kv->capacity + 15) / 16);
+    st = ensure_workspace(kv, part_bytes, (size_t)n_jobs * bound_splits * part_stride_of(d.hg_size) * sizeof(float));
     if (st.e != hipSuccess) return st;
     SplitArgs a{q, kl, vl, (int)kv->kv_dim, (int)positions, d.split_len, n_splits, n_heads * n_splits, group,
                 n_hg, (int)kv_lo, qscale, (float*)kv->ws, out, timing_pair(kv, s)};
@@ -924,7 +1203,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   } else {
     const size_t hd = kv->head_dim;
     const int n_qr = n_heads * group;
-    st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float));
+    st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float), (size_t)n_qr * kv->capacity * sizeof(float));
     if (st.e != hipSuccess) return st;
     float* scores = (float*)kv->ws;
     const dim3 g1((unsigned)((positions + 255) / 256), (unsigned)n_qr);

@@ -76,6 +76,34 @@ __device__ __forceinline__ double swap_sum_f64(double x) {
   }
 }
 
+// max(x, x of the lane 16 or 32 apart), on every lane, by a permlane swap
+// (VALU; no LDS round trip as a bpermute shuffle would take).
+template <int D>
+__device__ __forceinline__ float swap_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+}
+
+// x + (x of the lane 16 or 32 apart), on every lane (the same sum on both
+// lanes of a pair).
+template <int D>
+__device__ __forceinline__ float swap_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
 // Wave total in f64 on every lane: DPP within 16-lane rows, then the two
 // cross-row swaps (all VALU, no LDS round trips).
 __device__ __forceinline__ double wave_sum_f64(double x) {

@@ -26,6 +26,15 @@ struct rv_kv {
   size_t ws_bytes = 0;
   float* qbuf = nullptr;  // normalised + rotated q rows of the fused steps
   size_t qbuf_bytes = 0;
+  // Buffers a grown workspace, qbuf, staging or staged copy replaced: kept
+  // until rv_kv_free, since a graph captured earlier may still address them.
+  std::vector<void*> retired;
+  // The decode split merge's tickets: n_kv_heads * (kMaxMergeGroups + 1)
+  // counters, zero between calls (each call's last workgroup resets its own).
+  unsigned* tickets = nullptr;
+  // Recorded on the old stream when rv_kv_set_stream moves the cache to a
+  // new one, which then waits for it.
+  hipEvent_t order_ev = nullptr;
   // Prefill's staged copy of each layer's K/V tiles (MFMA type and LDS
   // layout), kept across calls so a reused prefix is converted once:
   // positions [0, staged_pos[layer]) are current for staged_mode[layer].
@@ -45,6 +54,9 @@ struct rv_kv {
   int64_t tune_decode_hg = 0;
   int64_t tune_prefill_impl = 0;  // 0 auto, 1 two wave groups, 2 software-pipelined
   int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups
+  int64_t tune_decode_depth = 0;  // tiles in flight per wave (1, 2, 4); 0 auto
+  int64_t tune_decode_fan = 0;    // splits folded per level-1 group; 0 auto
+  int64_t tune_decode_merge = 0;  // 0 separate merge kernel, 1 in-launch ticket merge
 
   // RV_TUNE_KERNEL_TIMING: event pairs around the dominant kernel of each
   // call, folded into timed_ms / timed_n when read (or when the pool fills).
@@ -67,11 +79,24 @@ struct HipStatus {
   const char* what = nullptr;
 };
 
-// Workspace (>= bytes) and tickets (>= n) on the cache's device.
-HipStatus ensure_workspace(rv_kv* kv, size_t bytes);
+// Level-1 merge groups per kv head the decode tickets provide for.
+constexpr int kMaxMergeGroups = 64;
+
+// Workspace of at least `bytes` on the cache's device. When it must grow it
+// is allocated at max(bytes, bound) (callers pass the most any call of the
+// same geometry can ask for at the cache's capacity, so a decode loop never
+// grows it), and the old buffer is retired, not freed. Growth under graph
+// capture is refused with hipErrorStreamCaptureUnsupported.
+HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t bound = 0);
 // Whether work on s is being captured into a graph.
 bool capturing(hipStream_t s);
+// The normalised-q buffer, with the workspace's growth rules.
 HipStatus ensure_qbuf(rv_kv* kv, size_t bytes);
+// RV_ERR_UNSUPPORTED for a call that would have to allocate under graph
+// capture, RV_ERR_HIP for any other HIP failure.
+inline int32_t status_code(hipError_t e) {
+  return e == hipErrorStreamCaptureUnsupported ? RV_ERR_UNSUPPORTED : RV_ERR_HIP;
+}
 
 // RV_TUNE_KERNEL_TIMING: the event pair the next dominant-kernel launch
 // records its own start and end into (hipExtLaunchKernelGGL), or two nulls
@@ -130,6 +155,11 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
                               const StageDst* sd, hipStream_t s);
 
 // ---- decode (rv_decode.hip) ------------------------------------------------------
+// The workspace the MFMA decode path can need for any call on this cache
+// (whole kv range, groups up to 16, up to its capacity) with the default
+// launch shape; 0 when the geometry takes another path. rv_kv_new reserves
+// it, so a decode call can be captured into a graph without a warm-up call.
+size_t decode_ws_bound(const rv_kv* kv);
 // out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all
 // `positions` of `layer`. q is the full post-RoPE query.
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
@@ -181,8 +211,10 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
 
 // rv_decode_step's validation alone (no launch), for callers that validate
 // a whole composite call before launching any of it.
-int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, rv_error* err);
+int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t position, size_t q_norm_len,
+                          size_t k_norm_len, rv_error* err);
 // rv_prefill_chunk's validation alone.
-int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start, rv_error* err);
+int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start,
+                            size_t q_norm_len, size_t k_norm_len, rv_error* err);
 
 }  // namespace rv

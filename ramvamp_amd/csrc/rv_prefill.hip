@@ -988,18 +988,16 @@ HipStatus ready_persistent(rv_kv* kv, size_t layer, uint32_t mode, hipStream_t s
     kv->staged_mode[layer] = mode;
   }
   if (stage_bytes > kv->staged_bytes[layer]) {
-    if (kv->staged[layer]) {
-      (void)hipStreamSynchronize(s);
-      (void)hipFree(kv->staged[layer]);
-      kv->staged[layer] = nullptr;
-      kv->staged_bytes[layer] = 0;
-    }
-    st.e = hipMalloc(&kv->staged[layer], stage_bytes);
+    // Never reached under capture (captured calls stage into the
+    // workspace); the replaced copy is retired, not freed.
+    void* p = nullptr;
+    st.e = hipMalloc(&p, stage_bytes);
     if (st.e != hipSuccess) {
-      kv->staged[layer] = nullptr;
       st.what = "hipMalloc prefill staging";
       return st;
     }
+    if (kv->staged[layer]) kv->retired.push_back(kv->staged[layer]);
+    kv->staged[layer] = p;
     kv->staged_bytes[layer] = stage_bytes;
   }
   return st;
@@ -1052,7 +1050,12 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   // reads, which only a captured call uses; eager calls reserve it too, so
   // capturing a call of a shape already run eagerly allocates nothing.
   const size_t call_stage_bytes = (size_t)n_kv * n_stage_tiles * tile_bytes;
-  st = ensure_workspace(kv, part_bytes + call_stage_bytes);
+  // Bound for the cache's capacity: default splits keep n_rb * n_kv *
+  // kv_splits under 512 rows of partials, and a call stages at most every
+  // tile of the capacity in two planes.
+  const size_t bound = std::max<size_t>(part_bytes, (size_t)512 * kPartStride * sizeof(float)) +
+                       (size_t)n_kv * ((kv->capacity + kBT - 1) / kBT) * 2 * 2 * kPlaneBytes;
+  st = ensure_workspace(kv, part_bytes + call_stage_bytes, bound);
   if (st.e != hipSuccess) return st;
   char* stage;
   int tile_stride, stage_lo;

@@ -387,3 +387,34 @@ def test_f16_decode_keeps_fp32_products_at_extreme_q(q_scale):
     out = np.zeros(q.size, np.float32)
     rv.decode_attention(q, kv, 0, scale, None, out)
     gate(out, ref.attention(q, 0, scale), what=f"f16 decode q x {q_scale}")
+
+
+@pytest.mark.parametrize("host_ptrs", [False, True])
+def test_norm_weight_lengths_are_refused_as_the_oracle_refuses_them(host_ptrs):
+    # primitives/norm.rs:72-83 LengthMismatch, q's weight before k's; no row is
+    # appended and out is untouched. With host pointers nothing is copied from
+    # a short weight (the check runs before any staging).
+    torch_cuda()
+    n_kv, n_q, hd = 4, 32, 128
+    say(f"case norm weight lengths host_ptrs={host_ptrs}")
+    rng = Rng(0x11E8)
+    w = rng.vec_in(hd, 0.5, 1.5)
+    q, k, v = rng.vec_in(n_q * hd, -1.0, 1.0), rng.vec_in(n_kv * hd, -1.0, 1.0), rng.vec_in(n_kv * hd, -1.0, 1.0)
+    cases = [(w[:hd - 1], w), (np.concatenate([w, w]), w[:3]), (w, w[:3]), (w, np.concatenate([w, w[:1]]))]
+    put = (lambda a: a) if host_ptrs else dev
+    for wq, wk in cases:
+        kv = rv.KvCache(1, n_kv, hd, 4, "f32")
+        ref = oracle.KvCache(1, n_kv, hd, 4, oracle.RV_ELEM_F32)
+        with pytest.raises(oracle.OracleError) as e:
+            ref.decode_step(0, q, k, v, wq, wk, 1e-6, 1e6, 0, 0.5)
+        want = e.value.payload()
+        out = np.full(q.size, np.nan, np.float32) if host_ptrs else dev(np.full(q.size, np.nan, np.float32))
+        with pytest.raises(rv.RamvampError) as g:
+            rv.decode_step(kv, 0, put(q), put(k), put(v), put(wq), put(wk), 1e-6, 1e6, 0, 0.5, out)
+        assert g.value.raw == want, (g.value.raw, want)
+        with pytest.raises(rv.RamvampError) as g:
+            rv.prefill_chunk(kv, 0, put(q.reshape(1, -1)), put(k.reshape(1, -1)), put(v.reshape(1, -1)), put(wq),
+                             put(wk), 1e-6, 1e6, 0, 0.5, out.reshape(1, -1) if host_ptrs else out.view(1, -1))
+        assert g.value.raw == want, (g.value.raw, want)
+        assert kv.len(0) == 0
+        assert np.all(np.isnan(out if host_ptrs else host(out)))

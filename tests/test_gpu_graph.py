@@ -117,3 +117,39 @@ def test_prefill_graph_replays_match_eager_and_leave_the_staged_copy_sound(mode)
         assert np.array_equal(got.view(np.uint32), want_short.view(np.uint32)), f"replay {rep}"
         again = eager(260)  # restages past the replay's zeroed rows
         assert np.array_equal(again.view(np.uint32), want_long.view(np.uint32)), f"eager after replay {rep}"
+
+
+def test_a_graph_captured_early_stays_valid_as_the_context_grows():
+    # The workspace is sized for the cache's capacity and never freed while
+    # the cache lives: a decode graph captured at ctx 512 on a fresh cache
+    # (no warm-up call) still replays correctly after eager calls at ctx
+    # 8192, into a NaN-filled out, bit for bit the eager result at 512.
+    torch = torch_cuda()
+    say("case early capture, context grows to 8192")
+    rng = Rng(0x6A80)
+    cap = 8192
+    kv = rv.KvCache(1, 4, 128, cap, "f32")
+    K = rng.vec_in(cap * 512, -1.0, 1.0).reshape(cap, -1)
+    V = rng.vec_in(cap * 512, -1.0, 1.0).reshape(cap, -1)
+    kv.append_rows(0, K[:512], V[:512])
+    q = dev(rng.vec_in(4096, -1.0, 1.0))
+    out = torch.full_like(q, float("nan"))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rv.decode_attention(q, kv, 0, scale, None, out)
+    out.fill_(float("nan"))
+    rv.decode_attention(q, kv, 0, scale, None, out)
+    want = host(out).copy()
+    for n in (1024, 4096, 8192):
+        kv.append_rows(0, K[kv.len(0):n], V[kv.len(0):n])
+        eager = torch.full_like(q, float("nan"))
+        rv.decode_attention(q, kv, 0, scale, None, eager)
+        assert not np.any(np.isnan(host(eager))), n
+        for rep in range(2):
+            out.fill_(float("nan"))
+            g.replay()
+            got = host(out)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, rep)

@@ -506,3 +506,33 @@ def test_decode_step_and_prefill_chunk_match_the_f64_composition():
         qn = _norm_rope_f64(qr[r], n_q, hd, wq, eps, theta, start + r)
         n = start + r + 1
         assert_close(got[r], reference_attention(qn, kall[:n], vall[:n], n_kv, hd, scale), 1e-4, 5e-5, f"row {r}")
+
+
+def test_norm_weight_lengths_are_checked_q_first_then_k():
+    # primitives/norm.rs:72-83: rmsnorm_in_place refuses a weight whose length
+    # differs from the head's, LengthMismatch {left: head_dim, right: len}; the
+    # callers normalise every q head before any k head (forward.rs:2622-2627,
+    # prefill.rs:2057-2076). Nothing is appended on the error.
+    n_kv, n_q, hd = 2, 4, 8
+    rng = Rng(0x11E7)
+    w = rng.vec_in(hd, 0.5, 1.5)
+    q, k, v = rng.vec_in(n_q * hd, -1.0, 1.0), rng.vec_in(n_kv * hd, -1.0, 1.0), rng.vec_in(n_kv * hd, -1.0, 1.0)
+    cases = [(w[:hd - 1], w, (oracle.RV_PRIM_LENGTH_MISMATCH, hd, hd - 1)),
+             (np.concatenate([w, w]), w[:3], (oracle.RV_PRIM_LENGTH_MISMATCH, hd, 2 * hd)),
+             (w, w[:3], (oracle.RV_PRIM_LENGTH_MISMATCH, hd, 3)),
+             (w, np.concatenate([w, w[:1]]), (oracle.RV_PRIM_LENGTH_MISMATCH, hd, hd + 1))]
+    for wq, wk, want in cases:
+        kv = oracle.KvCache(1, n_kv, hd, 4, oracle.RV_ELEM_F32)
+        with pytest.raises(oracle.OracleError) as e:
+            kv.decode_step(0, q, k, v, wq, wk, 1e-6, 1e6, 0, 0.5)
+        assert e.value.payload()[:3] == want and e.value.what == "rmsnorm_in_place: x vs weight"
+        assert kv.len(0) == 0
+        with pytest.raises(oracle.OracleError) as e:
+            kv.prefill_chunk(0, q.reshape(1, -1), k.reshape(1, -1), v.reshape(1, -1), wq, wk, 1e-6, 1e6, 0, 0.5)
+        assert e.value.payload()[:3] == want
+        assert kv.len(0) == 0
+    # an empty chunk normalises nothing, so it reports nothing
+    kv = oracle.KvCache(1, n_kv, hd, 4, oracle.RV_ELEM_F32)
+    out = kv.prefill_chunk(0, np.zeros((0, n_q * hd), np.float32), np.zeros((0, n_kv * hd), np.float32),
+                           np.zeros((0, n_kv * hd), np.float32), w[:1], w[:1], 1e-6, 1e6, 0, 0.5)
+    assert out.size == 0
