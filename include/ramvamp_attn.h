@@ -177,6 +177,22 @@ int32_t rv_decode_attention_kv_range_in(const rv_kv* kv, const float* q, size_t 
                                         size_t layer, float scale, size_t kv_lo, size_t kv_hi,
                                         size_t scratch_len, float* out, size_t out_len,
                                         uint32_t flags, rv_error* err);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). rv_decode_attention with device pointers only, whose
+ * split partials (or scores, on the generic path) live in a fixed
+ * file-scope device array of RV_NOALLOC_SCRATCH_BYTES that each GPU holds
+ * until the process ends, instead of the cache's workspace; it allocates
+ * nothing and makes no timing events. Same validation and results (bit for
+ * bit) as rv_decode_attention. RV_HOST_PTRS, or a call whose scratch need
+ * exceeds the array, is RV_ERR_UNSUPPORTED (a = bytes needed, b = the
+ * limit; a = 0 for host pointers). Every call on one GPU shares the array:
+ * calls that overlap on one GPU (other streams, other caches) race. */
+#define RV_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int32_t rv_decode_attention_noalloc(const rv_kv* kv, const float* q, size_t q_len, size_t layer,
+                                    float scale, float* out, size_t out_len, uint32_t flags,
+                                    rv_error* err);
+
 /* attention.rs:666 `attention_at`: positions 0..positions only (the causal
  * limit is a length). positions == 0 -> RV_ATTN_EMPTY_LAYER; positions
  * past len(layer) -> RV_KV_POSITION_OUT_OF_RANGE. */

@@ -23,13 +23,17 @@ from .attention import (  # noqa: F401
     decode_attention,
     decode_attention_in,
     decode_attention_kv_range_in,
+    decode_attention_noalloc,
     decode_step,
     prefill_chunk,
     scratch_len,
 )
 from ._lib import (  # noqa: F401  (knobs of KvCache.set_tuning)
+    RV_TUNE_DECODE_DEPTH,
+    RV_TUNE_DECODE_FAN,
     RV_TUNE_DECODE_HG,
     RV_TUNE_DECODE_IMPL,
+    RV_TUNE_DECODE_MERGE,
     RV_TUNE_DECODE_SPLIT_LEN,
     RV_TUNE_DECODE_WAVES,
     RV_TUNE_KERNEL_TIMING,

@@ -28,6 +28,10 @@ RV_TUNE_DECODE_HG = 5
 RV_TUNE_DECODE_IMPL = 6
 RV_TUNE_KERNEL_TIMING = 7
 RV_TUNE_PREFILL_IMPL = 8
+RV_TUNE_DECODE_DEPTH = 9
+RV_TUNE_DECODE_FAN = 10
+RV_TUNE_DECODE_MERGE = 11
+RV_NOALLOC_SCRATCH_BYTES = 8 << 20
 # include/ramvamp_gemv.h
 RV_QF_Q4_K = 1
 RV_QF_Q5_K = 2
@@ -91,6 +95,7 @@ SIGNATURES = {
                                  c_float, c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, c_float,
                                    c_float, c_size_t, c_float, _P, c_uint32, _E]),
+    "rv_decode_attention_noalloc": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
     "rv_kv_kernel_time": (c_int32, [_P, POINTER(c_double), POINTER(c_uint64), _E]),
     # include/ramvamp_gemv.h

@@ -355,6 +355,13 @@ def decode_attention(q, cache: KvCache, layer: int, scale: float, scratch, out):
     return _attn("rv_decode_attention", q, cache, layer, (scale,), out)
 
 
+def decode_attention_noalloc(q, cache: KvCache, layer: int, scale: float, out):
+    """rv_decode_attention_noalloc (no reference counterpart): decode_attention
+    with its split partials in the library's fixed device scratch, allocating
+    nothing; device tensors only (host arrays are refused)."""
+    return _attn("rv_decode_attention_noalloc", q, cache, layer, (scale,), out)
+
+
 def decode_attention_in(q, cache: KvCache, layer: int, scale: float, scratch, out):
     """attention.rs:484."""
     return _attn("rv_decode_attention_in", q, cache, layer, (scale, _scratch_len(scratch)), out)

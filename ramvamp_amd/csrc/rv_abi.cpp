@@ -428,6 +428,12 @@ int32_t rv_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t ca
     const rv::HipStatus st = rv::ensure_workspace(kv, rv::decode_ws_bound(kv));
     e = st.e;
   }
+  if (e == hipSuccess) {
+    // Set-up of rv_decode_attention_noalloc on this device (its scratch
+    // array's address), so that its calls never resolve it themselves.
+    void* scratch = nullptr;
+    (void)rv::noalloc_scratch(device, &scratch);
+  }
   if (e != hipSuccess) {
     rv_kv_free(kv);
     return hip_fail(err, e, "hipMalloc planes");
@@ -614,6 +620,35 @@ int32_t rv_kv_read_row(const rv_kv* kv, int plane_v, size_t layer, size_t pos, v
 int32_t rv_decode_attention(const rv_kv* kv, const float* q, size_t q_len, size_t layer, float scale, float* out,
                             size_t out_len, uint32_t flags, rv_error* err) {
   return attention_entry(kv, q, q_len, layer, false, 0, scale, 0, 0, true, false, 0, out, out_len, flags, err);
+}
+
+// No reference counterpart: rv_decode_attention on the device scratch array
+// (rv_decode.hip), allocating nothing.
+int32_t rv_decode_attention_noalloc(const rv_kv* ckv, const float* q, size_t q_len, size_t layer, float scale,
+                                    float* out, size_t out_len, uint32_t flags, rv_error* err) {
+  if (!ckv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  rv_kv* kv = const_cast<rv_kv*>(ckv);
+  if (flags & RV_HOST_PTRS)
+    return fail(err, RV_ERR_UNSUPPORTED, 0, rv::kNoAllocScratchBytes, 0, 0, "host pointers (staging allocates)");
+  Plan p;
+  int32_t rc = plan(kv, q_len, layer, false, 0, 0, kv->n_kv_heads, out_len, &p, err);
+  if (rc) return rc;
+  if (!q || !out) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, !q ? "q" : "out");
+  const size_t need = rv::decode_ws_need(kv, p.n_q_heads, p.positions, kv->n_kv_heads);
+  if (need > rv::kNoAllocScratchBytes)
+    return fail(err, RV_ERR_UNSUPPORTED, need, rv::kNoAllocScratchBytes, 0, 0, "decode scratch above the no-alloc limit");
+  DeviceGuard dg(kv->device);
+  void* base = nullptr;
+  rv::HipStatus hs = rv::noalloc_scratch(kv->device, &base);
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  const rv::Workspace ws{base, rv::kNoAllocScratchBytes};
+  hs = rv::launch_decode(kv, q, p.n_q_heads, layer, p.positions, scale, 0, kv->n_kv_heads, out, kv->stream, &ws);
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  if (flags & RV_SYNC) {
+    const hipError_t e = hipStreamSynchronize(kv->stream);
+    if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
+  }
+  return ok(err);
 }
 
 int32_t rv_decode_attention_in(const rv_kv* kv, const float* q, size_t q_len, size_t layer, float scale,

@@ -32,6 +32,7 @@
 #include "rv_internal.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace rv {
@@ -1108,13 +1109,25 @@ static void launch_tile(const TilePlan& p, const TimedPair& tp, hipStream_t s, i
 
 // Workspace and merge arguments of a tile plan; grows the workspace (sized
 // for the cache's capacity) on first need.
-static HipStatus tile_merge_args(rv_kv* kv, const TilePlan& p, int n_heads, int group, MergeArgs* mg) {
+static HipStatus tile_merge_args(rv_kv* kv, const TilePlan& p, int n_heads, int group, const Workspace* ws,
+                                 MergeArgs* mg) {
   const size_t need = tile_ws_floats(p, n_heads, group) * sizeof(float);
-  HipStatus st = ensure_workspace(kv, need, tile_ws_bound(kv, n_heads, group) * sizeof(float));
-  if (st.e != hipSuccess) return st;
-  mg->part = (float*)kv->ws;
+  HipStatus st;
+  if (ws) {
+    if (need > ws->bytes) {
+      st.e = hipErrorInvalidValue;
+      st.what = "decode scratch too small";
+      return st;
+    }
+    mg->part = (float*)ws->base;
+    mg->ws_bytes = (uint32_t)std::min<size_t>(ws->bytes, 0xFFFFFFF0u);
+  } else {
+    st = ensure_workspace(kv, need, tile_ws_bound(kv, n_heads, group) * sizeof(float));
+    if (st.e != hipSuccess) return st;
+    mg->part = (float*)kv->ws;
+    mg->ws_bytes = (uint32_t)std::min<size_t>(kv->ws_bytes, 0xFFFFFFF0u);
+  }
   mg->tickets = kv->tickets;
-  mg->ws_bytes = (uint32_t)std::min<size_t>(kv->ws_bytes, 0xFFFFFFF0u);
   mg->fan = p.fan;
   mg->n_grp = p.n_grp;
   mg->fused = p.fused;
@@ -1137,7 +1150,7 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const TilePlan p = plan_tile(kv, (long)positions, n_heads);
   MergeArgs mg;
-  HipStatus st = tile_merge_args(kv, p, n_heads, group, &mg);
+  HipStatus st = tile_merge_args(kv, p, n_heads, group, nullptr, &mg);
   if (st.e != hipSuccess) return st;
   const TimedPair tp = timing_pair(kv, s);
   const float qscale = scale * kLog2e;
@@ -1155,9 +1168,29 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
   return st;
 }
 
+size_t decode_ws_need(const rv_kv* kv, size_t n_q_heads, size_t positions, size_t n_heads) {
+  if (n_heads == 0) return 0;
+  const int group = (int)(n_q_heads / kv->n_kv_heads);
+  if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1)
+    return tile_ws_floats(plan_tile(kv, (long)positions, (int)n_heads), (int)n_heads, group) * sizeof(float);
+  if (kv->head_dim == kD) {
+    const DecodeShape d = pick_shape(kv, (int)positions, (int)n_heads, group);
+    const size_t n_splits = (positions + d.split_len - 1) / d.split_len;
+    return n_heads * (size_t)(group / d.hg_size) * n_splits * part_stride_of(d.hg_size) * sizeof(float);
+  }
+  return n_heads * (size_t)group * positions * sizeof(float);
+}
+
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
-                        float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s) {
+                        float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s, const Workspace* ws) {
   HipStatus st;
+  if (ws && decode_ws_need(kv, n_q_heads, positions, kv_hi - kv_lo) > ws->bytes) {
+    st.e = hipErrorInvalidValue;
+    st.what = "decode scratch too small";
+    return st;
+  }
+  // With a caller's workspace nothing may allocate: no timing events either.
+  auto timing = [&]() { return ws ? TimedPair{} : timing_pair(kv, s); };
   const int n_heads = (int)(kv_hi - kv_lo);
   if (n_heads == 0) return st;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
@@ -1167,9 +1200,9 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1) {
     const TilePlan p = plan_tile(kv, (long)positions, n_heads);
     MergeArgs mg;
-    st = tile_merge_args(kv, p, n_heads, group, &mg);
+    st = tile_merge_args(kv, p, n_heads, group, ws, &mg);
     if (st.e != hipSuccess) return st;
-    const TimedPair tp = timing_pair(kv, s);
+    const TimedPair tp = timing();
     const int kvd = (int)kv->kv_dim;
     if (kv->elem == RV_ELEM_F32)
       launch_tile<float, false, false>(p, tp, s, n_heads, q, kl, vl, kvd, (int)positions, group, (int)kv_lo, qscale,
@@ -1187,11 +1220,16 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     const int n_splits = (int)((positions + d.split_len - 1) / d.split_len);
     const int n_jobs = n_heads * n_hg;
     const size_t part_bytes = (size_t)n_jobs * n_splits * part_stride_of(d.hg_size) * sizeof(float);
-    const size_t bound_splits = std::max<size_t>(1, (kv->capacity + 15) / 16);
-    st = ensure_workspace(kv, part_bytes, (size_t)n_jobs * bound_splits * part_stride_of(d.hg_size) * sizeof(float));
-    if (st.e != hipSuccess) return st;
+    float* part = ws ? (float*)ws->base : nullptr;
+    if (!ws) {
+      const size_t bound_splits = std::max<size_t>(1, (kv->capacity + 15) / 16);
+      st = ensure_workspace(kv, part_bytes,
+                            (size_t)n_jobs * bound_splits * part_stride_of(d.hg_size) * sizeof(float));
+      if (st.e != hipSuccess) return st;
+      part = (float*)kv->ws;
+    }
     SplitArgs a{q, kl, vl, (int)kv->kv_dim, (int)positions, d.split_len, n_splits, n_heads * n_splits, group,
-                n_hg, (int)kv_lo, qscale, (float*)kv->ws, out, timing_pair(kv, s)};
+                n_hg, (int)kv_lo, qscale, part, out, timing()};
     if (kv->elem == RV_ELEM_F32) {
       if (d.waves == 4) launch_split_g<float, 4>(d.hg_size, a, s);
       else launch_split_g<float, 8>(d.hg_size, a, s);
@@ -1199,13 +1237,17 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
       if (d.waves == 4) launch_split_g<_Float16, 4>(d.hg_size, a, s);
       else launch_split_g<_Float16, 8>(d.hg_size, a, s);
     }
-    if (n_splits > 1) launch_merge((const float*)kv->ws, n_splits, d.hg_size, group, n_hg, n_jobs * d.hg_size, out, s);
+    if (n_splits > 1) launch_merge(part, n_splits, d.hg_size, group, n_hg, n_jobs * d.hg_size, out, s);
   } else {
     const size_t hd = kv->head_dim;
     const int n_qr = n_heads * group;
-    st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float), (size_t)n_qr * kv->capacity * sizeof(float));
-    if (st.e != hipSuccess) return st;
-    float* scores = (float*)kv->ws;
+    float* scores = ws ? (float*)ws->base : nullptr;
+    if (!ws) {
+      st = ensure_workspace(kv, (size_t)n_qr * positions * sizeof(float),
+                            (size_t)n_qr * kv->capacity * sizeof(float));
+      if (st.e != hipSuccess) return st;
+      scores = (float*)kv->ws;
+    }
     const dim3 g1((unsigned)((positions + 255) / 256), (unsigned)n_qr);
     const dim3 g3((unsigned)((hd + 63) / 64), (unsigned)n_qr);
     if (kv->elem == RV_ELEM_F32) {
@@ -1224,6 +1266,45 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   }
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "decode launch";
+  return st;
+}
+
+// ---- the no-alloc entry point's scratch ------------------------------------------
+// rv_decode_attention_noalloc's split partials (or scores, on the generic
+// path) live here instead of in the cache's workspace: a fixed array that
+// each GPU the library runs on holds until the process ends. In host code
+// the name is only a stand-in; the array's device address, one per device,
+// comes from hipGetSymbolAddress with that device current, and only that
+// address reaches kernels. Nothing in it must start at zero (every partial
+// is written before it is read). Calls that overlap on one GPU share it and
+// race.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+HipStatus noalloc_scratch(int device, void** ptr) {
+  HipStatus st;
+  *ptr = nullptr;
+  if (device < 0 || device >= kMaxScratchDevices) {
+    st.e = hipErrorInvalidDevice;
+    st.what = "device index for the no-alloc scratch";
+    return st;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    st.e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (st.e != hipSuccess) {
+      st.what = "hipGetSymbolAddress(scratch)";
+      return st;
+    }
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
   return st;
 }
 

@@ -162,8 +162,22 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
 size_t decode_ws_bound(const rv_kv* kv);
 // out[(h - kv_lo*group)*d + i] for the kv-head range [kv_lo, kv_hi), all
 // `positions` of `layer`. q is the full post-RoPE query.
+// A caller's workspace, used instead of the cache's (nothing is allocated,
+// no timing events are made); the launch fails if it is too small.
+struct Workspace {
+  void* base;
+  size_t bytes;
+};
 HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t layer, size_t positions,
-                        float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s);
+                        float scale, size_t kv_lo, size_t kv_hi, float* out, hipStream_t s,
+                        const Workspace* ws = nullptr);
+// Workspace bytes launch_decode needs for this call's geometry.
+size_t decode_ws_need(const rv_kv* kv, size_t n_q_heads, size_t positions, size_t n_heads);
+// rv_decode_attention_noalloc's device scratch: kNoAllocScratchBytes in a
+// file-scope device array (rv_decode.hip); its address on `device` (which
+// must be current), resolved once per device.
+constexpr size_t kNoAllocScratchBytes = RV_NOALLOC_SCRATCH_BYTES;
+HipStatus noalloc_scratch(int device, void** ptr);
 
 // The decode step's prologue carried into the tile kernel (forward.rs:
 // 2617-2633): q pre-norm (each workgroup normalizes and rotates its group's
