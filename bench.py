@@ -19,10 +19,19 @@ end on the launch stream (RV_TUNE_KERNEL_TIMING, hipExtLaunchKernelGGL).
 `traffic` is the HBM bytes per launch read from the committed rocprofv3
 counter summary, when present.
 
+`roofline.whole_call` is the same bytes over the whole call's time per layer
+(tile kernel + split-merge kernel, from the graph replay).
+
 `extra` carries the other configurations: prefill TFLOP/s of configs 3 and 4
-in the three arithmetic modes and the long-context f16 decode of config 5.
-`cpu_baseline` is the C restatement of the reference's CPU decode path
-(oracle/, AVX2+F16C, kv-head fan-out) on a bounded sample of config 2.
+in the three arithmetic modes, the long-context f16 decode of config 5 (the
+library's own split plan and BASELINE's 8 / 16 / 32 splits per kv head), the
+fused decode step of config 1, the decode context ladder (f16 cache, 64 ..
+32,768 positions, a 1-layer and a 48-layer arm, as benches/kernels.rs:168,
+:691-738), the widening legs (projections, batched projections, router,
+attention block), and each config's CPU baseline. `cpu_baseline` is the C
+restatement of the reference's CPU decode path (oracle/, AVX2+F16C, kv-head
+fan-out over 4 threads) on a bounded sample of config 2; the prefill
+baselines time the whole 512-row chunk over the box's cores (at most 16).
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -137,6 +146,10 @@ def bench_config2(torch, rv, synth, steps, warmup):
     for _ in range(warmup):
         graph.replay()
     per_step = timed(torch, graph.replay, steps) / steps
+    # The replay must rewrite every output: start it from NaN.
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
     graph_ok = bool(torch.equal(out, ref))
 
     byts = decode_bytes(4096, 4)
@@ -151,6 +164,7 @@ def bench_config2(torch, rv, synth, steps, warmup):
         "eager_us_per_layer": eager / 48 * 1e6,
         "eager_gbs": 48 * byts / eager / 1e9,
         "kernel_us": k_avg * 1e6 if k_avg else None,
+        "whole_call_gbs": byts / (per_step / 48) / 1e9,
         "kernel_launches_timed": k_n,
         "achieved_gbs": byts / k_avg / 1e9 if k_avg else None,
         "bytes_per_launch": byts,
@@ -211,8 +225,12 @@ def bench_config1(torch, rv, synth, iters=50):
             "bytes_per_call": nbytes}
 
 
-def bench_config5(torch, rv, synth, iters=50, n_caches=5):
-    """ctx 32,768 f16 KV, rotating 5 distinct caches (335 MB) past the 256 MB MALL."""
+def bench_config5(torch, rv, synth, iters=50, n_caches=5, split_lens=(0, 1024, 2048, 4096)):
+    """ctx 32,768 f16 KV, rotating 5 distinct caches (335 MB) past the 256 MB
+    MALL. One result per split length: 0 is the library's own plan (256
+    positions per split at this length: 128 splits per kv head); 1024 / 2048
+    / 4096 pin RV_TUNE_DECODE_SPLIT_LEN to BASELINE config 5's 32 / 16 / 8
+    splits per kv head."""
     n = 32768
     caches = []
     for i in range(n_caches):
@@ -224,34 +242,100 @@ def bench_config5(torch, rv, synth, iters=50, n_caches=5):
                                         synth.THETA)).cuda()
     out = torch.zeros_like(q)
     scale = float(synth.SCALE)
+    byts = decode_bytes(n, 2)
 
     def once():
         for kv in caches:
             rv.decode_attention(q, kv, 0, scale, None, out)
 
-    for _ in range(3):
-        once()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        once()
-    graph.replay()
-    per = timed(torch, graph.replay, iters) / (iters * n_caches)
-    tot, cnt = 0.0, 0
+    res = {}
+    for split_len in split_lens:
+        for kv in caches:
+            kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, split_len)
+        for _ in range(3):
+            once()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            once()
+        graph.replay()
+        per = timed(torch, graph.replay, iters) / (iters * n_caches)
+        del graph
+        tot, cnt = 0.0, 0
+        for kv in caches:
+            kv.set_tuning(rv.RV_TUNE_KERNEL_TIMING, 1)
+            kv.kernel_time()
+        for _ in range(iters):
+            once()
+        for kv in caches:
+            ms, c = kv.kernel_time()
+            kv.set_tuning(rv.RV_TUNE_KERNEL_TIMING, 0)
+            tot += ms
+            cnt += c
+        k_avg = tot / 1e3 / cnt
+        sl = split_len or 256
+        res["default" if split_len == 0 else f"splits_{n // sl}"] = {
+            "split_len": sl, "splits_per_kv_head": -(-n // sl),
+            "us_per_call": round(per * 1e6, 3), "gbs_call": round(byts / per / 1e9, 1),
+            "frac_call": round(byts / per / 1e9 / HBM_PEAK_GBS, 4),
+            "us_tile_kernel": round(k_avg * 1e6, 3), "gbs_tile_kernel": round(byts / k_avg / 1e9, 1),
+            "hbm_frac_tile_kernel": round(byts / k_avg / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": byts}
     for kv in caches:
-        kv.set_tuning(7, 1)
-        kv.kernel_time()
-    for _ in range(iters):
-        once()
-    for kv in caches:
-        ms, c = kv.kernel_time()
-        kv.set_tuning(7, 0)
-        tot += ms
-        cnt += c
-    k_avg = tot / 1e3 / cnt
-    byts = decode_bytes(n, 2)
-    return {"us_per_call": round(per * 1e6, 3), "gbs_call": round(byts / per / 1e9, 1),
-            "us_kernel": round(k_avg * 1e6, 3), "gbs_kernel": round(byts / k_avg / 1e9, 1),
-            "hbm_frac_kernel": round(byts / k_avg / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": byts}
+        kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, 0)
+    return res
+
+
+def bench_ladder(torch, rv, synth, ctxs=(64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384, 32768)):
+    """Decode attention against context length, as the reference's ladder
+    (benches/kernels.rs:168-214, :691-738): f16 cache (the reference's
+    format), GQA 32/4, d 128, the cache grown in place through the rungs.
+    Arm A: one layer, timed unit = one call, 48 calls on that layer per
+    replayed graph (its planes, up to 64 MiB, stay cache-resident). Arm B: 48
+    layers, one token's 48 calls per graph (up to 3 GiB of planes, streamed
+    from HBM). ns/pos = ns per call / context; the linearity ratio is
+    max(ns/pos) / min(ns/pos) over the rungs, as the reference prints it;
+    `fit` is the least-squares line us_per_call = floor + slope * context,
+    the GPU's fixed per-call cost and its per-position cost."""
+    cap = max(ctxs)
+    rng = np.random.default_rng(0x1ADD)
+    scale = float(synth.SCALE)
+    res = {}
+    for arm, layers in (("arm_a", 1), ("arm_b", 48)):
+        kv = rv.KvCache(layers, 4, 128, cap, "f16")
+        q = torch.from_numpy(rng.standard_normal((layers, synth.Q_DIM)).astype(np.float32)).cuda()
+        out = torch.zeros_like(q)
+        qs, outs = [q[l] for l in range(layers)], [out[l] for l in range(layers)]
+        have, rows = 0, []
+        for ctx in ctxs:
+            blk = rng.standard_normal((ctx - have, 512)).astype(np.float32)
+            for layer in range(layers):
+                kv.append_rows(layer, blk, blk[::-1].copy())
+            have = ctx
+
+            def step():
+                for i in range(48):
+                    layer = i % layers
+                    rv.decode_attention(qs[layer], kv, layer, scale, None, outs[layer])
+
+            for _ in range(3):
+                step()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            graph.replay()
+            iters = max(5, 100 * 1024 // max(ctx, 1024))
+            per = timed(torch, graph.replay, iters) / iters / 48
+            del graph
+            byts = decode_bytes(ctx, 2)
+            rows.append({"context": ctx, "us_per_call": round(per * 1e6, 3),
+                         "ms_per_token_48_layers": round(per * 48 * 1e3, 4),
+                         "ns_per_position": round(per * 1e9 / ctx, 4), "gbs": round(byts / per / 1e9, 1)})
+        del kv
+        res[arm] = rows
+        nsp = [r["ns_per_position"] for r in rows]
+        res[f"linearity_{arm}"] = round(max(nsp) / min(nsp), 3)
+        slope, floor = np.polyfit([r["context"] for r in rows], [r["us_per_call"] for r in rows], 1)
+        res[f"fit_{arm}"] = {"floor_us": round(float(floor), 3), "ns_per_position": round(float(slope) * 1e3, 4)}
+    return res
 
 
 PROJ_SHAPES = {"hidden": 2048, "q_dim": 4096, "kv_dim": 512}
@@ -484,11 +568,12 @@ def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
     }
 
 
-def cpu_configs(synth, threads):
-    """The oracle (the reference's CPU path restated, its kv-head fan-out over
-    `threads`) on bounded samples of configs 1, 3, 4 and 5, on this host.
-    Prefill samples the chunk's first rows and scales by the causal work
-    (row r attends start + r + 1 positions); decode times whole calls."""
+def cpu_configs(synth, threads, prefill_threads):
+    """The oracle (the reference's CPU path restated) on configs 1, 3, 4 and
+    5, on this host: decode with its kv-head fan-out over `threads` (the
+    reference's ceiling of 4 shards), prefill with the cost-balanced row split
+    over `prefill_threads` (the host's cores, capped at a GPU's CPU share), the
+    whole 512-row chunk timed (nothing extrapolated)."""
     import oracle
     res = {}
     # Config 1: the fused decode step after 512 cached rows.
@@ -506,25 +591,30 @@ def cpu_configs(synth, threads):
             times.append(time.perf_counter() - t0)
     res["config1"] = {"us_per_call": round(float(np.median(times)) * 1e6, 1), "cores": threads, "kind": "port",
                       "sample": "20 decode steps, median"}
-    # Configs 3 and 4: the first rows of the chunk, scaled to 512 rows.
-    for cfg, sample in ((3, 64), (4, 16)):
+    # Configs 3 and 4: the whole chunk, median of 3 after a warm-up.
+    for cfg in (3, 4):
         c = synth.CONFIGS[cfg]
         start = c.context
-        ref = oracle.KvCache(1, 4, 128, start + sample, oracle.RV_ELEM_F32)
+        ref = oracle.KvCache(1, 4, 128, start + c.rows, oracle.RV_ELEM_F32)
         if start:
             K, V = synth.cached_kv(cfg, 0, start)
             ref.append_rows(0, K, V)
-        q, k, v = synth.new_rows(cfg, sample)
+        q, k, v = synth.new_rows(cfg, c.rows)
         wq, wk = synth.norm_weight(cfg, synth.T_QN), synth.norm_weight(cfg, synth.T_KN)
-        t0 = time.perf_counter()
-        ref.prefill_chunk(0, q, k, v, wq, wk, synth.EPS, synth.THETA, start, synth.SCALE, threads=threads)
-        dt = time.perf_counter() - t0
-        work = lambda rows: rows * start + rows * (rows + 1) // 2
-        est = dt * work(c.rows) / work(sample)
+        times = []
+        for i in range(4):
+            ref.truncate(start)
+            t0 = time.perf_counter()
+            ref.prefill_chunk(0, q, k, v, wq, wk, synth.EPS, synth.THETA, start, synth.SCALE,
+                              threads=prefill_threads)
+            if i:
+                times.append(time.perf_counter() - t0)
+        per = float(np.median(times))
         flops = prefill_flops(c.rows, start)
-        res[f"config{cfg}"] = {"us_per_call": round(est * 1e6, 1), "tflops": round(flops / est / 1e12, 5),
-                               "cores": threads, "kind": "port",
-                               "sample": f"first {sample} of {c.rows} rows, scaled by causal work"}
+        res[f"config{cfg}"] = {"us_per_call": round(per * 1e6, 1), "tflops": round(flops / per / 1e12, 5),
+                               "cores": prefill_threads, "kind": "port",
+                               "sample": f"the whole {c.rows}-row chunk, 3 timed calls after a warm-up, median; "
+                                         f"row split over {prefill_threads} threads"}
     # Config 5: decode over 32768 f16 positions.
     ref = oracle.KvCache(1, 4, 128, 32768, oracle.RV_ELEM_F16)
     K, V = synth.cached_kv(5, 0, 32768)
@@ -650,7 +740,14 @@ def main():
         log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us")
         r5 = bench_config5(torch, rv, synth)
         extra["config5_decode_f16_ctx32768"] = r5
-        log(f"config 5: {r5['us_per_call']:.2f} us/call, kernel {r5['us_kernel']:.2f} us, {r5['gbs_kernel']:.0f} GB/s")
+        for name, r in r5.items():
+            log(f"config 5 {name} ({r['splits_per_kv_head']} splits/kv head): {r['us_per_call']:.2f} us/call, "
+                f"tile kernel {r['us_tile_kernel']:.2f} us, {r['gbs_call']:.0f} GB/s per call")
+        rl = bench_ladder(torch, rv, synth)
+        extra["decode_ladder_f16"] = rl
+        for arm in ("arm_a", "arm_b"):
+            log(f"ladder {arm}: " + ", ".join(f"{r['context']}:{r['us_per_call']:.2f}us" for r in rl[arm]) +
+                f"; linearity {rl['linearity_' + arm]}; fit {rl['fit_' + arm]}")
         rp = bench_projections(torch, rv)
         extra["projections_decode_layer"] = rp
         log(f"projections: {rp['us_per_layer']:.2f} us/layer, {rp['gbs']:.0f} GB/s of weights")
@@ -675,7 +772,8 @@ def main():
         if "projections_decode_layer" in extra:
             extra["projections_decode_layer"]["cpu_baseline"] = cpu_projections()
             threads = max(1, min(4, os.cpu_count() or 1))
-            for name, r in cpu_configs(synth, threads).items():
+            prefill_threads = max(1, min(16, os.cpu_count() or 1))  # a GPU box's CPU share is 16 cores
+            for name, r in cpu_configs(synth, threads, prefill_threads).items():
                 for key in extra:
                     if key.startswith(name + "_"):
                         extra[key]["cpu_baseline"] = r
@@ -700,9 +798,13 @@ def main():
         "us_per_layer": round(r2["us_per_layer"], 3),
         "roofline": {"bound": "hbm", "achieved": round(r2["achieved_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_tile_kernel<float, 4>",
+                     "kernel": "decode_tile_kernel<float, 4, 1>",
                      "us_per_launch": round(r2["kernel_us"], 3), "launches_timed": r2["kernel_launches_timed"],
-                     "bytes_per_launch": r2["bytes_per_launch"]},
+                     "bytes_per_launch": r2["bytes_per_launch"],
+                     "whole_call": {"kernels": "decode_tile_kernel + decode_merge_kernel",
+                                    "achieved": round(r2["whole_call_gbs"], 1),
+                                    "frac": round(r2["whole_call_gbs"] / HBM_PEAK_GBS, 4),
+                                    "us_per_call": round(r2["us_per_layer"], 3)}},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -329,25 +329,40 @@ def test_config2_layers_match_the_oracle_at_ctx_4096():
         say(f"config 2 layer {layer} max rel err {e:.3e}")
 
 
-def test_config5_long_context_f16_split_k():
-    torch_cuda()
-    say("case config 5")
+@pytest.fixture(scope="module")
+def config5_oracle():
+    """Config 5's cache rows, q, and the oracle's outputs on the f16 cache
+    and on the unrounded fp32 rows, computed once."""
     n = 32768
     K, V = synth.cached_kv(5, 0, n)
-    kv = rv.KvCache(1, 4, 128, n, "f16")
-    kv.append_rows(0, K, V)
     q = synth.rope_f64(synth.normal(synth.seed(5, synth.T_Q), synth.Q_DIM), 128, n, synth.THETA)
-    out = dev(np.zeros(q.size))
-    rv.decode_attention(dev(q), kv, 0, synth.SCALE, None, out)
-    got = host(out)
     ref16 = oracle.KvCache(1, 4, 128, n, oracle.RV_ELEM_F16)
     ref16.append_rows(0, K, V)
-    e16 = gate(got, ref16.attention(q, 0, synth.SCALE), what="config 5 vs f16 oracle")
+    want16 = ref16.attention(q, 0, synth.SCALE)
+    del ref16
     ref32 = oracle.KvCache(1, 4, 128, n, oracle.RV_ELEM_F32)
     ref32.append_rows(0, K, V)
     want32 = ref32.attention(q, 0, synth.SCALE)
-    assert_close(got, want32, 1e-3, 1.5e-3, "config 5 vs fp32 oracle (f16 storage bound)")
-    say(f"config 5 max rel err vs f16 oracle {e16:.3e}; vs fp32 oracle {rel_err(got, want32):.3e}")
+    return n, K, V, q, want16, want32
+
+
+@pytest.mark.parametrize("split_len", [0, 1024, 2048, 4096])
+def test_config5_long_context_f16_split_k(split_len, config5_oracle):
+    # BASELINE config 5: 8-32 KV splits (split_len 4096 / 2048 / 1024 pinned),
+    # and the library's own plan (0: 128 splits per kv head), each against
+    # the oracle on the same f16 cache and on the unrounded fp32 rows.
+    torch_cuda()
+    say(f"case config 5 split_len={split_len}")
+    n, K, V, q, want16, want32 = config5_oracle
+    kv = rv.KvCache(1, 4, 128, n, "f16")
+    kv.append_rows(0, K, V)
+    kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, split_len)
+    out = dev(np.full(q.size, np.nan, np.float32))
+    rv.decode_attention(dev(q), kv, 0, synth.SCALE, None, out)
+    got = host(out)
+    e16 = gate(got, want16, what=f"config 5 split {split_len} vs f16 oracle")
+    assert_close(got, want32, 1e-3, 1.5e-3, f"config 5 split {split_len} vs fp32 oracle (f16 storage bound)")
+    say(f"config 5 split {split_len}: max rel err vs f16 oracle {e16:.3e}; vs fp32 oracle {rel_err(got, want32):.3e}")
 
 
 def test_outputs_are_convex_combinations_of_v_rows():
