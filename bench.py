@@ -281,6 +281,20 @@ def bench_config5(torch, rv, synth, iters=50, n_caches=5, split_lens=(0, 1024, 2
             "hbm_frac_tile_kernel": round(byts / k_avg / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": byts}
     for kv in caches:
         kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, 0)
+    # The same graph shape over ONE cache (67 MB, which the 256 MB MALL can
+    # hold between calls): how much faster a MALL-resident cache streams
+    # than the five rotating ones the figures above use.
+    def one_cache():
+        for _ in range(n_caches):
+            rv.decode_attention(q, caches[0], 0, scale, None, out)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one_cache()
+    graph.replay()
+    per1 = timed(torch, graph.replay, iters) / (iters * n_caches)
+    del graph
+    res["default"]["us_per_call_one_cache_mall"] = round(per1 * 1e6, 3)
     return res
 
 
@@ -676,6 +690,8 @@ def main():
                     help="only run the prefill-chunk projection leg (512 rows), log it and exit (for profiling)")
     ap.add_argument("--block-only", action="store_true",
                     help="only run the attention-block leg (48 layers, ctx 4096), log it and exit (for profiling)")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="only run the config 5 leg (ctx 32768, f16, every split shape), log it and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -716,6 +732,13 @@ def main():
         for mode in ("f16", "exact"):
             rbp = bench_attn_block_prefill(torch, rv, synth, mode)
             log(f"attention block prefill {mode}: {rbp['us_per_layer']:.1f} us/layer for {rbp['rows']} rows")
+        return
+    if args.config5_only:
+        r5 = bench_config5(torch, rv, synth)
+        for name, r in r5.items():
+            log(f"config 5 {name} ({r['splits_per_kv_head']} splits/kv head): {r['us_per_call']:.2f} us/call, "
+                f"tile kernel {r['us_tile_kernel']:.2f} us")
+        log(f"config 5 default over one MALL-resident cache: {r5['default']['us_per_call_one_cache_mall']:.2f} us/call")
         return
     if args.prefill_only:
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
