@@ -7,8 +7,9 @@
 // Two kernels per call (plus a merge when the KV axis is split):
 //
 // 1. prefill_stage_kernel converts the layer's K and V rows [0, positions)
-//    once into the MFMA element type (f16 / bf16, or hi + lo f16 for the
-//    split mode) and lays each 64-position tile out exactly as the attention
+//    once into the MFMA element type (f16 / bf16, or for the split mode
+//    scaled hi + lo f16 K with each row's exponent, hi + lo bf16 V) and lays
+//    each 64-position tile out exactly as the attention
 //    kernel wants it in LDS: K row-major, V transposed with its positions
 //    permuted into the order the S^T accumulator produces P, both with their
 //    16-byte chunks XOR-swizzled so the MFMA operand reads are free of bank
@@ -29,10 +30,13 @@
 //    the B-operand layout P^T needs, so P never leaves registers.
 //
 // Arithmetic modes (flags RV_PREFILL_*):
-//   EXACT: each operand split as hi + lo f16 (lo = f16(x - hi)); products
-//          hi*hi + hi*lo + lo*hi, fp32 accumulate: ~2^-21 relative products,
-//          the fp32 parity mode, for operands within f16's range (below
-//          65504 in magnitude; full relative precision above 2^-14).
+//   EXACT, the fp32 parity mode, for any finite fp32 operands: each K row
+//          and q vector scaled by a power of two that puts its largest
+//          magnitude in [2^13, 2^14), split as hi + lo f16, products hi*hi +
+//          hi*lo + lo*hi in fp32 (~2^-21 of the row and vector maxima), the
+//          exponents undone exactly on the fp32 score; V as bf16 hi + lo and
+//          P as bf16 hi + mid + lo (bf16 keeps fp32's exponent range), five
+//          products per term (~2^-18 relative).
 //   F16 / BF16: one MFMA per product, fp32 accumulate.
 // Softmax is online in fp32 (exp2, log2(e) folded into the score scale), with
 // the running maximum moved only when a tile exceeds it by 2^8.
@@ -103,24 +107,37 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   typedef E EN __attribute__((ext_vector_type(StageLoad<T>::kE)));
-  constexpr int P = Op<MODE>::kSplit ? 2 : 1;
+  constexpr bool kSplit = Op<MODE>::kSplit;
+  constexpr int P = kSplit ? 2 : 1;
   constexpr int NE = StageLoad<T>::kE;
   const int plane = blockIdx.x & 1;
   const int tile = tile_lo + (int)(blockIdx.x >> 1) % n_tiles, kvh = (int)(blockIdx.x >> 1) / n_tiles;
   const int tid = threadIdx.x;
-  char* dst = stage + ((size_t)kvh * tile_stride + tile) * (2 * P * kPlaneBytes);
+  char* dst = stage + ((size_t)kvh * tile_stride + tile) * kTileBytes<MODE>;
   const int t0 = tile * kBT;
   StageLoad<T> ld;
   ld.load((plane ? vl : kl) + (size_t)kvh * kD, kv_dim, t0, positions, tid);
   if (plane == 0) {
-    // NE elements = a half (fp32) or a whole (f16) 16-byte chunk of row r.
+    // NE elements = a half (fp32) or a whole (f16) 16-byte chunk of row r,
+    // whose kD / NE threads are adjacent lanes; the split mode scales the row
+    // by its exponent (from their max over the row) and records it.
     const int c = StageLoad<T>::col(tid);
 #pragma unroll
     for (int j = 0; j < StageLoad<T>::kN; ++j) {
       const int r = StageLoad<T>::row(j, tid);
+      int ex = 0;
+      if constexpr (kSplit) {
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) amax = fmaxf(amax, fabsf(ld.get(j, e)));
+#pragma unroll
+        for (int w = 1; w < kD / NE; w <<= 1) amax = fmaxf(amax, __shfl_xor(amax, w, 64));
+        ex = scale_exponent(amax);
+        if (c == 0) *reinterpret_cast<int*>(dst + kScaleOffset + 4 * r) = ex;
+      }
       EN hi, lo;
 #pragma unroll
-      for (int e = 0; e < NE; ++e) split2v<E>(ld.get(j, e), hi, lo, e);
+      for (int e = 0; e < NE; ++e) split2v<E>(kSplit ? ldexpf(ld.get(j, e), ex) : ld.get(j, e), hi, lo, e);
       const int off = k_off(r, c / 8) + 2 * (c % 8);
       *reinterpret_cast<EN*>(dst + off) = hi;
       if constexpr (P == 2) *reinterpret_cast<EN*>(dst + kPlaneBytes + off) = lo;
@@ -133,15 +150,25 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
 #pragma unroll
     for (int e = 0; e < NE; ++e) vt[StageLoad<T>::row(j, tid)][StageLoad<T>::col(tid) + e] = ld.get(j, e);
   __syncthreads();
-  // Thread -> V^T row d = tid / 2, chunks 4 (tid % 2) .. +3.
+  // Thread -> V^T row d = tid / 2, chunks 4 (tid % 2) .. +3. The split mode
+  // scales the tile's column d by its exponent (from the column's max over
+  // the tile, both threads of d taking half) and records it.
   const int d = tid >> 1;
   char* vdst = dst + P * kPlaneBytes;
+  int cx = 0;
+  if constexpr (P == 2) {
+    float amax = 0.f;
+#pragma unroll 8
+    for (int t = 32 * (tid & 1); t < 32 * (tid & 1) + 32; ++t) amax = fmaxf(amax, fabsf(vt[t][d]));
+    cx = scale_exponent(fmaxf(amax, __shfl_xor(amax, 1, 64)));
+    if ((tid & 1) == 0) *reinterpret_cast<int*>(dst + kVScaleOffset + 4 * d) = cx;
+  }
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) {
     const int c = 4 * (tid & 1) + cc;
     V8 hi, lo;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) split2v<E>(vt[vt_pos(c, j)][d], hi, lo, j);
+    for (int j = 0; j < 8; ++j) split2v<E>(P == 2 ? ldexpf(vt[vt_pos(c, j)][d], cx) : vt[vt_pos(c, j)][d], hi, lo, j);
     *reinterpret_cast<V8*>(vdst + vt_off(d, c)) = hi;
     if constexpr (P == 2) *reinterpret_cast<V8*>(vdst + kPlaneBytes + vt_off(d, c)) = lo;
   }
@@ -246,10 +273,13 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   typedef typename Op<MODE>::V4 V4;
   constexpr bool kSplit = Op<MODE>::kSplit;
   constexpr int P = kSplit ? 2 : 1;
-  constexpr int M = 16 * W * MT;           // query vectors per workgroup
-  constexpr int TB = 2 * P * kPlaneBytes;  // bytes per staged tile
-  constexpr int LPW = TB / 1024 / W;       // direct-to-LDS loads per wave per tile
-  static_assert(LPW % 8 == 0, "pieces split evenly over the QK and PV loops");
+  constexpr int M = 16 * W * MT;       // query vectors per workgroup
+  constexpr int TB = kTileBytes<MODE>;  // bytes per staged tile
+  constexpr int LPW = TB / 1024 / W;   // direct-to-LDS loads per wave per tile
+  // Pieces issued among the QK MFMAs (spread over the four position blocks);
+  // the rest go among the PV MFMAs (over the eight d blocks).
+  constexpr int LQK = LPW / 8 * 4;
+  static_assert(TB % (1024 * W) == 0 && LQK >= 4, "whole pieces per wave");
   // Scores are kept relative to a running maximum that only moves when a
   // tile's maximum exceeds it by more than this (log2 units): P values stay
   // below 2^8 and most tiles skip rescaling the accumulators.
@@ -303,6 +333,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   int my_row[MT], my_head[MT], my_limit[MT];
   bool col_ok[MT];
   V8 qh[MT][4], ql[MT][4];
+  int qe[MT];  // the split mode's q exponents
   f32x4 o[MT][8];
   float m_run[MT], l_run[MT];
   // -m_run, or 0 while a column has seen no unmasked position: the non-split
@@ -325,10 +356,21 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     const float qs = col_ok[mt] ? (kSplit ? 1.f : qscale) : 0.f;
     float x[4][8];
     load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
+    // The split mode scales the vector by its exponent (from its max over
+    // the column's four lanes), undone on the fp32 scores.
+    qe[mt] = 0;
+    if constexpr (kSplit) {
+      float amax = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[s][e] * qs));
+      qe[mt] = scale_exponent(swap_max<32>(swap_max<16>(amax)));
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) split2v<E>(x[s][e] * qs, qh[mt][s], ql[mt][s], e);
+      for (int e = 0; e < 8; ++e) split2v<E>(kSplit ? ldexpf(x[s][e] * qs, qe[mt]) : x[s][e] * qs, qh[mt][s], ql[mt][s], e);
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
@@ -381,15 +423,22 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
           }
         }
       }
-      // Pieces [0, LPW/2) of the next tile, spread over the four blocks.
+      // Pieces [0, LQK) of the next tile, spread over the four blocks.
 #pragma unroll
-      for (int i = pb * (LPW / 2) / 4; i < (pb + 1) * (LPW / 2) / 4; ++i) issue_piece(j + NS - 1, nxt, i);
+      for (int i = pb * LQK / 4; i < (pb + 1) * LQK / 4; ++i) issue_piece(j + NS - 1, nxt, i);
     }
     if constexpr (kSplit) {
+      // Undo the q and K row exponents (exactly), then scale in fp32; this
+      // lane's positions are 16 pb + 4 kk + e.
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int pb = 0; pb < 4; ++pb) {
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 ke = *reinterpret_cast<const i32x4*>(kt + kScaleOffset + 4 * (16 * pb + 4 * kk));
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] = sc[mt][pb] * qscale + negm[mt];
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[mt][pb][e] = ldexpf(sc[mt][pb][e], -(qe[mt] + ke[e])) * qscale + negm[mt][e];
+      }
     }
     // Causal mask only where some row of the block stops inside the tile.
     if (t0 + kBT > all_see) {
@@ -472,7 +521,9 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       l_run[mt] += psum;
     }
     // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's);
-    // the V operands are read ahead of the MFMAs.
+    // the V operands are read ahead of the MFMAs. The split mode sums the
+    // tile into a fresh accumulator and folds it in with the tile's column
+    // exponents undone (this lane's O^T rows are d = 16 b + 4 kk + e).
     V8 va[8][2], val[8][2];
 #pragma unroll
     for (int b = 0; b < 8; ++b)
@@ -484,20 +535,34 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = kSplit ? f32x4{0.f, 0.f, 0.f, 0.f} : o[mt][b];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          o[mt][b] = Op<MODE>::mfma(va[b][s2], ph[mt][s2], o[mt][b]);
+          acc[mt] = Op<MODE>::mfma(va[b][s2], ph[mt][s2], acc[mt]);
           if constexpr (kSplit) {
-            o[mt][b] = Op<MODE>::mfma(val[b][s2], ph[mt][s2], o[mt][b]);
-            o[mt][b] = Op<MODE>::mfma(va[b][s2], pl[mt][s2], o[mt][b]);
+            acc[mt] = Op<MODE>::mfma(val[b][s2], ph[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(va[b][s2], pl[mt][s2], acc[mt]);
           }
         }
       }
-      // Pieces [LPW/2, LPW), spread over the eight d blocks.
+      if constexpr (kSplit) {
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 cx = *reinterpret_cast<const i32x4*>(kt + kVScaleOffset + 4 * (16 * b + 4 * kk));
 #pragma unroll
-      for (int i = b * (LPW / 2) / 8; i < (b + 1) * (LPW / 2) / 8; ++i) issue_piece(j + NS - 1, nxt, LPW / 2 + i);
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[mt][b][e] += ldexpf(acc[mt][e], -cx[e]);
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o[mt][b] = acc[mt];
+      }
+      // Pieces [LQK, LPW), spread over the eight d blocks.
+#pragma unroll
+      for (int i = LQK + b * (LPW - LQK) / 8; i < LQK + (b + 1) * (LPW - LQK) / 8; ++i) issue_piece(j + NS - 1, nxt, i);
     }
   }
   // The clamped prefetches past the last tile may still be landing in LDS:
@@ -975,6 +1040,11 @@ void launch_stage(const rv_kv* kv, size_t layer, uint32_t mode, size_t positions
 }
 
 int planes_of(uint32_t mode) { return (mode == RV_PREFILL_F16 || mode == RV_PREFILL_BF16) ? 1 : 2; }
+// Bytes of one staged tile in `mode` (the split mode's K row exponents
+// included).
+size_t tile_bytes_of(uint32_t mode) {
+  return planes_of(mode) == 2 ? (size_t)kTileBytes<kExact> : (size_t)kTileBytes<kF16>;
+}
 
 // The layer's persistent staged copy in `mode` (whole capacity, so tile
 // addresses never move), allocated or grown on need; a change of mode or a
@@ -982,7 +1052,7 @@ int planes_of(uint32_t mode) { return (mode == RV_PREFILL_F16 || mode == RV_PREF
 HipStatus ready_persistent(rv_kv* kv, size_t layer, uint32_t mode, hipStream_t s, int* cap_tiles) {
   HipStatus st;
   *cap_tiles = (int)((kv->capacity + kBT - 1) / kBT);
-  const size_t stage_bytes = (size_t)kv->n_kv_heads * *cap_tiles * 2 * planes_of(mode) * kPlaneBytes;
+  const size_t stage_bytes = (size_t)kv->n_kv_heads * *cap_tiles * tile_bytes_of(mode);
   if (kv->staged_mode[layer] != mode || stage_bytes > kv->staged_bytes[layer]) {
     kv->staged_pos[layer] = 0;
     kv->staged_mode[layer] = mode;
@@ -1045,16 +1115,16 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   }
   kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
   const size_t part_bytes = kv_splits > 1 ? (size_t)n_kv * n_rb * kv_splits * kPartStride * sizeof(float) : 0;
-  const size_t tile_bytes = (size_t)2 * planes * kPlaneBytes;
+  const size_t tile_bytes = tile_bytes_of(m);
   // Workspace: the split partials, then room to stage every tile this call
   // reads, which only a captured call uses; eager calls reserve it too, so
   // capturing a call of a shape already run eagerly allocates nothing.
   const size_t call_stage_bytes = (size_t)n_kv * n_stage_tiles * tile_bytes;
   // Bound for the cache's capacity: default splits keep n_rb * n_kv *
   // kv_splits under 512 rows of partials, and a call stages at most every
-  // tile of the capacity in two planes.
+  // tile of the capacity in the split mode's (largest) layout.
   const size_t bound = std::max<size_t>(part_bytes, (size_t)512 * kPartStride * sizeof(float)) +
-                       (size_t)n_kv * ((kv->capacity + kBT - 1) / kBT) * 2 * 2 * kPlaneBytes;
+                       (size_t)n_kv * ((kv->capacity + kBT - 1) / kBT) * tile_bytes_of(RV_PREFILL_EXACT);
   st = ensure_workspace(kv, part_bytes + call_stage_bytes, bound);
   if (st.e != hipSuccess) return st;
   char* stage;
@@ -1116,8 +1186,11 @@ HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t row
                                 hipStream_t s, StageDst* sd) {
   HipStatus st;
   *sd = StageDst{};
-  if (rows == 0 || kv->head_dim != kD || capturing(s)) return st;
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
+  // Split-mode tiles carry exponents over all of their rows, which rows
+  // appended one at a time would change: the attention call's stage kernel
+  // converts them from the cache instead.
+  if (rows == 0 || kv->head_dim != kD || capturing(s) || planes_of(m) == 2) return st;
   int tile_stride;
   st = ready_persistent(kv, layer, m, s, &tile_stride);
   if (st.e != hipSuccess) return st;

@@ -324,8 +324,6 @@ void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int 
     RV_PROLOGUE(1, kF16);
   else if (sm == kBF16)
     RV_PROLOGUE(1, kBF16);
-  else if (sm == kExact)
-    RV_PROLOGUE(1, kExact);
   else if (np == 1)
     RV_PROLOGUE(1, -1);
   else if (np == 2)
@@ -371,14 +369,16 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   // Staging: k and v heads only, head_dim 128; the grid covers the chunk's
   // last tile to its end.
   const bool staging = sd && sd->base;
-  if (staging && (n_q != 0 || hd != 128)) {
+  // The split mode's tiles are staged whole by the stage kernel (their
+  // exponents span all of a tile's rows), never row by row here.
+  if (staging && (n_q != 0 || hd != 128 || (sd->mode != RV_PREFILL_F16 && sd->mode != RV_PREFILL_BF16))) {
     st.e = hipErrorInvalidValue;
     st.what = "staged prologue geometry";
     return st;
   }
   const size_t end = cache_row + rows;
   const size_t grid_rows = staging ? rows + (kBT - end % kBT) % kBT : rows;
-  const int sm = !staging ? -1 : sd->mode == RV_PREFILL_F16 ? kF16 : sd->mode == RV_PREFILL_BF16 ? kBF16 : kExact;
+  const int sm = !staging ? -1 : sd->mode == RV_PREFILL_F16 ? kF16 : kBF16;
   const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
   // Staging: k slot blocks, then one block row per v head (its quads of
   // positions along x; grid_rows covers them).

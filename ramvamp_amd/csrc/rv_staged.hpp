@@ -47,6 +47,26 @@ struct Op<kBF16> {
 template <int MODE>
 constexpr int kPlanes = Op<MODE>::kSplit ? 2 : 1;
 
+// The split mode keeps any finite fp32 K and V in f16 hi + lo planes by
+// scaling with powers of two: each K row t by its exponent e_t, each V
+// column d of a tile by its exponent c_d (so a tile's exponents depend on all
+// of its rows, and only the stage kernel, converting whole tiles from the
+// cache, writes split-mode tiles). The tile ends with a 4 KiB region (whole
+// 1 KiB pieces, so every wave copies the same number of pieces per tile):
+// int32 e_t at byte kScaleOffset + 4 t, int32 c_d at byte kVScaleOffset + 4 d.
+constexpr int kScaleBytes = 4096;
+constexpr int kScaleOffset = 4 * kPlaneBytes;
+constexpr int kVScaleOffset = kScaleOffset + 4 * kBT;
+template <int MODE>
+constexpr int kTileBytes = 2 * kPlanes<MODE> * kPlaneBytes + (Op<MODE>::kSplit ? kScaleBytes : 0);
+
+// The power-of-two exponent e that puts amax * 2^e in [2^13, 2^14), or 0
+// for a zero or non-finite amax (such a row is staged as it is).
+__device__ __forceinline__ int scale_exponent(float amax) {
+  if (!(amax > 0.f) || !__builtin_isfinite(amax)) return 0;
+  return 14 - __builtin_amdgcn_frexp_expf(amax);
+}
+
 // hi = round(x); lo = round(x - hi), into element e of two vectors.
 template <typename E, typename V>
 __device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
@@ -57,7 +77,8 @@ __device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
 
 // ---- staged tile layout -------------------------------------------------------------
 // One tile = P planes of K, then P planes of V^T (P = 2 in the split mode:
-// hi, lo), each plane 16 KiB of 16-byte chunks (8 elements).
+// hi, lo; then the split mode's exponent region), each plane 16 KiB of
+// 16-byte chunks (8 elements).
 //   K plane: row t (64) x chunk c (16): elements d = 8c .. 8c+7, stored at
 //     byte 256 t + 16 (c ^ (t & 15)).
 //   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot

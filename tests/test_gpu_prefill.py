@@ -257,7 +257,8 @@ def test_prefill_errors_and_first_row_semantics():
     assert e.value.variant == "QLenIndivisible"
     rv.attention_at_rows(q[:0], kv, 0, 0, 0.1, out[:0])  # zero rows: a no-op
     rv.attention_at_rows(q[:1], kv, 0, 0, 0.1, out[:1])  # row 0 at start 0 sees only position 0
-    # split-f16 reproduces V to ~2^-22 relative (hi + lo of one f32)
+    # the split mode reproduces V to ~2^-22 relative (hi + lo f16 of the
+    # f32, scaled by its tile column's exponent)
     assert np.allclose(out[0].reshape(4, 8, 128), np.broadcast_to(K[0].reshape(4, 1, 128), (4, 8, 128)), rtol=1e-6,
                        atol=0)
 
@@ -287,3 +288,114 @@ def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits, impl):
     e = gate(host(out), want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode],
              what=f"tiles {vectors_rows}/{splits} {mode}")
     say(f"  max rel err {e:.3e}")
+
+
+def weighted_magnitude(q, K, V, n_kv, hd, start, scale):
+    """f64 sum_t p_t |V[t][d]| per output element: the size of the terms each
+    output sums, which bounds what fp32 arithmetic can resolve in it."""
+    rows, q_dim = q.shape
+    n_q = q_dim // hd
+    group = n_q // n_kv
+    qh = q.astype(np.float64).reshape(rows, n_q, hd)
+    Kh = K.astype(np.float64).reshape(-1, n_kv, hd)
+    Vh = np.abs(V.astype(np.float64)).reshape(-1, n_kv, hd)
+    mag = np.zeros((rows, n_q, hd))
+    for r in range(rows):
+        n = start + r + 1
+        for h in range(n_q):
+            s = Kh[:n, h // group] @ qh[r, h] * float(scale)
+            p = np.exp(s - s.max())
+            mag[r, h] = (p / p.sum()) @ Vh[:n, h // group]
+    return mag.reshape(rows, q_dim)
+
+
+@pytest.mark.parametrize("case", ["v_1e6", "v_1e-30", "v_rows_1e-30_to_1e6", "k_rows_1e-25_to_1", "q_1e-20"])
+def test_exact_mode_covers_finite_fp32(case):
+    """The fp32 parity mode over values far outside f16's range (attention.rs
+    takes any finite f32): |V| up to 1e6 and down to 1e-30, V and K rows
+    whose magnitudes span many decades within one 64-position tile, and tiny
+    q. Every output element must match the oracle to 1e-5 of the magnitude
+    of the terms it sums (sum_t p_t |V[t][d]|, in f64), which fp32 itself
+    only resolves to a few 1e-7. Scores stay O(10) in size: the mode's
+    scores carry ~2^-21 of |q| |k| (fp32's: ~2^-24), so scores of size S
+    move the softmax weights by ~S * 2^-21 relative."""
+    torch_cuda()
+    say(f"case exact range {case}")
+    rng = Rng(0xE7AC7 + len(case))
+    n_kv, n_q, hd, start, rows = 4, 32, 128, 70, 50
+    n_pos = start + rows
+    K = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
+    V = rng.vec_in(n_pos * n_kv * hd, -1.0, 1.0).reshape(n_pos, -1)
+    q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+    decades = rng.vec_in(n_pos, 0.0, 1.0).reshape(n_pos, 1)
+    if case == "v_1e6":
+        V = V * np.float32(1e6)
+    elif case == "v_1e-30":
+        V = V * np.float32(1e-30)
+    elif case == "v_rows_1e-30_to_1e6":
+        V = (V * np.power(10.0, -30.0 + 36.0 * decades)).astype(np.float32)
+    elif case == "k_rows_1e-25_to_1":
+        K = (K * np.power(10.0, -25.0 + 25.0 * decades)).astype(np.float32)
+    elif case == "q_1e-20":
+        q = q * np.float32(1e-20)
+    kv = rv.KvCache(1, n_kv, hd, n_pos, "f32")
+    ref = oracle.KvCache(1, n_kv, hd, n_pos, oracle.RV_ELEM_F32)
+    kv.append_rows(0, K, V)
+    ref.append_rows(0, K, V)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = dev(np.full(q.shape, np.nan))
+    rv.attention_at_rows(dev(q), kv, 0, start, scale, out, mode="exact")
+    want = ref.scatter_attention(q, 0, start, scale, THREADS)
+    got = host(out)
+    assert np.all(np.isfinite(got)), f"{case}: non-finite output"
+    mag = weighted_magnitude(q, K, V, n_kv, hd, start, scale)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    worst = float(np.max(err / np.maximum(mag, np.finfo(np.float64).tiny)))
+    say(f"  max |err| / sum p|v| = {worst:.3e}")
+    assert worst <= 1e-5, f"{case}: max |err| / sum_t p_t |v_t| = {worst:.3e} > 1e-5"
+
+
+def test_exact_prefill_chunk_with_large_values():
+    """prefill_chunk (RMSNorm + RoPE prologue, append, staged rows) in the
+    fp32 parity mode with V rows up to 1e6 and down to 1e-30 in magnitude:
+    the chunk's own rows go through the row prologue's staging (per-row K
+    exponents, bf16 V planes), the cached prefix through the stage kernel."""
+    torch_cuda()
+    say("case exact prefill_chunk wide V")
+    rng = Rng(0xB16)
+    n_kv, n_q, hd, start, rows = 4, 32, 128, 90, 70
+    kv, ref = twin(rng, n_kv, hd, 0, start + rows, "f32")
+    K0 = rng.vec_in(start * n_kv * hd, -1.0, 1.0).reshape(start, -1)
+    V0 = (rng.vec_in(start * n_kv * hd, -1.0, 1.0).reshape(start, -1) *
+          np.power(10.0, -30.0 + 36.0 * rng.vec_in(start, 0.0, 1.0).reshape(start, 1))).astype(np.float32)
+    kv.append_rows(0, K0, V0)
+    ref.append_rows(0, K0, V0)
+    q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
+    k = rng.vec_in(rows * n_kv * hd, -2.0, 2.0).reshape(rows, -1)
+    v = (rng.vec_in(rows * n_kv * hd, -1.0, 1.0).reshape(rows, -1) *
+         np.power(10.0, -30.0 + 36.0 * rng.vec_in(rows, 0.0, 1.0).reshape(rows, 1))).astype(np.float32)
+    wq, wk = rng.vec_in(hd, 0.9, 1.1), rng.vec_in(hd, 0.9, 1.1)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = dev(np.full(q.shape, np.nan))
+    rv.prefill_chunk(kv, 0, dev(q), dev(k), dev(v), dev(wq), dev(wk), 1e-6, 1e6, start, scale, out, mode="exact")
+    want = ref.prefill_chunk(0, q, k, v, wq, wk, 1e-6, 1e6, start, scale, threads=THREADS)
+    got = host(out)
+    assert np.all(np.isfinite(got))
+    # The magnitudes from the post-prologue q (RMSNorm + NeoX RoPE in f64,
+    # close enough to weight the terms) and the cache's K and V rows.
+    x = q.astype(np.float64).reshape(rows, n_q, hd)
+    x = x / np.sqrt(np.mean(x * x, axis=2, keepdims=True) + 1e-6) * wq.astype(np.float64)
+    ang = (start + np.arange(rows))[:, None] * np.power(1e6, -2.0 * np.arange(hd // 2) / hd)[None, :]
+    c, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    qp = np.concatenate([x[..., :hd // 2] * c - x[..., hd // 2:] * sn, x[..., :hd // 2] * sn + x[..., hd // 2:] * c],
+                        axis=2).reshape(rows, -1)
+    Kall = np.stack([kv.k_row(0, t) for t in range(start + rows)])
+    Vall = np.stack([kv.v_row(0, t) for t in range(start + rows)])
+    mag = weighted_magnitude(qp, Kall, Vall, n_kv, hd, start, scale)
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    worst = float(np.max(err / np.maximum(mag, np.finfo(np.float64).tiny)))
+    say(f"  max |err| / sum p|v| = {worst:.3e}")
+    assert worst <= 1e-5
+    for pos in (0, start - 1, start, start + rows - 1):
+        gate(kv.k_row(0, pos), ref.read_row(False, 0, pos), rel=2e-7, floor=1e-6, what="cache K")
+        gate(kv.v_row(0, pos), ref.read_row(True, 0, pos), rel=0, floor=1e-38, what="cache V")
