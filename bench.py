@@ -522,7 +522,7 @@ def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
             d(synth_weight_rows(rng, F["k"], KV, H)), F["v"], d(synth_weight_rows(rng, F["v"], KV, H)),
             d(synth.norm_weight(2, synth.T_QN)), d(synth.norm_weight(2, synth.T_KN)), F["o"],
             d(synth_weight_rows(rng, F["o"], H, Q))))
-    kv = rv.KvCache(n_layers, 4, 128, 4096 + 8, "f32")
+    kv = rv.KvCache(n_layers, 4, 128, 4096 + 64, "f32")
     for layer in range(n_layers):
         K, V = synth.cached_kv(2, layer, 4096)
         kv.append_rows(layer, K, V)
@@ -542,11 +542,41 @@ def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
         token()
     graph.replay()
     per = timed(torch, graph.replay, iters) / (iters * n_layers)
+    del graph
     wbytes = sum(t.numel() for t in (sets[0].wq, sets[0].wk, sets[0].wv, sets[0].wo))
     kv_bytes = 2 * 4099 * 512 * 4
+
+    # The token graph: the same blocks with the position in device memory,
+    # captured once and replayed for successive tokens (context 4096 + 1 ..
+    # 4096 + 2 + iters), every replay a new token.
+    kv.truncate(4096)
+    pos = torch.tensor([4096], dtype=torch.int32, device="cuda")
+    max_pos = kv.capacity() - 1
+
+    def token_dev():
+        for layer in range(n_layers):
+            B.attn_block_decode_dev(kv, layer, residual, Q, sets[layer % n_sets], synth.EPS, synth.THETA, pos,
+                                    max_pos, scale, scratch)
+        rv.position_advance(kv, pos, 1)
+
+    token_dev()  # eagerly: builds the (cos, sin) table
+    tg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(tg):
+        token_dev()
+    tg.replay()
+    per_dev = timed(torch, tg.replay, iters) / (iters * n_layers)
+    n_written = int(pos.item()) - 4096
+    for layer in range(n_layers):
+        kv.commit(layer, n_written)
+    del tg
     return {"us_per_layer": round(per * 1e6, 3), "ms_per_token_48_layers": round(per * n_layers * 1e3, 3),
             "bytes_per_layer": wbytes + kv_bytes, "gbs": round((wbytes + kv_bytes) / per / 1e9, 1),
-            "launches_per_layer": 4, "distinct_weight_sets": n_sets, "context": 4099}
+            "launches_per_layer": 4, "distinct_weight_sets": n_sets, "context": 4099,
+            "token_graph": {"us_per_layer": round(per_dev * 1e6, 3),
+                            "ms_per_token_48_layers": round(per_dev * n_layers * 1e3, 3),
+                            "tokens": n_written, "context_range": [4097, 4096 + n_written],
+                            "planned_positions": max_pos + 1,
+                            "note": "one graph replayed per token; position read from device memory"}}
 
 
 def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
@@ -728,7 +758,8 @@ def main():
         rr = bench_router(torch, rv)
         log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")
         rb = bench_attn_block(torch, rv, synth)
-        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token; "
+            f"token graph {rb['token_graph']['us_per_layer']:.2f} us/layer over {rb['token_graph']['tokens']} tokens")
         for mode in ("f16", "exact"):
             rbp = bench_attn_block_prefill(torch, rv, synth, mode)
             log(f"attention block prefill {mode}: {rbp['us_per_layer']:.1f} us/layer for {rbp['rows']} rows")
@@ -780,7 +811,8 @@ def main():
             f"{rpp['int8_tops']:.1f} int8 TOP/s")
         rb = bench_attn_block(torch, rv, synth)
         extra["attn_block_decode_layer"] = rb
-        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token")
+        log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token; "
+            f"token graph {rb['token_graph']['us_per_layer']:.2f} us/layer over {rb['token_graph']['tokens']} tokens")
         rr = bench_router(torch, rv)
         extra["router_128x2048_top8"] = rr
         log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")

@@ -237,6 +237,34 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
                        float theta, size_t position, float scale, float* out, size_t out_len,
                        uint32_t flags, rv_error* err);
 
+/* ---- token graph (no counterpart in the reference) ---------------------
+ * For callers that capture one token's layer steps into a HIP graph once and
+ * replay it for every token (the per-token decode loop of forward.rs:2568-2650
+ * without a host round trip per step). rv_decode_step with the token's
+ * position read from device memory (*d_position, a uint32) when the step
+ * runs: the row lands at position *d_position of the layer and q and k rotate
+ * at that position, so the cache is expected to hold exactly *d_position rows
+ * then (the reference's decode keeps position == len). The launch is planned
+ * for max_position + 1 positions (workgroups past the token's position find
+ * nothing to do and contribute nothing); *d_position above max_position is
+ * clamped to it. max_position >= capacity is RV_KV_CAPACITY_EXCEEDED. The
+ * host cursor does not move: rv_kv_commit adds the rows the replays wrote.
+ * The first call for a (theta, max_position) builds the (cos, sin) table and
+ * workspace and must not be captured; later calls may be. Device pointers
+ * only (RV_HOST_PTRS is RV_ERR_UNSUPPORTED); head_dim 128 and a group of at
+ * most 16 (else RV_ERR_UNSUPPORTED). Results equal rv_decode_step's within
+ * fp32 reassociation (the splits follow max_position, not the length). */
+int32_t rv_decode_step_dev(rv_kv* kv, size_t layer, const float* q, size_t q_len, const float* k,
+                           size_t k_len, const float* v, size_t v_len, const float* q_norm_w,
+                           size_t q_norm_len, const float* k_norm_w, size_t k_norm_len, float eps,
+                           float theta, const uint32_t* d_position, size_t max_position, float scale,
+                           float* out, size_t out_len, uint32_t flags, rv_error* err);
+/* Adds `rows` to the layer's length (the rows device-position steps wrote);
+ * past the capacity is RV_KV_CAPACITY_EXCEEDED and nothing changes. */
+int32_t rv_kv_commit(rv_kv* kv, size_t layer, size_t rows, rv_error* err);
+/* Queues *d_position += n on the cache's stream (a token graph's last node). */
+int32_t rv_position_advance(rv_kv* kv, uint32_t* d_position, uint32_t n, rv_error* err);
+
 /* model/prefill.rs:2055-2111 steps (d)-(f) for one layer of a chunk: the
  * same prologue per row at absolute position start+r, the whole chunk's
  * K/V appended, then causal attention where row r sees start+r+1 positions.

@@ -74,6 +74,16 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
                              const rv_attn_block_weights* w, float eps, float theta, size_t position,
                              float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err);
 
+/* No counterpart in the reference: rv_attn_block_decode with the decode step
+ * as rv_decode_step_dev (the token's position read from *d_position when the
+ * step runs, planned for max_position; the layer's host cursor does not move,
+ * rv_kv_commit adds the rows), for a token graph captured once and replayed
+ * per token. A null d_position is RV_ERR_NULL_ARG. */
+int32_t rv_attn_block_decode_dev(rv_kv* kv, size_t layer, float* residual, size_t hidden, size_t q_dim,
+                                 const rv_attn_block_weights* w, float eps, float theta,
+                                 const uint32_t* d_position, size_t max_position, float scale, void* scratch,
+                                 size_t scratch_len, uint32_t flags, rv_error* err);
+
 /* The same block for a prefill chunk of n_rows tokens at positions start ..
  * start + n_rows - 1 (model/prefill.rs:1975-2154, the attention half of a
  * layer): each residual row normalized (rmsnorm_rows), quantized both ways,

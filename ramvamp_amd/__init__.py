@@ -25,6 +25,8 @@ from .attention import (  # noqa: F401
     decode_attention_kv_range_in,
     decode_attention_noalloc,
     decode_step,
+    decode_step_dev,
+    position_advance,
     prefill_chunk,
     scratch_len,
 )

@@ -93,6 +93,10 @@ SIGNATURES = {
     "rv_attention_at_rows": (c_int32, [_P, _P, c_size_t, c_size_t, c_size_t, c_size_t, c_float, _P, c_uint32, _E]),
     "rv_decode_step": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t,
                                  c_float, c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_decode_step_dev": (c_int32, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P,
+                                     c_size_t, c_float, c_float, _P, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_kv_commit": (c_int32, [_P, c_size_t, c_size_t, _E]),
+    "rv_position_advance": (c_int32, [_P, _P, c_uint32, _E]),
     "rv_prefill_chunk": (c_int32, [_P, c_size_t, _P, _P, _P, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, c_float,
                                    c_float, c_size_t, c_float, _P, c_uint32, _E]),
     "rv_decode_attention_noalloc": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
@@ -135,6 +139,8 @@ SIGNATURES = {
                                         c_float, c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_attn_block_decode": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, POINTER(RvAttnBlockWeights), c_float,
                                        c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    "rv_attn_block_decode_dev": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, POINTER(RvAttnBlockWeights),
+                                           c_float, c_float, _P, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
 }
 
 _lib = None

@@ -274,6 +274,12 @@ class KvCache:
         err = L.RvError()
         _check(_lib().rv_kv_truncate(self._h, new_len, byref(err)), err)
 
+    def commit(self, layer: int, rows: int):
+        """rv_kv_commit (no reference counterpart): adds the rows that
+        device-position steps wrote to the layer's length."""
+        err = L.RvError()
+        _check(_lib().rv_kv_commit(self._h, layer, rows, byref(err)), err)
+
     def _row(self, plane_v: int, layer: int, pos: int) -> np.ndarray:
         self._bind_stream()  # the copy is ordered after work queued on torch's current stream
         out = np.empty(self.kv_dim(), dtype=np.uint16 if self.elem == "f16" else np.float32)
@@ -423,6 +429,39 @@ def decode_step(cache: KvCache, layer: int, q, k, v, q_norm_w, k_norm_w, eps: fl
     _check(_lib().rv_decode_step(cache.handle, layer, qa.ptr, qa.n, ka.ptr, ka.n, va.ptr, va.n, wq.ptr, wq.n, wk.ptr,
                                  wk.n, eps, theta, position, scale, oa.ptr, oa.n, flags, byref(err)), err)
     return out
+
+
+def _position_ptr(d_position) -> int:
+    """Address of a one-element int32 device tensor holding a token position."""
+    import torch
+
+    if not (isinstance(d_position, torch.Tensor) and d_position.is_cuda and d_position.dtype == torch.int32
+            and d_position.numel() >= 1):
+        raise TypeError("d_position must be an int32 device tensor with at least one element")
+    return d_position.data_ptr()
+
+
+def decode_step_dev(cache: KvCache, layer: int, q, k, v, q_norm_w, k_norm_w, eps: float, theta: float, d_position,
+                    max_position: int, scale: float, out):
+    """rv_decode_step_dev (no reference counterpart): decode_step at the
+    position ``d_position`` (int32 device tensor) holds when the step runs,
+    planned for ``max_position``; the layer's length does not move
+    (``KvCache.commit``). Device tensors only. For a token graph captured once
+    and replayed per token."""
+    qa, ka, va, wq, wk, oa = _Arg(q), _Arg(k), _Arg(v), _Arg(q_norm_w), _Arg(k_norm_w), _Arg(out, writable=True)
+    err = L.RvError()
+    flags = _flags(cache, (qa, ka, va, wq, wk, oa))
+    _check(_lib().rv_decode_step_dev(cache.handle, layer, qa.ptr, qa.n, ka.ptr, ka.n, va.ptr, va.n, wq.ptr, wq.n,
+                                     wk.ptr, wk.n, eps, theta, _position_ptr(d_position), max_position, scale, oa.ptr,
+                                     oa.n, flags, byref(err)), err)
+    return out
+
+
+def position_advance(cache: KvCache, d_position, n: int = 1):
+    """rv_position_advance: queues ``d_position += n`` on the cache's stream."""
+    cache._bind_stream()
+    err = L.RvError()
+    _check(_lib().rv_position_advance(cache.handle, _position_ptr(d_position), n, byref(err)), err)
 
 
 def prefill_chunk(cache: KvCache, layer: int, q_rows, k_rows, v_rows, q_norm_w, k_norm_w, eps: float, theta: float,

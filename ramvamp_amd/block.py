@@ -69,7 +69,26 @@ def attn_block_decode(cache: KvCache, layer: int, residual, q_dim: int, w: AttnB
     return residual
 
 
-_MODES = {"exact": L.RV_PREFILL_EXACT, "f16": L.RV_PREFILL_F16, "bf16": L.RV_PREFILL_BF16}
+def attn_block_decode_dev(cache: KvCache, layer: int, residual, q_dim: int, w: AttnBlockWeights, eps: float,
+                          theta: float, d_position, max_position: int, scale: float, scratch):
+    """rv_attn_block_decode_dev (no reference counterpart): attn_block_decode
+    at the position ``d_position`` (int32 device tensor) holds when the step
+    runs, planned for ``max_position``; the layer's length does not move
+    (``KvCache.commit``). ``scratch`` is required: a token graph keeps it."""
+    from .attention import _position_ptr
+    if not (hasattr(residual, "is_cuda") and residual.is_cuda and residual.is_contiguous()):
+        raise TypeError("residual must be a contiguous torch tensor on the GPU")
+    cache._bind_stream()
+    err = L.RvError()
+    cw = w._c()
+    _check(L.load().rv_attn_block_decode_dev(cache.handle, layer, c_void_p(residual.data_ptr()), residual.numel(),
+                                             q_dim, byref(cw), eps, theta, _position_ptr(d_position), max_position,
+                                             scale, c_void_p(scratch.data_ptr()), scratch.numel(), 0, byref(err)),
+           err)
+    return residual
+
+
+_MODES ={"exact": L.RV_PREFILL_EXACT, "f16": L.RV_PREFILL_F16, "bf16": L.RV_PREFILL_BF16}
 
 
 def prefill_scratch_bytes(n_rows: int, hidden: int, q_dim: int, kv_dim: int) -> int:

@@ -335,6 +335,70 @@ HipStatus ensure_qbuf(rv_kv* kv, size_t bytes) {
   return st;
 }
 
+// The device-position step's (cos, sin) table for positions [0, n) at
+// theta: each position's 64 pairs in f64 from the host's inverse
+// frequencies, cast to f32, exactly as rv_decode_step computes its one
+// position's (rope.rs:35-39), for whole blocks of 1024 positions up to the
+// capacity; extended (or rebuilt for another theta) on need, the replaced
+// table retired rather than freed.
+HipStatus ensure_rope_tab(rv_kv* kv, float theta, size_t n) {
+  HipStatus st;
+  if (kv->rope_tab && kv->rope_theta == theta && kv->rope_n >= n) return st;
+  if (capturing(kv->stream)) {
+    st.e = hipErrorStreamCaptureUnsupported;
+    st.what = "rope table growth under graph capture (run a device-position step uncaptured first)";
+    return st;
+  }
+  const size_t hd = kv->head_dim, half = hd / 2;
+  const size_t rows = std::min(kv->capacity, (n + 1023) / 1024 * 1024);
+  std::vector<float> host(rows * hd);
+  InvFreq inv;
+  fill_inv_freq(inv, hd, theta);
+  for (size_t p = 0; p < rows; ++p)
+    for (size_t i = 0; i < half; ++i) {
+      double sd, cd;
+      sincos((double)p * inv.f[i], &sd, &cd);
+      host[p * hd + i] = (float)cd;
+      host[p * hd + half + i] = (float)sd;
+    }
+  void* d = nullptr;
+  st.e = hipMalloc(&d, host.size() * sizeof(float));
+  if (st.e != hipSuccess) {
+    st.what = "hipMalloc rope table";
+    return st;
+  }
+  st.e = hipMemcpy(d, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+  if (st.e != hipSuccess) {
+    (void)hipFree(d);
+    st.what = "hipMemcpy rope table";
+    return st;
+  }
+  if (kv->rope_tab) kv->retired.push_back(kv->rope_tab);
+  kv->rope_tab = (float*)d;
+  kv->rope_n = rows;
+  kv->rope_theta = theta;
+  return st;
+}
+
+int32_t decode_step_dev_check(const rv_kv* kv, size_t layer, size_t q_len, size_t max_position, size_t q_norm_len,
+                              size_t k_norm_len, rv_error* err) {
+  // rv_decode_step's checks with the token's position on the device: the
+  // launch is planned for max_position, which must leave a row for it.
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  int32_t rc = check_rope_dim(kv, err);
+  if (rc) return rc;
+  const size_t hd = kv->head_dim;
+  if (q_len == 0 || q_len % hd) return fail(err, RV_ATTN_Q_LEN_INDIVISIBLE, q_len, hd);
+  if ((q_len / hd) % kv->n_kv_heads) return fail(err, RV_ATTN_GQA_GROUP_MISMATCH, q_len / hd, kv->n_kv_heads);
+  if ((rc = check_norm_weights(hd, q_norm_len, k_norm_len, err))) return rc;
+  if ((rc = check_layer(kv, layer, err))) return rc;
+  if (max_position >= kv->capacity) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
+  if (!decode_pro_supported(kv, q_len / hd))
+    return fail(err, RV_ERR_UNSUPPORTED, hd, q_len / hd / kv->n_kv_heads, 0, 0,
+                "device-position step: head_dim 128 and a group of at most 16");
+  return RV_OK;
+}
+
 }  // namespace rv
 
 extern "C" {
@@ -448,7 +512,7 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab})
       if (p) (void)hipFree(p);
     for (void* p : kv->staged)
       if (p) (void)hipFree(p);
@@ -804,6 +868,50 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
   hs = rv::launch_decode(kv, kv->qbuf, n_q, layer, len + 1, scale, 0, kv->n_kv_heads, dout, kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   return finish(kv, flags, dout, out, q_len, err);
+}
+
+// rv_decode_step with the token's position read from device memory when the
+// step runs, for a token graph captured once and replayed for every token.
+int32_t rv_decode_step_dev(rv_kv* kv, size_t layer, const float* q, size_t q_len, const float* k, size_t k_len,
+                           const float* v, size_t v_len, const float* q_norm_w, size_t q_norm_len,
+                           const float* k_norm_w, size_t k_norm_len, float eps, float theta,
+                           const uint32_t* d_position, size_t max_position, float scale, float* out, size_t out_len,
+                           uint32_t flags, rv_error* err) {
+  int32_t rc = rv::decode_step_dev_check(kv, layer, q_len, max_position, q_norm_len, k_norm_len, err);
+  if (rc) return rc;
+  if (k_len != kv->kv_dim) return fail(err, RV_KV_ROW_LEN_MISMATCH, k_len, kv->kv_dim, 0, 0, "k");
+  if (v_len != kv->kv_dim) return fail(err, RV_KV_ROW_LEN_MISMATCH, v_len, kv->kv_dim, 0, 0, "v");
+  if (out_len != q_len) return fail(err, RV_ATTN_OUT_LEN_MISMATCH, out_len, q_len);
+  if (!q || !k || !v || !q_norm_w || !k_norm_w || !out || !d_position)
+    return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "tensor");
+  if (flags & RV_HOST_PTRS) return fail(err, RV_ERR_UNSUPPORTED, flags, 0, 0, 0, "RV_HOST_PTRS (device pointers only)");
+  DeviceGuard dg(kv->device);
+  rv::HipStatus hs = rv::ensure_rope_tab(kv, theta, max_position + 1);
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  rv::DecodePro pro{k, v, q_norm_w, k_norm_w, eps, {}, {}, d_position, kv->rope_tab, (int)max_position};
+  hs = rv::launch_decode_pro(kv, q, q_len / kv->head_dim, layer, max_position + 1, scale, pro, out, kv->stream);
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  return finish(kv, flags, out, out, q_len, err);
+}
+
+// Rows that device-position steps wrote below the layer's capacity, added to
+// its host cursor (kv/mod.rs:336-368's bound).
+int32_t rv_kv_commit(rv_kv* kv, size_t layer, size_t rows, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  int32_t rc = check_layer(kv, layer, err);
+  if (rc) return rc;
+  if (rows > kv->capacity - kv->lens[layer]) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
+  kv->lens[layer] += rows;
+  return ok(err);
+}
+
+int32_t rv_position_advance(rv_kv* kv, uint32_t* d_position, uint32_t n, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  if (!d_position) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "d_position");
+  DeviceGuard dg(kv->device);
+  const rv::HipStatus hs = rv::launch_position_advance(d_position, n, kv->stream);
+  if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  return ok(err);
 }
 
 // model/prefill.rs:2055-2111 steps (d)-(f).

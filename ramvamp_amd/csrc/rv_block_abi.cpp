@@ -53,9 +53,12 @@ size_t rv_attn_block_scratch_bytes(size_t hidden, size_t q_dim, size_t kv_dim) {
   return 2 * align256(q_dim * sizeof(float)) + 2 * align256(kv_dim * sizeof(float)) + align256(proj);
 }
 
-int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hidden, size_t q_dim,
-                             const rv_attn_block_weights* w, float eps, float theta, size_t position,
-                             float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err) {
+// One token's block at a host position, or (d_position set) at the position
+// device memory holds when the step runs, planned for max_position.
+static int32_t block_decode(rv_kv* kv, size_t layer, float* residual, size_t hidden, size_t q_dim,
+                            const rv_attn_block_weights* w, float eps, float theta, size_t position,
+                            const uint32_t* d_position, size_t max_position, float scale, void* scratch,
+                            size_t scratch_len, uint32_t flags, rv_error* err) {
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, "kv");
   if (!w) return fail(err, RV_ERR_NULL_ARG, 0, 0, "weights");
   // forward.rs:2572 rmsnorm (norm.rs:38-40): an empty row has no mean.
@@ -66,7 +69,10 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
                 w->wk,    0,            c.k,     kv_dim, w->v_format, w->wv, 0,   c.v,   c.proj};
   int32_t rc;
   if ((rc = rv::in_proj_check(in, w->wq_len, w->wk_len, w->wv_len, err))) return rc;
-  if ((rc = rv::decode_step_check(kv, layer, q_dim, position, w->q_norm_len, w->k_norm_len, err))) return rc;
+  if ((rc = d_position
+                ? rv::decode_step_dev_check(kv, layer, q_dim, max_position, w->q_norm_len, w->k_norm_len, err)
+                : rv::decode_step_check(kv, layer, q_dim, position, w->q_norm_len, w->k_norm_len, err)))
+    return rc;
   rv::OutProj out{c.attn, q_dim, w->o_format, w->wo, 0, residual, hidden, true, c.proj};
   if ((rc = rv::out_proj_check(out, w->wo_len, err))) return rc;
   const size_t need = rv_attn_block_scratch_bytes(hidden, q_dim, kv_dim);
@@ -87,9 +93,12 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
   const hipStream_t s = kv->stream;
   rv::HipStatus st = rv::in_proj_launch(in, s);
   if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
-  if (!rc)
-    rc = rv_decode_step(kv, layer, c.q, q_dim, c.k, kv_dim, c.v, kv_dim, w->q_norm, w->q_norm_len, w->k_norm, w->k_norm_len, eps, theta, position,
-                        scale, c.attn, q_dim, 0, err);
+  if (!rc && d_position)
+    rc = rv_decode_step_dev(kv, layer, c.q, q_dim, c.k, kv_dim, c.v, kv_dim, w->q_norm, w->q_norm_len, w->k_norm,
+                            w->k_norm_len, eps, theta, d_position, max_position, scale, c.attn, q_dim, 0, err);
+  else if (!rc)
+    rc = rv_decode_step(kv, layer, c.q, q_dim, c.k, kv_dim, c.v, kv_dim, w->q_norm, w->q_norm_len, w->k_norm,
+                        w->k_norm_len, eps, theta, position, scale, c.attn, q_dim, 0, err);
   if (!rc) {
     st = rv::out_proj_launch(out, s);
     if (st.e != hipSuccess) rc = fail(err, RV_ERR_HIP, (uint64_t)st.e, 0, st.what);
@@ -101,6 +110,22 @@ int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hi
   if (prev >= 0 && prev != kv->device) (void)hipSetDevice(prev);
   if (!rc && err) *err = rv_error{RV_OK, 0, 0, 0, 0, nullptr};
   return rc;
+}
+
+int32_t rv_attn_block_decode(rv_kv* kv, size_t layer, float* residual, size_t hidden, size_t q_dim,
+                             const rv_attn_block_weights* w, float eps, float theta, size_t position,
+                             float scale, void* scratch, size_t scratch_len, uint32_t flags, rv_error* err) {
+  return block_decode(kv, layer, residual, hidden, q_dim, w, eps, theta, position, nullptr, 0, scale, scratch,
+                      scratch_len, flags, err);
+}
+
+int32_t rv_attn_block_decode_dev(rv_kv* kv, size_t layer, float* residual, size_t hidden, size_t q_dim,
+                                 const rv_attn_block_weights* w, float eps, float theta, const uint32_t* d_position,
+                                 size_t max_position, float scale, void* scratch, size_t scratch_len, uint32_t flags,
+                                 rv_error* err) {
+  if (!d_position) return fail(err, RV_ERR_NULL_ARG, 0, 0, "d_position");
+  return block_decode(kv, layer, residual, hidden, q_dim, w, eps, theta, 0, d_position, max_position, scale, scratch,
+                      scratch_len, flags, err);
 }
 
 // The prefill chunk's scratch: normalized rows, q/k/v rows, attention rows,

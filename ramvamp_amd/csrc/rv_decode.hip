@@ -449,6 +449,10 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   constexpr int NKC = 32 / E;  // K chunks per lane per tile
   constexpr int NVC = 32 / E;  // V chunks per lane per tile (4 rows x 8 elements)
   constexpr int NT = W * 64;
+  if constexpr (PRO) {
+    // A token graph's step: the token's position from device memory.
+    if (pro.d_pos) positions = min((int)*pro.d_pos, pro.max_pos) + 1;
+  }
   const int split = blockIdx.x % n_splits;
   const int hidx = blockIdx.x / n_splits;  // kv head within the range
   const int kvh = kv_lo + hidx;
@@ -462,11 +466,12 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   const bool col_ok = li < group;
 
   if constexpr (PRO) {
-    // The token's row (position positions - 1) lives in the last split:
+    // The token's row (position positions - 1) lives in the split that
+    // holds it (the last one unless a token graph planned for more):
     // wave 0 writes this kv head's k (RMSNorm, then the rotation of pairs
     // (i, i + 64), as norm.rs:18-26 and rope.rs:31-45, contraction off) and
     // v into the cache row; the barrier makes them visible to the tiles.
-    if (split == n_splits - 1) {
+    if (split == (positions - 1) / split_len) {
       if (wave == 0) {
 #pragma clang fp contract(off)
         const float* kr = pro.k + col;
@@ -475,7 +480,8 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
         const double ss = wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1);
         const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)pro.eps));
         const float a0 = k0 * inv * pro.k_w[lane], a1 = k1 * inv * pro.k_w[lane + 64];
-        const float c = pro.cs[lane], sn = pro.sn[lane];
+        const float* trow = pro.tab + (size_t)(positions - 1) * kD;
+        const float c = pro.d_pos ? trow[lane] : pro.cs[lane], sn = pro.d_pos ? trow[64 + lane] : pro.sn[lane];
         T* krow = const_cast<T*>(kl) + (size_t)(positions - 1) * kv_dim + col;
         T* vrow = const_cast<T*>(vl) + (size_t)(positions - 1) * kv_dim + col;
         store_plane<T>(krow + lane, a0 * c - a1 * sn);
@@ -530,6 +536,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
       ss = swap_sum_f64<16>(ss);
       ss = swap_sum_f64<32>(ss);
       const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)pro.eps));
+      const float* trow = pro.tab + (size_t)(positions - 1) * kD;
 #pragma unroll
       for (int c = 0; c < NKC / 2; ++c)
 #pragma unroll
@@ -537,8 +544,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
           const int d = E * (lk + 4 * c) + e;  // < 64
           const float a0 = qv[c * E + e] * inv * pro.q_w[d];
           const float a1 = qv[(c + NKC / 2) * E + e] * inv * pro.q_w[d + 64];
-          qv[c * E + e] = a0 * pro.cs[d] - a1 * pro.sn[d];
-          qv[(c + NKC / 2) * E + e] = a0 * pro.sn[d] + a1 * pro.cs[d];
+          const float cs = pro.d_pos ? trow[d] : pro.cs[d], sn = pro.d_pos ? trow[64 + d] : pro.sn[d];
+          qv[c * E + e] = a0 * cs - a1 * sn;
+          qv[(c + NKC / 2) * E + e] = a0 * sn + a1 * cs;
         }
     }
 #pragma unroll
@@ -1142,6 +1150,21 @@ size_t decode_ws_bound(const rv_kv* kv) {
 bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads) {
   return kv->head_dim == kD && n_q_heads % kv->n_kv_heads == 0 && n_q_heads / kv->n_kv_heads <= 16 &&
          kv->tune_decode_impl != 1;
+}
+
+namespace {
+// A token graph's last node: the next token's position (one lane's store).
+__global__ __launch_bounds__(64) void position_advance_kernel(uint32_t* __restrict__ p, uint32_t n) {
+  if (threadIdx.x == 0) p[0] += n;
+}
+}  // namespace
+
+HipStatus launch_position_advance(uint32_t* d_position, uint32_t n, hipStream_t s) {
+  HipStatus st;
+  hipLaunchKernelGGL(position_advance_kernel, dim3(1), dim3(64), 0, s, d_position, n);
+  st.e = hipGetLastError();
+  if (st.e != hipSuccess) st.what = "position advance launch";
+  return st;
 }
 
 HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, size_t layer, size_t positions,

@@ -46,6 +46,13 @@ struct rv_kv {
   // Staging for RV_HOST_PTRS calls.
   void* stage = nullptr;
   size_t stage_bytes = 0;
+  // The device-position decode step's (cos, sin) table: for positions
+  // [0, rope_n), 64 cos then 64 sin (f64 on the host, cast to f32, as the
+  // host-position step computes them) at rope_theta; grown, never freed
+  // while the cache lives (a captured token graph addresses it).
+  float* rope_tab = nullptr;
+  size_t rope_n = 0;
+  float rope_theta = 0.f;
 
   int64_t tune_decode_split_len = 0;
   int64_t tune_prefill_kv_split = 0;
@@ -182,9 +189,14 @@ HipStatus noalloc_scratch(int device, void** ptr);
 // The decode step's prologue carried into the tile kernel (forward.rs:
 // 2617-2633): q pre-norm (each workgroup normalizes and rotates its group's
 // heads as it loads them), and the token's pre-norm k and v rows, which the
-// workgroup of the last split writes into the cache row positions - 1
-// (k normalized and rotated) before its tiles read it. (cos, sin) of the
-// token's position for pair i, computed on the host in f64.
+// workgroup of the split holding position positions - 1 writes into that
+// cache row (k normalized and rotated) before its tiles read it. (cos, sin)
+// of the token's position for pair i, computed on the host in f64.
+// With d_pos (a token graph's step, replayed for every token), the token's
+// position is read from device memory instead: positions = min(*d_pos,
+// max_pos) + 1, the launch planned for max_pos + 1 positions (splits past
+// the token write empty partials), and (cos, sin) read from tab (the
+// cache's rope_tab: 64 cos then 64 sin per position).
 struct DecodePro {
   const float* k;
   const float* v;
@@ -192,10 +204,15 @@ struct DecodePro {
   const float* k_w;
   float eps;
   float cs[64], sn[64];
+  const uint32_t* d_pos = nullptr;
+  const float* tab = nullptr;
+  int max_pos = 0;
 };
 // True when launch_decode_pro covers the geometry (head_dim 128, group <= 16:
 // the MFMA tile kernel); the caller then skips the row prologue.
 bool decode_pro_supported(const rv_kv* kv, size_t n_q_heads);
+// *d_position += n on s (a kernel, so a captured graph can carry it).
+HipStatus launch_position_advance(uint32_t* d_position, uint32_t n, hipStream_t s);
 // The whole decode step over positions (the token's row is positions - 1).
 HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, size_t layer, size_t positions,
                             float scale, const DecodePro& pro, float* out, hipStream_t s);
@@ -230,5 +247,10 @@ int32_t decode_step_check(const rv_kv* kv, size_t layer, size_t q_len, size_t po
 // rv_prefill_chunk's validation alone.
 int32_t prefill_chunk_check(const rv_kv* kv, size_t layer, size_t rows, size_t q_dim, size_t start,
                             size_t q_norm_len, size_t k_norm_len, rv_error* err);
+// rv_decode_step_dev's validation alone.
+int32_t decode_step_dev_check(const rv_kv* kv, size_t layer, size_t q_len, size_t max_position, size_t q_norm_len,
+                              size_t k_norm_len, rv_error* err);
+// The device-position step's (cos, sin) table covering positions [0, n).
+HipStatus ensure_rope_tab(rv_kv* kv, float theta, size_t n);
 
 }  // namespace rv
