@@ -171,7 +171,7 @@ def bench_config2(torch, rv, synth, steps, warmup):
     }
 
 
-def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
+def bench_prefill(torch, rv, synth, cfg, mode, iters=20, tune=None):
     c = synth.CONFIGS[cfg]
     start, rows = c.context, c.rows
     q, k, v = synth.new_rows(cfg, rows)
@@ -180,6 +180,8 @@ def bench_prefill(torch, rv, synth, cfg, mode, iters=20):
     dwq, dwk = torch.from_numpy(wq).cuda(), torch.from_numpy(wk).cuda()
     out = torch.zeros_like(dq)
     kv = rv.KvCache(1, 4, 128, start + rows, "f32")
+    for knob, value in (tune or {}).items():
+        kv.set_tuning(knob, value)
     if start:
         K, V = synth.cached_kv(cfg, 0, start)
         kv.append_rows(0, K, V)
@@ -776,6 +778,10 @@ def main():
             r = bench_prefill(torch, rv, synth, cfg, mode)
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")
+        for cfg in (3, 4):
+            r = bench_prefill(torch, rv, synth, cfg, "f16", tune={rv.RV_TUNE_PREFILL_FUSE: 2})
+            log(f"config {cfg} f16, rows appended inside the attention launch: {r['us_per_call']:.1f} us/call, "
+                f"kernel {r['us_attention_kernel']:.1f} us")
         return
     r2 = bench_config2(torch, rv, synth, args.steps, args.warmup)
     log(f"config 2: {r2['us_per_layer']:.2f} us/layer (graph), {r2['eager_us_per_layer']:.2f} us/layer (eager), "
@@ -789,6 +795,10 @@ def main():
             extra[f"config{cfg}_prefill_{mode}"] = r
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")
+        for cfg in (3, 4):  # the chunk's rows appended inside the attention launch (opt-in)
+            r = bench_prefill(torch, rv, synth, cfg, "f16", tune={rv.RV_TUNE_PREFILL_FUSE: 2})
+            extra[f"config{cfg}_prefill_f16_one_launch"] = r
+            log(f"config {cfg} f16 one launch: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us")
         r1 = bench_config1(torch, rv, synth)
         extra["config1_decode_step_ctx512"] = r1
         log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us")

@@ -291,6 +291,8 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
 #define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1, 2 or 4 (f16 planes) */
 #define RV_TUNE_DECODE_FAN 10      /* decode splits folded per level-1 merge group (the rest in a second level) */
 #define RV_TUNE_DECODE_MERGE 11    /* 0: decode splits merged by a second kernel, 1: inside the tile launch (ticket) */
+#define RV_TUNE_PREFILL_FUSE 12    /* an F16/BF16 prefill chunk's k/v rows: 0 auto (= 1), 1 appended by a row
+                                      prologue launch before the attention launch, 2 inside the attention launch */
 int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
 
 /* No reference counterpart: benchmark instrumentation. With

@@ -31,6 +31,7 @@ RV_TUNE_PREFILL_IMPL = 8
 RV_TUNE_DECODE_DEPTH = 9
 RV_TUNE_DECODE_FAN = 10
 RV_TUNE_DECODE_MERGE = 11
+RV_TUNE_PREFILL_FUSE = 12
 RV_NOALLOC_SCRATCH_BYTES = 8 << 20
 # include/ramvamp_gemv.h
 RV_QF_Q4_K = 1

@@ -512,7 +512,8 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab,
+                    (void*)kv->chunk_flags})
       if (p) (void)hipFree(p);
     for (void* p : kv->staged)
       if (p) (void)hipFree(p);
@@ -954,7 +955,32 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
   rv::fill_inv_freq(inv, hd, theta);
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};
   rv::HipStatus hs;
-  if (rv::prefill_supported(kv, p.group, start + rows)) {
+  if (rv::prefill_supported(kv, p.group, start + rows) && kv->tune_prefill_fuse == 2 &&
+      rv::chunk_fusable(kv, p.group, flags, kv->stream)) {
+    // One launch: the attention kernel appends the chunk's k/v rows (k
+    // prologue included) into the cache and the staged tiles and runs the q
+    // prologue in its query loads; (cos, sin) from the cache's table.
+    rv::StageDst sd;
+    hs = rv::ensure_rope_tab(kv, theta, start + rows);
+    if (hs.e == hipSuccess) hs = rv::ensure_chunk_flags(kv);
+    // The (cos, sin) rows a captured call of this shape writes (it takes the
+    // row-prologue path), so that capturing it allocates nothing.
+    if (hs.e == hipSuccess) hs = rv::ensure_qbuf(kv, rows * hd * sizeof(float));
+    if (hs.e == hipSuccess) hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
+    if (hs.e == hipSuccess && !sd.base) {
+      hs.e = hipErrorInvalidValue;
+      hs.what = "fused prefill chunk without a staged copy";
+    }
+    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+    kv->lens[layer] = len + rows;
+    if (++kv->chunk_epoch == 0) ++kv->chunk_epoch;
+    const rv::ChunkFuse cf{dk, dv, dwk, eps, kv->rope_tab, kv->k_layer(layer), kv->v_layer(layer),
+                           kv->elem == RV_ELEM_F16, (int)kv->kv_dim, kv->chunk_flags, (int)kv->chunk_flag_stride,
+                           kv->chunk_epoch};
+    const rv::QNorm qn{dwq, eps, kv->rope_tab + start * hd};
+    hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, &qn, kv->stream, &cf);
+    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
+  } else if (rv::prefill_supported(kv, p.group, start + rows)) {
     // k/v prologue + append (also into the layer's staged tiles) and the
     // rows' (cos, sin) table; the q prologue runs inside the attention
     // kernel's query loads.
@@ -996,6 +1022,7 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_DECODE_DEPTH: kv->tune_decode_depth = value; break;
     case RV_TUNE_DECODE_FAN: kv->tune_decode_fan = value; break;
     case RV_TUNE_DECODE_MERGE: kv->tune_decode_merge = value; break;
+    case RV_TUNE_PREFILL_FUSE: kv->tune_prefill_fuse = value; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }
   return ok(err);

@@ -53,6 +53,13 @@ struct rv_kv {
   float* rope_tab = nullptr;
   size_t rope_n = 0;
   float rope_theta = 0.f;
+  // A prefill chunk whose attention launch appends its own rows: one flag
+  // per (kv head, row block), set to the call's epoch once that block's rows
+  // are in the staged copy, then the launch's ticket counter (zero between
+  // calls). Allocated on first use, zeroed, never freed while the cache lives.
+  unsigned* chunk_flags = nullptr;
+  size_t chunk_flag_stride = 0;  // row blocks per kv head
+  unsigned chunk_epoch = 0;
 
   int64_t tune_decode_split_len = 0;
   int64_t tune_prefill_kv_split = 0;
@@ -64,6 +71,7 @@ struct rv_kv {
   int64_t tune_decode_depth = 0;  // tiles in flight per wave (1, 2, 4); 0 auto
   int64_t tune_decode_fan = 0;    // splits folded per level-1 group; 0 auto
   int64_t tune_decode_merge = 0;  // 0 separate merge kernel, 1 in-launch ticket merge
+  int64_t tune_prefill_fuse = 0;  // chunk rows: 0 auto (= 1), 1 by the row prologue, 2 by the attention launch
 
   // RV_TUNE_KERNEL_TIMING: event pairs around the dominant kernel of each
   // call, folded into timed_ms / timed_n when read (or when the pool fills).
@@ -151,8 +159,9 @@ struct StageDst {
 // Rows of (q, k, v) at RoPE positions pos0 + r: q heads RMSNormed with q_w
 // and rotated into q_out (rows x n_q x head_dim; n_q may be 0), k heads
 // RMSNormed with k_w and rotated into the cache at cache_row + r, v heads
-// copied there. With rope_tab, each row's (cos, sin) pairs as f32 are also
-// written there (rows x head_dim/2 x 2), for a fused q prologue downstream.
+// copied there. With rope_tab, each row's (cos, sin) as f32 are also written
+// there (per row head_dim/2 cos, then head_dim/2 sin), for a fused q
+// prologue downstream.
 // With sd (head_dim 128 only), the k and v rows as the cache holds them are
 // also written into the staged tiles at cache_row + r, and the rest of the
 // last tile is zeroed.
@@ -219,12 +228,32 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
 
 // ---- prefill (rv_prefill.hip) -------------------------------------------------
 // The q prologue fused into the prefill kernels' query loads: RMSNorm with
-// w and eps, rotation with the rows' (cos, sin) table from
-// launch_row_prologue.
+// w and eps, rotation with the rows' (cos, sin) table (from
+// launch_row_prologue, or the cache's rope_tab): row r's at tab + r * 128,
+// 64 cos then 64 sin.
 struct QNorm {
   const float* w = nullptr;
   float eps = 0.f;
   const float* tab = nullptr;
+};
+// A prefill chunk's k/v rows appended by the attention launch itself (f16 /
+// bf16 staged copy, head_dim 128): each workgroup writes its own rows' k
+// (RMSNorm + RoPE) and v into the cache planes and the staged copy, then
+// raises its row block's flag; tiles holding other blocks' rows are read only
+// once their flags carry `epoch`. k == nullptr: the rows are already in place.
+struct ChunkFuse {
+  const float* k = nullptr;  // the chunk's raw rows, rows x kv_dim
+  const float* v = nullptr;
+  const float* k_w = nullptr;
+  float eps = 0.f;
+  const float* tab = nullptr;  // (cos, sin) by absolute position, as QNorm's
+  void* kp = nullptr;          // the layer's cache planes at position 0
+  void* vp = nullptr;
+  int f16_cache = 0;
+  int kv_dim = 0;
+  unsigned* flags = nullptr;  // [n_kv][flag_stride], then the ticket counter
+  int flag_stride = 0;
+  unsigned epoch = 0;
 };
 // Before a prefill chunk appends `rows` rows at pos0 = len(layer) and runs
 // launch_prefill: readies the layer's persistent staged copy in `mode`
@@ -236,9 +265,18 @@ struct QNorm {
 HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t rows, uint32_t mode,
                                 hipStream_t s, StageDst* sd);
 // Row r of q_rows (rows x q_dim) attends positions 0..start+r+1; q_rows are
-// post-RoPE, or the raw projections when qn is given.
+// post-RoPE, or the raw projections when qn is given. With cf (and its k
+// set), the chunk's rows [start, start + rows) are appended by this launch
+// (F16/BF16 modes with a persistent staged copy only: chunk_fusable).
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
-                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s);
+                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s,
+                         const ChunkFuse* cf = nullptr);
+// Whether a prefill chunk in `mode` on stream s can append its rows inside
+// the attention launch (F16/BF16, head_dim 128, not under graph capture).
+bool chunk_fusable(const rv_kv* kv, size_t group, uint32_t mode, hipStream_t s);
+// The flags and ticket counter of fused chunks, allocated and zeroed on
+// first use (not under graph capture).
+HipStatus ensure_chunk_flags(rv_kv* kv);
 
 // rv_decode_step's validation alone (no launch), for callers that validate
 // a whole composite call before launching any of it.

@@ -250,8 +250,8 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
     sn[p] = (float)sd;
     cs[p] = (float)cd;
     if (tab && blockIdx.y == 0 && i < half) {
-      tab[((size_t)r * half + i) * 2] = cs[p];
-      tab[((size_t)r * half + i) * 2 + 1] = sn[p];
+      tab[(size_t)r * hd + i] = cs[p];
+      tab[(size_t)r * hd + half + i] = sn[p];
     }
   }
   // The slots' norms first, branch-free within a block that rotates (its v
