@@ -222,8 +222,8 @@ __device__ __forceinline__ bool aligned16(const void* a, const void* b = nullptr
 // order: row block-major, the kv heads next, the split holding a row block's
 // own rows (the last split) first. Unit (kv head h, row block b, last split)
 // writes block b's k and v rows of head h into the cache planes and the
-// staged copy with write-through (agent-scope) stores, waits for them to
-// complete and sets flag (h, b) to the call's epoch. Before a wave issues the
+// staged copy, waits for the stores, writes them back with an agent-scope
+// release and sets flag (h, b) to the call's epoch. Before a wave issues the
 // direct-to-LDS loads of a staged tile holding chunk rows it waits until the
 // flags of every row block in that tile carry the epoch; no workgroup reads
 // a tile's lines before then, so its XCD's L2 holds no stale copy of them.
