@@ -222,9 +222,39 @@ def bench_config1(torch, rv, synth, iters=50):
     wall = timed(torch, once, iters) / iters
     k_avg, _ = kernel_avg(torch, kv, once, iters, lead_cycles=400_000)
     nbytes = 2 * (start + 1) * 512 * 4 + 2 * 4096 * 4
+
+    # The same step from a token graph: 32 device-position steps per replay
+    # (contexts 513 .. 544, each followed by its position advance), the
+    # position reset to 512 before each replay; no host work per step.
+    n_graph = 32
+    kvg = rv.KvCache(1, 4, 128, start + 64, "f32")
+    kvg.append_rows(0, K, V)
+    pos = torch.tensor([start], dtype=torch.int32, device="cuda")
+
+    def steps():
+        for _ in range(n_graph):
+            rv.decode_step_dev(kvg, 0, q, k, v, wq, wk, synth.EPS, synth.THETA, pos, start + 63, synth.SCALE, out)
+            rv.position_advance(kvg, pos, 1)
+
+    steps()  # eagerly: builds the (cos, sin) table
+    pos.fill_(start)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        steps()
+
+    def replay():
+        pos.fill_(start)
+        graph.replay()
+
+    replay()
+    per_step = timed(torch, replay, iters) / (iters * n_graph)
+    del graph
     return {"us_per_call": round(wall * 1e6, 2), "us_attention_kernel": round(k_avg * 1e6, 2),
             "gbs_kernel": round(nbytes / k_avg / 1e9, 1), "hbm_frac_kernel": round(nbytes / k_avg / 1e9 / HBM_PEAK_GBS, 4),
-            "bytes_per_call": nbytes}
+            "bytes_per_call": nbytes,
+            "token_graph": {"us_per_step": round(per_step * 1e6, 2), "steps_per_replay": n_graph,
+                            "contexts": [start + 1, start + n_graph],
+                            "note": "decode_step_dev + position_advance per step, position reset per replay"}}
 
 
 def bench_config5(torch, rv, synth, iters=50, n_caches=5, split_lens=(0, 1024, 2048, 4096)):
@@ -801,7 +831,8 @@ def main():
             log(f"config {cfg} f16 one launch: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us")
         r1 = bench_config1(torch, rv, synth)
         extra["config1_decode_step_ctx512"] = r1
-        log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us")
+        log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us, "
+            f"token graph {r1['token_graph']['us_per_step']:.2f} us/step")
         r5 = bench_config5(torch, rv, synth)
         extra["config5_decode_f16_ctx32768"] = r5
         for name, r in r5.items():
