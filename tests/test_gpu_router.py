@@ -1,8 +1,9 @@
 """GPU parity of the router decision (include/ramvamp_router.h;
 model/forward.rs:2658-2705): expert indices and weights bit-identical to
 the oracle's, per row, at the model's shape (128 experts over a 2048-wide
-row, top 8, with and without renormalization), odd sizes, a batch of
-prefill rows, exact ties, and the validation order."""
+row, top 8, with and without renormalization), odd sizes, batches of
+prefill rows (including the sizes that group 2 and 4 rows per workgroup,
+with a ragged last group), exact ties, and the validation order."""
 import numpy as np
 import pytest
 
@@ -26,7 +27,8 @@ def check(torch, x, router, top_k, norm):
 
 
 @pytest.mark.parametrize("n_rows,hidden,n_experts,top_k", [(1, 2048, 128, 8), (7, 2048, 128, 8), (64, 2048, 128, 8),
-                                                           (3, 33, 5, 5), (2, 4096, 257, 3)])
+                                                           (3, 33, 5, 5), (2, 4096, 257, 3), (513, 2048, 128, 8),
+                                                           (1027, 2048, 128, 8), (1030, 100, 300, 4)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_router_is_bit_identical_to_the_oracle(n_rows, hidden, n_experts, top_k, norm):
     torch = torch_cuda()
