@@ -517,14 +517,14 @@ def bench_attn_block_prefill(torch, rv, synth, mode="f16", iters=20):
 
 
 def bench_router(torch, rv, iters=50, n_experts=128, hidden=2048, top_k=8):
-    """The router decision (forward.rs:2658-2705) for one decode row and for
-    a 512-row prefill chunk, 128 experts over a 2048-wide row, top 8 with
-    renormalization, host-timed back to back."""
+    """The router decision (forward.rs:2658-2705) for one decode row, a
+    512-row prefill chunk and 1024 rows, 128 experts over a 2048-wide row,
+    top 8 with renormalization, host-timed back to back."""
     from ramvamp_amd import router as R
     rng = np.random.default_rng(0x40)
     w = torch.from_numpy((rng.standard_normal((n_experts, hidden)) * 0.03).astype(np.float32)).cuda()
     out = {}
-    for rows in (1, 512):
+    for rows in (1, 512, 1024):
         x = torch.from_numpy(rng.standard_normal((rows, hidden)).astype(np.float32)).cuda()
         ex = torch.empty(rows, top_k, dtype=torch.int32, device="cuda")
         wt = torch.empty(rows, top_k, device="cuda")
@@ -752,6 +752,8 @@ def main():
                     help="only run the prefill-chunk projection leg (512 rows), log it and exit (for profiling)")
     ap.add_argument("--block-only", action="store_true",
                     help="only run the attention-block leg (48 layers, ctx 4096), log it and exit (for profiling)")
+    ap.add_argument("--router-only", action="store_true",
+                    help="only run the router leg (1, 512 and 1024 rows), log it and exit (for profiling)")
     ap.add_argument("--config5-only", action="store_true",
                     help="only run the config 5 leg (ctx 32768, f16, every split shape), log it and exit (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -786,9 +788,12 @@ def main():
         log(f"prefill projections: {rpp['us_per_layer']:.2f} us/layer for {rpp['rows']} rows, "
             f"{rpp['int8_tops']:.1f} int8 TOP/s")
         return
-    if args.block_only:
+    if args.router_only:
         rr = bench_router(torch, rv)
-        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")
+        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows, "
+            f"{rr['us_1024_rows']:.1f} us for 1024 rows")
+        return
+    if args.block_only:
         rb = bench_attn_block(torch, rv, synth)
         log(f"attention block: {rb['us_per_layer']:.2f} us/layer, {rb['ms_per_token_48_layers']:.3f} ms per token; "
             f"token graph {rb['token_graph']['us_per_layer']:.2f} us/layer over {rb['token_graph']['tokens']} tokens")
@@ -856,7 +861,8 @@ def main():
             f"token graph {rb['token_graph']['us_per_layer']:.2f} us/layer over {rb['token_graph']['tokens']} tokens")
         rr = bench_router(torch, rv)
         extra["router_128x2048_top8"] = rr
-        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows")
+        log(f"router: {rr['us_1_rows']:.1f} us for 1 row, {rr['us_512_rows']:.1f} us for 512 rows, "
+            f"{rr['us_1024_rows']:.1f} us for 1024 rows")
         for mode in ("f16", "exact"):
             rbp = bench_attn_block_prefill(torch, rv, synth, mode)
             extra[f"attn_block_prefill_config4_{mode}"] = rbp
