@@ -773,12 +773,16 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
 // range, block of 16 output columns). Thread t takes columns 4*(t % 4) .. +3
 // of the block and the splits t/4, t/4 + 64, ...; it issues all of a round's
 // loads (kMergePer splits, 16-byte o loads) before folding any, in split
-// order, so up to 256 splits cost one memory round trip. The 64 split lanes
-// then merge in a fixed tree through LDS (lane i with lane i + w, w = 32 ..
-// 1). The order is fixed by n_splits alone. Measured against one workgroup
-// per query head (8 split lanes, 3-level tree) and one wave per 4 columns
-// (a 64-lane butterfly), this spread was the fastest: the merge's bytes
-// come from other XCDs' writes, and a CU's share of them bounds its time.
+// order, so up to 256 splits cost one memory round trip. Each wave's 16
+// split lanes per column quad then fold by cross-lane exchange (lane i with
+// lane i ^ 4, 8, 16, 32), and lane k of wave 0 folds the four waves through
+// LDS in wave order: one barrier (a 6-level LDS tree with a barrier per
+// level cost 0.12 µs more per call). The order is fixed by n_splits alone.
+// Measured against one workgroup per query head (8 split lanes, 3-level
+// tree) and one wave per 4 columns (a 64-lane butterfly), this spread was
+// the fastest: the merge's bytes come from other XCDs' writes, and a CU's
+// share of them bounds its time. Non-temporal stores of the partials in the
+// tile kernel made the call 0.18 µs slower.
 constexpr int kMergeLanes = 64;
 constexpr int kMergeBlock = 16;  // output columns per workgroup
 template <int MP>  // splits per lane per round: 1, 2 or 4 (up to 64, 128, 256 splits in one round)
@@ -813,27 +817,34 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         M = mn;
       }
   }
-  __shared__ float sm_m[kMergeLanes][4], sm_l[kMergeLanes][4];
-  __shared__ f32x4 sm_o[kMergeLanes][4];
-  sm_m[sl][k] = M;
-  sm_l[sl][k] = L;
-  sm_o[sl][k] = O;
-  for (int w = kMergeLanes / 2; w >= 1; w >>= 1) {
-    __syncthreads();
-    if (sl < w) {
-      const float m2 = sm_m[sl + w][k], l2 = sm_l[sl + w][k];
-      const f32x4 o2 = sm_o[sl + w][k];
-      const float mn = fmaxf(M, m2);
-      const float a = __builtin_amdgcn_exp2f(M - mn), c = __builtin_amdgcn_exp2f(m2 - mn);
-      L = L * a + l2 * c;
-      O = O * a + o2 * c;
-      M = mn;
-      sm_m[sl][k] = M;
-      sm_l[sl][k] = L;
-      sm_o[sl][k] = O;
-    }
+  auto fold = [&](float m2, float l2, f32x4 o2) {
+    const float mn = fmaxf(M, m2);
+    const float a = __builtin_amdgcn_exp2f(M - mn), c = __builtin_amdgcn_exp2f(m2 - mn);
+    L = L * a + l2 * c;
+    O = O * a + o2 * c;
+    M = mn;
+  };
+  // A wave's 16 split lanes of each column quad (lane bits 2..5) fold by
+  // cross-lane exchange, then lane k of wave 0 folds the four waves in order.
+#pragma unroll
+  for (int off = 4; off < 64; off <<= 1) {
+    f32x4 o2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o2[e] = __shfl_xor(O[e], off, 64);
+    fold(__shfl_xor(M, off, 64), __shfl_xor(L, off, 64), o2);
   }
-  if (sl == 0) {
+  __shared__ float sm_m[4][4], sm_l[4][4];
+  __shared__ f32x4 sm_o[4][4];
+  const int wave = tid >> 6;
+  if ((tid & 63) < 4) {
+    sm_m[wave][k] = M;
+    sm_l[wave][k] = L;
+    sm_o[wave][k] = O;
+  }
+  __syncthreads();
+  if (tid < 4) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w) fold(sm_m[w][k], sm_l[w][k], sm_o[w][k]);
     const f32x4 r = O / L;  // out may be only 4-byte aligned
     float* op = out + (size_t)h * kD + d;
     op[0] = r[0];
