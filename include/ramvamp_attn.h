@@ -288,7 +288,7 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
                                       MFMA operands split hi/lo), 1 VALU subgroups, 2 MFMA tiles with fp32 operands */
 #define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
 #define RV_TUNE_PREFILL_IMPL 8     /* prefill attention kernel: 0 auto, 1 two wave groups, 2 software-pipelined */
-#define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1, 2 or 4 (f16 planes) */
+#define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1 (default), 2 or 4 (f16 planes) */
 #define RV_TUNE_DECODE_FAN 10      /* decode splits folded per level-1 merge group (the rest in a second level) */
 #define RV_TUNE_DECODE_MERGE 11    /* 0: decode splits merged by a second kernel, 1: inside the tile launch (ticket) */
 #define RV_TUNE_PREFILL_FUSE 12    /* an F16/BF16 prefill chunk's k/v rows: 0 auto (= 1), 1 appended by a row

@@ -302,12 +302,12 @@ struct Chunk<_Float16> {
 //   O^T[d][m] += sum_t V[t][d] P^T[t][m]: 8 x 4 MFMAs; the accumulator layout
 //     of S^T is exactly the B layout P^T needs (step r takes rows 4k + r), and
 //     lane (i, k) holds V[4k + r][8i .. 8i+7], so output block b is d = 8i + b.
-// Each wave keeps D tiles in flight in a register ring: the first D tiles'
-// loads are issued before anything waits, and the loads of tile j + D are
-// issued as soon as tile j has been computed (scheduling barriers keep the
-// compiler from sinking them to their first use). The kernel is held to 256
-// registers so that two waves fit per SIMD and a grid of ~2048 waves is
-// resident at once. The waves merge through LDS; the workgroup then writes
+// Each wave keeps D tiles in flight in a register ring (D = 1 by default):
+// the first D tiles' loads are issued before anything waits, and the loads
+// of tile j + D are issued as soon as tile j has been computed (scheduling
+// barriers keep the compiler from sinking them to their first use). The
+// kernel is held to 256 registers so that two waves fit per SIMD and a grid
+// of ~2048 waves is resident at once. The waves merge through LDS; the workgroup then writes
 // `out` (one split) or its partial (o, max, sum) row; the splits of a kv head
 // are folded by decode_merge_kernel or, with MergeArgs::fused, inside the
 // same launch (the in-launch split merge below).
@@ -1019,11 +1019,14 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 }
 
 // Launch shape of the MFMA tile kernel. Default, from sweeps on MI355X:
-// 4-wave workgroups, each wave holding its share of the split's 16-position
-// tiles in a register ring `depth` deep, with the split long enough for
-// about kTileWaves waves in all (two per SIMD, all resident at once: the
-// kernel is capped at 256 registers) and every tile in flight when the ring
-// allows it (f16 planes: 4 tiles per wave, fp32: 2). The splits of a kv head
+// 4-wave workgroups, each wave taking its share of the split's 16-position
+// tiles one at a time (ring depth 1: the next tile's loads issue once the
+// current one is computed), with the split long enough for about kTileWaves
+// waves in all (two per SIMD, all resident at once). Deeper rings (2 or 4
+// tiles in flight per wave, the tuning knob) measured 5-13 % slower at
+// every context from 512 to 32768 positions, f16 and fp32: the other
+// resident wave of the SIMD covers a wave's load latency, and fewer
+// requests in flight per CU stream faster. The splits of a kv head
 // are folded by decode_merge_kernel; the in-launch ticket merge (fused) is a
 // tuning option: its hand-off (device-scope stores acknowledged, a
 // memory-side atomic, loads that miss L2) costs more than the second launch.
@@ -1038,9 +1041,8 @@ struct TilePlan {
   bool fused;
 };
 
-static int tile_depth(const rv_kv* kv, int waves, int split_len) {
-  const int tpw = (split_len / 16 + waves - 1) / waves;  // tiles per wave
-  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : tpw;
+static int tile_depth(const rv_kv* kv) {
+  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : 1;
   const int dmax = kv->elem == RV_ELEM_F32 ? 2 : 4;  // register ring: 64 (f32) or 32 (f16) VGPRs per tile
   d = std::min(d, dmax);
   return d >= 4 ? 4 : d >= 2 ? 2 : 1;
@@ -1059,7 +1061,7 @@ static TilePlan plan_tile(const rv_kv* kv, long positions, int n_heads) {
   len = std::max<long>(len, step);
   p.split_len = (int)((len + step - 1) / step * step);
   p.n_splits = (int)((positions + p.split_len - 1) / p.split_len);
-  p.depth = tile_depth(kv, p.waves, p.split_len);
+  p.depth = tile_depth(kv);
   p.fused = kv->tune_decode_merge == 1;
   int fan = (int)kv->tune_decode_fan;
   if (fan <= 0) {

@@ -256,6 +256,33 @@ def test_kernel_variants_agree_with_the_oracle(impl, waves, elem):
             gate(out, ref.attention(q, 0, 0.3, positions=p), what=f"impl {impl} waves {waves} split {split_len} p {p}")
 
 
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_ring_depths_are_bit_identical(elem):
+    """The tile kernel's register ring (RV_TUNE_DECODE_DEPTH 2 and 4; the
+    default takes one tile at a time) changes only how many tiles' loads are
+    in flight, never the arithmetic order: every depth gives depth 1's bits,
+    and those pass the oracle gate."""
+    torch_cuda()
+    say(f"case ring depths elem={elem}")
+    rng = Rng(0xDE97 + (elem == "f16"))
+    kv, ref = twin_caches(rng, 1, 4, 128, 2049, elem)
+    q = rng.vec_in(32 * 128, -2.0, 2.0)
+    for waves in (4, 8):
+        kv.set_tuning(rv.RV_TUNE_DECODE_WAVES, waves)
+        for split_len in (0, 256, 4096):
+            kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, split_len)
+            outs = {}
+            for depth in (1, 2, 4):
+                kv.set_tuning(rv.RV_TUNE_DECODE_DEPTH, depth)
+                out = np.full(q.size, np.nan, np.float32)
+                rv.decode_attention(q, kv, 0, 0.3, None, out)
+                outs[depth] = out
+            what = f"waves {waves} split {split_len}"
+            gate(outs[1], ref.attention(q, 0, 0.3), what=what)
+            for depth in (2, 4):
+                assert np.array_equal(outs[depth].view(np.uint32), outs[1].view(np.uint32)), f"{what} depth {depth}"
+
+
 def test_config1_decode_step_matches_the_oracle():
     # BASELINE config 1: cached rows 0..511 built by the fused prefill prologue,
     # then the fused decode step at position 512 (prologue + append + decode).
