@@ -302,7 +302,8 @@ struct Chunk<_Float16> {
 //   O^T[d][m] += sum_t V[t][d] P^T[t][m]: 8 x 4 MFMAs; the accumulator layout
 //     of S^T is exactly the B layout P^T needs (step r takes rows 4k + r), and
 //     lane (i, k) holds V[4k + r][8i .. 8i+7], so output block b is d = 8i + b.
-// Each wave keeps D tiles in flight in a register ring (D = 1 by default):
+// Each wave keeps D tiles in flight in a register ring (D = 1 when the grid
+// holds two waves per SIMD):
 // the first D tiles' loads are issued before anything waits, and the loads
 // of tile j + D are issued as soon as tile j has been computed (scheduling
 // barriers keep the compiler from sinking them to their first use). The
@@ -1021,14 +1022,16 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 }
 
 // Launch shape of the MFMA tile kernel. Default, from sweeps on MI355X:
-// 4-wave workgroups, each wave taking its share of the split's 16-position
-// tiles one at a time (ring depth 1: the next tile's loads issue once the
-// current one is computed), with the split long enough for about kTileWaves
-// waves in all (two per SIMD, all resident at once). Deeper rings (2 or 4
-// tiles in flight per wave, the tuning knob) measured 5-13 % slower at
-// every context from 512 to 32768 positions, f16 and fp32: the other
-// resident wave of the SIMD covers a wave's load latency, and fewer
-// requests in flight per CU stream faster. The splits of a kv head
+// 4-wave workgroups, with the split long enough for about kTileWaves waves
+// in all (two per SIMD, all resident at once), each wave taking its share
+// of the split's 16-position tiles one at a time (ring depth 1: the next
+// tile's loads issue once the current one is computed). With two or four
+// of a wave's tiles in flight instead (the previous default wherever a
+// wave had several tiles: from 16384 positions on) the call measured 0-6 %
+// slower (config 5, f16 at 32768: 19.6 vs 18.6 µs; fp32 at 16384: 19.1 vs
+// 17.9 µs): the SIMD's other resident wave covers a wave's load latency.
+// A pinned split that leaves fewer waves than that keeps a slot per tile
+// (32 splits per kv head at 32768: 23.0 vs 25.3 µs). The splits of a kv head
 // are folded by decode_merge_kernel; the in-launch ticket merge (fused) is a
 // tuning option: its hand-off (device-scope stores acknowledged, a
 // memory-side atomic, loads that miss L2) costs more than the second launch.
@@ -1043,8 +1046,14 @@ struct TilePlan {
   bool fused;
 };
 
-static int tile_depth(const rv_kv* kv) {
-  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : 1;
+// Ring depth: one tile at a time when the whole cache's grid (every kv head,
+// so a kv-head range picks the same depth) holds about kTileWaves waves;
+// with fewer waves (a pinned long split), a slot per tile of the wave's
+// share up to the ring's limit, since no other wave covers the loads.
+static int tile_depth(const rv_kv* kv, int waves, int split_len, int n_splits) {
+  const int tpw = (split_len / 16 + waves - 1) / waves;  // tiles per wave
+  const long grid_waves = (long)n_splits * (long)kv->n_kv_heads * waves;
+  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : grid_waves >= kTileWaves ? 1 : tpw;
   const int dmax = kv->elem == RV_ELEM_F32 ? 2 : 4;  // register ring: 64 (f32) or 32 (f16) VGPRs per tile
   d = std::min(d, dmax);
   return d >= 4 ? 4 : d >= 2 ? 2 : 1;
@@ -1063,7 +1072,7 @@ static TilePlan plan_tile(const rv_kv* kv, long positions, int n_heads) {
   len = std::max<long>(len, step);
   p.split_len = (int)((len + step - 1) / step * step);
   p.n_splits = (int)((positions + p.split_len - 1) / p.split_len);
-  p.depth = tile_depth(kv);
+  p.depth = tile_depth(kv, p.waves, p.split_len, p.n_splits);
   p.fused = kv->tune_decode_merge == 1;
   int fan = (int)kv->tune_decode_fan;
   if (fan <= 0) {
