@@ -285,7 +285,8 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
 #define RV_TUNE_PREFILL_ROWS 4     /* query rows per prefill tile: 8 or 16 */
 #define RV_TUNE_DECODE_HG 5        /* query heads per VALU decode workgroup: 1, 2, 4 or 8 */
 #define RV_TUNE_DECODE_IMPL 6      /* decode kernel: 0 auto (MFMA tiles when head_dim 128 and group <= 16; f16 planes on f16
-                                      MFMA operands split hi/lo), 1 VALU subgroups, 2 MFMA tiles with fp32 operands */
+                                      MFMA operands split hi/lo), 1 VALU subgroups, 2 MFMA tiles with fp32 operands,
+                                      3 MFMA tiles staged through LDS (4-wave workgroups) */
 #define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
 #define RV_TUNE_PREFILL_IMPL 8     /* prefill attention kernel: 0 auto, 1 two wave groups, 2 software-pipelined */
 #define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1 (default), 2 or 4 (f16 planes) */

@@ -440,7 +440,7 @@ __device__ __forceinline__ bool last_of(unsigned* t, unsigned n, int tid) {
 // element b of a lane's four V rows: the S^T accumulator is already the B
 // layout), and the output scaled back at the end; so the loads and the
 // output layout are the fp32 path's.
-template <typename T, int W, int D, bool PRO = false, bool H16 = false>
+template <typename T, int W, int D, bool PRO = false, bool H16 = false, bool LDS = false>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void decode_tile_kernel(
     const float* __restrict__ q, PlanePtr<PRO, T> kl, PlanePtr<PRO, T> vl, int kv_dim, int positions, int split_len,
     int n_splits, int group, int kv_lo, float qscale, MergeArgs mg, float* __restrict__ out,
@@ -450,6 +450,16 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   constexpr int NKC = 32 / E;  // K chunks per lane per tile
   constexpr int NVC = 32 / E;  // V chunks per lane per tile (4 rows x 8 elements)
   constexpr int NT = W * 64;
+  // The LDS form stages 64-position tiles (16 positions per wave) of K and V
+  // for the whole workgroup, two stages of kStage bytes; the waves' merge
+  // below reuses the same bytes once the ring is drained.
+  static_assert(!LDS || (W == 4 && D == 1 && !PRO), "LDS staging: 4 waves, one tile per step, no prologue");
+  constexpr int kRowB = kD * (int)sizeof(T);  // bytes of one position's head slice
+  constexpr int kPlaneB = 64 * kRowB;         // one plane of a staged tile
+  constexpr int kStage = 2 * kPlaneB;
+  constexpr int kOBytes = W * 16 * (kD + 4) * (int)sizeof(float);
+  constexpr int kLdsBytes = LDS ? (2 * kStage > kOBytes ? 2 * kStage : kOBytes) : kOBytes;
+  __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
   if constexpr (PRO) {
     // A token graph's step: the token's position from device memory.
     if (pro.d_pos) positions = min((int)*pro.d_pos, pro.max_pos) + 1;
@@ -668,25 +678,79 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   // counts: a tile's first MFMAs start as its first chunks land), D tiles
   // ahead of their use; the last round computes what is left and loads
   // nothing.
-  CT kr[D][NKC], vr[D][NVC];
+  if constexpr (LDS) {
+    // Staged form: step jt's 64 positions (wave w computes the 16 at 16 w)
+    // land in LDS by direct-to-LDS loads, each 1 KiB piece from one wave,
+    // while the previous step is computed. Row r's 16-byte K chunks are
+    // stored XOR-permuted by r % 16 and V's (fp32) with bit 4 of the chunk
+    // folded into bit 0, so the operand reads below are free of bank
+    // conflicts; the operands and their clamping are the register form's.
+    constexpr int kLPW = kStage / 1024 / W;  // pieces per wave per stage
+    const int n_steps = (n_tiles + W - 1) / W;
+    auto kq = [](int r, int q) { return q ^ (r & 15); };
+    auto vq = [](int q) { return sizeof(T) == 4 ? q ^ ((q >> 4) & 1) : q; };
+    auto stage = [&](int jt, int st) {
+      jt = min(jt, n_steps - 1);  // past the last step: the last again (never read)
 #pragma unroll
-  for (int i = 0; i < D; ++i) load_tile(i, kr[i], vr[i]);
-  __builtin_amdgcn_sched_barrier(0);
-  scale_q();
-  const int n_rounds = (my_tiles + D - 1) / D;
-  for (int rr = 0; rr + 1 < n_rounds; ++rr) {
+      for (int ii = 0; ii < kLPW; ++ii) {
+        const int piece = wave + W * ii;
+        const int o = piece * 1024 + 16 * lane, plane = o / kPlaneB, ob = o % kPlaneB;
+        const int r = ob / kRowB, q = (ob % kRowB) / 16;
+        const int t = min(t_begin + 64 * jt + r, t_end - 1);
+        const T* src = (plane == 0 ? kl + (size_t)t * kv_dim + col + kq(r, q) * (16 / (int)sizeof(T))
+                                   : vl + (size_t)t * kv_dim + col + vq(q) * (16 / (int)sizeof(T)));
+        lds_load16(src, (lds_void*)(lds_raw + st * kStage + piece * 1024));
+      }
+    };
+    auto read_tile = [&](int st, CT (&kb)[NKC], CT (&vb)[NVC]) {
+      const char* base = lds_raw + st * kStage;
+      const int rk = 16 * wave + li;
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-      compute(rr * D + i, kr[i], vr[i]);
-      load_tile((rr + 1) * D + i, kr[i], vr[i]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int c = 0; c < NKC; ++c) kb[c] = *reinterpret_cast<const CT*>(base + rk * kRowB + kq(rk, lk + 4 * c) * 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rv = 16 * wave + 4 * lk + r;
+#pragma unroll
+        for (int h = 0; h < 8 / E; ++h)
+          vb[r * (8 / E) + h] = *reinterpret_cast<const CT*>(base + kPlaneB + rv * kRowB +
+                                                             vq((8 * li + E * h) * (int)sizeof(T) / 16) * 16);
+      }
+    };
+    if (n_steps > 0) {
+      stage(0, 0);
+      scale_q();
+      for (int jt = 0; jt < n_steps; ++jt) {
+        wait_vmcnt<0>();  // this wave's pieces of step jt have landed
+        __syncthreads();       // everyone's have, and step jt - 1's stage is free
+        stage(jt + 1, (jt + 1) & 1);
+        CT kb[NKC], vb[NVC];
+        read_tile(jt & 1, kb, vb);
+        if (wave + jt * W < n_tiles) compute(jt, kb, vb);
+      }
+      wait_vmcnt<0>();
     }
-  }
-  if (n_rounds > 0) {
-    const int j0 = (n_rounds - 1) * D;
+    __syncthreads();  // the ring's bytes become the merge's
+  } else {
+    CT kr[D][NKC], vr[D][NVC];
 #pragma unroll
-    for (int i = 0; i < D; ++i)
-      if (j0 + i < my_tiles) compute(j0 + i, kr[i], vr[i]);
+    for (int i = 0; i < D; ++i) load_tile(i, kr[i], vr[i]);
+    __builtin_amdgcn_sched_barrier(0);
+    scale_q();
+    const int n_rounds = (my_tiles + D - 1) / D;
+    for (int rr = 0; rr + 1 < n_rounds; ++rr) {
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        compute(rr * D + i, kr[i], vr[i]);
+        load_tile((rr + 1) * D + i, kr[i], vr[i]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (n_rounds > 0) {
+      const int j0 = (n_rounds - 1) * D;
+#pragma unroll
+      for (int i = 0; i < D; ++i)
+        if (j0 + i < my_tiles) compute(j0 + i, kr[i], vr[i]);
+    }
   }
   l_run = swap_sum<16>(l_run);
   l_run = swap_sum<32>(l_run);
@@ -696,7 +760,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int b = 0; b < 8; ++b) o[b] *= 1.f / kPScale;  // the probabilities' scale, exactly
   }
   // o[b][r] = O^T[d = 8*(4*lk + r) + b][m = li]. Merge the W waves in LDS.
-  __shared__ __attribute__((aligned(16))) float sm_o[W][16][kD + 4];
+  auto sm_o = reinterpret_cast<float (*)[16][kD + 4]>(lds_raw);
   __shared__ float sm_ml[W][16][2];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -1044,6 +1108,7 @@ constexpr int kFanOne = 16;
 struct TilePlan {
   int waves, depth, split_len, n_splits, fan, n_grp;
   bool fused;
+  bool lds;  // RV_TUNE_DECODE_IMPL 3: tiles staged through LDS (4 waves, depth 1)
 };
 
 // Ring depth: one tile at a time when the whole cache's grid (every kv head,
@@ -1073,6 +1138,8 @@ static TilePlan plan_tile(const rv_kv* kv, long positions, int n_heads) {
   p.split_len = (int)((len + step - 1) / step * step);
   p.n_splits = (int)((positions + p.split_len - 1) / p.split_len);
   p.depth = tile_depth(kv, p.waves, p.split_len, p.n_splits);
+  p.lds = kv->tune_decode_impl == 3 && p.waves == 4;
+  if (p.lds) p.depth = 1;
   p.fused = kv->tune_decode_merge == 1;
   int fan = (int)kv->tune_decode_fan;
   if (fan <= 0) {
@@ -1122,6 +1189,14 @@ static void launch_tile(const TilePlan& p, const TimedPair& tp, hipStream_t s, i
                         const void* kl, const void* vl, int kv_dim, int positions, int group, int kv_lo, float qscale,
                         const MergeArgs& mg, float* out, const Pro& pro) {
   const dim3 grid((unsigned)(n_heads * p.n_splits));
+  if constexpr (!PRO) {
+    if (p.lds) {
+      launch_timed(tp, decode_tile_kernel<T, 4, 1, false, H16, true>, grid, dim3(256), s, q, (PlanePtr<false, T>)kl,
+                   (PlanePtr<false, T>)vl, kv_dim, positions, p.split_len, p.n_splits, group, kv_lo, qscale, mg, out,
+                   pro);
+      return;
+    }
+  }
 #define RV_TILE(W, D)                                                                                              \
   launch_tile_wd<T, W, D, PRO, H16>(tp, grid, s, q, kl, vl, kv_dim, positions, p.split_len, p.n_splits, group, kv_lo, \
                                     qscale, mg, out, pro)

@@ -155,4 +155,22 @@ __device__ __forceinline__ void load8(const _Float16* __restrict__ p, float (&x)
   for (int i = 0; i < 8; ++i) x[i] = (float)h[i];
 }
 
+// 16 bytes per lane from global memory straight into LDS at the wave-uniform
+// base `l` + 16 * lane (global_load_lds_dwordx4). The device-only guard keeps
+// the host pass, which has no such builtin, from dropping the kernels' stubs.
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void lds_load16(const void* g, lds_void* l) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace rv

@@ -67,7 +67,7 @@ struct rv_kv {
   int64_t tune_prefill_rows = 0;
   int64_t tune_decode_hg = 0;
   int64_t tune_prefill_impl = 0;  // 0 auto, 1 two wave groups, 2 software-pipelined
-  int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups
+  int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups, 3 LDS-staged tiles
   int64_t tune_decode_depth = 0;  // tiles in flight per wave (1, 2, 4); 0 auto
   int64_t tune_decode_fan = 0;    // splits folded per level-1 group; 0 auto
   int64_t tune_decode_merge = 0;  // 0 separate merge kernel, 1 in-launch ticket merge

@@ -283,6 +283,32 @@ def test_ring_depths_are_bit_identical(elem):
                 assert np.array_equal(outs[depth].view(np.uint32), outs[1].view(np.uint32)), f"{what} depth {depth}"
 
 
+@pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_lds_staged_tiles_give_the_register_form_bits(elem):
+    """RV_TUNE_DECODE_IMPL 3 stages each 64-position step through LDS with
+    direct-to-LDS loads; the MFMA operands (and their clamping past a split's
+    end) are the register form's, so the outputs are its bits, at one tile
+    per split, ragged splits and long ones."""
+    torch_cuda()
+    say(f"case lds-staged elem={elem}")
+    rng = Rng(0x1D5 + (elem == "f16"))
+    kv, ref = twin_caches(rng, 1, 4, 128, 2049, elem)
+    q = rng.vec_in(32 * 128, -2.0, 2.0)
+    for split_len in (0, 64, 200, 1024, 4096):
+        kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, split_len)
+        for p in (1, 17, 64, 65, 2049):
+            outs = {}
+            for impl in (0, 3):
+                kv.set_tuning(rv.RV_TUNE_DECODE_IMPL, impl)
+                out = np.full(q.size, np.nan, np.float32)
+                rv.attention_at(q, kv, 0, p, 0.3, None, out)
+                outs[impl] = out
+            what = f"split {split_len} p {p}"
+            gate(outs[3], ref.attention(q, 0, 0.3, positions=p), what=what)
+            assert np.array_equal(outs[3].view(np.uint32), outs[0].view(np.uint32)), what
+    kv.set_tuning(rv.RV_TUNE_DECODE_IMPL, 0)
+
+
 def test_config1_decode_step_matches_the_oracle():
     # BASELINE config 1: cached rows 0..511 built by the fused prefill prologue,
     # then the fused decode step at position 512 (prologue + append + decode).
