@@ -848,18 +848,24 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
 // Measured against one workgroup per query head (8 split lanes, 3-level
 // tree) and one wave per 4 columns (a 64-lane butterfly), this spread was
 // the fastest: the merge's bytes come from other XCDs' writes, and a CU's
-// share of them bounds its time. Non-temporal stores of the partials in the
-// tile kernel made the call 0.18 µs slower.
+// share of them bounds its time. 32 columns per workgroup (kMergeQuads 8:
+// 512 threads, each partial's 128-byte line read by one workgroup instead
+// of two) made the call 0.25 µs slower; non-temporal stores of the partials
+// in the tile kernel, 0.18 µs slower.
 constexpr int kMergeLanes = 64;
-constexpr int kMergeBlock = 16;  // output columns per workgroup
+constexpr int kMergeQuads = 4;                   // column quads per workgroup (16 columns)
+constexpr int kMergeBlock = 4 * kMergeQuads;     // output columns per workgroup
+constexpr int kMergeThreads = 64 * kMergeQuads;  // 64 split lanes per column quad
 template <int MP>  // splits per lane per round: 1, 2 or 4 (up to 64, 128, 256 splits in one round)
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part, int n_splits, int stride,
-                                                           int G, int group, int n_hg, float* __restrict__ out) {
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(const float* __restrict__ part, int n_splits,
+                                                                     int stride, int G, int group, int n_hg,
+                                                                     float* __restrict__ out) {
   constexpr int kMergePer = MP;
+  constexpr int QW = kMergeQuads;  // waves, and quads per lane group
   const int blk = blockIdx.x % (kD / kMergeBlock), h = blockIdx.x / (kD / kMergeBlock);  // h: q head in the range
   const int hidx = h / group, hh = h % group;
   const int g = hh % G, job = hidx * n_hg + hh / G;
-  const int tid = threadIdx.x, k = tid & 3, sl = tid >> 2;
+  const int tid = threadIdx.x, k = tid % QW, sl = tid / QW;
   const int d = blk * kMergeBlock + 4 * k;
   const float* base = part + (size_t)job * n_splits * stride;
   float M = kNegSentinel, L = 0.f;
@@ -891,27 +897,27 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     O = O * a + o2 * c;
     M = mn;
   };
-  // A wave's 16 split lanes of each column quad (lane bits 2..5) fold by
-  // cross-lane exchange, then lane k of wave 0 folds the four waves in order.
+  // A wave's split lanes of each column quad fold by cross-lane exchange,
+  // then lane k of wave 0 folds the waves in order.
 #pragma unroll
-  for (int off = 4; off < 64; off <<= 1) {
+  for (int off = QW; off < 64; off <<= 1) {
     f32x4 o2;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o2[e] = __shfl_xor(O[e], off, 64);
     fold(__shfl_xor(M, off, 64), __shfl_xor(L, off, 64), o2);
   }
-  __shared__ float sm_m[4][4], sm_l[4][4];
-  __shared__ f32x4 sm_o[4][4];
+  __shared__ float sm_m[QW][QW], sm_l[QW][QW];
+  __shared__ f32x4 sm_o[QW][QW];
   const int wave = tid >> 6;
-  if ((tid & 63) < 4) {
+  if ((tid & 63) < QW) {
     sm_m[wave][k] = M;
     sm_l[wave][k] = L;
     sm_o[wave][k] = O;
   }
   __syncthreads();
-  if (tid < 4) {
+  if (tid < QW) {
 #pragma unroll
-    for (int w = 1; w < 4; ++w) fold(sm_m[w][k], sm_l[w][k], sm_o[w][k]);
+    for (int w = 1; w < QW; ++w) fold(sm_m[w][k], sm_l[w][k], sm_o[w][k]);
     const f32x4 r = O / L;  // out may be only 4-byte aligned
     float* op = out + (size_t)h * kD + d;
     op[0] = r[0];
@@ -1075,13 +1081,13 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
                          hipStream_t s) {
   const dim3 grid((unsigned)(n_q * (kD / kMergeBlock)));
   if (n_splits <= kMergeLanes)
-    hipLaunchKernelGGL(decode_merge_kernel<1>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+    hipLaunchKernelGGL(decode_merge_kernel<1>, grid, dim3(kMergeThreads), 0, s, part, n_splits, part_stride_of(G), G, group,
                        n_hg, out);
   else if (n_splits <= 2 * kMergeLanes)
-    hipLaunchKernelGGL(decode_merge_kernel<2>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+    hipLaunchKernelGGL(decode_merge_kernel<2>, grid, dim3(kMergeThreads), 0, s, part, n_splits, part_stride_of(G), G, group,
                        n_hg, out);
   else
-    hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(256), 0, s, part, n_splits, part_stride_of(G), G, group,
+    hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(kMergeThreads), 0, s, part, n_splits, part_stride_of(G), G, group,
                        n_hg, out);
 }
 
