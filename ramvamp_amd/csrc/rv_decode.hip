@@ -1092,24 +1092,30 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 }
 
 // Launch shape of the MFMA tile kernel. Default, from sweeps on MI355X:
-// 4-wave workgroups, with the split long enough for about kTileWaves waves
-// in all (two per SIMD, all resident at once), each wave taking its share
-// of the split's 16-position tiles one at a time (ring depth 1: the next
-// tile's loads issue once the current one is computed). With two or four
-// of a wave's tiles in flight instead (the previous default wherever a
-// wave had several tiles: from 16384 positions on) the call measured 0-6 %
-// slower (config 5, f16 at 32768: 19.6 vs 18.6 µs; fp32 at 16384: 19.1 vs
-// 17.9 µs): the SIMD's other resident wave covers a wave's load latency.
-// A pinned split that leaves fewer waves than that keeps a slot per tile
-// (32 splits per kv head at 32768: 23.0 vs 25.3 µs). The splits of a kv head
+// 4-wave workgroups; splits of one 64-position step (one 16-position tile
+// per wave) while that keeps at most one workgroup per CU (4 kv heads: up
+// to 4096 positions), then an even share of the positions in 16-position
+// steps on one workgroup per CU up to 128 positions each, then on two (so
+// about kTileWaves waves, two per SIMD, all resident at once: 128 splits
+// of 256 positions per kv head at 32768). Between those points this runs
+// 7-14 % faster than whole 64-position steps (fp32: 4097 positions 9.7 vs
+// 11.1 µs, 6000 10.4 vs 12.0, 8192 12.0 vs 13.0; f16: 20000 14.6 vs
+// 15.0), which leave a few CUs running two workgroups. Each wave takes its
+// share of the split's tiles one at a time (ring depth 1: the next tile's
+// loads issue once the current one is computed): two or four of a wave's
+// tiles in flight measured 0-6 % slower (config 5, f16 at 32768: 19.6 vs
+// 18.6 µs; fp32 at 16384: 19.1 vs 17.9 µs), since the SIMD's other
+// resident wave covers a wave's load latency. A pinned split that leaves
+// fewer waves keeps a slot per tile. The splits of a kv head
 // are folded by decode_merge_kernel; the in-launch ticket merge (fused) is a
 // tuning option: its hand-off (device-scope stores acknowledged, a
 // memory-side atomic, loads that miss L2) costs more than the second launch.
 // With fused, groups of up to kFanOne splits fold in one level, more in
-// groups of about sqrt(n_splits). Every field but split_len derives from
-// split_len and positions alone, so a kv-head range takes the same reduction
-// tree as the whole call.
+// groups of about sqrt(n_splits). The split length is sized for the
+// cache's kv heads and every other field derives from it and positions, so
+// a kv-head range takes the same reduction tree as the whole call.
 constexpr int kTileWaves = 2048;
+constexpr long kCUs = 256;  // MI355X compute units
 constexpr int kFanOne = 16;
 struct TilePlan {
   int waves, depth, split_len, n_splits, fan, n_grp;
@@ -1117,31 +1123,45 @@ struct TilePlan {
   bool lds;  // RV_TUNE_DECODE_IMPL 3: tiles staged through LDS (4 waves, depth 1)
 };
 
-// Ring depth: one tile at a time when the whole cache's grid (every kv head,
-// so a kv-head range picks the same depth) holds about kTileWaves waves;
-// with fewer waves (a pinned long split), a slot per tile of the wave's
-// share up to the ring's limit, since no other wave covers the loads.
+// Ring depth: one tile at a time for the default plan, or when the whole
+// cache's grid (every kv head, so a kv-head range picks the same depth)
+// holds about kTileWaves waves; for a pinned long split with fewer waves, a
+// slot per tile of the wave's share up to the ring's limit, since no other
+// wave covers the loads.
 static int tile_depth(const rv_kv* kv, int waves, int split_len, int n_splits) {
   const int tpw = (split_len / 16 + waves - 1) / waves;  // tiles per wave
   const long grid_waves = (long)n_splits * (long)kv->n_kv_heads * waves;
-  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : grid_waves >= kTileWaves ? 1 : tpw;
+  const bool one = kv->tune_decode_split_len <= 0 || grid_waves >= kTileWaves;  // the default plan, or a full grid
+  int d = kv->tune_decode_depth > 0 ? (int)kv->tune_decode_depth : one ? 1 : tpw;
   const int dmax = kv->elem == RV_ELEM_F32 ? 2 : 4;  // register ring: 64 (f32) or 32 (f16) VGPRs per tile
   d = std::min(d, dmax);
   return d >= 4 ? 4 : d >= 2 ? 2 : 1;
 }
 
-static TilePlan plan_tile(const rv_kv* kv, long positions, int n_heads) {
+static TilePlan plan_tile(const rv_kv* kv, long positions) {
   TilePlan p;
   p.waves = kv->tune_decode_waves == 8 ? 8 : 4;
   const int step = p.waves * 16;
   long len = kv->tune_decode_split_len;
-  if (len <= 0) {
-    const long tiles = (positions + 15) / 16 * n_heads;
-    const long tpw = (tiles + kTileWaves - 1) / kTileWaves;  // tiles per wave for ~kTileWaves waves
-    len = tpw * step;
+  bool fine = false;  // a default length in 16-position steps
+  if (len <= 0 && positions * (long)kv->n_kv_heads > (long)kCUs * step) {
+    // Past one step per workgroup on one workgroup per CU, whole steps would
+    // leave a few CUs running two workgroups (4097 positions: 65 splits x 4
+    // kv heads = 260 workgroups, 11.2 vs 8.9 us per call at 4096). The
+    // split instead takes an even share of the positions in 16-position
+    // steps: one workgroup per CU up to 128 positions each, then two (the
+    // longer splits' waves run two or more tiles each). Sized for the whole
+    // cache's kv heads, so a kv-head range takes the whole call's splits.
+    const long share = positions * (long)kv->n_kv_heads;
+    long per = (share + kCUs - 1) / kCUs;
+    if (per > 2 * step) per = (share + 2 * kCUs - 1) / (2 * kCUs);
+    len = std::max<long>((per + 15) / 16 * 16, step);
+    fine = true;
+  } else if (len <= 0) {
+    len = step;  // one step per workgroup, at most one workgroup per CU
   }
   len = std::max<long>(len, step);
-  p.split_len = (int)((len + step - 1) / step * step);
+  p.split_len = fine ? (int)len : (int)((len + step - 1) / step * step);
   p.n_splits = (int)((positions + p.split_len - 1) / p.split_len);
   p.depth = tile_depth(kv, p.waves, p.split_len, p.n_splits);
   p.lds = kv->tune_decode_impl == 3 && p.waves == 4;
@@ -1276,7 +1296,7 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
                             float scale, const DecodePro& pro, float* out, hipStream_t s) {
   const int n_heads = (int)kv->n_kv_heads;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
-  const TilePlan p = plan_tile(kv, (long)positions, n_heads);
+  const TilePlan p = plan_tile(kv, (long)positions);
   MergeArgs mg;
   HipStatus st = tile_merge_args(kv, p, n_heads, group, nullptr, &mg);
   if (st.e != hipSuccess) return st;
@@ -1300,7 +1320,7 @@ size_t decode_ws_need(const rv_kv* kv, size_t n_q_heads, size_t positions, size_
   if (n_heads == 0) return 0;
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1)
-    return tile_ws_floats(plan_tile(kv, (long)positions, (int)n_heads), (int)n_heads, group) * sizeof(float);
+    return tile_ws_floats(plan_tile(kv, (long)positions), (int)n_heads, group) * sizeof(float);
   if (kv->head_dim == kD) {
     const DecodeShape d = pick_shape(kv, (int)positions, (int)n_heads, group);
     const size_t n_splits = (positions + d.split_len - 1) / d.split_len;
@@ -1326,7 +1346,7 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   const void* vl = kv->v_layer(layer);
   const float qscale = scale * kLog2e;
   if (kv->head_dim == kD && group <= 16 && kv->tune_decode_impl != 1) {
-    const TilePlan p = plan_tile(kv, (long)positions, n_heads);
+    const TilePlan p = plan_tile(kv, (long)positions);
     MergeArgs mg;
     st = tile_merge_args(kv, p, n_heads, group, ws, &mg);
     if (st.e != hipSuccess) return st;

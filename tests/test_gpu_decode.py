@@ -218,6 +218,31 @@ def test_kv_range_union_is_bit_identical_to_the_whole_call():
         assert np.array_equal(got.view(np.uint32), whole.view(np.uint32)), units
 
 
+@pytest.mark.parametrize("n_pos", [5000, 20000])
+def test_kv_range_union_matches_the_whole_call_with_the_default_plan(n_pos):
+    # The default split length is sized for the cache's kv heads, not the
+    # range's, so each head's reduction tree is the whole call's at any
+    # length (here past one workgroup per CU, where it grows in 16-position
+    # steps).
+    torch_cuda()
+    say(f"case kv range union, default plan, n_pos={n_pos}")
+    rng = Rng(0x7A17 + n_pos)
+    kv, ref = twin_caches(rng, 1, 4, 128, n_pos, "f16")
+    q = rng.vec_in(32 * 128, -1.0, 1.0)
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    whole = np.zeros(q.size, np.float32)
+    rv.decode_attention(q, kv, 0, scale, None, whole)
+    gate(whole, ref.attention(q, 0, scale), what="whole")
+    for units in (1, 2, 4):
+        got = np.full(q.size, np.nan, np.float32)
+        for u in range(units):
+            r = oracle.kv_head_range(4, units, u, u + 1)
+            part = np.full(len(r) * 1024, np.nan, np.float32)
+            rv.decode_attention_kv_range_in(q, kv, 0, scale, r, 10 ** 6, part)
+            got[r.start * 1024:r.stop * 1024] = part
+        assert np.array_equal(got.view(np.uint32), whole.view(np.uint32)), units
+
+
 @pytest.mark.parametrize("split_len", [16, 32, 48, 64, 128, 1024, 0])
 def test_split_lengths_agree_within_tolerance(split_len):
     torch_cuda()
