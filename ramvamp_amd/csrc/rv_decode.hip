@@ -1095,12 +1095,13 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 // 4-wave workgroups; splits of one 64-position step (one 16-position tile
 // per wave) while that keeps at most one workgroup per CU (4 kv heads: up
 // to 4096 positions), then an even share of the positions in 16-position
-// steps on one workgroup per CU up to 128 positions each, then on two (so
+// steps on one workgroup per CU up to 448 positions each, then on two (so
 // about kTileWaves waves, two per SIMD, all resident at once: 128 splits
-// of 256 positions per kv head at 32768). Between those points this runs
-// 7-14 % faster than whole 64-position steps (fp32: 4097 positions 9.7 vs
-// 11.1 µs, 6000 10.4 vs 12.0, 8192 12.0 vs 13.0; f16: 20000 14.6 vs
-// 15.0), which leave a few CUs running two workgroups. Each wave takes its
+// of 256 positions per kv head at 32768). Between the powers of two this
+// runs 7-14 % faster than whole steps with two workgroups per CU past 128
+// positions (fp32: 4097 positions 9.7 vs 11.1 µs, 6000 10.4 vs 12.0,
+// 12000 14.6 vs 16.1; f16: 12000 11.2 vs 12.5, 20000 13.9 vs 15.0), which
+// leave a few CUs running two workgroups. Each wave takes its
 // share of the split's tiles one at a time (ring depth 1: the next tile's
 // loads issue once the current one is computed): two or four of a wave's
 // tiles in flight measured 0-6 % slower (config 5, f16 at 32768: 19.6 vs
@@ -1147,14 +1148,16 @@ static TilePlan plan_tile(const rv_kv* kv, long positions) {
   if (len <= 0 && positions * (long)kv->n_kv_heads > (long)kCUs * step) {
     // Past one step per workgroup on one workgroup per CU, whole steps would
     // leave a few CUs running two workgroups (4097 positions: 65 splits x 4
-    // kv heads = 260 workgroups, 11.2 vs 8.9 us per call at 4096). The
-    // split instead takes an even share of the positions in 16-position
-    // steps: one workgroup per CU up to 128 positions each, then two (the
-    // longer splits' waves run two or more tiles each). Sized for the whole
-    // cache's kv heads, so a kv-head range takes the whole call's splits.
+    // kv heads = 260 workgroups, 11.1 vs 9.7 us per call). The split instead
+    // takes an even share of the positions in 16-position steps: one
+    // workgroup per CU up to 7 steps (448 positions) each, then two (at
+    // 32768 positions that is 256 each, 18.4 vs 18.7 us for one workgroup
+    // of 512; at 28000 one workgroup of 448 takes 16.5 vs 17.2 us). Sized
+    // for the whole cache's kv heads, so a kv-head range takes the whole
+    // call's splits.
     const long share = positions * (long)kv->n_kv_heads;
     long per = (share + kCUs - 1) / kCUs;
-    if (per > 2 * step) per = (share + 2 * kCUs - 1) / (2 * kCUs);
+    if (per > 7 * step) per = (share + 2 * kCUs - 1) / (2 * kCUs);
     len = std::max<long>((per + 15) / 16 * 16, step);
     fine = true;
   } else if (len <= 0) {
