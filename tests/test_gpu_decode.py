@@ -218,6 +218,22 @@ def test_kv_range_union_is_bit_identical_to_the_whole_call():
         assert np.array_equal(got.view(np.uint32), whole.view(np.uint32)), units
 
 
+def test_decode_across_the_split_plan_regimes():
+    # The default plan changes shape at these lengths (4 kv heads): whole
+    # 64-position splits up to 4096, then even 16-position shares on one
+    # workgroup per CU up to 448 positions each (28672), then on two.
+    torch_cuda()
+    rng = Rng(0x5A1F)
+    kv, ref = twin_caches(rng, 1, 4, 128, 28673, "f16")
+    q = rng.vec_in(32 * 128, -1.0, 1.0)
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    for p in (4096, 4097, 8192, 8193, 28672, 28673):
+        say(f"case split plan regime positions={p}")
+        out = np.full(q.size, np.nan, np.float32)
+        rv.attention_at(q, kv, 0, p, scale, None, out)
+        gate(out, ref.attention(q, 0, scale, positions=p), what=f"positions {p}")
+
+
 @pytest.mark.parametrize("n_pos", [5000, 20000])
 def test_kv_range_union_matches_the_whole_call_with_the_default_plan(n_pos):
     # The default split length is sized for the cache's kv heads, not the
