@@ -1116,7 +1116,6 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 // cache's kv heads and every other field derives from it and positions, so
 // a kv-head range takes the same reduction tree as the whole call.
 constexpr int kTileWaves = 2048;
-constexpr long kCUs = 256;  // MI355X compute units
 constexpr int kFanOne = 16;
 struct TilePlan {
   int waves, depth, split_len, n_splits, fan, n_grp;

@@ -96,6 +96,8 @@ struct HipStatus {
 
 // Level-1 merge groups per kv head the decode tickets provide for.
 constexpr int kMaxMergeGroups = 64;
+// Compute units of the MI355X, which the launch plans balance work over.
+constexpr long kCUs = 256;
 
 // Workspace of at least `bytes` on the cache's device. When it must grow it
 // is allocated at max(bytes, bound) (callers pass the most any call of the

@@ -1394,20 +1394,49 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const int planes = planes_of(m);
   const size_t positions = start + rows;
   const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);  // tiles this call reads
-  // 128 query vectors per workgroup (16 rows of a group of 8), or 64 when
-  // 128-vector blocks would leave CUs idle (fewer than 256 workgroups) or the
-  // tuning asks for it. The split mode keeps 128 when the range is long
+  // 128 query vectors per workgroup (16 rows of a group of 8) or 64: the
+  // tuning's choice, else the cost model below for F16/BF16, else 64 when
+  // 128-vector blocks would leave CUs idle (fewer than 256 workgroups). The
+  // split mode keeps 128 when the range is long
   // enough for a KV split to fill the chip (at least 16 tiles): its
   // one-group kernel gains more from 32 columns per wave than the split and
   // its merge cost (config 4: 123 vs 134 us).
   int vectors = 128;
-  if (kv->tune_prefill_rows > 0)
+  int kv_splits = (int)kv->tune_prefill_kv_split;
+  if (kv->tune_prefill_rows > 0) {
     vectors = kv->tune_prefill_rows * group <= 64 ? 64 : 128;
-  else if ((long)((rows * group + 127) / 128) * n_kv < 256 && !(planes == 2 && n_stage_tiles >= 16))
+  } else if (planes == 1 && kv_splits <= 0 && group <= 64) {
+    // F16/BF16: the shape with the least modelled time. A workgroup holds a
+    // CU (its LDS), so workgroups past kCUs run as further rounds; a round
+    // costs ~9 us of fixed work plus the longest block's tiles at 0.68 us
+    // (64 vectors) or 0.98 us (128) each, and a KV split adds its merge
+    // (~8 us). Fitted to configs 3 and 4 (14.4 and 51.2 us kernels) and to
+    // 128-vector blocks without a split (69.6 us at config 4); 128-vector
+    // blocks with a split measured slower than the model and are not
+    // offered. Whole 512-row chunks keep 64 vectors and no split; other
+    // sizes avoid a last round of a few workgroups (520 rows: 260
+    // workgroups of 64 vectors, 98 vs 58 us at 512) and splits the chip
+    // does not need (448 rows: 224 workgroups).
+    double best = 1e30;
+    for (int v : {64, 128}) {
+      const long rb = (long)((rows + v / group - 1) / (v / group));
+      for (int sp = 1; sp <= (v == 64 ? kMaxKvSplits : 1); ++sp) {
+        const long wgs = rb * n_kv * sp;
+        if (sp > 1 && (wgs > 2 * kCUs || n_stage_tiles / sp < 8)) break;
+        const double round_us = 9.0 + (double)((n_stage_tiles + sp - 1) / sp) * (v == 64 ? 0.68 : 0.98);
+        const double cost = (double)((wgs + kCUs - 1) / kCUs) * round_us + (sp > 1 ? 8.0 : 0.0);
+        if (cost < best) {
+          best = cost;
+          vectors = v;
+          kv_splits = sp;
+        }
+      }
+    }
+  } else if ((long)((rows * group + 127) / 128) * n_kv < 256 && !(planes == 2 && n_stage_tiles >= 16)) {
     vectors = 64;
+  }
   const int qr = vectors / group;
   const int n_rb = (int)((rows + qr - 1) / qr);
-  int kv_splits = (int)kv->tune_prefill_kv_split;
   if (kv_splits <= 0) {
     // Split the KV axis until about 256 workgroups are in flight, keeping at
     // least 8 K/V tiles per split of the longest block.

@@ -64,6 +64,26 @@ def test_rows_match_per_row_attention_at(mode, elem, impl):
         say(f"  max rel err {e:.3e}")
 
 
+@pytest.mark.parametrize("mode", ["f16", "bf16"])
+def test_ragged_chunk_shapes_match_the_oracle(mode):
+    # Chunk sizes the F16/BF16 launch plan maps to other shapes than 512
+    # rows: 224 workgroups without a KV split (448 rows), 128-vector blocks
+    # where 64-vector ones would spill past one workgroup per CU (520, 768).
+    torch_cuda()
+    rng = Rng(0x4A66ED)
+    for start, rows in [(700, 448), (700, 520), (200, 768)]:
+        say(f"case ragged chunk start={start} rows={rows} mode={mode}")
+        kv, ref = twin(rng, 4, 128, start + rows, start + rows, "f32")
+        q = rng.vec_in(rows * 32 * 128, -2.0, 2.0).reshape(rows, -1)
+        scale = np.float32(1.0) / np.sqrt(np.float32(128))
+        out = dev(np.zeros(q.shape))
+        rv.attention_at_rows(dev(q), kv, 0, start, scale, out, mode=mode)
+        want = ref.scatter_attention(q, 0, start, scale, THREADS)
+        e = gate(host(out), want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode],
+                 what=f"ragged chunk {(start, rows)} {mode}")
+        say(f"  max rel err {e:.3e}")
+
+
 @pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
 def test_config3_prefill_chunk_matches_the_oracle(mode):
     torch_cuda()
