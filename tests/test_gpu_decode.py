@@ -234,6 +234,24 @@ def test_decode_across_the_split_plan_regimes():
         gate(out, ref.attention(q, 0, scale, positions=p), what=f"positions {p}")
 
 
+@pytest.mark.parametrize("elem,lengths", [("f16", (64, 65, 200, 256, 257)), ("f32", (64, 65, 128, 129))])
+def test_decode_short_contexts_in_one_split(elem, lengths):
+    # Up to 128 KiB of K and V per kv head (f16: 256 positions, fp32: 128)
+    # the default plan takes one split per kv head with no merge launch,
+    # each wave walking several tiles; one position more goes back to
+    # 64-position splits and the merge.
+    torch_cuda()
+    rng = Rng(0x5B07 + len(elem))
+    kv, ref = twin_caches(rng, 1, 4, 128, max(lengths), elem)
+    q = rng.vec_in(32 * 128, -1.0, 1.0)
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    for p in lengths:
+        say(f"case short context {elem} positions={p}")
+        out = np.full(q.size, np.nan, np.float32)
+        rv.attention_at(q, kv, 0, p, scale, None, out)
+        gate(out, ref.attention(q, 0, scale, positions=p), what=f"{elem} positions {p}")
+
+
 @pytest.mark.parametrize("n_pos", [5000, 20000])
 def test_kv_range_union_matches_the_whole_call_with_the_default_plan(n_pos):
     # The default split length is sized for the cache's kv heads, not the
