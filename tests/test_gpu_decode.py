@@ -252,6 +252,33 @@ def test_decode_short_contexts_in_one_split(elem, lengths):
         gate(out, ref.attention(q, 0, scale, positions=p), what=f"{elem} positions {p}")
 
 
+@pytest.mark.parametrize("elem,n_pos,fan", [("f16", 300, 0), ("f32", 4096, 0), ("f16", 4096, 64), ("f16", 20000, 0)])
+def test_in_launch_ticket_merge_matches_the_oracle(elem, n_pos, fan):
+    # RV_TUNE_DECODE_MERGE 1: the last workgroup of each group of splits folds
+    # the group inside the tile launch, and with more than one group the last
+    # group folds their rows (300: 5 splits in one group; 4096: 64 splits in
+    # 8 groups of 8, or one group with fan 64; 20000: 63 splits of 320).
+    # Three calls in a row: the last arriver resets each ticket, so every
+    # call folds in the same order and gives the same bits.
+    torch_cuda()
+    say(f"case ticket merge elem={elem} n_pos={n_pos} fan={fan}")
+    rng = Rng(0x71C7 + n_pos + fan)
+    kv, ref = twin_caches(rng, 1, 4, 128, n_pos, elem)
+    kv.set_tuning(rv.RV_TUNE_DECODE_MERGE, 1)
+    if fan:
+        kv.set_tuning(rv.RV_TUNE_DECODE_FAN, fan)
+    q = rng.vec_in(32 * 128, -1.0, 1.0)
+    scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    outs = []
+    for _ in range(3):
+        out = np.full(q.size, np.nan, np.float32)
+        rv.decode_attention(q, kv, 0, scale, None, out)
+        outs.append(out)
+    gate(outs[0], ref.attention(q, 0, scale), what=f"ticket merge {elem} {n_pos} fan {fan}")
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
 @pytest.mark.parametrize("n_pos", [5000, 20000])
 def test_kv_range_union_matches_the_whole_call_with_the_default_plan(n_pos):
     # The default split length is sized for the cache's kv heads, not the
