@@ -342,6 +342,25 @@ def test_kernel_variants_agree_with_the_oracle(impl, waves, elem):
             gate(out, ref.attention(q, 0, 0.3, positions=p), what=f"impl {impl} waves {waves} split {split_len} p {p}")
 
 
+@pytest.mark.parametrize("hg", [1, 2, 4, 8])
+def test_valu_head_groups_agree_with_the_oracle(hg):
+    """RV_TUNE_DECODE_HG: the VALU kernel's query heads per workgroup (the
+    largest of 8/4/2/1 dividing the group, up to the tuned count), for a
+    group of 8 and a group of 20, which only the VALU kernel takes."""
+    torch_cuda()
+    for n_q in (32, 80):
+        say(f"case VALU head groups hg={hg} n_q={n_q}")
+        rng = Rng(0x46A0 + 8 * hg + n_q)
+        kv, ref = twin_caches(rng, 1, 4, 128, 700, "f32")
+        kv.set_tuning(6, 1)
+        kv.set_tuning(5, hg)
+        q = rng.vec_in(n_q * 128, -2.0, 2.0)
+        for p in (1, 64, 700):
+            out = np.zeros(q.size, np.float32)
+            rv.attention_at(q, kv, 0, p, 0.3, None, out)
+            gate(out, ref.attention(q, 0, 0.3, positions=p), what=f"hg {hg} n_q {n_q} p {p}")
+
+
 @pytest.mark.parametrize("elem", ["f32", "f16"])
 def test_ring_depths_are_bit_identical(elem):
     """The tile kernel's register ring (RV_TUNE_DECODE_DEPTH 2 and 4; the
