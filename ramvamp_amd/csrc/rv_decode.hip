@@ -1159,12 +1159,15 @@ static TilePlan plan_tile(const rv_kv* kv, long positions) {
     if (per > 7 * step) per = (share + 2 * kCUs - 1) / (2 * kCUs);
     len = std::max<long>((per + 15) / 16 * 16, step);
     fine = true;
-  } else if (len <= 0 && positions * 2 * (long)kv->head_dim * (kv->elem == RV_ELEM_F32 ? 4 : 2) <= (128L << 10)) {
-    // Up to 128 KiB of K and V per kv head: one split per kv head, its waves
-    // taking the tiles one at a time, and no merge launch (graph-replayed
-    // calls: f16 128 positions 4.1 vs 6.1 us, 256 5.2 vs 6.2; fp32 128 6.0
-    // vs 7.3; one split is slower from 256 KiB: f16 512 7.3 vs 6.2, fp32
-    // 256 8.3 vs 7.3).
+  } else if (len <= 0 && positions <= 3L * step &&
+             positions * 2 * (long)kv->head_dim * (kv->elem == RV_ELEM_F32 ? 4 : 2) <= (128L << 10)) {
+    // At most 3 tiles per wave and 128 KiB of K and V per kv head: one split
+    // per kv head, its waves taking the tiles one at a time, and no merge
+    // launch. Graph-replayed calls, one layer (cache-resident) / 48 layers,
+    // against 64-position splits: f16 128 positions 4.1 / 4.2 vs 6.1 / 6.2
+    // us, 192 4.6 / 5.6 vs 6.2 / 6.3; fp32 128 6.0 / 6.9 vs 7.3 / 7.5. Each
+    // further tile per wave is another memory round trip: f16 256 (4 per
+    // wave) 5.2 / 6.9 vs 6.2 / 6.3, fp32 256 8.3 vs 7.3.
     len = positions;
   } else if (len <= 0) {
     len = step;  // one step per workgroup, at most one workgroup per CU

@@ -234,12 +234,12 @@ def test_decode_across_the_split_plan_regimes():
         gate(out, ref.attention(q, 0, scale, positions=p), what=f"positions {p}")
 
 
-@pytest.mark.parametrize("elem,lengths", [("f16", (64, 65, 200, 256, 257)), ("f32", (64, 65, 128, 129))])
+@pytest.mark.parametrize("elem,lengths", [("f16", (64, 65, 150, 192, 193)), ("f32", (64, 65, 128, 129))])
 def test_decode_short_contexts_in_one_split(elem, lengths):
-    # Up to 128 KiB of K and V per kv head (f16: 256 positions, fp32: 128)
-    # the default plan takes one split per kv head with no merge launch,
-    # each wave walking several tiles; one position more goes back to
-    # 64-position splits and the merge.
+    # Up to 3 tiles per wave and 128 KiB of K and V per kv head (f16: 192
+    # positions, fp32: 128) the default plan takes one split per kv head
+    # with no merge launch, each wave walking several tiles; one position
+    # more goes back to 64-position splits and the merge.
     torch_cuda()
     rng = Rng(0x5B07 + len(elem))
     kv, ref = twin_caches(rng, 1, 4, 128, max(lengths), elem)

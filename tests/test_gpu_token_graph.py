@@ -44,11 +44,11 @@ def _bits(a):
 
 
 @pytest.mark.parametrize("elem,n_pos,cap", [("f32", 1000, 1200), ("f16", 1000, 1200), ("f32", 5, 8192),
-                                           ("f16", 100, 250)])
+                                           ("f16", 100, 180)])
 def test_decode_step_graph_replays_follow_the_eager_steps(elem, n_pos, cap):
     # (f32, 5, 8192): the launch is planned for 8192 positions while the
     # layers hold 5..10: almost every split is empty and must contribute
-    # nothing to the merge. (f16, 100, 250): planned for 249 positions, one
+    # nothing to the merge. (f16, 100, 180): planned for 179 positions, one
     # split per kv head and no merge, the layers holding 100..106.
     torch = torch_cuda()
     say(f"case token graph decode_step_dev elem={elem} n_pos={n_pos} cap={cap}")
