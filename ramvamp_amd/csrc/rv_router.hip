@@ -65,16 +65,30 @@ __device__ __forceinline__ void chunk_sum(float (&acc)[R], const f32x4 (&w)[kChu
   }
 }
 
+// The staged form (one row per workgroup, at most 128 experts, hidden a
+// multiple of 64, 16-byte aligned weights): the weight rows reach the sums
+// through LDS in 64-value chunks. Each thread loads 8 of a chunk's 2048
+// 16-byte quads (a wave: 4 experts' 16 consecutive quads each), three
+// chunks ahead, and stores them into a 2-deep ring (rows padded to 68
+// floats); lane e of waves 0 and 1 then sums expert e's chunk from LDS, so
+// no wave's load touches 64 scattered rows.
+constexpr int kStagedChunk = 64;
+constexpr int kStagedRow = kStagedChunk + 4;  // floats per staged expert row
+constexpr int kStagedExperts = 128;
+constexpr size_t kStagedBytes = 2 * kStagedExperts * kStagedRow * sizeof(float);
+
 // R rows per workgroup (blockIdx.x * R ..), each with its LDS region of
 // router_lds_floats(hidden, n_experts) floats; every weight chunk a thread
-// loads feeds all R rows' sums.
-template <int R>
+// loads feeds all R rows' sums. STAGED (R = 1): the staged form above.
+template <int R, bool STAGED>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __restrict__ x, int n_rows, int hidden,
                                                                 const float* __restrict__ router, int n_experts,
                                                                 int top_k, int norm, uint32_t* __restrict__ experts,
                                                                 float* __restrict__ weights) {
 #pragma clang fp contract(off)
+  static_assert(!STAGED || R == 1, "the staged form takes one row");
   extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ __attribute__((aligned(16))) float wl[STAGED ? 2 * kStagedExperts * kStagedRow : 4];
   const int rs = (int)router_lds_floats(hidden, n_experts);  // floats per row region (a multiple of 4)
   const int row0 = (int)blockIdx.x * R, nr = min(R, n_rows - row0);
   auto xs_of = [&](int r) { return smem + (size_t)r * rs; };                 // [hidden]
@@ -88,6 +102,87 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __r
     for (int i = tid; i < hidden; i += kRouterThreads) xs_of(r)[i] = xr[i];
   }
   __syncthreads();
+  if constexpr (STAGED) {
+    const int nc = hidden / kStagedChunk;
+    // Chunk c's quads of this thread (clamped to the last chunk, so every
+    // prefetch is issued and the wait before a stash counts only newer
+    // loads; experts past the last repeat it).
+    auto fetch = [&](int c, f32x4 (&dst)[8]) {
+      c = min(c, nc - 1);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int f = k * kRouterThreads + tid, e = min(f >> 4, n_experts - 1);
+        dst[k] = *reinterpret_cast<const f32x4*>(router + (size_t)e * hidden + c * kStagedChunk + 4 * (f & 15));
+      }
+    };
+    auto stash = [&](const f32x4 (&src)[8], int buf) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int f = k * kRouterThreads + tid;
+        *reinterpret_cast<f32x4*>(&wl[(buf * kStagedExperts + (f >> 4)) * kStagedRow + 4 * (f & 15)]) = src[k];
+      }
+    };
+    // Lanes 0..127: chunk c's rounded products, then the serial additions.
+    float acc = 0.f;
+    auto sum_chunk = [&](int c, int buf) {
+      if (tid >= kStagedExperts) return;  // waves 2 and 3 only stage
+      const float* wr = &wl[(buf * kStagedExperts + tid) * kStagedRow];
+      const float* xr = smem + c * kStagedChunk;
+      float p[kStagedChunk];
+#pragma unroll
+      for (int q = 0; q < kStagedChunk / 4; ++q) {
+        const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr + 4 * q), x4 = *reinterpret_cast<const f32x4*>(xr + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[4 * q + j] = w4[j] * x4[j];
+      }
+#pragma unroll
+      for (int k = 0; k < kStagedChunk; ++k) acc += p[k];
+    };
+    // Chunk j sits in ring slot j & 1 once staged; while the sums read chunk
+    // c, chunk c + 1 is stashed into the other slot (read last in iteration
+    // c - 1, before its barrier) and chunk c + 4 fetched into the registers
+    // it leaves.
+    f32x4 r0[8], r1[8], r2[8], r3[8];
+    fetch(0, r0);
+    fetch(1, r1);
+    fetch(2, r2);
+    fetch(3, r3);
+    stash(r0, 0);
+    fetch(4, r0);
+    __syncthreads();
+    int c = 0;
+    for (; c + 4 <= nc; c += 4) {
+      sum_chunk(c, 0);
+      stash(r1, 1);
+      fetch(c + 5, r1);
+      __syncthreads();
+      sum_chunk(c + 1, 1);
+      stash(r2, 0);
+      fetch(c + 6, r2);
+      __syncthreads();
+      sum_chunk(c + 2, 0);
+      stash(r3, 1);
+      fetch(c + 7, r3);
+      __syncthreads();
+      sum_chunk(c + 3, 1);
+      stash(r0, 0);
+      fetch(c + 8, r0);
+      __syncthreads();
+    }
+    // Up to three chunks left: c in slot 0, c + 1 and c + 2 in r1 and r2.
+    if (c < nc) {
+      sum_chunk(c, 0);
+      stash(r1, 1);
+      __syncthreads();
+    }
+    if (c + 1 < nc) {
+      sum_chunk(c + 1, 1);
+      stash(r2, 0);
+      __syncthreads();
+    }
+    if (c + 2 < nc) sum_chunk(c + 2, 0);
+    if (tid < n_experts) smem[hidden + tid] = acc;  // prob_of(0)
+  } else {
   const bool vec = hidden % 4 == 0 && ((uintptr_t)router & 15) == 0;
   const int nc = vec ? hidden / kChunk : 0;  // whole chunks; the rest one value at a time
   for (int g0 = 0; g0 < n_experts; g0 += kRouterThreads) {
@@ -157,6 +252,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __r
 #pragma unroll
       for (int r = 0; r < R; ++r) prob_of(r)[g0 + tid] = acc[r];
     }
+  }
   }
   __syncthreads();
   if (tid < nr) {  // thread r: row r's maximum
@@ -259,18 +355,25 @@ extern "C" int32_t rv_router_topk(const float* x, size_t n_rows, size_t hidden, 
     int R = 1;
     while (R < 4 && n_rows >= (size_t)(2 * R) * 256 && (size_t)(2 * R) * row_bytes <= lds_cap) R *= 2;
     const unsigned grid = (unsigned)((n_rows + R - 1) / R);
-#define RV_ROUTER(RR)                                                                                             \
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&rv::router_kernel<RR>),                               \
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_cap);                           \
-  hipLaunchKernelGGL(rv::router_kernel<RR>, dim3(grid), dim3(rv::kRouterThreads), (unsigned)(RR * row_bytes), s, x,  \
-                     (int)n_rows, (int)hidden, router, (int)n_experts, (int)top_k, norm_topk_prob ? 1 : 0, experts,  \
-                     weights)
+    // One row per workgroup with at most 128 experts: the staged form when
+    // the chunks divide the row and the ring fits beside the row's region.
+    const bool staged = R == 1 && n_experts <= (size_t)rv::kStagedExperts && hidden % rv::kStagedChunk == 0 &&
+                        ((uintptr_t)router & 15) == 0 && row_bytes + rv::kStagedBytes <= lds_cap;
+#define RV_ROUTER(RR, ST)                                                                                         \
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&rv::router_kernel<RR, ST>),                           \
+                            hipFuncAttributeMaxDynamicSharedMemorySize,                                          \
+                            (int)(ST ? lds_cap - rv::kStagedBytes : lds_cap));                                   \
+  hipLaunchKernelGGL((rv::router_kernel<RR, ST>), dim3(grid), dim3(rv::kRouterThreads), (unsigned)(RR * row_bytes), \
+                     s, x, (int)n_rows, (int)hidden, router, (int)n_experts, (int)top_k, norm_topk_prob ? 1 : 0,    \
+                     experts, weights)
     if (R == 4) {
-      RV_ROUTER(4);
+      RV_ROUTER(4, false);
     } else if (R == 2) {
-      RV_ROUTER(2);
+      RV_ROUTER(2, false);
+    } else if (staged) {
+      RV_ROUTER(1, true);
     } else {
-      RV_ROUTER(1);
+      RV_ROUTER(1, false);
     }
 #undef RV_ROUTER
     const hipError_t e = hipGetLastError();

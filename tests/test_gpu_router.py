@@ -28,7 +28,9 @@ def check(torch, x, router, top_k, norm):
 
 @pytest.mark.parametrize("n_rows,hidden,n_experts,top_k", [(1, 2048, 128, 8), (7, 2048, 128, 8), (64, 2048, 128, 8),
                                                            (3, 33, 5, 5), (2, 4096, 257, 3), (513, 2048, 128, 8),
-                                                           (1027, 2048, 128, 8), (1030, 100, 300, 4)])
+                                                           (1027, 2048, 128, 8), (1030, 100, 300, 4),
+                                                           (2, 64, 60, 4), (3, 192, 128, 2), (1, 320, 100, 6),
+                                                           (1, 4096, 128, 8)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_router_is_bit_identical_to_the_oracle(n_rows, hidden, n_experts, top_k, norm):
     torch = torch_cuda()
