@@ -4,9 +4,11 @@
 // One workgroup per row. Thread e computes expert e's logit as dot_f32 does
 // (forward.rs:1231-1238): one serial f32 sum, each product rounded before it
 // is added (contraction off), in index order. The row is staged in LDS; each
-// thread streams its own expert's weight row with 16-byte loads, one
-// 32-value chunk ahead of the sum (rows 16-byte aligned; otherwise 4-byte
-// loads in the same order). The softmax (softmax.rs:18-40) takes the max over
+// thread streams its own expert's weight row with 16-byte loads, chunks
+// ahead of the sum (rows 16-byte aligned; otherwise 4-byte loads in the
+// same order), or, for one row and at most 128 experts, the workgroup stages
+// 64-value chunks of every row through LDS with coalesced loads (the staged
+// form below). The softmax (softmax.rs:18-40) takes the max over
 // the logits, each thread its exponential in f64, and one thread the f64 sum
 // in expert order (the reference's order) and the f32 reciprocal. The top-k
 // (strict >: the first index wins ties; the winner set to -inf) runs as a
