@@ -6,7 +6,7 @@
 // is added (contraction off), in index order. The row is staged in LDS; each
 // thread streams its own expert's weight row with 16-byte loads, chunks
 // ahead of the sum (rows 16-byte aligned; otherwise 4-byte loads in the
-// same order), or, for one row and at most 128 experts, the workgroup stages
+// same order), or, for 1 or 2 rows and at most 128 experts, the workgroup stages
 // 64-value chunks of every row through LDS with coalesced loads (the staged
 // form below). The softmax (softmax.rs:18-40) takes the max over
 // the logits, each thread its exponential in f64, and one thread the f64 sum
@@ -67,13 +67,13 @@ __device__ __forceinline__ void chunk_sum(float (&acc)[R], const f32x4 (&w)[kChu
   }
 }
 
-// The staged form (one row per workgroup, at most 128 experts, hidden a
-// multiple of 64, 16-byte aligned weights): the weight rows reach the sums
+// The staged form (1 or 2 rows per workgroup, at most 128 experts, hidden
+// a multiple of 64, 16-byte aligned weights): the weight rows reach the sums
 // through LDS in 64-value chunks. Each thread loads 8 of a chunk's 2048
 // 16-byte quads (a wave: 4 experts' 16 consecutive quads each), three
 // chunks ahead, and stores them into a 2-deep ring (rows padded to 68
-// floats); lane e of waves 0 and 1 then sums expert e's chunk from LDS, so
-// no wave's load touches 64 scattered rows.
+// floats); lane e of waves 0 and 1 then sums expert e's chunk from LDS for
+// each row, so no wave's load touches 64 scattered rows.
 constexpr int kStagedChunk = 64;
 constexpr int kStagedRow = kStagedChunk + 4;  // floats per staged expert row
 constexpr int kStagedExperts = 128;
@@ -81,14 +81,13 @@ constexpr size_t kStagedBytes = 2 * kStagedExperts * kStagedRow * sizeof(float);
 
 // R rows per workgroup (blockIdx.x * R ..), each with its LDS region of
 // router_lds_floats(hidden, n_experts) floats; every weight chunk a thread
-// loads feeds all R rows' sums. STAGED (R = 1): the staged form above.
+// loads feeds all R rows' sums. STAGED: the staged form above.
 template <int R, bool STAGED>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __restrict__ x, int n_rows, int hidden,
                                                                 const float* __restrict__ router, int n_experts,
                                                                 int top_k, int norm, uint32_t* __restrict__ experts,
                                                                 float* __restrict__ weights) {
 #pragma clang fp contract(off)
-  static_assert(!STAGED || R == 1, "the staged form takes one row");
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ __attribute__((aligned(16))) float wl[STAGED ? 2 * kStagedExperts * kStagedRow : 4];
   const int rs = (int)router_lds_floats(hidden, n_experts);  // floats per row region (a multiple of 4)
@@ -124,21 +123,27 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __r
         *reinterpret_cast<f32x4*>(&wl[(buf * kStagedExperts + (f >> 4)) * kStagedRow + 4 * (f & 15)]) = src[k];
       }
     };
-    // Lanes 0..127: chunk c's rounded products, then the serial additions.
-    float acc = 0.f;
+    // Lanes 0..127, for each of the R rows: chunk c's rounded products, then
+    // the row's serial additions (the rows' chains are independent).
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
     auto sum_chunk = [&](int c, int buf) {
       if (tid >= kStagedExperts) return;  // waves 2 and 3 only stage
       const float* wr = &wl[(buf * kStagedExperts + tid) * kStagedRow];
-      const float* xr = smem + c * kStagedChunk;
-      float p[kStagedChunk];
 #pragma unroll
-      for (int q = 0; q < kStagedChunk / 4; ++q) {
-        const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr + 4 * q), x4 = *reinterpret_cast<const f32x4*>(xr + 4 * q);
+      for (int r = 0; r < R; ++r) {
+        const float* xr = xs_of(r) + c * kStagedChunk;
+        float p[kStagedChunk];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[4 * q + j] = w4[j] * x4[j];
+        for (int q = 0; q < kStagedChunk / 4; ++q) {
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(wr + 4 * q), x4 = *reinterpret_cast<const f32x4*>(xr + 4 * q);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[4 * q + j] = w4[j] * x4[j];
+        }
+#pragma unroll
+        for (int k = 0; k < kStagedChunk; ++k) acc[r] += p[k];
       }
-#pragma unroll
-      for (int k = 0; k < kStagedChunk; ++k) acc += p[k];
     };
     // Chunk j sits in ring slot j & 1 once staged; while the sums read chunk
     // c, chunk c + 1 is stashed into the other slot (read last in iteration
@@ -183,7 +188,10 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(const float* __r
       __syncthreads();
     }
     if (c + 2 < nc) sum_chunk(c + 2, 0);
-    if (tid < n_experts) smem[hidden + tid] = acc;  // prob_of(0)
+    if (tid < n_experts) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) prob_of(r)[tid] = acc[r];
+    }
   } else {
   const bool vec = hidden % 4 == 0 && ((uintptr_t)router & 15) == 0;
   const int nc = vec ? hidden / kChunk : 0;  // whole chunks; the rest one value at a time
@@ -357,10 +365,11 @@ extern "C" int32_t rv_router_topk(const float* x, size_t n_rows, size_t hidden, 
     int R = 1;
     while (R < 4 && n_rows >= (size_t)(2 * R) * 256 && (size_t)(2 * R) * row_bytes <= lds_cap) R *= 2;
     const unsigned grid = (unsigned)((n_rows + R - 1) / R);
-    // One row per workgroup with at most 128 experts: the staged form when
-    // the chunks divide the row and the ring fits beside the row's region.
-    const bool staged = R == 1 && n_experts <= (size_t)rv::kStagedExperts && hidden % rv::kStagedChunk == 0 &&
-                        ((uintptr_t)router & 15) == 0 && row_bytes + rv::kStagedBytes <= lds_cap;
+    // At most 128 experts and 1 or 2 rows per workgroup: the staged form
+    // when the chunks divide the row and the ring fits beside the rows'
+    // regions (4 rows staged measured slower: 72.4 vs 63.9 us for 1024 rows).
+    const bool staged = R <= 2 && n_experts <= (size_t)rv::kStagedExperts && hidden % rv::kStagedChunk == 0 &&
+                        ((uintptr_t)router & 15) == 0 && (size_t)R * row_bytes + rv::kStagedBytes <= lds_cap;
 #define RV_ROUTER(RR, ST)                                                                                         \
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&rv::router_kernel<RR, ST>),                           \
                             hipFuncAttributeMaxDynamicSharedMemorySize,                                          \
@@ -370,6 +379,8 @@ extern "C" int32_t rv_router_topk(const float* x, size_t n_rows, size_t hidden, 
                      experts, weights)
     if (R == 4) {
       RV_ROUTER(4, false);
+    } else if (R == 2 && staged) {
+      RV_ROUTER(2, true);
     } else if (R == 2) {
       RV_ROUTER(2, false);
     } else if (staged) {
