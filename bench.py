@@ -611,6 +611,85 @@ def bench_attn_block(torch, rv, synth, iters=20, n_layers=48, n_sets=24):
                             "note": "one graph replayed per token; position read from device memory"}}
 
 
+def bench_floors(torch, iters=50):
+    """The limits the decode and prefill kernels are judged against, measured
+    on this box with the probe launches of include/ramvamp_floors.h, each in
+    a 48-launch graph (as config 2 replays its layers): an empty launch; a
+    plain streaming read of one config-2 call's bytes (16.8 MB, 48 distinct
+    buffers: 807 MB, past the 256 MB MALL) and of one config-5 call's (67.1
+    MB, 5 rotating buffers: 336 MB) at several workgroup counts; and the
+    issue rate of the MFMA forms (independent chains, 1 and 4 waves per
+    SIMD), timed with events around one long launch."""
+    from ctypes import byref, c_void_p
+
+    from ramvamp_amd import _lib as L
+
+    lib = L.load()
+    err = L.RvError()
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(f"floor probe failed: {rc} {err.what}")
+
+    def stream():
+        return c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def graph_us(fn, n_launch=48):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for _ in range(5):
+            g.replay()
+        t = timed(torch, g.replay, iters)
+        del g
+        return t / iters / n_launch * 1e6
+
+    res = {}
+    res["empty_launch_us_in_graph"] = round(graph_us(lambda: [ok(lib.rv_floor_empty(stream(), byref(err)))
+                                                              for _ in range(48)]), 3)
+    sink = torch.zeros(1 << 16, device="cuda")
+    for name, nbytes, n_buf, grids in (("decode_ctx4096_f32", decode_bytes(4096, 4), 48, (256, 512, 1024, 2048)),
+                                       ("decode_ctx32768_f16", decode_bytes(32768, 2), 5, (512, 1024, 2048, 4096))):
+        nb = (nbytes + 15) // 16 * 16
+        bufs = [torch.ones(nb // 4, device="cuda") for _ in range(n_buf)]
+        row = {"bytes": nbytes, "buffers": n_buf}
+        for n_wg in grids:
+            def fn(n_wg=n_wg):
+                for i in range(48):
+                    ok(lib.rv_floor_stream_read(c_void_p(bufs[i % n_buf].data_ptr()), nb, n_wg,
+                                                c_void_p(sink.data_ptr()), stream(), byref(err)))
+            us = graph_us(fn)
+            row[f"us_{n_wg}_wg"] = round(us, 3)
+        best = min(v for k, v in row.items() if k.startswith("us_"))
+        row["best_us"] = best
+        row["best_gbs"] = round(nbytes / best / 1e3, 1)
+        row["best_frac"] = round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4)
+        res[f"stream_read_{name}"] = row
+        del bufs
+    flops = {L.RV_FLOOR_MFMA_F16_16X16X32: ("f16_16x16x32", 16384, 4000),
+             L.RV_FLOOR_MFMA_F16_32X32X16: ("f16_32x32x16", 32768, 2000),
+             L.RV_FLOOR_MFMA_F32_16X16X4: ("f32_16x16x4", 2048, 4000)}
+    for form, (name, f, it) in flops.items():
+        row = {}
+        for waves_per_simd in (1, 2, 4):
+            n_wg = 256 * waves_per_simd
+            for _ in range(2):  # warm-up
+                ok(lib.rv_floor_mfma(form, 4, it, n_wg, c_void_p(sink.data_ptr()), stream(), byref(err)))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ok(lib.rv_floor_mfma(form, 4, it, n_wg, c_void_p(sink.data_ptr()), stream(), byref(err)))
+            e1.record()
+            torch.cuda.synchronize()
+            s_ = e0.elapsed_time(e1) / 1e3
+            tf = n_wg * 4 * it * 4 * f / s_ / 1e12
+            row[f"tflops_{waves_per_simd}_waves_per_simd"] = round(tf, 1)
+            row[f"ns_per_mfma_per_simd_{waves_per_simd}_waves"] = round(s_ / (waves_per_simd * it * 4) * 1e9, 2)
+        res[f"mfma_{name}"] = row
+    return res
+
+
 def cpu_baseline(synth, budget_s=12.0, n_layers=48, sample_layers=8):
     """The oracle (C restatement of ramvamp's AVX2+F16C decode path with its
     kv-head fan-out over min(4, cores) threads, forward.rs:1914-2063) on the
@@ -756,6 +835,8 @@ def main():
                     help="only run the router leg (1, 512 and 1024 rows), log it and exit (for profiling)")
     ap.add_argument("--config5-only", action="store_true",
                     help="only run the config 5 leg (ctx 32768, f16, every split shape), log it and exit (for profiling)")
+    ap.add_argument("--floors", action="store_true",
+                    help="only measure the floors (empty launch, streaming reads, MFMA issue rates), log them and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -778,6 +859,9 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log("copied 10 x 64 MiB")
+        return
+    if args.floors:
+        log(json.dumps(bench_floors(torch), indent=1))
         return
     if args.projections_only:
         rp = bench_projections(torch, rv)
@@ -813,10 +897,6 @@ def main():
             r = bench_prefill(torch, rv, synth, cfg, mode)
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")
-        for cfg in (3, 4):
-            r = bench_prefill(torch, rv, synth, cfg, "f16", tune={rv.RV_TUNE_PREFILL_FUSE: 2})
-            log(f"config {cfg} f16, rows appended inside the attention launch: {r['us_per_call']:.1f} us/call, "
-                f"kernel {r['us_attention_kernel']:.1f} us")
         return
     r2 = bench_config2(torch, rv, synth, args.steps, args.warmup)
     log(f"config 2: {r2['us_per_layer']:.2f} us/layer (graph), {r2['eager_us_per_layer']:.2f} us/layer (eager), "
@@ -825,15 +905,13 @@ def main():
                                "gbs": round(r2["eager_gbs"], 1)},
              "config2_graph_matches_eager": r2["graph_matches_eager"]}
     if not args.no_extra:
+        extra["floors"] = bench_floors(torch)
+        log("floors: " + json.dumps(extra["floors"]))
         for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
             r = bench_prefill(torch, rv, synth, cfg, mode)
             extra[f"config{cfg}_prefill_{mode}"] = r
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")
-        for cfg in (3, 4):  # the chunk's rows appended inside the attention launch (opt-in)
-            r = bench_prefill(torch, rv, synth, cfg, "f16", tune={rv.RV_TUNE_PREFILL_FUSE: 2})
-            extra[f"config{cfg}_prefill_f16_one_launch"] = r
-            log(f"config {cfg} f16 one launch: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us")
         r1 = bench_config1(torch, rv, synth)
         extra["config1_decode_step_ctx512"] = r1
         log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us, "

@@ -246,9 +246,13 @@ int32_t rv_decode_step(rv_kv* kv, size_t layer, const float* q, size_t q_len, co
  * at that position, so the cache is expected to hold exactly *d_position rows
  * then (the reference's decode keeps position == len). The launch is planned
  * for max_position + 1 positions (workgroups past the token's position find
- * nothing to do and contribute nothing); *d_position above max_position is
- * clamped to it. max_position >= capacity is RV_KV_CAPACITY_EXCEEDED. The
- * host cursor does not move: rv_kv_commit adds the rows the replays wrote.
+ * nothing to do and contribute nothing). max_position >= capacity is
+ * RV_KV_CAPACITY_EXCEEDED. A step that finds *d_position (as an unsigned
+ * value) above max_position writes no cache row and leaves `out` untouched,
+ * and records RV_KV_CAPACITY_EXCEEDED in the cache's device status, which
+ * rv_kv_device_status and rv_kv_commit report (the device form of append's
+ * refusal when a layer is full, kv/mod.rs:352-357). The host cursor does not
+ * move: rv_kv_commit adds the rows the replays wrote.
  * The first call for a (theta, max_position) builds the (cos, sin) table and
  * workspace and must not be captured; later calls may be. Device pointers
  * only (RV_HOST_PTRS is RV_ERR_UNSUPPORTED); head_dim 128 and a group of at
@@ -260,8 +264,18 @@ int32_t rv_decode_step_dev(rv_kv* kv, size_t layer, const float* q, size_t q_len
                            float theta, const uint32_t* d_position, size_t max_position, float scale,
                            float* out, size_t out_len, uint32_t flags, rv_error* err);
 /* Adds `rows` to the layer's length (the rows device-position steps wrote);
- * past the capacity is RV_KV_CAPACITY_EXCEEDED and nothing changes. */
+ * past the capacity is RV_KV_CAPACITY_EXCEEDED and nothing changes. It first
+ * synchronises the cache's stream and reports a device status left by a
+ * refused step exactly as rv_kv_device_status does (nothing changes then
+ * either). */
 int32_t rv_kv_commit(rv_kv* kv, size_t layer, size_t rows, rv_error* err);
+/* No reference counterpart (the reference has no device-side steps). Waits
+ * for the cache's stream, then returns the status a device-position step
+ * recorded since the last read and clears it: RV_OK, or
+ * RV_KV_CAPACITY_EXCEEDED with a = the first refused layer, b = the
+ * positions that step was planned for (its max_position + 1, the capacity it
+ * was given), c = the position it read. */
+int32_t rv_kv_device_status(rv_kv* kv, rv_error* err);
 /* Queues *d_position += n on the cache's stream (a token graph's last node). */
 int32_t rv_position_advance(rv_kv* kv, uint32_t* d_position, uint32_t n, rv_error* err);
 
@@ -290,10 +304,8 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
 #define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
 #define RV_TUNE_PREFILL_IMPL 8     /* prefill attention kernel: 0 auto, 1 two wave groups, 2 software-pipelined */
 #define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1 (default), 2 or 4 (f16 planes) */
-#define RV_TUNE_DECODE_FAN 10      /* decode splits folded per level-1 merge group (the rest in a second level) */
-#define RV_TUNE_DECODE_MERGE 11    /* 0: decode splits merged by a second kernel, 1: inside the tile launch (ticket) */
-#define RV_TUNE_PREFILL_FUSE 12    /* an F16/BF16 prefill chunk's k/v rows: 0 auto (= 1), 1 appended by a row
-                                      prologue launch before the attention launch, 2 inside the attention launch */
+#define RV_TUNE_DECODE_MERGE 11    /* decode split merge: 0 auto, 1 inside the tile launch (a first level inside each
+                                      XCD's L2, then across XCDs), 2 a second kernel */
 int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
 
 /* No reference counterpart: benchmark instrumentation. With
@@ -305,6 +317,37 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err);
  * milliseconds and the number of timed launches since the last read, and
  * resets both. */
 int32_t rv_kv_kernel_time(rv_kv* kv, double* total_ms, uint64_t* launches, rv_error* err);
+
+/* No reference counterpart: the device memory this cache holds, in bytes.
+ * rv_kv_projected_bytes is the reference's planes-only budget
+ * (kv/mod.rs:237-259: 2 * n_layers * capacity * kv_dim * element size);
+ * this adds what the device path keeps beside the planes. *now is what is
+ * allocated at the call (planes, workspace including buffers a growth
+ * retired, normalised-q buffer, host-pointer staging, the (cos, sin) table,
+ * tickets and status, and every layer's prefill staged copy made so far);
+ * *bound is that total once every layer holds a staged copy sized for its
+ * capacity in the costliest prefill mode (EXACT tiles: 17/16 of the layer's
+ * f32 planes or 17/8 of its f16 planes; F16/BF16 tiles take half the f32
+ * planes or all of the f16 planes) and
+ * the table covers the capacity; growth past it comes only from a prefill
+ * chunk or RV_HOST_PTRS call larger than any before. Either may be null. */
+int32_t rv_kv_device_bytes(rv_kv* kv, uint64_t* now, uint64_t* bound, rv_error* err);
+/* No reference counterpart: rv_kv_device_bytes' *bound for a cache of this
+ * geometry before any call has grown it, computed from the geometry alone
+ * (no device needed): rv_kv_projected_bytes' planes, the decode workspace
+ * rv_kv_new reserves (at least 1 MiB), the merge tickets and status words,
+ * an EXACT staged copy per layer over its capacity (head_dim 128; none
+ * otherwise) and the (cos, sin) table over the capacity
+ * (capacity * head_dim * 4 bytes). Errors as rv_kv_projected_bytes. */
+int32_t rv_kv_projected_device_bytes(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t capacity,
+                                     rv_elem elem, uint64_t* bytes, rv_error* err);
+
+/* No reference counterpart: diagnostics. *ok = 1 when the cache's device
+ * deals the workgroups of a launch to its XCDs round robin (checked by a
+ * probe when the cache was made), which the in-launch XCD merge of the
+ * decode splits relies on; 0 otherwise (the decode then merges in a second
+ * launch). */
+int32_t rv_kv_xcd_dealing(rv_kv* kv, int32_t* ok, rv_error* err);
 
 #ifdef __cplusplus
 }

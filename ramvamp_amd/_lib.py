@@ -29,9 +29,7 @@ RV_TUNE_DECODE_IMPL = 6
 RV_TUNE_KERNEL_TIMING = 7
 RV_TUNE_PREFILL_IMPL = 8
 RV_TUNE_DECODE_DEPTH = 9
-RV_TUNE_DECODE_FAN = 10
 RV_TUNE_DECODE_MERGE = 11
-RV_TUNE_PREFILL_FUSE = 12
 RV_NOALLOC_SCRATCH_BYTES = 8 << 20
 # include/ramvamp_gemv.h
 RV_QF_Q4_K = 1
@@ -39,6 +37,10 @@ RV_QF_Q5_K = 2
 RV_QF_Q6_K = 3
 RV_QF_Q8_0 = 4
 RV_QF_Q8_K = 5
+# include/ramvamp_floors.h
+RV_FLOOR_MFMA_F16_16X16X32 = 0
+RV_FLOOR_MFMA_F16_32X32X16 = 1
+RV_FLOOR_MFMA_F32_16X16X4 = 2
 
 
 class RvError(ctypes.Structure):
@@ -103,6 +105,10 @@ SIGNATURES = {
     "rv_decode_attention_noalloc": (c_int32, [_P, _P, c_size_t, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_kv_set_tuning": (c_int32, [_P, c_int32, c_int64, _E]),
     "rv_kv_kernel_time": (c_int32, [_P, POINTER(c_double), POINTER(c_uint64), _E]),
+    "rv_kv_device_status": (c_int32, [_P, _E]),
+    "rv_kv_device_bytes": (c_int32, [_P, POINTER(c_uint64), POINTER(c_uint64), _E]),
+    "rv_kv_xcd_dealing": (c_int32, [_P, POINTER(c_int32), _E]),
+    "rv_kv_projected_device_bytes": (c_int32, [c_size_t, c_size_t, c_size_t, c_size_t, c_int, POINTER(c_uint64), _E]),
     # include/ramvamp_gemv.h
     "rv_quant_block_weights": (c_size_t, [c_uint32]),
     "rv_quant_block_bytes": (c_size_t, [c_uint32]),
@@ -142,6 +148,10 @@ SIGNATURES = {
                                        c_float, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
     "rv_attn_block_decode_dev": (c_int32, [_P, c_size_t, _P, c_size_t, c_size_t, POINTER(RvAttnBlockWeights),
                                            c_float, c_float, _P, c_size_t, c_float, _P, c_size_t, c_uint32, _E]),
+    # include/ramvamp_floors.h
+    "rv_floor_empty": (c_int32, [_P, _E]),
+    "rv_floor_stream_read": (c_int32, [_P, c_size_t, c_uint32, _P, _P, _E]),
+    "rv_floor_mfma": (c_int32, [c_int32, c_uint32, c_uint32, c_uint32, _P, _P, _E]),
 }
 
 _lib = None

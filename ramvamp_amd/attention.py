@@ -20,7 +20,7 @@ reference read the same here. Differences, all forced by the device:
 from __future__ import annotations
 
 import ctypes
-from ctypes import byref, c_double, c_size_t, c_uint64, c_void_p
+from ctypes import byref, c_double, c_int32, c_size_t, c_uint64, c_void_p
 
 import numpy as np
 
@@ -276,9 +276,45 @@ class KvCache:
 
     def commit(self, layer: int, rows: int):
         """rv_kv_commit (no reference counterpart): adds the rows that
-        device-position steps wrote to the layer's length."""
+        device-position steps wrote to the layer's length; a step refused on
+        the device (its position past max_position) raises KvError
+        CapacityExceeded here, as device_status does."""
+        self._bind_stream()
         err = L.RvError()
         _check(_lib().rv_kv_commit(self._h, layer, rows, byref(err)), err)
+
+    def device_status(self):
+        """rv_kv_device_status (no reference counterpart): waits for the
+        cache's stream; raises KvError CapacityExceeded (layer, planned
+        positions) when a device-position step refused its position since the
+        last read, and clears the status."""
+        self._bind_stream()
+        err = L.RvError()
+        _check(_lib().rv_kv_device_status(self._h, byref(err)), err)
+
+    def device_bytes(self):
+        """rv_kv_device_bytes: (bytes allocated now, bound with every layer's
+        staged copy at capacity) of device memory this cache holds."""
+        now, bound, err = c_uint64(), c_uint64(), L.RvError()
+        _check(_lib().rv_kv_device_bytes(self._h, byref(now), byref(bound), byref(err)), err)
+        return now.value, bound.value
+
+    @staticmethod
+    def projected_device_bytes(n_layers, n_kv_heads, head_dim, capacity, elem="f16") -> int:
+        """rv_kv_projected_device_bytes: device_bytes()'s bound for a fresh
+        cache of this geometry (planes, decode workspace, tickets, an EXACT
+        staged copy per layer, the (cos, sin) table), from the geometry alone."""
+        out, err = c_uint64(), L.RvError()
+        _check(_lib().rv_kv_projected_device_bytes(n_layers, n_kv_heads, head_dim, capacity, _elem_code(elem),
+                                                   byref(out), byref(err)), err)
+        return int(out.value)
+
+    def xcd_ok(self) -> bool:
+        """rv_kv_xcd_dealing: whether the device deals a launch's workgroups
+        to its XCDs round robin (the in-launch XCD merge needs it)."""
+        ok, err = c_int32(), L.RvError()
+        _check(_lib().rv_kv_xcd_dealing(self._h, byref(ok), byref(err)), err)
+        return bool(ok.value)
 
     def _row(self, plane_v: int, layer: int, pos: int) -> np.ndarray:
         self._bind_stream()  # the copy is ordered after work queued on torch's current stream

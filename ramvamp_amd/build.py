@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libramvamp_attn.so")
 SOURCES = ["rv_abi.cpp", "rv_prologue.hip", "rv_decode.hip", "rv_prefill.hip", "rv_quant.hip", "rv_gemv_abi.cpp",
-           "rv_block_abi.cpp", "rv_router.hip"]
+           "rv_block_abi.cpp", "rv_router.hip", "rv_floors.hip"]
 # Per-source extra flags. The prefill kernels hold MFMA accumulators and
 # their softmax operands together; the default heuristic places the
 # accumulators in AGPRs and copies them through VGPRs every tile, so their

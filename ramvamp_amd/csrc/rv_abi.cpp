@@ -140,7 +140,7 @@ struct Stager {
     void* p = nullptr;
     e = hipMalloc(&p, bytes);
     if (e != hipSuccess) return false;
-    if (kv->stage) kv->retired.push_back(kv->stage);
+    if (kv->stage) kv->retire(kv->stage, kv->stage_bytes);
     kv->stage = p;
     kv->stage_bytes = bytes;
     return true;
@@ -309,7 +309,7 @@ HipStatus ensure_workspace(rv_kv* kv, size_t bytes, size_t bound) {
     st.what = "hipMalloc workspace";
     return st;
   }
-  if (kv->ws) kv->retired.push_back(kv->ws);
+  if (kv->ws) kv->retire(kv->ws, kv->ws_bytes);
   kv->ws = p;
   kv->ws_bytes = want;
   return st;
@@ -329,7 +329,7 @@ HipStatus ensure_qbuf(rv_kv* kv, size_t bytes) {
     st.what = "hipMalloc qbuf";
     return st;
   }
-  if (kv->qbuf) kv->retired.push_back(kv->qbuf);
+  if (kv->qbuf) kv->retire(kv->qbuf, kv->qbuf_bytes);
   kv->qbuf = (float*)p;
   kv->qbuf_bytes = bytes;
   return st;
@@ -373,7 +373,7 @@ HipStatus ensure_rope_tab(rv_kv* kv, float theta, size_t n) {
     st.what = "hipMemcpy rope table";
     return st;
   }
-  if (kv->rope_tab) kv->retired.push_back(kv->rope_tab);
+  if (kv->rope_tab) kv->retire(kv->rope_tab, kv->rope_n * kv->head_dim * sizeof(float));
   kv->rope_tab = (float*)d;
   kv->rope_n = rows;
   kv->rope_theta = theta;
@@ -484,10 +484,11 @@ int32_t rv_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t ca
   if (e == hipSuccess) e = hipMalloc(&kv->v, plane_bytes);
   if (e == hipSuccess) e = hipMemset(kv->k, 0, plane_bytes);
   if (e == hipSuccess) e = hipMemset(kv->v, 0, plane_bytes);
-  const size_t ticket_bytes = n_kv_heads * (rv::kMaxMergeGroups + 1) * sizeof(unsigned);
+  const size_t ticket_bytes = rv::ticket_words(kv) * sizeof(unsigned);
   if (e == hipSuccess) e = hipMalloc(&kv->tickets, ticket_bytes);
   if (e == hipSuccess) e = hipMemset(kv->tickets, 0, ticket_bytes);
   if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) kv->xcd_ok = rv::xcd_dealing_ok(device);
   if (e == hipSuccess) {
     const rv::HipStatus st = rv::ensure_workspace(kv, rv::decode_ws_bound(kv));
     e = st.e;
@@ -512,8 +513,7 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab,
-                    (void*)kv->chunk_flags})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab})
       if (p) (void)hipFree(p);
     for (void* p : kv->staged)
       if (p) (void)hipFree(p);
@@ -889,7 +889,8 @@ int32_t rv_decode_step_dev(rv_kv* kv, size_t layer, const float* q, size_t q_len
   DeviceGuard dg(kv->device);
   rv::HipStatus hs = rv::ensure_rope_tab(kv, theta, max_position + 1);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
-  rv::DecodePro pro{k, v, q_norm_w, k_norm_w, eps, {}, {}, d_position, kv->rope_tab, (int)max_position};
+  rv::DecodePro pro{k, v, q_norm_w, k_norm_w, eps, {}, {}, d_position, kv->rope_tab, (int)max_position,
+                    rv::dev_status(kv), (uint32_t)layer};
   hs = rv::launch_decode_pro(kv, q, q_len / kv->head_dim, layer, max_position + 1, scale, pro, out, kv->stream);
   if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   return finish(kv, flags, out, out, q_len, err);
@@ -901,8 +902,77 @@ int32_t rv_kv_commit(rv_kv* kv, size_t layer, size_t rows, rv_error* err) {
   if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
   int32_t rc = check_layer(kv, layer, err);
   if (rc) return rc;
+  if ((rc = rv_kv_device_status(kv, err))) return rc;
   if (rows > kv->capacity - kv->lens[layer]) return fail(err, RV_KV_CAPACITY_EXCEEDED, layer, kv->capacity);
   kv->lens[layer] += rows;
+  return ok(err);
+}
+
+// The status word a device-position step leaves when it refuses a position
+// past its plan (rv_decode.hip): [0] code, [1] layer, [2] position read,
+// [3] the step's max_position + 1. Read after the stream drains, then cleared.
+int32_t rv_kv_device_status(rv_kv* kv, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  DeviceGuard dg(kv->device);
+  uint32_t w[4] = {0, 0, 0, 0};
+  hipError_t e = kv->stream ? hipStreamSynchronize(kv->stream) : hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(w, rv::dev_status(kv), sizeof(w), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(err, e, "read the device status");
+  if (w[0] == 0) return ok(err);
+  const uint32_t zero[4] = {0, 0, 0, 0};
+  e = hipMemcpy(rv::dev_status(kv), zero, sizeof(zero), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(err, e, "clear the device status");
+  return fail(err, (int32_t)w[0], w[1], w[3], w[2], 0, "device-position step past its planned positions");
+}
+
+int32_t rv_kv_device_bytes(rv_kv* kv, uint64_t* now, uint64_t* bound, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  const size_t planes = 2 * kv->n_layers * kv->plane * kv->elem_size();
+  size_t staged = 0;
+  for (size_t b : kv->staged_bytes) staged += b;
+  const size_t base = planes + kv->ws_bytes + kv->qbuf_bytes + kv->stage_bytes + kv->retired_bytes +
+                      rv::ticket_words(kv) * sizeof(unsigned);
+  const size_t tab = kv->rope_n * kv->head_dim * sizeof(float);
+  if (now) *now = (uint64_t)(base + tab + staged);
+  if (bound) {
+    // Every layer's staged copy at its capacity in the costliest mode, the
+    // table over the whole capacity; a copy already made in another mode
+    // was retired (counted in base) when it was replaced.
+    const size_t per_layer = rv::prefill_stage_bound(kv);
+    size_t st = 0;
+    for (size_t b : kv->staged_bytes) st += std::max(b, per_layer);
+    const size_t tab_cap = std::max(tab, kv->capacity * kv->head_dim * sizeof(float));
+    *bound = (uint64_t)(base + tab_cap + st);
+  }
+  return ok(err);
+}
+
+int32_t rv_kv_projected_device_bytes(size_t n_layers, size_t n_kv_heads, size_t head_dim, size_t capacity,
+                                     rv_elem elem, uint64_t* bytes, rv_error* err) {
+  uint64_t planes = 0;
+  int32_t rc = rv_kv_projected_bytes(n_layers, n_kv_heads, head_dim, capacity, elem, &planes, err);
+  if (rc) return rc;
+  if (!bytes) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "bytes");
+  // The host fields the sizing reads, as rv_kv_new sets them (no device
+  // memory is touched).
+  rv_kv g;
+  g.n_layers = n_layers;
+  g.n_kv_heads = n_kv_heads;
+  g.head_dim = head_dim;
+  g.capacity = capacity;
+  g.elem = elem;
+  g.kv_dim = n_kv_heads * head_dim;
+  const size_t ws = std::max<size_t>(rv::decode_ws_bound(&g), (size_t)1 << 20);
+  const size_t staged = n_layers * rv::prefill_stage_bound(&g);
+  const size_t tab = capacity * head_dim * sizeof(float);
+  *bytes = planes + ws + rv::ticket_words(&g) * sizeof(unsigned) + staged + tab;
+  return ok(err);
+}
+
+int32_t rv_kv_xcd_dealing(rv_kv* kv, int32_t* ok_out, rv_error* err) {
+  if (!kv) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "kv");
+  if (!ok_out) return fail(err, RV_ERR_NULL_ARG, 0, 0, 0, 0, "ok");
+  *ok_out = kv->xcd_ok ? 1 : 0;
   return ok(err);
 }
 
@@ -955,32 +1025,7 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
   rv::fill_inv_freq(inv, hd, theta);
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};
   rv::HipStatus hs;
-  if (rv::prefill_supported(kv, p.group, start + rows) && kv->tune_prefill_fuse == 2 &&
-      rv::chunk_fusable(kv, p.group, flags, kv->stream)) {
-    // One launch: the attention kernel appends the chunk's k/v rows (k
-    // prologue included) into the cache and the staged tiles and runs the q
-    // prologue in its query loads; (cos, sin) from the cache's table.
-    rv::StageDst sd;
-    hs = rv::ensure_rope_tab(kv, theta, start + rows);
-    if (hs.e == hipSuccess) hs = rv::ensure_chunk_flags(kv);
-    // The (cos, sin) rows a captured call of this shape writes (it takes the
-    // row-prologue path), so that capturing it allocates nothing.
-    if (hs.e == hipSuccess) hs = rv::ensure_qbuf(kv, rows * hd * sizeof(float));
-    if (hs.e == hipSuccess) hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
-    if (hs.e == hipSuccess && !sd.base) {
-      hs.e = hipErrorInvalidValue;
-      hs.what = "fused prefill chunk without a staged copy";
-    }
-    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
-    kv->lens[layer] = len + rows;
-    if (++kv->chunk_epoch == 0) ++kv->chunk_epoch;
-    const rv::ChunkFuse cf{dk, dv, dwk, eps, kv->rope_tab, kv->k_layer(layer), kv->v_layer(layer),
-                           kv->elem == RV_ELEM_F16, (int)kv->kv_dim, kv->chunk_flags, (int)kv->chunk_flag_stride,
-                           kv->chunk_epoch};
-    const rv::QNorm qn{dwq, eps, kv->rope_tab + start * hd};
-    hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, &qn, kv->stream, &cf);
-    if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
-  } else if (rv::prefill_supported(kv, p.group, start + rows)) {
+  if (rv::prefill_supported(kv, p.group, start + rows)) {
     // k/v prologue + append (also into the layer's staged tiles) and the
     // rows' (cos, sin) table; the q prologue runs inside the attention
     // kernel's query loads.
@@ -1020,9 +1065,7 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_PREFILL_IMPL: kv->tune_prefill_impl = value; break;
     case RV_TUNE_KERNEL_TIMING: kv->timing = value != 0; break;
     case RV_TUNE_DECODE_DEPTH: kv->tune_decode_depth = value; break;
-    case RV_TUNE_DECODE_FAN: kv->tune_decode_fan = value; break;
     case RV_TUNE_DECODE_MERGE: kv->tune_decode_merge = value; break;
-    case RV_TUNE_PREFILL_FUSE: kv->tune_prefill_fuse = value; break;
     default: return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)knob, 0, 0, 0, "tuning knob");
   }
   return ok(err);

@@ -74,6 +74,11 @@ static int32_t block_decode(rv_kv* kv, size_t layer, float* residual, size_t hid
                 : rv::decode_step_check(kv, layer, q_dim, position, w->q_norm_len, w->k_norm_len, err)))
     return rc;
   rv::OutProj out{c.attn, q_dim, w->o_format, w->wo, 0, residual, hidden, true, c.proj};
+  if (d_position) {
+    // A refused step (past max_position) leaves the residual as it was.
+    out.gate_pos = d_position;
+    out.gate_max = (uint32_t)max_position;
+  }
   if ((rc = rv::out_proj_check(out, w->wo_len, err))) return rc;
   const size_t need = rv_attn_block_scratch_bytes(hidden, q_dim, kv_dim);
   if (scratch_len < need) return fail(err, RV_PRIM_LENGTH_MISMATCH, scratch_len, need, "attn_block scratch");

@@ -10,13 +10,11 @@
 // loaded straight into registers in the MFMA operand layouts; softmax is
 // online (running max and sum per query head, exp2 with log2(e) folded into
 // q). The splits of one kv head are merged by a second kernel with an fp32
-// log-sum-exp combine (decode_merge_kernel). The workgroups of one kv head
-// run on different XCDs, whose L2s are not coherent; an in-launch merge (the
-// last workgroup of a group of splits folds them, the hand-off made with
-// device-scope partial stores and loads and a relaxed agent-scope ticket,
-// no L2 write-back) is built as a tuning option and measured slower: its
-// chain of acknowledged stores, a memory-side atomic and L2-missing loads
-// costs more than the second launch.
+// log-sum-exp combine (decode_merge_kernel), or inside the tile launch (the
+// XCD merge: the splits that share an XCD fold in its L2, then one row per
+// XCD crosses), a tuning option that measured slower at the headline shape
+// (its two acknowledged stores and two atomic round trips in series cost
+// more than the second launch).
 //
 // VALU path (head_dim 128, any group; groups over 16 use it by default):
 // decode_split_kernel, one workgroup per (kv head, subgroup of G query heads,
@@ -310,7 +308,7 @@ struct Chunk<_Float16> {
 // kernel is held to 256 registers so that two waves fit per SIMD and a grid
 // of ~2048 waves is resident at once. The waves merge through LDS; the workgroup then writes
 // `out` (one split) or its partial (o, max, sum) row; the splits of a kv head
-// are folded by decode_merge_kernel or, with MergeArgs::fused, inside the
+// are folded by decode_merge_kernel or, in MergeMode kMergeXcd, inside the
 // same launch (the in-launch split merge below).
 // With PRO the decode step's prologue runs here too (DecodePro): the planes
 // are then written (the token's row) as well as read, so they are not
@@ -320,30 +318,37 @@ struct NoPro {};
 template <bool PRO, typename T>
 using PlanePtr = std::conditional_t<PRO, const T*, const T* __restrict__>;
 
-// ---- in-launch split merge ------------------------------------------------------------
-// The workgroups of one kv head run on different XCDs, whose L2 caches are not
-// kept coherent with each other for ordinary stores. The partial rows are
-// therefore written and read with device-scope (sc1) buffer accesses, which
-// the L2 writes through and does not serve from a possibly stale line: the
-// cache-policy form of a relaxed agent-scope atomic store / load. A
-// workgroup's partial stores are complete (vmcnt 0) before its ticket is
-// taken with a relaxed agent-scope atomic add, so the workgroup that draws
-// the last ticket of a group of splits sees every partial of the group; no
-// L2 write-back or invalidate is needed. That workgroup folds the group in
-// split order and resets the ticket to 0 for the next call. Splits are
-// folded in groups of `fan` (level 1); with more than one group, each
-// group's result is a level-2 partial row and the last group to finish
-// folds those, again in order. The tree depends only on n_splits and fan,
-// so every kv head's result is the same whichever workgroup merges it.
+// ---- in-launch split merge (the XCD merge) ----------------------------------------------
+// The dispatcher deals a launch's workgroups to the 8 XCDs round robin, so
+// workgroups whose indices agree mod 8 share an XCD and its L2 (the physical
+// XCD of a slot changes between launches; the grouping does not). The L2s of
+// different XCDs are not kept coherent with each other for ordinary stores.
+// Level 1: the splits of a kv head with s = r (mod 8) share slot r's L2;
+// each writes its partial row with plain stores, waits until they are
+// complete (vmcnt 0), and takes a ticket; the last of the group folds the
+// group's rows (loads that skip the CU's L1 and read that L2) in split order.
+// Level 2: the group's row is written with device-scope (sc1) stores, which
+// the L2 writes through; after a second ticket the last of the <= 8 groups
+// folds their rows with device-scope loads, in group order. Each last
+// arriver resets its ticket for the next call; no L2 write-back or
+// invalidate is needed, and no workgroup waits on another. The fold order
+// depends only on n_splits, so every kv head's result (and a kv-head range's)
+// is the same whichever workgroups finish last.
 constexpr int kPolicyDevice = 16;  // the sc1 bit of the buffer instructions' cache policy
+constexpr int kPolicyL2 = 1;       // the sc0 bit: the load misses the CU's L1 and reads its XCD's L2
+
+// How the splits of a kv head are folded.
+enum MergeMode : int {
+  kMergeKernel = 0,  // partials only; decode_merge_kernel folds them in a second launch
+  kMergeXcd = 1,     // in-launch: a first level inside each XCD's L2, then one row per XCD across
+};
 
 struct MergeArgs {
-  float* part;         // [n_heads][n_splits][stride]
-  float* part2;        // [n_heads][n_grp][stride]
-  unsigned* tickets;   // [n_heads][n_grp] level 1, then [n_heads] level 2; zero between calls
+  float* part;         // [n_heads][n_splits][stride], then [n_heads][8] level-2 rows
+  unsigned* xt;        // counter (slot, head) at line slot * xpad + head, level 2 at line 8 * xpad + head
   uint32_t ws_bytes;   // bytes addressable from `part` (the buffer accesses' bound)
-  int fan, n_grp;
-  bool fused;          // false: partials only, decode_merge_kernel folds them
+  int xpad;            // kv heads of the cache (lines per XCD slot)
+  int mode;            // MergeMode
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(float* base, uint32_t bytes) {
@@ -358,9 +363,12 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // starting `row0` rows into the buffer, in row order: thread -> (head g, 4
 // consecutive d). Writes a partial row at dst_row (when out is null) or the
 // normalised output out[g * kD + d].
-template <int NT>
+// Rows row0, row0 + step, ...; loaded with cache policy LP (device scope for
+// rows other XCDs wrote, L2 for rows this XCD wrote); a partial row out is
+// stored at device scope.
+template <int NT, int LP = kPolicyDevice>
 __device__ void fold_rows(__amdgpu_buffer_rsrc_t rs, uint32_t row0, int cnt, int stride, int group, uint32_t dst_row,
-                          float* out, int tid) {
+                          float* out, int tid, uint32_t step = 1) {
   constexpr int kChunk = 8;
   for (int j = tid; j < group * (kD / 4); j += NT) {
     const int g = j / (kD / 4), d = (j % (kD / 4)) * 4;
@@ -371,12 +379,12 @@ __device__ void fold_rows(__amdgpu_buffer_rsrc_t rs, uint32_t row0, int cnt, int
       float mv[kChunk], lv[kChunk];
 #pragma unroll
       for (int i = 0; i < kChunk; ++i) {
-        const uint32_t row = (row0 + (uint32_t)min(b0 + i, cnt - 1)) * (uint32_t)stride * 4u;
-        ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, row + (uint32_t)(g * kD + d) * 4u, 0, kPolicyDevice);
+        const uint32_t row = (row0 + step * (uint32_t)min(b0 + i, cnt - 1)) * (uint32_t)stride * 4u;
+        ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, row + (uint32_t)(g * kD + d) * 4u, 0, LP);
         mv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              rs, row + (uint32_t)(group * kD + 2 * g) * 4u, 0, kPolicyDevice));
+                                              rs, row + (uint32_t)(group * kD + 2 * g) * 4u, 0, LP));
         lv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              rs, row + (uint32_t)(group * kD + 2 * g + 1) * 4u, 0, kPolicyDevice));
+                                              rs, row + (uint32_t)(group * kD + 2 * g + 1) * 4u, 0, LP));
       }
       float mc = M;
 #pragma unroll
@@ -417,6 +425,8 @@ __device__ void fold_rows(__amdgpu_buffer_rsrc_t rs, uint32_t row0, int cnt, int
 // Takes this workgroup's ticket on `t` once all its threads' partial stores
 // are complete; true for the workgroup that drew the last of `n` tickets,
 // which also resets the counter for the next call.
+// The counter is device-wide (an agent-scope atomic: gfx950 issues the same
+// instruction for workgroup scope, and it is coherent across XCDs).
 __device__ __forceinline__ bool last_of(unsigned* t, unsigned n, int tid) {
   __shared__ unsigned sm_ticket;
   wait_stores();
@@ -461,8 +471,22 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   constexpr int kLdsBytes = LDS ? (2 * kStage > kOBytes ? 2 * kStage : kOBytes) : kOBytes;
   __shared__ __attribute__((aligned(1024))) char lds_raw[kLdsBytes];
   if constexpr (PRO) {
-    // A token graph's step: the token's position from device memory.
-    if (pro.d_pos) positions = min((int)*pro.d_pos, pro.max_pos) + 1;
+    // A token graph's step: the token's position from device memory. One
+    // past the plan is refused (as append refuses a full layer): no row is
+    // written, `out` is left as it was, and the first refusal is recorded.
+    if (pro.d_pos) {
+      const uint32_t p = *pro.d_pos;
+      if (p > (uint32_t)pro.max_pos) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && pro.status[0] == 0) {
+          pro.status[1] = pro.layer;
+          pro.status[2] = p;
+          pro.status[3] = (uint32_t)pro.max_pos + 1;
+          pro.status[0] = RV_KV_CAPACITY_EXCEEDED;
+        }
+        return;
+      }
+      positions = (int)p + 1;
+    }
   }
   const int split = blockIdx.x % n_splits;
   const int hidx = blockIdx.x / n_splits;  // kv head within the range
@@ -775,7 +799,17 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   __syncthreads();
   const int stride = part_stride_of(group);
   const __amdgpu_buffer_rsrc_t rs = ws_rsrc(mg.part, mg.ws_bytes);
-  const uint32_t my_row = (uint32_t)(hidx * n_splits + split);
+  // XCD mode. Workgroups whose blockIdx agree mod 8 run on the same XCD (the
+  // dispatcher deals workgroups to the 8 XCDs round robin; a probe at set-up
+  // checks it), so the splits s of a kv head with s = r (mod 8) share an L2:
+  // level-1 group r (its members' splits are r, r + 8, ...: fixed by n_splits
+  // alone). A group of one writes its row straight to level 2.
+  const int x_slot = split & 7;  // = (blockIdx.x - hidx * n_splits) mod 8
+  const int x_n1 = (n_splits - 1 - x_slot) / 8 + 1;
+  const uint32_t x_l2_row0 = (uint32_t)(gridDim.x + hidx * 8);
+  const bool dev_rows = mg.mode == kMergeXcd && x_n1 == 1;
+  const uint32_t my_row =
+      mg.mode == kMergeXcd && x_n1 == 1 ? x_l2_row0 + (uint32_t)x_slot : (uint32_t)(hidx * n_splits + split);
   for (int j = tid; j < group * (kD / 4); j += NT) {
     const int g = j / (kD / 4), d = (j % (kD / 4)) * 4;
     float M = sm_ml[0][g][0];
@@ -797,7 +831,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
       op[2] = r[2];
       op[3] = r[3];
     } else {
-      if (mg.fused) {  // device-scope stores for the in-launch hand-off
+      if (dev_rows) {  // device-scope stores for a hand-off across XCDs
         const uint32_t row = my_row * (uint32_t)stride * 4u;
         __builtin_amdgcn_raw_buffer_store_b128(O, rs, row + (uint32_t)(g * kD + d) * 4u, 0, kPolicyDevice);
         if (d == 0) {
@@ -816,23 +850,25 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
     }
   }
-  if (n_splits == 1 || !mg.fused) return;
-
-  // Level 1: the last workgroup of this split's group folds the group.
-  const int grp = split / mg.fan;
-  const int g_lo = grp * mg.fan, g_n = min(mg.fan, n_splits - g_lo);
-  if (!last_of(mg.tickets + hidx * mg.n_grp + grp, (unsigned)g_n, tid)) return;
+  if (n_splits == 1 || mg.mode == kMergeKernel) return;
   float* const head_out = out + (size_t)hidx * group * kD;
-  if (mg.n_grp == 1) {
-    fold_rows<NT>(rs, (uint32_t)(hidx * n_splits), n_splits, stride, group, 0, head_out, tid);
-    return;
+
+  // Level 1, inside this XCD: the last member to finish folds the group's
+  // rows (plain stores, complete in this L2 before the ticket; loads that
+  // skip the CU's L1 and hit this L2) in split order, and writes the group's
+  // row to level 2 at device scope. Each counter has its own 128-byte line:
+  // atomics on one line serialize.
+  if (x_n1 > 1) {
+    const int key = (int)(blockIdx.x & 7);  // the XCD slot this launch dealt the workgroup
+    if (!last_of(mg.xt + (size_t)(key * mg.xpad + hidx) * 32, (unsigned)x_n1, tid)) return;
+    fold_rows<NT, kPolicyL2>(rs, (uint32_t)(hidx * n_splits + x_slot), x_n1, stride, group,
+                             x_l2_row0 + (uint32_t)x_slot, nullptr, tid, 8u);
   }
-  // part2 lies in the same buffer, n_heads * n_splits rows after part.
-  const uint32_t l2_row0 = (uint32_t)(gridDim.x + hidx * mg.n_grp);
-  fold_rows<NT>(rs, (uint32_t)(hidx * n_splits + g_lo), g_n, stride, group, l2_row0 + (uint32_t)grp, nullptr, tid);
-  // Level 2: the last group of this kv head folds the groups' rows.
-  if (!last_of(mg.tickets + (gridDim.x / n_splits) * mg.n_grp + hidx, (unsigned)mg.n_grp, tid)) return;
-  fold_rows<NT>(rs, l2_row0, mg.n_grp, stride, group, 0, head_out, tid);
+  // Level 2, across XCDs: the last group to finish folds the <= 8 group rows
+  // in group order (device-scope rows and loads).
+  const int n2 = min(8, n_splits);
+  if (!last_of(mg.xt + (size_t)(8 * mg.xpad + hidx) * 32, (unsigned)n2, tid)) return;
+  fold_rows<NT>(rs, x_l2_row0, n2, stride, group, 0, head_out, tid);
 }
 
 // fp32 log-sum-exp merge of the splits of every (kv head, subgroup of G
@@ -1108,18 +1144,14 @@ static void launch_merge(const float* part, int n_splits, int G, int group, int 
 // 18.6 µs; fp32 at 16384: 19.1 vs 17.9 µs), since the SIMD's other
 // resident wave covers a wave's load latency. A pinned split that leaves
 // fewer waves keeps a slot per tile. The splits of a kv head
-// are folded by decode_merge_kernel; the in-launch ticket merge (fused) is a
-// tuning option: its hand-off (device-scope stores acknowledged, a
-// memory-side atomic, loads that miss L2) costs more than the second launch.
-// With fused, groups of up to kFanOne splits fold in one level, more in
-// groups of about sqrt(n_splits). The split length is sized for the
-// cache's kv heads and every other field derives from it and positions, so
-// a kv-head range takes the same reduction tree as the whole call.
+// are folded by decode_merge_kernel, or by the XCD merge (merge_mode). The
+// split length is sized for the cache's kv heads and every other field
+// derives from it and positions, so a kv-head range takes the same
+// reduction tree as the whole call.
 constexpr int kTileWaves = 2048;
-constexpr int kFanOne = 16;
 struct TilePlan {
-  int waves, depth, split_len, n_splits, fan, n_grp;
-  bool fused;
+  int waves, depth, split_len, n_splits;
+  int merge;  // MergeMode
   bool lds;  // RV_TUNE_DECODE_IMPL 3: tiles staged through LDS (4 waves, depth 1)
 };
 
@@ -1138,9 +1170,30 @@ static int tile_depth(const rv_kv* kv, int waves, int split_len, int n_splits) {
   return d >= 4 ? 4 : d >= 2 ? 2 : 1;
 }
 
+// RV_TUNE_DECODE_MERGE: 0 auto, 1 the in-launch XCD merge, 2 the separate
+// merge kernel. The XCD merge needs the dispatcher's round-robin dealing,
+// which rv_kv_new checks on the cache's device (kv->xcd_ok); without it every
+// choice is the separate kernel. Auto takes the XCD merge up to kXcdAuto
+// splits per kv head, where each split is its own level-1 group and only the
+// hand-off across XCDs remains (48-layer graphs, µs per call, separate kernel
+// vs XCD merge: f32 129 positions (3 splits) 7.65 vs 6.85, 257 7.84 vs 7.06,
+// 512 7.86 vs 7.19; f16 193 6.36 vs 5.54, 512 6.60 vs 5.88). Past 8 splits
+// the first level adds a second ticket round trip and the XCD merge loses
+// (f32 513: 7.95 vs 8.43, 4096: 8.90 vs 9.42; f16 32768: 18.1 vs 19.4).
+constexpr int kXcdAuto = 8;
+static int merge_mode(const rv_kv* kv, int n_splits) {
+  if (!kv->xcd_ok) return kMergeKernel;
+  switch (kv->tune_decode_merge) {
+    case 1: return kMergeXcd;
+    case 2: return kMergeKernel;
+    default: return n_splits <= kXcdAuto ? kMergeXcd : kMergeKernel;
+  }
+}
+
 static TilePlan plan_tile(const rv_kv* kv, long positions) {
   TilePlan p;
-  p.waves = kv->tune_decode_waves == 8 ? 8 : 4;
+  const int64_t tw = kv->tune_decode_waves;
+  p.waves = tw == 8 ? 8 : tw == 2 ? 2 : tw == 1 ? 1 : 4;
   const int step = p.waves * 16;
   long len = kv->tune_decode_split_len;
   bool fine = false;  // a default length in 16-position steps
@@ -1178,24 +1231,13 @@ static TilePlan plan_tile(const rv_kv* kv, long positions) {
   p.depth = tile_depth(kv, p.waves, p.split_len, p.n_splits);
   p.lds = kv->tune_decode_impl == 3 && p.waves == 4;
   if (p.lds) p.depth = 1;
-  p.fused = kv->tune_decode_merge == 1;
-  int fan = (int)kv->tune_decode_fan;
-  if (fan <= 0) {
-    fan = p.n_splits;
-    if (p.n_splits > kFanOne) {
-      fan = 1;
-      while (fan * fan < p.n_splits) ++fan;
-    }
-  }
-  fan = std::max(fan, (p.n_splits + kMaxMergeGroups - 1) / kMaxMergeGroups);
-  p.fan = std::min(fan, p.n_splits);
-  p.n_grp = (p.n_splits + p.fan - 1) / p.fan;
+  p.merge = merge_mode(kv, p.n_splits);
   return p;
 }
 
 // Workspace floats of a plan: level-1 rows, then level-2 rows.
 static size_t tile_ws_floats(const TilePlan& p, int n_heads, int group) {
-  const size_t rows = (size_t)n_heads * (p.n_splits + (p.n_grp > 1 ? p.n_grp : 0));
+  const size_t rows = (size_t)n_heads * (p.n_splits + (p.merge == kMergeXcd ? 8 : 0));
   return rows * part_stride_of(group);
 }
 
@@ -1211,7 +1253,7 @@ static size_t tile_ws_bound(const rv_kv* kv, int n_heads, int group) {
   else
     splits = std::min<long>(splits, kTileWaves / 4 / n_heads + 2);
   splits = std::max<long>(splits, 1);
-  return (size_t)n_heads * 2 * (size_t)splits * part_stride_of(group);
+  return (size_t)n_heads * (2 * (size_t)splits + 8) * part_stride_of(group);
 }
 
 template <typename T, int W, int D, bool PRO, bool H16, typename Pro>
@@ -1244,6 +1286,14 @@ static void launch_tile(const TilePlan& p, const TimedPair& tp, hipStream_t s, i
     if (p.depth == 1) RV_TILE(8, 1);
     else if (p.depth == 2) RV_TILE(8, 2);
     else RV_TILE(8, D4);
+  } else if (p.waves == 2) {
+    if (p.depth == 1) RV_TILE(2, 1);
+    else if (p.depth == 2) RV_TILE(2, 2);
+    else RV_TILE(2, D4);
+  } else if (p.waves == 1) {
+    if (p.depth == 1) RV_TILE(1, 1);
+    else if (p.depth == 2) RV_TILE(1, 2);
+    else RV_TILE(1, D4);
   } else {
     if (p.depth == 1) RV_TILE(4, 1);
     else if (p.depth == 2) RV_TILE(4, 2);
@@ -1272,10 +1322,9 @@ static HipStatus tile_merge_args(rv_kv* kv, const TilePlan& p, int n_heads, int 
     mg->part = (float*)kv->ws;
     mg->ws_bytes = (uint32_t)std::min<size_t>(kv->ws_bytes, 0xFFFFFFF0u);
   }
-  mg->tickets = kv->tickets;
-  mg->fan = p.fan;
-  mg->n_grp = p.n_grp;
-  mg->fused = p.fused;
+  mg->xt = xcd_tickets(kv);
+  mg->xpad = (int)xcd_ticket_pad(kv);
+  mg->mode = p.merge;
   return st;
 }
 
@@ -1322,7 +1371,8 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
   else
     launch_tile<_Float16, true, false>(p, tp, s, n_heads, q_raw, kl, vl, (int)kv->kv_dim, (int)positions, group, 0,
                                        qscale, mg, out, pro);
-  if (p.n_splits > 1 && !p.fused) launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
+  if (p.n_splits > 1 && p.merge == kMergeKernel)
+    launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "decode launch";
   return st;
@@ -1373,7 +1423,8 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
     else
       launch_tile<_Float16, false, true>(p, tp, s, n_heads, q, kl, vl, kvd, (int)positions, group, (int)kv_lo, qscale,
                                          mg, out, NoPro{});
-    if (p.n_splits > 1 && !p.fused) launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
+    if (p.n_splits > 1 && p.merge == kMergeKernel)
+      launch_merge(mg.part, p.n_splits, group, group, 1, n_heads * group, out, s);
   } else if (kv->head_dim == kD) {
     const DecodeShape d = pick_shape(kv, (int)positions, n_heads, group);
     const int n_hg = group / d.hg_size;
@@ -1427,6 +1478,49 @@ HipStatus launch_decode(rv_kv* kv, const float* q, size_t n_q_heads, size_t laye
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "decode launch";
   return st;
+}
+
+// ---- the dispatcher's XCD dealing ---------------------------------------------------
+namespace {
+// Each workgroup records the XCD it runs on (the XCC_ID hardware register).
+__global__ __launch_bounds__(64) void xcd_probe_kernel(uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = __builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xf;  // HW_REG_XCC_ID
+}
+constexpr int kProbeBlocks = 1024;
+std::mutex g_xcd_mu;
+int g_xcd_state[64] = {};  // per device: 0 unknown, 1 ok, 2 not
+}  // namespace
+
+// Whether, on `device` (current), the workgroups of a launch whose indices
+// agree mod 8 run on one XCD: four probe launches of 1024 workgroups, every
+// workgroup's XCC_ID compared with that of workgroup b mod 8, and the 8 slots
+// on 8 distinct XCDs. Cached per device.
+bool xcd_dealing_ok(int device) {
+  if (device < 0 || device >= 64) return false;
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  if (g_xcd_state[device]) return g_xcd_state[device] == 1;
+  bool ok = true;
+  uint32_t* d = nullptr;
+  std::vector<uint32_t> h(kProbeBlocks);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess || prop.multiProcessorCount != (int)kCUs ||
+      hipMalloc(&d, kProbeBlocks * sizeof(uint32_t)) != hipSuccess)
+    ok = false;
+  for (int rep = 0; ok && rep < 4; ++rep) {
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(kProbeBlocks), dim3(64), 0, nullptr, d);
+    if (hipMemcpy(h.data(), d, kProbeBlocks * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) {
+      ok = false;
+      break;
+    }
+    unsigned seen = 0;
+    for (int b = 0; b < 8; ++b) seen |= 1u << h[b];
+    ok = seen == 0xffu;
+    for (int b = 8; ok && b < kProbeBlocks; ++b) ok = h[b] == h[b % 8];
+  }
+  if (d) (void)hipFree(d);
+  (void)hipGetLastError();
+  g_xcd_state[device] = ok ? 1 : 2;
+  return ok;
 }
 
 // ---- the no-alloc entry point's scratch ------------------------------------------

@@ -408,7 +408,15 @@ HipStatus out_proj_launch(const OutProj& p, hipStream_t s) {
     a.n_seg = 1;
     a.seg[0] = {p.o_format, p.wo, p.rb, p.o, p.add ? p.o : nullptr};
     a.n_rows[0] = (int)p.hidden;
+    a.gate_pos = p.gate_pos;
+    a.gate_max = p.gate_max;
     return launch_fused_proj(a, s);
+  }
+  if (p.gate_pos) {
+    HipStatus st;
+    st.e = hipErrorNotSupported;
+    st.what = "a device-position gate needs the fused output projection (q_dim <= 8192)";
+    return st;
   }
   auto* acts = reinterpret_cast<rv_block_q8_k*>(p.scratch);
   float* dst = p.add ? reinterpret_cast<float*>((char*)p.scratch + align16(p.q_dim / 256 * sizeof(rv_block_q8_k)))

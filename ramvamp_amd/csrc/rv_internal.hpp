@@ -29,8 +29,14 @@ struct rv_kv {
   // Buffers a grown workspace, qbuf, staging or staged copy replaced: kept
   // until rv_kv_free, since a graph captured earlier may still address them.
   std::vector<void*> retired;
-  // The decode split merge's tickets: n_kv_heads * (kMaxMergeGroups + 1)
-  // counters, zero between calls (each call's last workgroup resets its own).
+  size_t retired_bytes = 0;
+  void retire(void* p, size_t bytes) {
+    retired.push_back(p);
+    retired_bytes += bytes;
+  }
+  // The XCD split merge's tickets, zero between calls (each call's last
+  // arriver resets its own): 9 * n_kv_heads counters, one per 128-byte line;
+  // then the device status words (rv_kv_device_status).
   unsigned* tickets = nullptr;
   // Recorded on the old stream when rv_kv_set_stream moves the cache to a
   // new one, which then waits for it.
@@ -53,13 +59,6 @@ struct rv_kv {
   float* rope_tab = nullptr;
   size_t rope_n = 0;
   float rope_theta = 0.f;
-  // A prefill chunk whose attention launch appends its own rows: one flag
-  // per (kv head, row block), set to the call's epoch once that block's rows
-  // are in the staged copy, then the launch's ticket counter (zero between
-  // calls). Allocated on first use, zeroed, never freed while the cache lives.
-  unsigned* chunk_flags = nullptr;
-  size_t chunk_flag_stride = 0;  // row blocks per kv head
-  unsigned chunk_epoch = 0;
 
   int64_t tune_decode_split_len = 0;
   int64_t tune_prefill_kv_split = 0;
@@ -69,9 +68,10 @@ struct rv_kv {
   int64_t tune_prefill_impl = 0;  // 0 auto, 1 two wave groups, 2 software-pipelined
   int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups, 3 LDS-staged tiles
   int64_t tune_decode_depth = 0;  // tiles in flight per wave (1, 2, 4); 0 auto
-  int64_t tune_decode_fan = 0;    // splits folded per level-1 group; 0 auto
-  int64_t tune_decode_merge = 0;  // 0 separate merge kernel, 1 in-launch ticket merge
-  int64_t tune_prefill_fuse = 0;  // chunk rows: 0 auto (= 1), 1 by the row prologue, 2 by the attention launch
+  int64_t tune_decode_merge = 0;  // 0 auto, 1 in-launch XCD merge, 2 separate merge kernel
+  // The dispatcher deals a launch's workgroups to the XCDs round robin on this
+  // device (checked at rv_kv_new): the XCD merge may rely on it.
+  bool xcd_ok = false;
 
   // RV_TUNE_KERNEL_TIMING: event pairs around the dominant kernel of each
   // call, folded into timed_ms / timed_n when read (or when the pool fills).
@@ -88,14 +88,25 @@ struct rv_kv {
 
 namespace rv {
 
+// Layout of rv_kv::tickets (see there). The XCD merge's counters sit one per
+// 128-byte line (atomics on one line serialize): (XCD slot, kv head) at line
+// slot * n_kv_heads + head, level 2 at line 8 * n_kv_heads + head.
+inline size_t xcd_ticket_pad(const rv_kv* kv) { return kv->n_kv_heads; }
+inline size_t xcd_ticket_off(const rv_kv*) { return 0; }
+inline size_t status_off(const rv_kv* kv) { return 9 * 32 * kv->n_kv_heads; }
+inline size_t ticket_words(const rv_kv* kv) { return status_off(kv) + 32; }
+inline unsigned* xcd_tickets(const rv_kv* kv) { return kv->tickets ? kv->tickets + xcd_ticket_off(kv) : nullptr; }
+inline unsigned* dev_status(const rv_kv* kv) { return kv->tickets ? kv->tickets + status_off(kv) : nullptr; }
+// Whether the workgroups of a launch whose indices agree mod 8 run on one XCD
+// on `device` (a probe, once per device; the device must be current).
+bool xcd_dealing_ok(int device);
+
 // Result of a launch helper: hipSuccess or the first failing HIP call.
 struct HipStatus {
   hipError_t e = hipSuccess;
   const char* what = nullptr;
 };
 
-// Level-1 merge groups per kv head the decode tickets provide for.
-constexpr int kMaxMergeGroups = 64;
 // Compute units of the MI355X, which the launch plans balance work over.
 constexpr long kCUs = 256;
 
@@ -218,6 +229,11 @@ struct DecodePro {
   const uint32_t* d_pos = nullptr;
   const float* tab = nullptr;
   int max_pos = 0;
+  // With d_pos: a position above max_pos is refused (no row written, out
+  // untouched) and recorded here: [0] RV_KV_CAPACITY_EXCEEDED, [1] layer,
+  // [2] the position, [3] max_pos + 1 (the first refusal since the last read).
+  uint32_t* status = nullptr;
+  uint32_t layer = 0;
 };
 // True when launch_decode_pro covers the geometry (head_dim 128, group <= 16:
 // the MFMA tile kernel); the caller then skips the row prologue.
@@ -238,25 +254,6 @@ struct QNorm {
   float eps = 0.f;
   const float* tab = nullptr;
 };
-// A prefill chunk's k/v rows appended by the attention launch itself (f16 /
-// bf16 staged copy, head_dim 128): each workgroup writes its own rows' k
-// (RMSNorm + RoPE) and v into the cache planes and the staged copy, then
-// raises its row block's flag; tiles holding other blocks' rows are read only
-// once their flags carry `epoch`. k == nullptr: the rows are already in place.
-struct ChunkFuse {
-  const float* k = nullptr;  // the chunk's raw rows, rows x kv_dim
-  const float* v = nullptr;
-  const float* k_w = nullptr;
-  float eps = 0.f;
-  const float* tab = nullptr;  // (cos, sin) by absolute position, as QNorm's
-  void* kp = nullptr;          // the layer's cache planes at position 0
-  void* vp = nullptr;
-  int f16_cache = 0;
-  int kv_dim = 0;
-  unsigned* flags = nullptr;  // [n_kv][flag_stride], then the ticket counter
-  int flag_stride = 0;
-  unsigned epoch = 0;
-};
 // Before a prefill chunk appends `rows` rows at pos0 = len(layer) and runs
 // launch_prefill: readies the layer's persistent staged copy in `mode`
 // (stages the rows the prefix gained since it was last current, up to pos0)
@@ -267,18 +264,13 @@ struct ChunkFuse {
 HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t rows, uint32_t mode,
                                 hipStream_t s, StageDst* sd);
 // Row r of q_rows (rows x q_dim) attends positions 0..start+r+1; q_rows are
-// post-RoPE, or the raw projections when qn is given. With cf (and its k
-// set), the chunk's rows [start, start + rows) are appended by this launch
-// (F16/BF16 modes with a persistent staged copy only: chunk_fusable).
+// post-RoPE, or the raw projections when qn is given.
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
-                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s,
-                         const ChunkFuse* cf = nullptr);
-// Whether a prefill chunk in `mode` on stream s can append its rows inside
-// the attention launch (F16/BF16, head_dim 128, not under graph capture).
-bool chunk_fusable(const rv_kv* kv, size_t group, uint32_t mode, hipStream_t s);
-// The flags and ticket counter of fused chunks, allocated and zeroed on
-// first use (not under graph capture).
-HipStatus ensure_chunk_flags(rv_kv* kv);
+                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s);
+
+// The largest staged copy one layer's prefill can hold (EXACT tiles over the
+// whole capacity).
+size_t prefill_stage_bound(const rv_kv* kv);
 
 // rv_decode_step's validation alone (no launch), for callers that validate
 // a whole composite call before launching any of it.

@@ -198,239 +198,26 @@ __device__ __forceinline__ bool aligned16(const void* a, const void* b = nullptr
   return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0;
 }
 
-// ---- a chunk appended by its own attention launch (ChunkFuse) ---------------------
-//
-// Workgroups take tickets in launch order and work on units in ticket
-// order: row block-major, the kv heads next, the split holding a row block's
-// own rows (the last split) first. Unit (kv head h, row block b, last split)
-// writes block b's k and v rows of head h into the cache planes and the
-// staged copy, waits for the stores, writes them back with an agent-scope
-// release and sets flag (h, b) to the call's epoch. Before a wave issues the
-// direct-to-LDS loads of a staged tile holding chunk rows it waits until the
-// flags of every row block in that tile carry the epoch; no workgroup reads
-// a tile's lines before then, so its XCD's L2 holds no stale copy of them.
-// A unit only waits on blocks at or below its own, whose units hold lower
-// tickets and so are running or done: every wait ends. The unit's last tile,
-// which holds its own rows and later rows no flag covers yet, is built in
-// LDS instead (rows of lower blocks recomputed from the raw rows, rows
-// before the chunk read from the cache planes, rows past its own as zeros).
-
-// Until every store this thread issued has completed (a compiler barrier too).
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// A row block's flag: the block's stores (complete in this workgroup's L2)
-// are written back to memory by the agent-scope release, then the flag is
-// raised with a relaxed agent-scope store.
-__device__ __forceinline__ void raise_flag(unsigned* f, unsigned epoch) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __hip_atomic_store(f, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Waits (bounded) until the flags of the chunk's row blocks [b_lo, b_hi] of
-// kv head kvh carry `epoch`; one lane per flag, the wave together.
-__device__ __forceinline__ void wait_flags(const ChunkFuse& cf, int kvh, int b_lo, int b_hi, int lane) {
-  const unsigned* f = cf.flags + (size_t)kvh * cf.flag_stride;
-  for (int spin = 0; spin < (1 << 22); ++spin) {
-    bool ok = true;
-    for (int b = b_lo + lane; b <= b_hi; b += 64)
-      ok = ok && __hip_atomic_load(f + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == cf.epoch;
-    if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  asm volatile("" ::: "memory");  // the tile's loads stay behind the wait
-}
-
-// The unit's rows for kv head kvh, 16 threads per row (thread c holds
-// d = 8c .. 8c + 7): positions [min(own_lo, 64 own_tile), 64 own_tile + 64).
-// Own rows [own_lo, own_hi] go to the cache planes and the staged copy; rows
-// in own_tile go to the LDS tile `own`; when own_hi ends the chunk, the staged
-// rows past it in own_tile are zeroed. k RMSNorm as the row prologue's (f64
-// sum of squares over the row, `x * inv * w` in f32), the rotation of pairs
-// (d, d + 64) with the position's (cos, sin); the values staged are those the
-// cache holds (an f16 cache's rounding included), then rounded to E. The
-// loads of up to PM passes of rows are all issued before any is used.
-template <int MODE, int NT>
-__device__ void fuse_rows(const ChunkFuse& cf, int kvh, int start, int own_lo, int own_hi, int own_tile, char* own,
-                          char* stage, int tile_stride, bool chunk_end, int tid) {
-#pragma clang fp contract(off)
-  typedef typename Op<MODE>::E E;
-  typedef E E8 __attribute__((ext_vector_type(8)));
-  typedef uint16_t U8 __attribute__((ext_vector_type(8)));
-  typedef uint64_t U2 __attribute__((ext_vector_type(2)));
-  constexpr int TB = kTileBytes<MODE>;
-  constexpr int RP = NT / 16;  // rows per pass
-  constexpr int PM = 4;        // passes per batch of loads
-  const int c = tid & 15;
-  const int p_first = min(own_lo, own_tile * kBT), p_end = (own_tile + 1) * kBT;
-  const size_t col = (size_t)kvh * kD + 8 * c;
-  // Raw rows 16-byte aligned (the common case): 16-byte loads. The (cos,
-  // sin) table always is.
-  const bool vec = aligned16(cf.k, cf.v);
-  float w[8];
-  ld8(cf.k_w + 8 * c, aligned16(cf.k_w), w);
-  for (int base = p_first + tid / 16; base < p_end; base += PM * RP) {
-    float x[PM][8], z[PM][8], cs[PM][8], sn[PM][8];
-#pragma unroll
-    for (int i = 0; i < PM; ++i) {
-      const int p = base + i * RP;
-      if (p >= p_end || p > own_hi) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[i][e] = z[i][e] = 0.f;
-      } else if (p < start) {
-        if (cf.f16_cache) {
-          load8((const _Float16*)cf.kp + (size_t)p * cf.kv_dim + col, x[i]);
-          load8((const _Float16*)cf.vp + (size_t)p * cf.kv_dim + col, z[i]);
-        } else {
-          load8((const float*)cf.kp + (size_t)p * cf.kv_dim + col, x[i]);
-          load8((const float*)cf.vp + (size_t)p * cf.kv_dim + col, z[i]);
-        }
-      } else {
-        ld8(cf.k + (size_t)(p - start) * cf.kv_dim + col, vec, x[i]);
-        ld8(cf.v + (size_t)(p - start) * cf.kv_dim + col, vec, z[i]);
-        ld8(cf.tab + (size_t)p * kD + 8 * (c & 7), true, cs[i]);
-        ld8(cf.tab + (size_t)p * kD + 64 + 8 * (c & 7), true, sn[i]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < PM; ++i) {
-      const int p = base + i * RP;  // the same for the row's 16 threads
-      if (p >= p_end) continue;
-      float y[8];  // k as the cache holds it
-      uint16_t yb[8], zb[8];  // an f16 cache's bits
-      if (p >= start && p <= own_hi) {
-        double ss = 0.0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += (double)x[i][e] * (double)x[i][e];
-        ss += dpp_f64<DPP_QUAD_XOR1>(ss);
-        ss += dpp_f64<DPP_QUAD_XOR2>(ss);
-        ss += dpp_f64<DPP_ROW_HALF_MIRROR>(ss);
-        ss += dpp_f64<DPP_ROW_MIRROR>(ss);
-        const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)cf.eps));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float a = x[i][e] * inv * w[e];
-          const float b = __shfl_xor(a, 8, 64);  // the pair's other half
-          y[e] = c < 8 ? a * cs[i][e] - b * sn[i][e] : b * sn[i][e] + a * cs[i][e];
-        }
-        if (cf.f16_cache) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            yb[e] = f32_to_f16_bits(y[e]);
-            zb[e] = f32_to_f16_bits(z[i][e]);
-            y[e] = (float)__builtin_bit_cast(_Float16, yb[e]);
-            z[i][e] = (float)__builtin_bit_cast(_Float16, zb[e]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = x[i][e];
-      }
-      E8 ke, ve;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        ke[e] = (E)y[e];
-        ve[e] = (E)z[i][e];
-      }
-      const int t = p % kBT;
-      const bool mine = p >= own_lo && p <= own_hi;
-      if (mine) {
-        if (cf.f16_cache) {
-          U8 kb, vb;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kb[e] = yb[e];
-            vb[e] = zb[e];
-          }
-          *reinterpret_cast<U8*>((uint16_t*)cf.kp + (size_t)p * cf.kv_dim + col) = kb;
-          *reinterpret_cast<U8*>((uint16_t*)cf.vp + (size_t)p * cf.kv_dim + col) = vb;
-        } else {
-          float* kd = (float*)cf.kp + (size_t)p * cf.kv_dim + col;
-          float* vd = (float*)cf.vp + (size_t)p * cf.kv_dim + col;
-          *reinterpret_cast<f32x4*>(kd) = f32x4{y[0], y[1], y[2], y[3]};
-          *reinterpret_cast<f32x4*>(kd + 4) = f32x4{y[4], y[5], y[6], y[7]};
-          *reinterpret_cast<f32x4*>(vd) = f32x4{z[i][0], z[i][1], z[i][2], z[i][3]};
-          *reinterpret_cast<f32x4*>(vd + 4) = f32x4{z[i][4], z[i][5], z[i][6], z[i][7]};
-        }
-      }
-      // The V bits as one vector (a bit cast per E element here compiled to
-      // eight stores of element 0).
-      const U8 vw = __builtin_bit_cast(U8, ve);
-      if (mine || (chunk_end && p > own_hi)) {
-        char* tile = stage + ((size_t)kvh * tile_stride + p / kBT) * TB;
-        *reinterpret_cast<U2*>(tile + k_off(t, c)) = __builtin_bit_cast(U2, ke);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) *reinterpret_cast<uint16_t*>(tile + kPlaneBytes + vt_byte(8 * c + e, t)) = vw[e];
-      }
-      if (p >= own_tile * kBT) {
-        *reinterpret_cast<E8*>(own + k_off(t, c)) = ke;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) *reinterpret_cast<uint16_t*>(own + kPlaneBytes + vt_byte(8 * c + e, t)) = vw[e];
-      }
-    }
-  }
-}
-
-// A fused unit's ticket, in launch order (the last workgroup to draw one
-// resets the counter for the next call), passed to every thread through the
-// LDS word `slot`, which is free again on return.
-__device__ __forceinline__ int draw_ticket(const ChunkFuse& cf, int n_kv, int tid, int* slot) {
-  if (tid == 0) {
-    unsigned* ctr = cf.flags + (size_t)n_kv * cf.flag_stride;
-    const unsigned t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (t == gridDim.x - 1) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *slot = (int)t;
-  }
-  __syncthreads();
-  const int t = *slot;
-  __syncthreads();
-  return t;
-}
-
 // Units of a launch: (split, row block, kv head) of a unit index, by
-// blockIdx (each XCD a contiguous run, kv-head-major) or, fused, by ticket.
+// blockIdx (each XCD a contiguous run, kv-head-major).
 struct Unit {
   int split, rb, kvh;
   bool live;
 };
-template <bool FUSE>
-__device__ __forceinline__ Unit unit_of(const ChunkFuse& cf, int n_units, int n_rb, int kv_splits, int tid,
-                                        int* slot) {
+__device__ __forceinline__ Unit unit_of(int n_units, int n_rb, int kv_splits) {
+  // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
+  // XCD b % 8). Units (kv head, row block, split) are numbered kv-head-major
+  // and each XCD takes a contiguous run of them, so the workgroups sharing
+  // an XCD's L2 stream the same kv head's tiles at about the same time.
   Unit u;
-  if constexpr (FUSE) {
-    const int n_kv = n_units / (n_rb * kv_splits);
-    const int t = draw_ticket(cf, n_kv, tid, slot);
-    u.live = t < n_units;
-    u.rb = t / (n_kv * kv_splits);
-    u.kvh = (t / kv_splits) % n_kv;
-    u.split = kv_splits - 1 - t % kv_splits;
-  } else {
-    // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
-    // XCD b % 8). Units (kv head, row block, split) are numbered kv-head-major
-    // and each XCD takes a contiguous run of them, so the workgroups sharing
-    // an XCD's L2 stream the same kv head's tiles at about the same time.
-    const int per_xcd = (n_units + 7) / 8;
-    const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-    u.live = (int)(blockIdx.x / 8) < per_xcd && unit < n_units;
-    u.split = unit % kv_splits;
-    u.rb = (unit / kv_splits) % n_rb;
-    u.kvh = unit / (kv_splits * n_rb);
-  }
+  const int per_xcd = (n_units + 7) / 8;
+  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  u.live = (int)(blockIdx.x / 8) < per_xcd && unit < n_units;
+  u.split = unit % kv_splits;
+  u.rb = (unit / kv_splits) % n_rb;
+  u.kvh = unit / (kv_splits * n_rb);
   return u;
 }
-
-// Tiles a fused unit's wave may read from the staged copy: [tt_lo, ready_to)
-// known complete; ready(tile) waits for the chunk row blocks in tiles
-// [ready_to, tile] (rows per block qr), then extends the range.
-struct TileGate {
-  int ready_to;
-  __device__ __forceinline__ void ready(const ChunkFuse& cf, int kvh, int start, int rows, int qr, int tile,
-                                        int lane) {
-    if (tile < ready_to) return;
-    const int p_lo = max(ready_to * kBT, start), p_hi = min(tile * kBT + kBT, start + rows) - 1;
-    if (p_hi >= p_lo) wait_flags(cf, kvh, (p_lo - start) / qr, (p_hi - start) / qr, lane);
-    ready_to = tile + 1;
-  }
-};
 
 // This lane's 32 elements of one query vector, d = 8kk + 32s + e, from qp
 // (already offset by 8kk). With qn_w, qp is the raw projection and the q
@@ -503,15 +290,14 @@ __device__ __forceinline__ float sum8(bf16x8 v, float acc) {
 // per iteration), and the groups' (O, max, sum) are merged through LDS at the
 // end. With G = 2 two waves share each SIMD, so one's softmax overlaps the
 // other's MFMAs.
-template <int MODE, int G, int W, int MT, int NS, bool FUSE>
+template <int MODE, int G, int W, int MT, int NS>
 __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __restrict__ q,
                                                              const char* __restrict__ stage, int n_stage_tiles,
                                                              int q_stride, int rows, int start, int group, int n_rb,
                                                              int n_units, int kv_splits, float qscale,
                                                              const float* __restrict__ qn_w, float qn_eps,
                                                              const float* __restrict__ qn_tab,
-                                                             float* __restrict__ part, float* __restrict__ out,
-                                                             ChunkFuse cf) {
+                                                             float* __restrict__ part, float* __restrict__ out) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   typedef typename Op<MODE>::V4 V4;
@@ -533,11 +319,9 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   static_assert((size_t)(G - 1) * W * 64 * kX * 4 <= (size_t)G * NS * TB, "group exchange fits the ring");
 
   __shared__ __attribute__((aligned(1024))) char lds[G][NS][TB];
-  // A fused unit's last tile, built in place (see ChunkFuse above).
-  __shared__ __attribute__((aligned(1024))) char own_lds[FUSE ? TB : 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const Unit un = unit_of<FUSE>(cf, n_units, n_rb, kv_splits, tid, reinterpret_cast<int*>(&lds[0][0][0]));
+  const Unit un = unit_of(n_units, n_rb, kv_splits);
   if (!un.live) return;
   const int split = un.split, rb = un.rb, kvh = un.kvh;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -554,22 +338,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   const int n = tt_hi - tt_lo;
   const int n_mine = (n - grp + G - 1) / G;  // this group's tiles: tt_lo + G j + grp
   const int n_iter = (n + G - 1) / G;        // iterations (every group, lockstep)
-  // Fused: the last split writes the block's rows and builds its last tile
-  // (tile n_tiles - 1, the last of the group (n - 1) % G) in own_lds; that
-  // group loads one tile fewer from the staged copy.
-  const bool builds = FUSE && split == kv_splits - 1 && n > 0;
-  const bool own_here = builds && (n - 1) % G == grp;
-  const int n_load = n_mine - (own_here ? 1 : 0);
-  if constexpr (FUSE) {
-    if (builds) {
-      fuse_rows<MODE, G * W * 64>(cf, kvh, start, start + r0, wg_limit - 1, n_tiles - 1, own_lds,
-                                  const_cast<char*>(stage), n_stage_tiles, r0 + rows_here == rows, tid);
-      wait_stores();
-      __syncthreads();
-      if (tid == 0) raise_flag(cf.flags + (size_t)kvh * cf.flag_stride + rb, cf.epoch);
-    }
-  }
-  TileGate gate{tt_lo};
+  const int n_load = n_mine;
 
   // The group's tile j (clamped to its last loaded one, so every wave issues
   // the same number of loads per iteration) into stage s: wave w copies the
@@ -578,9 +347,6 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   auto issue_piece = [&](int j, int s, int i) {
     if (n_load <= 0) return;
     const int tile = tt_lo + G * min(j, n_load - 1) + grp;
-    if constexpr (FUSE) {
-      if (i == 0) gate.ready(cf, kvh, start, rows, qr, tile, lane);  // a tile's pieces go out from piece 0
-    }
     const char* g = src + (size_t)tile * TB;
     const int piece = 1024 * (wv + W * i);
     lds_load16(g + piece, (lds_void*)&lds[grp][s][piece]);
@@ -653,7 +419,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       for (int i = 0; i < LPW; ++i) issue_piece(j + NS - 1, nxt, i);
       continue;
     }
-    const char* kt = own_here && j == n_mine - 1 ? own_lds : lds[grp][s];
+    const char* kt = lds[grp][s];
     const char* vt = kt + P * kPlaneBytes;
     const int t0 = (tt_lo + G * j + grp) * kBT;
 
@@ -909,15 +675,14 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 //   PV(j) on the MFMAs     || mask and column maxima of S(j+1) on the VALU;
 // with tile j + NS - 1's loads issued among the QK MFMAs. One wave's MFMA
 // and VALU streams are independent within each step, so they overlap.
-template <int MODE, int MT, int NS, bool FUSE>
+template <int MODE, int MT, int NS>
 __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict__ q,
                                                         const char* __restrict__ stage, int n_stage_tiles,
                                                         int q_stride, int rows, int start, int group, int n_rb,
                                                         int n_units, int kv_splits, float qscale,
                                                         const float* __restrict__ qn_w, float qn_eps,
                                                         const float* __restrict__ qn_tab,
-                                                        float* __restrict__ part, float* __restrict__ out,
-                                                        ChunkFuse cf) {
+                                                        float* __restrict__ part, float* __restrict__ out) {
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   typedef typename Op<MODE>::V4 V4;
@@ -930,11 +695,9 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
   constexpr float kRescale = 8.0f;
 
   __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
-  // A fused unit's last tile, built in place (see ChunkFuse above).
-  __shared__ __attribute__((aligned(1024))) char own_lds[FUSE ? TB : 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const Unit un = unit_of<FUSE>(cf, n_units, n_rb, kv_splits, tid, reinterpret_cast<int*>(&lds[0][0]));
+  const Unit un = unit_of(n_units, n_rb, kv_splits);
   if (!un.live) return;
   const int split = un.split, rb = un.rb, kvh = un.kvh;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -948,20 +711,7 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
   const int tt_lo = (int)((long)n_tiles * split / kv_splits);
   const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
   const int n = tt_hi - tt_lo;
-  // Fused: the last split writes the block's rows and builds its last tile
-  // in own_lds, loading one tile fewer from the staged copy.
-  const bool builds = FUSE && split == kv_splits - 1 && n > 0;
-  const int n_load = n - (builds ? 1 : 0);
-  if constexpr (FUSE) {
-    if (builds) {
-      fuse_rows<MODE, 256>(cf, kvh, start, start + r0, wg_limit - 1, n_tiles - 1, own_lds, const_cast<char*>(stage),
-                           n_stage_tiles, r0 + rows_here == rows, tid);
-      wait_stores();
-      __syncthreads();
-      if (tid == 0) raise_flag(cf.flags + (size_t)kvh * cf.flag_stride + rb, cf.epoch);
-    }
-  }
-  TileGate gate{tt_lo};
+  const int n_load = n;
 
   // Tile j (clamped to the last loaded one, so every iteration issues LPW
   // loads per wave and the wait counts stay exact) into stage j % NS.
@@ -969,9 +719,6 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
   auto issue_piece = [&](int j, int i) {
     if (n_load <= 0) return;
     const int tile = tt_lo + min(j, n_load - 1);
-    if constexpr (FUSE) {
-      if (i == 0) gate.ready(cf, kvh, start, rows, qr, tile, lane);  // a tile's pieces go out from piece 0
-    }
     const char* g = src + (size_t)tile * TB;
     const int piece = 1024 * (wave + W * i);
     lds_load16(g + piece, (lds_void*)&lds[j % NS][piece]);
@@ -1016,7 +763,7 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
   // tile j + NS - 2's pieces are issued among the MFMAs (the caller is
   // iteration j - 1, whose loads target tile (j - 1) + NS - 1).
   auto qk = [&](int j, f32x4 (&dst)[MT][4], bool loads) {
-    const char* kt = builds && j == n - 1 ? own_lds : lds[j % NS];
+    const char* kt = lds[j % NS];
     V8 ka[2][4];
     auto read_k = [&](int pb, int buf) {
 #pragma unroll
@@ -1109,7 +856,7 @@ __global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict
     }
   };
   auto pv = [&](int j) {
-    const char* vt = (builds && j == n - 1 ? own_lds : lds[j % NS]) + kPlaneBytes;
+    const char* vt = lds[j % NS] + kPlaneBytes;
     V8 va[2][2];
     auto read_v = [&](int b, int buf) {
 #pragma unroll
@@ -1244,56 +991,44 @@ struct PrefillArgs {
   float* part;
   float* out;
   TimedPair tp;
-  ChunkFuse cf;  // cf.k set: the chunk's rows are appended by the launch
 };
 
-template <int MODE, int G, int W, int MT, int NS, bool FUSE>
+template <int MODE, int G, int W, int MT, int NS>
 void launch_main(const PrefillArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
-  launch_timed(a.tp, prefill_kernel<MODE, G, W, MT, NS, FUSE>, dim3(blocks), dim3(G * W * 64), s, a.q,
+  launch_timed(a.tp, prefill_kernel<MODE, G, W, MT, NS>, dim3(blocks), dim3(G * W * 64), s, a.q,
                (const char*)a.stage, a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units,
-               a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out, a.cf);
+               a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
 // F16 / BF16: two groups of 4 waves (2 per SIMD), each with two 32 KiB
 // stages; 128 query vectors = 2 column blocks per wave, 64 = 1. The split
 // mode's 64 KiB tiles allow one group: 4 waves with two stages.
-template <int MODE, int MT, int NS, bool FUSE>
+template <int MODE, int MT, int NS>
 void launch_sp(const PrefillArgs& a, hipStream_t s) {
   const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
-  launch_timed(a.tp, prefill_sp_kernel<MODE, MT, NS, FUSE>, dim3(blocks), dim3(256), s, a.q, (const char*)a.stage,
+  launch_timed(a.tp, prefill_sp_kernel<MODE, MT, NS>, dim3(blocks), dim3(256), s, a.q, (const char*)a.stage,
                a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale,
-               a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out, a.cf);
+               a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
-template <int MODE, bool FUSE>
-void launch_mode_f(int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
+template <int MODE>
+void launch_mode(int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
   constexpr bool kSplit = Op<MODE>::kSplit;
   if constexpr (!kSplit) {
     if (impl == 2) {
       if (vectors == 64)
-        launch_sp<MODE, 1, 4, FUSE>(a, s);
+        launch_sp<MODE, 1, 4>(a, s);
       else
-        launch_sp<MODE, 2, 4, FUSE>(a, s);
+        launch_sp<MODE, 2, 4>(a, s);
       return;
     }
   }
   constexpr int G = kSplit ? 1 : 2;
   if (vectors == 64)
-    launch_main<MODE, G, 4, 1, 2, FUSE>(a, s);
+    launch_main<MODE, G, 4, 1, 2>(a, s);
   else
-    launch_main<MODE, G, 4, 2, 2, FUSE>(a, s);
-}
-
-template <int MODE>
-void launch_mode(int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
-  if constexpr (!Op<MODE>::kSplit) {
-    if (a.cf.k) {
-      launch_mode_f<MODE, true>(vectors, impl, a, s);
-      return;
-    }
-  }
-  launch_mode_f<MODE, false>(vectors, impl, a, s);
+    launch_main<MODE, G, 4, 2, 2>(a, s);
 }
 
 void launch_attention(uint32_t mode, int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
@@ -1360,7 +1095,7 @@ HipStatus ready_persistent(rv_kv* kv, size_t layer, uint32_t mode, hipStream_t s
       st.what = "hipMalloc prefill staging";
       return st;
     }
-    if (kv->staged[layer]) kv->retired.push_back(kv->staged[layer]);
+    if (kv->staged[layer]) kv->retire(kv->staged[layer], kv->staged_bytes[layer]);
     kv->staged[layer] = p;
     kv->staged_bytes[layer] = stage_bytes;
   }
@@ -1368,6 +1103,12 @@ HipStatus ready_persistent(rv_kv* kv, size_t layer, uint32_t mode, hipStream_t s
 }
 
 }  // namespace
+
+size_t prefill_stage_bound(const rv_kv* kv) {
+  if (kv->head_dim != kD) return 0;
+  const size_t cap_tiles = (kv->capacity + kBT - 1) / kBT;
+  return kv->n_kv_heads * cap_tiles * tile_bytes_of(RV_PREFILL_EXACT);
+}
 
 // head_dim 128 and a group that divides 64 (so a workgroup's 64 or 128
 // columns are whole rows of the group); any other geometry runs each row
@@ -1378,16 +1119,9 @@ bool prefill_supported(const rv_kv* kv, size_t group, size_t positions) {
 }
 
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
-                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s,
-                         const ChunkFuse* cf) {
+                         size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s) {
   HipStatus st;
   if (rows == 0) return st;
-  const bool fused = cf && cf->k;
-  if (fused && (!chunk_fusable(kv, n_q_heads / kv->n_kv_heads, mode, s) || !kv->chunk_flags)) {
-    st.e = hipErrorInvalidValue;
-    st.what = "fused prefill chunk outside its scope";
-    return st;
-  }
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const int n_kv = (int)kv->n_kv_heads;
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
@@ -1479,8 +1213,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   }
   PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
                 (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
-                qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s),
-                fused ? *cf : ChunkFuse{}};
+                qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s)};
   // Attention kernel: the software-pipelined one for short KV ranges (at most
   // 16 tiles per split, e.g. a chunk on an empty cache), where its single
   // barrier per tile and four-wave workgroups finish sooner; the two-group
@@ -1538,41 +1271,6 @@ HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t row
   sd->mode = m;
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill stage launch";
-  return st;
-}
-
-bool chunk_fusable(const rv_kv* kv, size_t group, uint32_t mode, hipStream_t s) {
-  const uint32_t m = mode & RV_PREFILL_MODE_MASK;
-  return (m == RV_PREFILL_F16 || m == RV_PREFILL_BF16) && prefill_supported(kv, group, 0) && !capturing(s);
-}
-
-HipStatus ensure_chunk_flags(rv_kv* kv) {
-  HipStatus st;
-  if (kv->chunk_flags) return st;
-  if (capturing(kv->stream)) {
-    st.e = hipErrorStreamCaptureUnsupported;
-    st.what = "prefill chunk flags under graph capture";
-    return st;
-  }
-  // A row block holds at least one row (64 / group of them, or 128 / group);
-  // the ticket counter follows the flags.
-  const size_t stride = kv->capacity + 1;
-  const size_t bytes = (kv->n_kv_heads * stride + 1) * sizeof(unsigned);
-  void* p = nullptr;
-  st.e = hipMalloc(&p, bytes);
-  if (st.e != hipSuccess) {
-    st.what = "hipMalloc prefill chunk flags";
-    return st;
-  }
-  // Ordered before the first fused launch on the same stream (never captured).
-  st.e = hipMemsetAsync(p, 0, bytes, kv->stream);
-  if (st.e != hipSuccess) {
-    (void)hipFree(p);
-    st.what = "hipMemsetAsync prefill chunk flags";
-    return st;
-  }
-  kv->chunk_flags = (unsigned*)p;
-  kv->chunk_flag_stride = stride;
   return st;
 }
 

@@ -384,6 +384,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
   __shared__ rv_block_q8_k lk[kFusedMaxKBlocks];
   __shared__ rv_block_q8_0 l0[kFusedMax0Blocks];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (a.gate_pos && *a.gate_pos > a.gate_max) return;  // the whole grid: its decode step was refused
   const int first = (int)blockIdx.x * kFusedWaves;
   // The segments this workgroup's rows touch decide which forms it needs.
   bool need_k = false, need_0 = false;

@@ -35,6 +35,10 @@ struct FusedProjArgs {
   int n_rows[3];
   const float* norm_w;
   float eps;
+  // Optional: a token graph's device position; above gate_max the launch
+  // writes nothing (its decode step was refused).
+  const uint32_t* gate_pos;
+  uint32_t gate_max;
 };
 
 // The attention projections of one token (forward.rs:2574-2646) as the C
@@ -71,6 +75,10 @@ struct OutProj {
   size_t hidden;
   bool add;          // o[i] += dot (the residual add) instead of o[i] = dot
   void* scratch;     // out_proj_scratch_bytes(q_dim, hidden, add) bytes
+  // Optional (fused launch only): nothing is written when *gate_pos >
+  // gate_max (a token graph's refused decode step).
+  const uint32_t* gate_pos = nullptr;
+  uint32_t gate_max = 0;
 };
 size_t in_proj_scratch_bytes(size_t hidden, bool norm);
 size_t out_proj_scratch_bytes(size_t q_dim, size_t hidden, bool add);

@@ -131,3 +131,52 @@ def test_mirror_argument_checks_reject_bad_device_tensors():
         ro = np.zeros(4, np.float32)
         ro.flags.writeable = False
         A._Arg(ro, writable=True)
+
+
+def test_projected_device_bytes_adds_what_the_device_path_keeps(lib):
+    """rv_kv_projected_device_bytes (a fresh cache's rv_kv_device_bytes
+    bound): rv_kv_projected_bytes' planes plus the decode workspace, tickets,
+    one EXACT staged copy per layer and the (cos, sin) table. Pinned by what
+    the header states of each part rather than by restating the sum:
+    - it exceeds the planes, and the excess grows by exactly one staged copy
+      plus one pair of planes per added layer (the workspace, tickets and
+      table do not depend on the layer count);
+    - an EXACT staged copy is 17/16 of a layer's f32 planes (17/8 of its f16
+      planes): 64-position tiles of two split planes of 2-byte elements plus
+      4 KiB of exponents per 64 KiB of f32 K and V;
+    - the table is capacity * head_dim * 4 bytes: doubling the capacity of a
+      head_dim-128 cache adds 2x the planes, the staged copies and the table,
+      and a decode workspace no smaller;
+    - a head_dim other than 128 has no staged copy and the 1 MiB workspace."""
+    from ctypes import byref, c_uint64
+
+    def proj(L_, H, D, C, elem):
+        out, err = c_uint64(), L.RvError()
+        rc = lib.rv_kv_projected_device_bytes(L_, H, D, C, elem, byref(out), byref(err))
+        assert rc == 0, (rc, err.what)
+        return out.value
+
+    def planes(L_, H, D, C, elem):
+        out, err = c_uint64(), L.RvError()
+        assert lib.rv_kv_projected_bytes(L_, H, D, C, elem, byref(out), byref(err)) == 0
+        return out.value
+
+    for elem, ratio in ((L.RV_ELEM_F32, (17, 16)), (L.RV_ELEM_F16, (17, 8))):
+        one, two = proj(1, 4, 128, 4096, elem), proj(2, 4, 128, 4096, elem)
+        layer_planes = planes(1, 4, 128, 4096, elem)
+        staged = (two - one) - layer_planes
+        assert staged * ratio[1] == layer_planes * ratio[0], (elem, staged, layer_planes)
+        # config 2's cache: 48 layers at 4096 positions, fp32.
+        p48 = proj(48, 4, 128, 4096, elem)
+        assert p48 == one + 47 * (two - one)
+        fixed = one - layer_planes - staged  # workspace + tickets + table
+        assert fixed >= 1 << 20 and fixed >= 4096 * 128 * 4
+        big = proj(1, 4, 128, 8192, elem)
+        assert big - (2 * layer_planes + 2 * staged) >= fixed + 4096 * 128 * 4
+    # No staged copy off head_dim 128: the difference per layer is the planes.
+    a, b = proj(1, 2, 64, 1000, L.RV_ELEM_F16), proj(3, 2, 64, 1000, L.RV_ELEM_F16)
+    assert b - a == 2 * planes(1, 2, 64, 1000, L.RV_ELEM_F16)
+    assert a - planes(1, 2, 64, 1000, L.RV_ELEM_F16) >= (1 << 20) + 1000 * 64 * 4
+    # Invalid geometries fail as rv_kv_projected_bytes does.
+    out, err = c_uint64(), L.RvError()
+    assert lib.rv_kv_projected_device_bytes(0, 4, 128, 16, L.RV_ELEM_F16, byref(out), byref(err)) == 1

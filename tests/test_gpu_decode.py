@@ -252,31 +252,55 @@ def test_decode_short_contexts_in_one_split(elem, lengths):
         gate(out, ref.attention(q, 0, scale, positions=p), what=f"{elem} positions {p}")
 
 
-@pytest.mark.parametrize("elem,n_pos,fan", [("f16", 300, 0), ("f32", 4096, 0), ("f16", 4096, 64), ("f16", 20000, 0)])
-def test_in_launch_ticket_merge_matches_the_oracle(elem, n_pos, fan):
-    # RV_TUNE_DECODE_MERGE 1: the last workgroup of each group of splits folds
-    # the group inside the tile launch, and with more than one group the last
-    # group folds their rows (300: 5 splits in one group; 4096: 64 splits in
-    # 8 groups of 8, or one group with fan 64; 20000: 63 splits of 320).
-    # Three calls in a row: the last arriver resets each ticket, so every
-    # call folds in the same order and gives the same bits.
+@pytest.mark.parametrize("elem,n_pos,waves,split_len", [
+    ("f32", 4096, 4, 0), ("f32", 4096, 2, 32), ("f32", 4096, 1, 16), ("f16", 32768, 4, 0), ("f16", 300, 4, 0),
+    ("f32", 1000, 4, 64), ("f16", 20000, 1, 0), ("f32", 129, 1, 16), ("f16", 8193, 2, 0)])
+def test_in_launch_xcd_merge_matches_the_oracle(elem, n_pos, waves, split_len):
+    # RV_TUNE_DECODE_MERGE 1: the splits of a kv head that share an XCD (s =
+    # r mod 8) are folded inside that XCD's L2 by the last to finish, then
+    # the last of the <= 8 group rows folds them across XCDs. Shapes: whole
+    # and partial groups of 8 (4096 / 64: 8 per group; 1000 / 64: 16 splits;
+    # 300: 5 splits, each its own group; 129 / 16: 9 splits, one group of
+    # 2), 1-, 2- and 4-wave workgroups. Three calls in a row give the same
+    # bits (every ticket is reset by its last arriver), the kv-range union is
+    # bit-identical to the whole call, and the result is within the fp32 gate
+    # of the oracle and of the separate merge kernel.
     torch_cuda()
-    say(f"case ticket merge elem={elem} n_pos={n_pos} fan={fan}")
-    rng = Rng(0x71C7 + n_pos + fan)
+    say(f"case xcd merge elem={elem} n_pos={n_pos} waves={waves} split_len={split_len}")
+    rng = Rng(0x8CD + n_pos + 7 * waves + split_len)
     kv, ref = twin_caches(rng, 1, 4, 128, n_pos, elem)
-    kv.set_tuning(rv.RV_TUNE_DECODE_MERGE, 1)
-    if fan:
-        kv.set_tuning(rv.RV_TUNE_DECODE_FAN, fan)
+    if not kv.xcd_ok():
+        pytest.skip("the device does not deal workgroups to XCDs round robin")
     q = rng.vec_in(32 * 128, -1.0, 1.0)
     scale = np.float32(1.0) / np.sqrt(np.float32(128))
+    want = ref.attention(q, 0, scale)
+    kv.set_tuning(rv.RV_TUNE_DECODE_WAVES, waves)
+    if split_len:
+        kv.set_tuning(rv.RV_TUNE_DECODE_SPLIT_LEN, split_len)
+    kv.set_tuning(rv.RV_TUNE_DECODE_MERGE, 2)
+    sep = np.full(q.size, np.nan, np.float32)
+    rv.decode_attention(q, kv, 0, scale, None, sep)
+    kv.set_tuning(rv.RV_TUNE_DECODE_MERGE, 1)
     outs = []
     for _ in range(3):
         out = np.full(q.size, np.nan, np.float32)
         rv.decode_attention(q, kv, 0, scale, None, out)
         outs.append(out)
-    gate(outs[0], ref.attention(q, 0, scale), what=f"ticket merge {elem} {n_pos} fan {fan}")
+    gate(outs[0], want, what=f"xcd merge {elem} {n_pos}")
+    gate(outs[0], sep.astype(np.float64), what="xcd merge vs merge kernel")
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    got = np.full(q.size, np.nan, np.float32)
+    for u in range(4):
+        r = oracle.kv_head_range(4, 4, u, u + 1)
+        part = np.full(len(r) * 1024, np.nan, np.float32)
+        rv.decode_attention_kv_range_in(q, kv, 0, scale, r, 10 ** 6, part)
+        got[r.start * 1024:r.stop * 1024] = part
+    assert np.array_equal(got.view(np.uint32), outs[0].view(np.uint32))
+    for p in (1, 17, n_pos // 2 + 1):
+        out = np.full(q.size, np.nan, np.float32)
+        rv.attention_at(q, kv, 0, p, scale, None, out)
+        gate(out, ref.attention(q, 0, scale, positions=p), what=f"xcd merge attention_at p={p}")
 
 
 @pytest.mark.parametrize("n_pos", [5000, 20000])

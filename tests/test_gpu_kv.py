@@ -115,3 +115,44 @@ def test_layer_views_cover_exactly_the_cursor():
     p2, _ = kv.k_layer(2)
     assert p2 - p0 == 2 * 10 * 32 * 4  # layer * capacity * kv_dim * 4 bytes
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("elem", ["f16", "f32"])
+def test_device_bytes_account_for_everything_the_cache_allocates(elem):
+    """rv_kv_device_bytes: a fresh cache holds its planes, workspace and
+    tickets, and its bound is rv_kv_projected_device_bytes of its geometry;
+    prefill chunks add one staged copy per layer they touch (within the
+    bound when in the bound's EXACT mode; an F16 copy is smaller), and the
+    device-position step's (cos, sin) table. `now` never exceeds `bound`
+    while nothing outgrows the bound's assumptions."""
+    torch = torch_cuda()
+    say(f"case device bytes elem={elem}")
+    n_layers, n_kv, hd, cap = 3, 4, 128, 256
+    kv = rv.KvCache(n_layers, n_kv, hd, cap, elem)
+    now0, bound0 = kv.device_bytes()
+    planes = rv.KvCache.projected_bytes(n_layers, n_kv, hd, cap, elem)
+    assert bound0 == rv.KvCache.projected_device_bytes(n_layers, n_kv, hd, cap, elem)
+    assert planes < now0 < bound0
+    rng = Rng(0xB17E)
+    rows = 64
+    q = dev(rng.vec_in(rows * 32 * hd, -1, 1))
+    k, v = dev(rng.vec_in(rows * n_kv * hd, -1, 1)), dev(rng.vec_in(rows * n_kv * hd, -1, 1))
+    w = dev(np.ones(hd, np.float32))
+    out = torch.zeros(rows * 32 * hd, device="cuda")
+    rv.prefill_chunk(kv, 0, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="exact")
+    rv.prefill_chunk(kv, 1, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="f16")
+    torch.cuda.synchronize()
+    now1, bound1 = kv.device_bytes()
+    tiles = (cap + 63) // 64
+    exact_copy, f16_copy = n_kv * tiles * (4 * 16384 + 4096), n_kv * tiles * 2 * 16384
+    qbuf = rows * hd * 4  # the chunk's (cos, sin) rows
+    assert now1 - now0 >= exact_copy + f16_copy + qbuf, (now1 - now0)
+    assert now1 <= bound1 and bound1 >= bound0
+    pos = torch.tensor([rows], dtype=torch.int32, device="cuda")
+    q1 = dev(rng.vec_in(32 * hd, -1, 1))
+    k1, v1 = dev(rng.vec_in(n_kv * hd, -1, 1)), dev(rng.vec_in(n_kv * hd, -1, 1))
+    o1 = torch.zeros(32 * hd, device="cuda")
+    rv.decode_step_dev(kv, 0, q1, k1, v1, w, w, 1e-6, 1e6, pos, cap - 1, 0.088, o1)
+    torch.cuda.synchronize()
+    now2, bound2 = kv.device_bytes()
+    assert now2 - now1 >= cap * hd * 4 and now2 <= bound2

@@ -171,6 +171,90 @@ def test_decode_step_dev_rejections():
 
 
 @pytest.mark.parametrize("elem", ["f32", "f16"])
+def test_a_device_position_past_the_plan_is_refused_on_the_device(elem):
+    """A device-position step whose *d_position (read as unsigned) is past
+    its max_position writes no cache row and leaves `out` as it was, eagerly
+    and in a graph replay, and records CapacityExceeded (layer, max_position +
+    1) in the cache's device status, as KvCache::append refuses a full layer
+    (kv/mod.rs:352-357); rv_kv_commit reports it too and moves no cursor. An
+    int32 -1 (0xFFFFFFFF) is past every plan. The attention block's device
+    form leaves the residual untouched the same way."""
+    torch = torch_cuda()
+    say(f"case device position past the plan elem={elem}")
+    rng = Rng(0x70CA)
+    (kv,), _ = _caches(rng, 1, 2, 2, 128, 4, 16, elem)
+    q, k, v = dev(rng.vec_in(8 * 128, -1, 1)), dev(rng.vec_in(256, -1, 1)), dev(rng.vec_in(256, -1, 1))
+    w = dev(np.ones(128, np.float32))
+    out = torch.zeros(8 * 128, device="cuda")
+    max_pos = 9
+    # Rows past a layer's length cannot be read until committed; the planes
+    # start zeroed (rv_kv_new), so every row a step did not write stays zero.
+    rows_before = [(kv.k_row(layer, p), kv.v_row(layer, p)) for layer in range(2) for p in range(4)]
+    for bad in (10, 15, -1):
+        pos = torch.tensor([bad], dtype=torch.int32, device="cuda")
+        out.fill_(float("nan"))
+        rv.decode_step_dev(kv, 1, q, k, v, w, w, EPS, THETA, pos, max_pos, 0.1, out)
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(out).all()), bad
+        with pytest.raises(rv.KvError) as ei:
+            kv.device_status()
+        assert ei.value.variant == "CapacityExceeded" and ei.value.fields["layer"] == 1
+        assert ei.value.fields["capacity"] == max_pos + 1 and ei.value.raw[3] == (bad & 0xFFFFFFFF)
+        kv.device_status()  # read once, cleared
+    # In a graph: the first replay at position 9 writes row 9, the second (10)
+    # is refused.
+    pos = torch.tensor([max_pos], dtype=torch.int32, device="cuda")
+    rv.decode_step_dev(kv, 0, q, k, v, w, w, EPS, THETA, pos, max_pos, 0.1, out)  # builds the table
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rv.decode_step_dev(kv, 0, q, k, v, w, w, EPS, THETA, pos, max_pos, 0.1, out)
+        rv.position_advance(kv, pos, 1)
+    out.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(out).any())
+    kv.device_status()
+    out.fill_(float("nan"))
+    g.replay()  # position 10
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(out).all()) and int(pos.item()) == max_pos + 2
+    with pytest.raises(rv.KvError) as ei:
+        kv.commit(0, 1)
+    assert ei.value.variant == "CapacityExceeded" and ei.value.fields["layer"] == 0 and kv.len(0) == 4
+    kv.commit(0, 12)  # the status was read and cleared: every row becomes readable
+    kv.commit(1, 12)
+    assert np.any(kv.k_row(0, 9) != 0) and np.any(kv.v_row(0, 9) != 0)
+    for layer in range(2):
+        for p in range(16):
+            k_, v_ = kv.k_row(layer, p), kv.v_row(layer, p)
+            if p < 4:
+                k0, v0 = rows_before[layer * 4 + p]
+                assert np.array_equal(k_, k0) and np.array_equal(v_, v0), (layer, p)
+            elif (layer, p) != (0, 9):  # the accepted steps' row
+                assert not np.any(k_) and not np.any(v_), (layer, p)
+
+    from test_gpu_block import Layer
+
+    Q = oracle
+    hd, n_heads, n_kv, hidden, cap = 128, 32, 4, 2048, 64
+    q_dim, kv_dim = n_heads * hd, n_kv * hd
+    nrng = np.random.default_rng(0xB70E)
+    lay = Layer(torch, nrng, hidden, q_dim, kv_dim, hd, Q.RV_QF_Q4_K, Q.RV_QF_Q6_K, Q.RV_QF_Q5_K)
+    (kb,), _ = _caches(Rng(0xB70F), 1, 1, n_kv, hd, 8, cap, elem)
+    sc = torch.empty(B.scratch_bytes(hidden, q_dim, kv_dim), dtype=torch.uint8, device="cuda")
+    res = torch.from_numpy((1.5 * nrng.standard_normal(hidden)).astype(np.float32)).cuda()
+    keep = res.clone()
+    pos = torch.tensor([40], dtype=torch.int32, device="cuda")
+    B.attn_block_decode_dev(kb, 0, res, q_dim, lay.dev, EPS, THETA, pos, 20, 0.088, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(res, keep)
+    with pytest.raises(rv.KvError) as ei:
+        kb.device_status()
+    assert ei.value.variant == "CapacityExceeded" and ei.value.fields["capacity"] == 21
+
+
+@pytest.mark.parametrize("elem", ["f32", "f16"])
 def test_block_graph_replays_follow_the_eager_blocks(elem):
     """The attention block of two layers per token captured once with the
     position on the device; each replay's residual equals eager
