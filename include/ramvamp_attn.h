@@ -294,15 +294,14 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
  * Exposed for benchmarking sweeps; results never depend on them beyond
  * floating-point reassociation within the stated tolerance. */
 #define RV_TUNE_DECODE_SPLIT_LEN 1 /* positions per decode split (rounded to the workgroup step) */
-#define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill row tile (1..8) */
+#define RV_TUNE_PREFILL_KV_SPLIT 2 /* KV splits per prefill block of query vectors (1..8) */
 #define RV_TUNE_DECODE_WAVES 3     /* waves per MFMA decode workgroup: 4 (default) or 8; VALU path: 4 or 8 (default) */
-#define RV_TUNE_PREFILL_ROWS 4     /* query rows per prefill tile: 8 or 16 */
+#define RV_TUNE_PREFILL_ROWS 4     /* EXACT prefill: query rows per workgroup, 8 or 16 (group 8) */
 #define RV_TUNE_DECODE_HG 5        /* query heads per VALU decode workgroup: 1, 2, 4 or 8 */
 #define RV_TUNE_DECODE_IMPL 6      /* decode kernel: 0 auto (MFMA tiles when head_dim 128 and group <= 16; f16 planes on f16
                                       MFMA operands split hi/lo), 1 VALU subgroups, 2 MFMA tiles with fp32 operands,
                                       3 MFMA tiles staged through LDS (4-wave workgroups) */
 #define RV_TUNE_KERNEL_TIMING 7    /* 1: time the dominant kernel of every call with HIP events (not under capture) */
-#define RV_TUNE_PREFILL_IMPL 8     /* prefill attention kernel: 0 auto, 1 two wave groups, 2 software-pipelined */
 #define RV_TUNE_DECODE_DEPTH 9     /* 16-position tiles in flight per decode wave: 1 (default), 2 or 4 (f16 planes) */
 #define RV_TUNE_DECODE_MERGE 11    /* decode split merge: 0 auto, 1 inside the tile launch (a first level inside each
                                       XCD's L2, then across XCDs), 2 a second kernel */

@@ -38,7 +38,6 @@ from ._lib import (  # noqa: F401  (knobs of KvCache.set_tuning)
     RV_TUNE_DECODE_SPLIT_LEN,
     RV_TUNE_DECODE_WAVES,
     RV_TUNE_KERNEL_TIMING,
-    RV_TUNE_PREFILL_IMPL,
     RV_TUNE_PREFILL_KV_SPLIT,
     RV_TUNE_PREFILL_ROWS,
 )

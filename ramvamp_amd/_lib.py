@@ -27,7 +27,6 @@ RV_TUNE_PREFILL_ROWS = 4
 RV_TUNE_DECODE_HG = 5
 RV_TUNE_DECODE_IMPL = 6
 RV_TUNE_KERNEL_TIMING = 7
-RV_TUNE_PREFILL_IMPL = 8
 RV_TUNE_DECODE_DEPTH = 9
 RV_TUNE_DECODE_MERGE = 11
 RV_NOALLOC_SCRATCH_BYTES = 8 << 20

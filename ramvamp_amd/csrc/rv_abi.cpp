@@ -513,7 +513,8 @@ void rv_kv_free(rv_kv* kv) {
     DeviceGuard dg(kv->device);
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
     else (void)hipDeviceSynchronize();
-    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab})
+    for (void* p : {kv->k, kv->v, kv->ws, (void*)kv->qbuf, kv->stage, (void*)kv->tickets, (void*)kv->rope_tab,
+                    (void*)kv->pf_tickets})
       if (p) (void)hipFree(p);
     for (void* p : kv->staged)
       if (p) (void)hipFree(p);
@@ -1026,18 +1027,26 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
   Plan p{q_dim / hd, q_dim / hd / kv->n_kv_heads, 0};
   rv::HipStatus hs;
   if (rv::prefill_supported(kv, p.group, start + rows)) {
-    // k/v prologue + append (also into the layer's staged tiles) and the
-    // rows' (cos, sin) table; the q prologue runs inside the attention
-    // kernel's query loads.
+    // k/v prologue + append, also into the layer's staged tiles. Where the
+    // chunk's rows are staged as they are appended (F16 / BF16, uncaptured),
+    // the same launch writes the q heads in the attention kernel's prepared
+    // layout; otherwise it writes the rows' (cos, sin) table and the q
+    // prologue runs inside the attention kernel's query loads.
     rv::StageDst sd;
-    hs = rv::ensure_qbuf(kv, rows * hd * sizeof(float));
-    if (hs.e == hipSuccess) hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
+    hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
+    const bool prep = sd.base != nullptr;
     if (hs.e == hipSuccess)
-      hs = rv::launch_row_prologue(kv, layer, len, nullptr, nullptr, 0, dk, dv, rows, nullptr, dwk, eps, inv, start,
-                                   kv->qbuf, &sd, kv->stream);
+      hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, start + rows, kv->n_kv_heads, p.group)
+                                    : rows * hd * sizeof(float));
+    const rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, start + rows, p.group, scale) : rv::QPrep{};
+    if (hs.e == hipSuccess)
+      hs = rv::launch_row_prologue(kv, layer, len, prep ? dq : nullptr, nullptr, prep ? p.n_q_heads : 0, dk, dv, rows,
+                                   prep ? dwq : nullptr, dwk, eps, inv, start, prep ? nullptr : kv->qbuf, &sd,
+                                   kv->stream, prep ? &qp : nullptr);
     if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
     kv->lens[layer] = len + rows;
-    const rv::QNorm qn{dwq, eps, kv->qbuf};
+    rv::QNorm qn{dwq, eps, kv->qbuf};
+    if (prep) qn.prepped = (const char*)kv->qbuf;
     hs = rv::launch_prefill(kv, dq, rows, p.n_q_heads, layer, start, scale, dout, flags, &qn, kv->stream);
     if (hs.e != hipSuccess) return hip_fail(err, hs.e, hs.what);
   } else {
@@ -1062,7 +1071,6 @@ int32_t rv_kv_set_tuning(rv_kv* kv, int32_t knob, int64_t value, rv_error* err) 
     case RV_TUNE_PREFILL_ROWS: kv->tune_prefill_rows = value; break;
     case RV_TUNE_DECODE_HG: kv->tune_decode_hg = value; break;
     case RV_TUNE_DECODE_IMPL: kv->tune_decode_impl = value; break;
-    case RV_TUNE_PREFILL_IMPL: kv->tune_prefill_impl = value; break;
     case RV_TUNE_KERNEL_TIMING: kv->timing = value != 0; break;
     case RV_TUNE_DECODE_DEPTH: kv->tune_decode_depth = value; break;
     case RV_TUNE_DECODE_MERGE: kv->tune_decode_merge = value; break;

@@ -165,6 +165,21 @@ __device__ __forceinline__ void lds_load16(const void* g, lds_void* l) {
 #endif
 }
 
+// The same copy issued from inline assembly, to the LDS byte offset `l`: the
+// compiler does not see it write LDS, so it adds no wait for it before later
+// LDS reads (for the builtin it waits for every outstanding load before any
+// LDS read whose address it cannot tell apart, which serialises a ring of
+// stages indexed at run time). The caller orders every read of the
+// destination after the copy itself: wait_vmcnt, then a barrier when other
+// waves read it. m0 is an input operand, so the compiler loads it; the
+// s_nop covers the one wait state between an m0 write and an LDS DMA.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t l) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(l) : "memory");
+#endif
+}
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
+
 // s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 template <int N>

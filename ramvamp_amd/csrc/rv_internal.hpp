@@ -49,6 +49,10 @@ struct rv_kv {
   std::vector<void*> staged;
   std::vector<size_t> staged_bytes, staged_pos;
   std::vector<uint32_t> staged_mode;
+  // The F16 / BF16 prefill's split-fold tickets: one 128-byte line per
+  // (kv head, 256-vector block) unit, zero between calls.
+  unsigned* pf_tickets = nullptr;
+  size_t pf_ticket_units = 0;
   // Staging for RV_HOST_PTRS calls.
   void* stage = nullptr;
   size_t stage_bytes = 0;
@@ -65,7 +69,6 @@ struct rv_kv {
   int64_t tune_decode_waves = 0;
   int64_t tune_prefill_rows = 0;
   int64_t tune_decode_hg = 0;
-  int64_t tune_prefill_impl = 0;  // 0 auto, 1 two wave groups, 2 software-pipelined
   int64_t tune_decode_impl = 0;  // 0 auto (MFMA tiles: head_dim 128, group <= 16), 1 VALU subgroups, 3 LDS-staged tiles
   int64_t tune_decode_depth = 0;  // tiles in flight per wave (1, 2, 4); 0 auto
   int64_t tune_decode_merge = 0;  // 0 auto, 1 in-launch XCD merge, 2 separate merge kernel
@@ -178,10 +181,26 @@ struct StageDst {
 // With sd (head_dim 128 only), the k and v rows as the cache holds them are
 // also written into the staged tiles at cache_row + r, and the rest of the
 // last tile is zeroed.
+// With qp (and sd, so the chunk's q heads run in the same launch), q heads
+// go into the prepared layout of the F16 / BF16 prefill instead of q_out.
+struct QPrep {
+  char* base = nullptr;
+  int group = 0;       // query heads per kv head
+  int qr = 0;          // rows per unit: its columns / group
+  int n_rb = 0;        // units per kv head
+  float qscale = 0.f;  // log2(e) * softmax scale
+};
+// Columns per unit of the F16 / BF16 prefill kernel for a chunk whose last
+// row sees `positions` positions; the prepared queries' layout follows it.
+int p32_vectors(size_t positions);
+// Bytes of the prepared queries of a chunk of `rows` rows ending at
+// `positions`, and their layout.
+size_t qprep_bytes(size_t rows, size_t positions, size_t n_kv_heads, size_t group);
+QPrep qprep_plan(char* base, size_t rows, size_t positions, size_t group, float scale);
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
                               const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
-                              const StageDst* sd, hipStream_t s);
+                              const StageDst* sd, hipStream_t s, const QPrep* qp = nullptr);
 
 // ---- decode (rv_decode.hip) ------------------------------------------------------
 // The workspace the MFMA decode path can need for any call on this cache
@@ -249,10 +268,14 @@ HipStatus launch_decode_pro(rv_kv* kv, const float* q_raw, size_t n_q_heads, siz
 // w and eps, rotation with the rows' (cos, sin) table (from
 // launch_row_prologue, or the cache's rope_tab): row r's at tab + r * 128,
 // 64 cos then 64 sin.
+// With `prepped` (F16 / BF16 only), the queries are already normed, rotated,
+// scaled and rounded in the prepared layout (QPrep) and w, eps, tab and the
+// q rows are not read.
 struct QNorm {
   const float* w = nullptr;
   float eps = 0.f;
   const float* tab = nullptr;
+  const char* prepped = nullptr;
 };
 // Before a prefill chunk appends `rows` rows at pos0 = len(layer) and runs
 // launch_prefill: readies the layer's persistent staged copy in `mode`
@@ -267,6 +290,9 @@ HipStatus prepare_prefill_stage(rv_kv* kv, size_t layer, size_t pos0, size_t row
 // post-RoPE, or the raw projections when qn is given.
 HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q_heads, size_t layer,
                          size_t start, float scale, float* out, uint32_t mode, const QNorm* qn, hipStream_t s);
+
+// The F16 / BF16 prefill's fold tickets for `units` units (not under capture).
+HipStatus ensure_prefill_tickets(rv_kv* kv, size_t units);
 
 // The largest staged copy one layer's prefill can hold (EXACT tiles over the
 // whole capacity).

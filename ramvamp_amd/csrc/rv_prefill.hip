@@ -168,7 +168,8 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
     const int c = 4 * (tid & 1) + cc;
     V8 hi, lo;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) split2v<E>(P == 2 ? ldexpf(vt[vt_pos(c, j)][d], cx) : vt[vt_pos(c, j)][d], hi, lo, j);
+    for (int j = 0; j < 8; ++j)
+      split2v<E>(P == 2 ? ldexpf(vt[vt_pos_m<MODE>(c, j)][d], cx) : vt[vt_pos_m<MODE>(c, j)][d], hi, lo, j);
     *reinterpret_cast<V8*>(vdst + vt_off(d, c)) = hi;
     if constexpr (P == 2) *reinterpret_cast<V8*>(vdst + kPlaneBytes + vt_off(d, c)) = lo;
   }
@@ -667,284 +668,419 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   }
 }
 
-// Software-pipelined single-group kernel (F16 / BF16): 4 waves, one per
-// SIMD, each owning MT column blocks; tiles stream through a ring of NS
-// 32 KiB stages. Iteration j, after one barrier:
-//   (rare) rescale O, the sum and S(j) when S(j)'s maximum moved m_run;
-//   QK(j+1) on the MFMAs   || P(j) = exp2(S(j)) and its sums on the VALU;
-//   PV(j) on the MFMAs     || mask and column maxima of S(j+1) on the VALU;
-// with tile j + NS - 1's loads issued among the QK MFMAs. One wave's MFMA
-// and VALU streams are independent within each step, so they overlap.
-template <int MODE, int MT, int NS>
-__global__ __launch_bounds__(256) void prefill_sp_kernel(const float* __restrict__ q,
-                                                        const char* __restrict__ stage, int n_stage_tiles,
-                                                        int q_stride, int rows, int start, int group, int n_rb,
-                                                        int n_units, int kv_splits, float qscale,
-                                                        const float* __restrict__ qn_w, float qn_eps,
-                                                        const float* __restrict__ qn_tab,
-                                                        float* __restrict__ part, float* __restrict__ out) {
-  typedef typename Op<MODE>::E E;
-  typedef typename Op<MODE>::V8 V8;
-  typedef typename Op<MODE>::V4 V4;
-  static_assert(!Op<MODE>::kSplit, "one plane per operand");
-  static_assert(NS >= 3, "K(j+1), V(j) and the loads of a later tile need three stages");
-  constexpr int W = 4;
-  constexpr int M = 16 * W * MT;
-  constexpr int TB = 2 * kPlaneBytes;
-  constexpr int LPW = TB / 1024 / W;  // 8
-  constexpr float kRescale = 8.0f;
+// ---- F16 / BF16: v_mfma_f32_32x32x16 tiles --------------------------------------------
+//
+// prefill32_kernel: one workgroup of 8 waves per (kv head, block of 256 query
+// vectors, KV split); wave w owns the 32 columns [32 w, 32 w + 32) (column m
+// is head m / qr, row m % qr of the block, qr = 256 / group). Every wave
+// computes every 64-position tile of the workgroup's range for its columns,
+// so one staged tile in LDS feeds 256 columns and each operand read feeds an
+// MFMA of 32 columns (twice the columns per LDS byte of a 16x16 tile). The
+// two waves sharing a SIMD are left to the hardware's interleaving: with
+// both issuing QK, softmax and PV in the same order one's VALU work runs
+// under the other's MFMAs (a prototype that offset the two wave groups by a
+// tile phase measured 12-16 % slower). Per tile, per wave:
+//   S^T[t][m] = sum_d K[t][d] Q[m][d]: A = K (32 positions x 16 d, one
+//     16-byte chunk of a staged K row per lane), B = Q^T (this lane's column
+//     lc = lane % 32 at d = 16 ks + 8 g + i, g = lane / 32), in registers;
+//     2 position blocks x 8 d steps = 16 MFMAs into two 32x32 accumulators
+//     started at -max (scores arrive relative to the running maximum);
+//   lane (lc, g) then holds rows 32 pb + 8 (r / 4) + 4 g + r % 4 of column
+//     lc in register r: the column's maximum is this lane's 32 values and its
+//     partner's (one permlane32 swap), and registers 8 h .. 8 h + 7 of block
+//     pb, rounded, are exactly the B operand P^T of PV step (pb, h) (the V^T
+//     tile is staged with its positions in that order, vt_pos32);
+//   O^T[d][m] += sum_t V^T[d][t] P^T[t][m]: 4 d blocks x 4 steps = 16 MFMAs.
+// Tiles stream through a 4-stage ring by direct-to-LDS loads, 3 tiles ahead.
+// The KV range is split across workgroups when the chunk has too few query
+// blocks to fill the chip; the splits of a block run on one XCD (blockIdx
+// agreeing mod 8: the dispatcher deals workgroups to the XCDs round robin),
+// write their partial (O, max, sum) columns with plain stores and take a
+// ticket, and the last to finish folds them in split order from that XCD's
+// L2 (no second launch, no workgroup waits on another).
+constexpr int kP32Stages = 4;
+constexpr int kP32TileBytes = 2 * kPlaneBytes;
+constexpr int kP32Part = 130;  // floats per partial column: O[128], max, sum
+constexpr int kPolicyL2 = 1;   // the sc0 bit: the load misses the CU's L1 and reads its XCD's L2
 
-  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const Unit un = unit_of(n_units, n_rb, kv_splits);
-  if (!un.live) return;
-  const int split = un.split, rb = un.rb, kvh = un.kvh;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lm = lane & 15, kk = lane >> 4;
-  const int qr = M / group;
-  const int r0 = rb * qr;
-  const int rows_here = min(qr, rows - r0);
-  const int wg_limit = start + r0 + rows_here;
-  const int all_see = start + r0 + 1;
-  const int n_tiles = (wg_limit + kBT - 1) / kBT;
-  const int tt_lo = (int)((long)n_tiles * split / kv_splits);
-  const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
-  const int n = tt_hi - tt_lo;
-  const int n_load = n;
-
-  // Tile j (clamped to the last loaded one, so every iteration issues LPW
-  // loads per wave and the wait counts stay exact) into stage j % NS.
-  const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
-  auto issue_piece = [&](int j, int i) {
-    if (n_load <= 0) return;
-    const int tile = tt_lo + min(j, n_load - 1);
-    const char* g = src + (size_t)tile * TB;
-    const int piece = 1024 * (wave + W * i);
-    lds_load16(g + piece, (lds_void*)&lds[j % NS][piece]);
-  };
-  if (n > 0) {
-#pragma unroll
-    for (int j = 0; j < NS - 1; ++j)
-#pragma unroll
-      for (int i = 0; i < LPW; ++i) issue_piece(j, i);
+template <int MODE>
+struct Op32;
+template <>
+struct Op32<kF16> {
+  __device__ static f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-
-  int my_row[MT], my_head[MT], my_limit[MT];
-  bool col_ok[MT];
-  V8 qh[MT][4];
-  f32x4 o[MT][8];
-  float m_run[MT], l_run[MT];
-  f32x4 negm[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * (wave * MT + mt) + lm;
-    my_head[mt] = m / qr;
-    my_row[mt] = r0 + m % qr;
-    col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
-    my_limit[mt] = col_ok[mt] ? start + my_row[mt] + 1 : 0;
-    const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
-                      (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
-    const float qs = col_ok[mt] ? qscale : 0.f;
-    float x[4][8];
-    load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qh[mt][s2][e] = (E)(x[s2][e] * qs);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[mt] = kNegSentinel;
-    l_run[mt] = 0.f;
-    negm[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+};
+template <>
+struct Op32<kBF16> {
+  __device__ static f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+};
 
-  // S^T of tile j into dst (relative to the running max); with `loads`,
-  // tile j + NS - 2's pieces are issued among the MFMAs (the caller is
-  // iteration j - 1, whose loads target tile (j - 1) + NS - 1).
-  auto qk = [&](int j, f32x4 (&dst)[MT][4], bool loads) {
-    const char* kt = lds[j % NS];
-    V8 ka[2][4];
-    auto read_k = [&](int pb, int buf) {
+// This lane's 64 elements of one query vector, x[ks][i] = q[16 ks + 8 g + i]
+// (its partner lane, 32 apart, holds the other 64), with the q prologue's
+// operands when qn_w is given: the loads only (Q32Loads::issue), so the
+// caller can queue the first tiles' loads behind them before anything
+// waits, then the prologue (finish): RMSNorm with an f64 sum of squares over
+// the pair, then `x * inv * w` and the rotation of the pairs (d, d + 64)
+// (both in this lane: ks and ks + 4), in the reference's separately rounded
+// f32 operations, with the row's (cos, sin) from tab_row (64 cos, then 64
+// sin), as the row prologue would.
+struct Q32Loads {
+  float x[8][8];
+  float w0[4][8], w1[4][8], cs[4][8], sn[4][8];
+  __device__ __forceinline__ void issue(const float* qp, int g, const float* __restrict__ qn_w,
+                                        const float* __restrict__ tab_row) {
+    const bool vec = aligned16(qp, qn_w, tab_row);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) ka[buf][ks] = *reinterpret_cast<const V8*>(kt + k_off(16 * pb + lm, 4 * ks + kk));
-    };
-    read_k(0, 0);
+    for (int ks = 0; ks < 8; ++ks) ld8(qp + 16 * ks + 8 * g, vec, x[ks]);
+    if (!qn_w) return;
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-      if (pb < 3) read_k(pb + 1, (pb + 1) & 1);
+    for (int ks = 0; ks < 4; ++ks) {
+      const int i = 16 * ks + 8 * g;
+      ld8(qn_w + i, vec, w0[ks]);
+      ld8(qn_w + i + 64, vec, w1[ks]);
+      ld8(tab_row + i, vec, cs[ks]);
+      ld8(tab_row + 64 + i, vec, sn[ks]);
+    }
+  }
+  __device__ __forceinline__ void finish(bool norm, float qn_eps) {
+#pragma clang fp contract(off)
+    if (!norm) return;
+    double ss = 0.0;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        dst[mt][pb] = negm[mt];
+    for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) dst[mt][pb] = Op<MODE>::mfma(ka[pb & 1][ks], qh[mt][ks], dst[mt][pb]);
+      for (int e = 0; e < 8; ++e) ss += (double)x[ks][e] * (double)x[ks][e];
+    ss = swap_sum_f64<32>(ss);
+    const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)qn_eps));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a0 = x[ks][e] * inv * w0[ks][e], a1 = x[ks + 4][e] * inv * w1[ks][e];
+        x[ks][e] = a0 * cs[ks][e] - a1 * sn[ks][e];
+        x[ks + 4][e] = a0 * sn[ks][e] + a1 * cs[ks][e];
       }
-      if (loads) {
-#pragma unroll
-        for (int i = pb * LPW / 4; i < (pb + 1) * LPW / 4; ++i) issue_piece(j + NS - 2, i);
-      }
-    }
-  };
-  // Mask (only where a row of the block stops inside the tile) and column
-  // maxima of S(j); returns whether any column must move its maximum.
-  float mx[MT];
-  auto scan = [&](int j, f32x4 (&sc)[MT][4]) -> bool {
-    const int t0 = (tt_lo + j) * kBT;
-    if (t0 + kBT > all_see) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
-    }
-    bool grow = false;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float x = max3f(sc[mt][0][0], sc[mt][0][1], sc[mt][0][2]);
-      x = max3f(x, sc[mt][0][3], sc[mt][1][0]);
-      x = max3f(x, sc[mt][1][1], sc[mt][1][2]);
-      x = max3f(x, sc[mt][1][3], sc[mt][2][0]);
-      x = max3f(x, sc[mt][2][1], sc[mt][2][2]);
-      x = max3f(x, sc[mt][2][3], sc[mt][3][0]);
-      x = max3f(x, sc[mt][3][1], sc[mt][3][2]);
-      x = __builtin_elementwise_maximum(x, sc[mt][3][3]);
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      x = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      mx[mt] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-      grow = grow || mx[mt] > kRescale || m_run[mt] == kNegSentinel;
-    }
-    return __builtin_amdgcn_ballot_w64(grow) != 0;
-  };
-  // Move the running maxima to S(j)'s (see prefill_kernel) and rescale.
-  auto rescale = [&](f32x4 (&sc)[MT][4]) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const bool fresh = m_run[mt] == kNegSentinel;
-      const float d = fresh ? fmaxf(mx[mt], kNegSentinel) : fmaxf(mx[mt], 0.f);
-      if (!fresh) {
-        const float alpha = __builtin_amdgcn_exp2f(-d);
-        l_run[mt] *= alpha;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
-        m_run[mt] += d;
-      } else {
-        m_run[mt] = d;
-      }
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) sc[mt][pb] -= d;
-      const float nm = m_run[mt] == kNegSentinel ? 0.f : -m_run[mt];
-      negm[mt] = f32x4{nm, nm, nm, nm};
-    }
-  };
-  V8 ph[MT][2];
-  auto make_p = [&](f32x4 (&sc)[MT][4]) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        f32x4 p;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e]);
-        const V4 hi = __builtin_convertvector(p, V4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
-      }
-      l_run[mt] = sum8(ph[mt][1], sum8(ph[mt][0], l_run[mt]));
-    }
-  };
-  auto pv = [&](int j) {
-    const char* vt = lds[j % NS] + kPlaneBytes;
-    V8 va[2][2];
-    auto read_v = [&](int b, int buf) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) va[buf][s2] = *reinterpret_cast<const V8*>(vt + vt_off(16 * b + lm, 4 * s2 + kk));
-    };
-    read_v(0, 0);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      if (b < 7) read_v(b + 1, (b + 1) & 1);
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) o[mt][b] = Op<MODE>::mfma(va[b & 1][s2], ph[mt][s2], o[mt][b]);
-    }
-  };
+  }
+};
 
-  f32x4 sa[MT][4], sb[MT][4];
-  bool grow = false;
-  if (n > 0) {
-    wait_vmcnt<(NS - 2) * LPW>();
-    __syncthreads();
-    qk(0, sa, false);
-    grow = scan(0, sa);
-  }
-  // One iteration with cur = S(j), nxt <- S(j + 1); tile j + 1 is resident
-  // once at most NS - 3 tiles of loads are in flight.
-  auto step = [&](int j, f32x4 (&cur)[MT][4], f32x4 (&nxt)[MT][4]) {
-    wait_vmcnt<(NS - 3) * LPW>();
-    __syncthreads();
-    if (grow) rescale(cur);
-    qk(j + 1, nxt, true);
-    make_p(cur);
-    pv(j);
-    grow = scan(j + 1, nxt);
+// The last split's fold of a unit's columns over its S splits: split sp's
+// partial column (O chunks 8 db + 2 jj + g of this lane from
+// o_off(sp, chunk), max and sum from ml_off(sp); this split's own stored
+// like the others), weighted by 2^(max_sp - M) over M = the splits' maximum
+// and summed in split order, 32 d (one db block) at a time;
+// emit(db, block, 1 / L) for each. S is fixed at compile time so every load
+// is unconditional and the next block's loads (S <= 4) are in flight while
+// one is folded.
+template <int S, typename OffFn, typename MlFn, typename Emit>
+__device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o_off, MlFn ml_off, int g,
+                                       Emit emit) {
+  constexpr bool kAhead = S <= 4;
+  f32x4 buf[kAhead ? 2 : 1][S][4];
+  auto load_block = [&](int db, f32x4 (&b)[S][4]) {
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        b[sp][jj] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(sp, 8 * db + 2 * jj + g), 0, kPolicyL2);
   };
-  int j = 0;
-  for (; j + 2 < n; j += 2) {
-    step(j, sa, sb);
-    step(j + 1, sb, sa);
+  float ms[S], ls[S];
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, ml_off(sp), 0, kPolicyL2);
+    ms[sp] = __builtin_bit_cast(float, (uint32_t)v[0]);
+    ls[sp] = __builtin_bit_cast(float, (uint32_t)v[1]);
   }
-  if (j + 1 < n) {
-    step(j, sa, sb);
-    ++j;
-    // Last tile, from sb.
-    if (grow) rescale(sb);
-    make_p(sb);
-    pv(j);
-  } else if (j < n) {
-    if (grow) rescale(sa);
-    make_p(sa);
-    pv(j);
+  load_block(0, buf[0]);
+  float M = ms[0];
+#pragma unroll
+  for (int sp = 1; sp < S; ++sp) M = fmaxf(M, ms[sp]);
+  float a[S], L = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp) {
+    a[sp] = __builtin_amdgcn_exp2f(ms[sp] - M);
+    L += ls[sp] * a[sp];
   }
-  wait_vmcnt<0>();
-
+  const float inv = 1.0f / L;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    l_run[mt] += __shfl_xor(l_run[mt], 16, 64);
-    l_run[mt] += __shfl_xor(l_run[mt], 32, 64);
-  }
-  if (kv_splits == 1) {
+  for (int db = 0; db < 4; ++db) {
+    f32x4 (&cur)[S][4] = buf[kAhead ? (db & 1) : 0];
+    if (kAhead && db + 1 < 4) load_block(db + 1, buf[(db + 1) & 1]);
+    f32x16 acc{};
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (!col_ok[mt]) continue;
-      const float inv = 1.0f / l_run[mt];
-      float* op = out + (size_t)my_row[mt] * q_stride + (size_t)(kvh * group + my_head[mt]) * kD;
+    for (int sp = 0; sp < S; ++sp)
 #pragma unroll
-      for (int b = 0; b < 8; ++b)
+      for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) op[16 * b + 4 * kk + e] = o[mt][b][e] * inv;
-    }
-    return;
-  }
-  float* mine = part + (((size_t)kvh * n_rb + rb) * kv_splits + split) * kPartStride;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * (wave * MT + mt) + lm;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) *reinterpret_cast<f32x4*>(&mine[(size_t)m * kD + 16 * b + 4 * kk]) = o[mt][b];
-    if (kk == 0) {
-      mine[128 * kD + 2 * m] = m_run[mt];
-      mine[128 * kD + 2 * m + 1] = l_run[mt];
-    }
+        for (int e = 0; e < 4; ++e) acc[4 * jj + e] += cur[sp][jj][e] * a[sp];
+    emit(db, acc, inv);
+    if (!kAhead && db + 1 < 4) load_block(db + 1, buf[0]);
   }
 }
 
-// Log-sum-exp merge of the S KV splits: one 256-thread workgroup per (kv
-// head, row block, 8 columns), thread -> (column, 4 consecutive d). Every
-// split's partial is loaded before any is folded (one memory round trip).
+template <int MODE, int W>
+__global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restrict__ q, const char* __restrict__ stage,
+                                                        int n_stage_tiles, int q_stride, int rows, int start,
+                                                        int group, int n_rb, int n_units, int per_xcd, int kv_splits,
+                                                        float qscale, const float* __restrict__ qn_w, float qn_eps,
+                                                        const float* __restrict__ qn_tab,
+                                                        const char* __restrict__ qprep, float* __restrict__ part,
+                                                        uint32_t part_bytes, unsigned* __restrict__ tickets,
+                                                        float* __restrict__ out) {
+  typedef typename Op<MODE>::E E;
+  typedef typename Op<MODE>::V8 V8;
+  constexpr int TB = kP32TileBytes, NS = kP32Stages;
+  constexpr int V = 32 * W;        // columns per unit
+  constexpr int PW = 32 / W;       // 1 KiB pieces per wave per tile
+  // Scores may exceed the running maximum by 2^kRescale (log2 units) before
+  // it moves: P stays below 2^8 and most tiles skip rescaling O.
+  constexpr float kRescale = 8.0f;
+  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
+  __shared__ unsigned sm_ticket;
+
+  // Unit (kv head, row block) and split: the splits of a unit share blockIdx
+  // mod 8 (one XCD); each XCD takes a contiguous run of units, kv-head-major,
+  // so its L2 holds about one kv head's tiles.
+  const int slot = (int)(blockIdx.x & 7), rest = (int)(blockIdx.x >> 3);
+  const int split = rest % kv_splits, ui = rest / kv_splits;
+  const int u = slot * per_xcd + ui;
+  if (ui >= per_xcd || u >= n_units) return;
+  const int kvh = u / n_rb, rb = u % n_rb;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, lc = lane & 31;
+  const int qr = V / group;
+  const int r0 = rb * qr, rows_here = min(qr, rows - r0);
+  const int wg_limit = start + r0 + rows_here;  // positions the block's last row sees
+  const int all_see = start + r0 + 1;           // positions every row of the block sees
+  const int n_tiles = (wg_limit + kBT - 1) / kBT;
+  const int tt_lo = (int)((long)n_tiles * split / kv_splits);
+  const int n = (int)((long)n_tiles * (split + 1) / kv_splits) - tt_lo;
+  const int m = 32 * w + lc;  // this lane's column
+  const int head = m / qr, row = r0 + m % qr;
+  const bool col_ok = m % qr < rows_here;
+  const int my_limit = start + row + 1;
+
+  // The column's query vector: prepared by the chunk's row prologue (eight
+  // 16-byte loads), or loaded and put through the q prologue here (loads
+  // first, so they return ahead of the tiles'); then the first three tiles.
+  Q32Loads ql;
+  V8 qv[8];
+  const int q_row = col_ok ? row : r0;
+  if (qprep) {
+    const V8* qp = reinterpret_cast<const V8*>(qprep) + ((size_t)u * W + w) * 8 * 64 + lane;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qv[ks] = qp[64 * ks];
+  } else {
+    ql.issue(q + (size_t)q_row * q_stride + (size_t)(kvh * group + head) * kD, g, qn_w,
+             qn_tab ? qn_tab + (size_t)q_row * kD : nullptr);
+  }
+  const char* src = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB + 16 * lane;
+  // The units sharing an XCD walk their splits' tiles from different
+  // starting points (the online softmax takes tiles in any order), so they
+  // do not all request the same lines of that XCD's L2 at once.
+  const int rot = n > 0 ? (int)((long)ui * n / per_xcd) : 0;
+  auto tile_of = [&](int j) { return j + rot < n ? j + rot : j + rot - n; };
+  // Step j's tile into stage j % NS: 32 pieces of 1 KiB, wave w copies w, w + 8, ...
+  auto issue = [&](int j) {
+    const char* t = src + (size_t)tile_of(j) * TB;
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int piece = 1024 * (w + W * i);
+      lds_dma16(t + piece, lds_offset(&lds[j % NS][piece]));
+    }
+  };
+  for (int j = 0; j < 3 && j < n; ++j) issue(j);
+  if (qprep) {
+    if (!col_ok) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qv[ks] = V8{};
+    }
+  } else {
+    ql.finish(qn_w != nullptr, qn_eps);
+    const float qs = col_ok ? qscale : 0.f;  // log2(e) * scale, before rounding to the MFMA type
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[ks][e] = (E)(ql.x[ks][e] * qs);
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+  float m_run = kNegSentinel, l_run = 0.f;
+  float negm = 0.f;  // -m_run, or 0 while the column has seen no position
+  for (int j = 0; j < n; ++j) {
+    // Tile j has landed once at most the later tiles issued are in flight;
+    // the barrier makes every wave's pieces visible and retires stage
+    // (j - 1) % NS, which the loads below overwrite.
+    if (j + 2 < n) wait_vmcnt<2 * PW>();
+    else if (j + 1 < n) wait_vmcnt<PW>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (j + 3 < n) issue(j + 3);
+    const char* kt = lds[j % NS];
+    const char* vt = kt + kPlaneBytes;
+    const int t0 = (tt_lo + tile_of(j)) * kBT;
+    f32x16 sc[2];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+      V8 ka[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) ka[ks] = *reinterpret_cast<const V8*>(kt + k_off(32 * pb + lc, 2 * ks + g));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[pb][r] = negm;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) sc[pb] = Op32<MODE>::mfma(ka[ks], qv[ks], sc[pb]);
+    }
+    // Causal mask only where some row of the block stops inside the tile.
+    if (t0 + kBT > all_see) {
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (t0 + 32 * pb + 8 * (r >> 2) + 4 * g + (r & 3) >= my_limit) sc[pb][r] = -INFINITY;
+    }
+    float mx = max3f(sc[0][0], sc[0][1], sc[0][2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = max3f(mx, sc[0][r], sc[0][r + 1]);
+    mx = max3f(mx, sc[0][15], sc[1][0]);
+#pragma unroll
+    for (int r = 1; r < 15; r += 2) mx = max3f(mx, sc[1][r], sc[1][r + 1]);
+    mx = __builtin_elementwise_maximum(mx, sc[1][15]);
+    {
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    }
+    if (__builtin_amdgcn_ballot_w64(mx > kRescale || m_run == kNegSentinel)) {
+      // A column still at the sentinel takes the tile's maximum outright (its
+      // O and sum are zero); others move up by d >= 0 and rescale.
+      const bool fresh = m_run == kNegSentinel;
+      const float d = fresh ? fmaxf(mx, kNegSentinel) : fmaxf(mx, 0.f);
+      if (!fresh) {
+        const float alpha = __builtin_amdgcn_exp2f(-d);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        m_run += d;
+      } else {
+        m_run = d;
+      }
+      sc[0] -= d;
+      sc[1] -= d;
+      negm = m_run == kNegSentinel ? 0.f : -m_run;
+    }
+    // P^T of PV step (pb, h): registers 8 h .. 8 h + 7 of block pb, rounded;
+    // the row sums are of exactly the rounded P the products use.
+    V8 ph[2][2];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ph[pb][h][i] = (E)__builtin_amdgcn_exp2f(sc[pb][8 * h + i]);
+        l_run = sum8(ph[pb][h], l_run);
+      }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      V8 va[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) va[c] = *reinterpret_cast<const V8*>(vt + vt_off(32 * db + lc, 2 * c + g));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[db] = Op32<MODE>::mfma(va[c], ph[c >> 1][c & 1], o[db]);
+    }
+  }
+  l_run = swap_sum<32>(l_run);  // the column's other half of the positions
+
+  // The output goes through LDS (the tile ring is free once every wave is
+  // past its last tile): put() writes 32 d of this lane's column, o-layout
+  // o[db][4 jj + e] = O^T[32 db + 8 jj + 4 g + e][m], into the wave's 16 KiB
+  // region as 16-byte chunks c = d / 4 of row lc, swizzled to chunk c ^ lc
+  // (the 32 lanes of one chunk hit distinct banks); flush() then reads whole
+  // rows back, 512 contiguous bytes per half-wave, and stores each column's
+  // row of out with 16-byte stores.
+  float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)w * 32 * kD;
+  auto put = [&](int db, const f32x16& v, float inv) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int c = 8 * db + 2 * jj + g;
+      *reinterpret_cast<f32x4*>(obuf + lc * kD + 4 * (c ^ lc)) =
+          f32x4{v[4 * jj] * inv, v[4 * jj + 1] * inv, v[4 * jj + 2] * inv, v[4 * jj + 3] * inv};
+    }
+  };
+  auto flush = [&]() {
+    const bool vec = aligned16(out) && q_stride % 4 == 0;
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + g, mm = 32 * w + r;  // row r of the region: column mm
+      if (mm % qr >= rows_here) continue;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(obuf + r * kD + 4 * (lc ^ r));
+      float* op = out + (size_t)(r0 + mm % qr) * q_stride + (size_t)(kvh * group + mm / qr) * kD + 4 * lc;
+      if (vec) {
+        *reinterpret_cast<f32x4*>(op) = x;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) op[e] = x[e];
+      }
+    }
+  };
+  if (kv_splits == 1) {
+    __syncthreads();  // every wave is past the ring
+    const float inv = 1.0f / l_run;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) put(db, o[db], inv);
+    flush();
+    return;
+  }
+  // This split's partial, laid out so a wave's stores and loads are
+  // contiguous: O as 16-byte chunks c (d = 4c .. 4c + 3) of all 256 columns,
+  // chunk-major, then (max, sum) per column. Lane (lc, g) holds chunks
+  // c = 8 db + 2 jj + g of its column.
+  const size_t slice = (size_t)u * kv_splits;  // this unit's first split
+  const size_t ml_base = (size_t)n_units * kv_splits * 32 * V;  // f32x4 units
+  {
+    f32x4* ob = reinterpret_cast<f32x4*>(part) + (slice + split) * 32 * V + m;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        ob[(size_t)(8 * db + 2 * jj + g) * V] =
+            f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
+    if (g == 0)
+      reinterpret_cast<float2*>(reinterpret_cast<f32x4*>(part) + ml_base)[(slice + split) * V + m] =
+          float2{m_run, l_run};
+  }
+  // The last split to finish (its ticket the unit's last) folds the unit.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    unsigned* t = tickets + (size_t)u * 32;  // one 128-byte line per unit
+    const unsigned got = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (got == (unsigned)kv_splits - 1) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_ticket = got;
+  }
+  __syncthreads();
+  if (sm_ticket != (unsigned)kv_splits - 1) return;
+  // Fold in split order from this XCD's L2 (the same bits whichever split
+  // finishes last; this split's own partial was stored above like the
+  // others').
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)part_bytes, 0x00020000);
+  auto o_off = [&](int sp, int c) { return (uint32_t)((((slice + sp) * 32 + c) * V + m) * 16); };
+  auto ml_off = [&](int sp) { return (uint32_t)(ml_base * 16 + ((slice + sp) * V + m) * 8); };
+  switch (kv_splits) {
+    case 2: fold32<2>(rs, o_off, ml_off, g, put); break;
+    case 3: fold32<3>(rs, o_off, ml_off, g, put); break;
+    case 4: fold32<4>(rs, o_off, ml_off, g, put); break;
+    case 5: fold32<5>(rs, o_off, ml_off, g, put); break;
+    case 6: fold32<6>(rs, o_off, ml_off, g, put); break;
+    case 7: fold32<7>(rs, o_off, ml_off, g, put); break;
+    default: fold32<8>(rs, o_off, ml_off, g, put); break;
+  }
+  flush();
+}
+
 template <int S>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int n_rb, int n_cb,
                                                             int qr, int rows, int group, int q_stride,
@@ -1001,42 +1137,44 @@ void launch_main(const PrefillArgs& a, hipStream_t s) {
                a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
 }
 
-// F16 / BF16: two groups of 4 waves (2 per SIMD), each with two 32 KiB
-// stages; 128 query vectors = 2 column blocks per wave, 64 = 1. The split
-// mode's 64 KiB tiles allow one group: 4 waves with two stages.
-template <int MODE, int MT, int NS>
-void launch_sp(const PrefillArgs& a, hipStream_t s) {
-  const unsigned blocks = (unsigned)((a.n_units + 7) / 8 * 8);
-  launch_timed(a.tp, prefill_sp_kernel<MODE, MT, NS>, dim3(blocks), dim3(256), s, a.q, (const char*)a.stage,
-               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.kv_splits, a.qscale,
-               a.qn_w, a.qn_eps, a.qn_tab, a.part, a.out);
-}
-
-template <int MODE>
-void launch_mode(int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
-  constexpr bool kSplit = Op<MODE>::kSplit;
-  if constexpr (!kSplit) {
-    if (impl == 2) {
-      if (vectors == 64)
-        launch_sp<MODE, 1, 4>(a, s);
-      else
-        launch_sp<MODE, 2, 4>(a, s);
-      return;
-    }
-  }
-  constexpr int G = kSplit ? 1 : 2;
+// EXACT: one group of 4 waves with two 64 KiB stages; 128 query vectors =
+// 2 column blocks per wave, 64 = 1.
+void launch_exact(int vectors, const PrefillArgs& a, hipStream_t s) {
   if (vectors == 64)
-    launch_main<MODE, G, 4, 1, 2>(a, s);
+    launch_main<kExact, 1, 4, 1, 2>(a, s);
   else
-    launch_main<MODE, G, 4, 2, 2>(a, s);
+    launch_main<kExact, 1, 4, 2, 2>(a, s);
 }
 
-void launch_attention(uint32_t mode, int vectors, int impl, const PrefillArgs& a, hipStream_t s) {
-  switch (mode) {
-    case RV_PREFILL_F16: launch_mode<kF16>(vectors, impl, a, s); break;
-    case RV_PREFILL_BF16: launch_mode<kBF16>(vectors, impl, a, s); break;
-    default: launch_mode<kExact>(vectors, impl, a, s);
-  }
+// F16 / BF16: prefill32_kernel over n_units (kv head, 256-vector block)
+// units, kv_splits workgroups each.
+struct P32Args {
+  const float* q;
+  const char* stage;
+  int n_stage_tiles, q_stride, rows, start, group, n_rb, n_units, per_xcd, kv_splits;
+  float qscale;
+  const float* qn_w;
+  float qn_eps;
+  const float* qn_tab;
+  const char* qprep;
+  float* part;
+  uint32_t part_bytes;
+  unsigned* tickets;
+  float* out;
+  TimedPair tp;
+};
+template <int MODE>
+void launch_p32(const P32Args& a, int vectors, hipStream_t s) {
+  const unsigned blocks = (unsigned)(8 * a.per_xcd * a.kv_splits);
+#define RV_P32(W)                                                                                                  \
+  launch_timed(a.tp, prefill32_kernel<MODE, W>, dim3(blocks), dim3(64 * W), s, a.q, a.stage, a.n_stage_tiles,      \
+               a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.per_xcd, a.kv_splits, a.qscale, a.qn_w, \
+               a.qn_eps, a.qn_tab, a.qprep, a.part, a.part_bytes, a.tickets, a.out)
+  if (vectors == 128)
+    RV_P32(4);
+  else
+    RV_P32(8);
+#undef RV_P32
 }
 
 // Stage tiles [lo, hi) of every kv head of `layer` (positions at or past
@@ -1067,6 +1205,24 @@ void launch_stage(const rv_kv* kv, size_t layer, uint32_t mode, size_t positions
     launch_stage_m<_Float16>(mode, (const _Float16*)kv->k_layer(layer), (const _Float16*)kv->v_layer(layer), n_kv,
                              kv_dim, (int)positions, tile_stride, lo, hi, stage, s);
 }
+
+}  // namespace
+
+// 128 columns (4 waves) while the chunk's rows see at most 16 tiles: there
+// the longest unit's chain of tiles bounds the launch, and halving the
+// columns per tile halves its length; 256 (8 waves) beyond, where one staged
+// tile feeding twice the columns halves the L2 traffic.
+int p32_vectors(size_t positions) { return (positions + kBT - 1) / kBT <= 16 ? 128 : 256; }
+size_t qprep_bytes(size_t rows, size_t positions, size_t n_kv_heads, size_t group) {
+  const size_t v = (size_t)p32_vectors(positions), qr = v / group;
+  return n_kv_heads * ((rows + qr - 1) / qr) * v * 128 * 2;
+}
+QPrep qprep_plan(char* base, size_t rows, size_t positions, size_t group, float scale) {
+  const int qr = p32_vectors(positions) / (int)group;
+  return QPrep{base, (int)group, qr, (int)((rows + qr - 1) / qr), scale * kLog2e};
+}
+
+namespace {
 
 int planes_of(uint32_t mode) { return (mode == RV_PREFILL_F16 || mode == RV_PREFILL_BF16) ? 1 : 2; }
 // Bytes of one staged tile in `mode` (the split mode's K row exponents
@@ -1125,72 +1281,69 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   const int group = (int)(n_q_heads / kv->n_kv_heads);
   const int n_kv = (int)kv->n_kv_heads;
   const uint32_t m = mode & RV_PREFILL_MODE_MASK;
-  const int planes = planes_of(m);
+  const bool split_mode = planes_of(m) == 2;
+  if (split_mode && qn && qn->prepped) {
+    st.e = hipErrorInvalidValue;
+    st.what = "prepared queries in the split mode";
+    return st;
+  }
   const size_t positions = start + rows;
   const int n_stage_tiles = (int)((positions + kBT - 1) / kBT);  // tiles this call reads
-  // 128 query vectors per workgroup (16 rows of a group of 8) or 64: the
-  // tuning's choice, else the cost model below for F16/BF16, else 64 when
-  // 128-vector blocks would leave CUs idle (fewer than 256 workgroups). The
-  // split mode keeps 128 when the range is long
-  // enough for a KV split to fill the chip (at least 16 tiles): its
-  // one-group kernel gains more from 32 columns per wave than the split and
-  // its merge cost (config 4: 123 vs 134 us).
-  int vectors = 128;
-  int kv_splits = (int)kv->tune_prefill_kv_split;
-  if (kv->tune_prefill_rows > 0) {
-    vectors = kv->tune_prefill_rows * group <= 64 ? 64 : 128;
-  } else if (planes == 1 && kv_splits <= 0 && group <= 64) {
-    // F16/BF16: the shape with the least modelled time. A workgroup holds a
-    // CU (its LDS), so workgroups past kCUs run as further rounds; a round
-    // costs ~9 us of fixed work plus the longest block's tiles at 0.68 us
-    // (64 vectors) or 0.98 us (128) each, and a KV split adds its merge
-    // (~8 us). Fitted to configs 3 and 4 (14.4 and 51.2 us kernels) and to
-    // 128-vector blocks without a split (69.6 us at config 4); 128-vector
-    // blocks with a split measured slower than the model and are not
-    // offered. Whole 512-row chunks keep 64 vectors and no split; other
-    // sizes avoid a last round of a few workgroups (520 rows: 260
-    // workgroups of 64 vectors, 98 vs 58 us at 512) and splits the chip
-    // does not need (448 rows: 224 workgroups).
-    double best = 1e30;
-    for (int v : {64, 128}) {
-      const long rb = (long)((rows + v / group - 1) / (v / group));
-      for (int sp = 1; sp <= (v == 64 ? kMaxKvSplits : 1); ++sp) {
-        const long wgs = rb * n_kv * sp;
-        if (sp > 1 && (wgs > 2 * kCUs || n_stage_tiles / sp < 8)) break;
-        const double round_us = 9.0 + (double)((n_stage_tiles + sp - 1) / sp) * (v == 64 ? 0.68 : 0.98);
-        const double cost = (double)((wgs + kCUs - 1) / kCUs) * round_us + (sp > 1 ? 8.0 : 0.0);
-        if (cost < best) {
-          best = cost;
-          vectors = v;
-          kv_splits = sp;
-        }
-      }
-    }
-  } else if ((long)((rows * group + 127) / 128) * n_kv < 256 && !(planes == 2 && n_stage_tiles >= 16)) {
-    vectors = 64;
-  }
-  const int qr = vectors / group;
-  const int n_rb = (int)((rows + qr - 1) / qr);
-  if (kv_splits <= 0) {
-    // Split the KV axis until about 256 workgroups are in flight, keeping at
-    // least 8 K/V tiles per split of the longest block.
-    const long wgs = (long)n_rb * n_kv;
-    kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 8));
-  }
-  kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
-  const size_t part_bytes = kv_splits > 1 ? (size_t)n_kv * n_rb * kv_splits * kPartStride * sizeof(float) : 0;
   const size_t tile_bytes = tile_bytes_of(m);
+  int kv_splits = (int)kv->tune_prefill_kv_split;
+  int vectors, n_rb, per_xcd = 0;
+  size_t part_bytes = 0;
+  if (!split_mode) {
+    // F16 / BF16 (prefill32_kernel): 256-vector blocks; the KV axis is split
+    // until about kCUs workgroups run, each split keeping at least 4 tiles of
+    // the longest block, and only where the XCD fold is available.
+    vectors = p32_vectors(positions);
+    const int qr = vectors / group;
+    n_rb = (int)((rows + qr - 1) / qr);
+    const long units = (long)n_rb * n_kv;
+    if (kv_splits <= 0) kv_splits = (int)std::min<long>((kCUs + units - 1) / units, std::max(1, n_stage_tiles / 4));
+    if (!kv->xcd_ok) kv_splits = 1;
+    kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
+    per_xcd = (int)((units + 7) / 8);
+    if (kv_splits > 1) part_bytes = (size_t)units * kv_splits * vectors * kP32Part * sizeof(float);
+  } else {
+    // EXACT (prefill_kernel, one group of 4 waves): 128 query vectors per
+    // workgroup, or 64 when 128-vector blocks would give fewer than 256
+    // workgroups, but 128 when the range has at least 16 tiles, so that a KV
+    // split fills the chip (config 4: 2 splits; its kernel gains more from 32
+    // columns per wave than the split and merge cost: 125 vs 135 us).
+    vectors = 128;
+    if (kv->tune_prefill_rows > 0)
+      vectors = kv->tune_prefill_rows * group <= 64 ? 64 : 128;
+    else if ((long)((rows * group + 127) / 128) * n_kv < 256 && n_stage_tiles < 16)
+      vectors = 64;
+    const int qr = vectors / group;
+    n_rb = (int)((rows + qr - 1) / qr);
+    if (kv_splits <= 0) {
+      // Split the KV axis until about 256 workgroups are in flight, keeping
+      // at least 8 K/V tiles per split of the longest block.
+      const long wgs = (long)n_rb * n_kv;
+      kv_splits = (int)std::min<long>((256 + wgs - 1) / wgs, std::max<long>(1, n_stage_tiles / 8));
+    }
+    kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
+    if (kv_splits > 1) part_bytes = (size_t)n_kv * n_rb * kv_splits * kPartStride * sizeof(float);
+  }
   // Workspace: the split partials, then room to stage every tile this call
   // reads, which only a captured call uses; eager calls reserve it too, so
   // capturing a call of a shape already run eagerly allocates nothing.
   const size_t call_stage_bytes = (size_t)n_kv * n_stage_tiles * tile_bytes;
-  // Bound for the cache's capacity: default splits keep n_rb * n_kv *
-  // kv_splits under 512 rows of partials, and a call stages at most every
+  // Bound for the cache's capacity: default splits keep the partials under
+  // about kCUs workgroups' worth (256 rows of 128 columns in EXACT, 256
+  // units of 256 columns for F16 / BF16), and a call stages at most every
   // tile of the capacity in the split mode's (largest) layout.
-  const size_t bound = std::max<size_t>(part_bytes, (size_t)512 * kPartStride * sizeof(float)) +
+  const size_t bound = std::max<size_t>(part_bytes, (size_t)kCUs * 256 * kP32Part * sizeof(float)) +
                        (size_t)n_kv * ((kv->capacity + kBT - 1) / kBT) * tile_bytes_of(RV_PREFILL_EXACT);
   st = ensure_workspace(kv, part_bytes + call_stage_bytes, bound);
   if (st.e != hipSuccess) return st;
+  if (!split_mode && kv_splits > 1) {
+    st = ensure_prefill_tickets(kv, (size_t)n_rb * n_kv);
+    if (st.e != hipSuccess) return st;
+  }
   char* stage;
   int tile_stride, stage_lo;
   float* part = (float*)kv->ws;
@@ -1211,38 +1364,73 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
     staged_pos = std::max(staged_pos, positions);
     stage = (char*)kv->staged[layer];
   }
-  PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
-                (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
-                qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, timing_pair(kv, s)};
-  // Attention kernel: the software-pipelined one for short KV ranges (at most
-  // 16 tiles per split, e.g. a chunk on an empty cache), where its single
-  // barrier per tile and four-wave workgroups finish sooner; the two-group
-  // one for long ranges.
-  int impl = (int)kv->tune_prefill_impl;
-  if (impl <= 0) impl = (n_stage_tiles + kv_splits - 1) / kv_splits <= 16 ? 2 : 1;
   launch_stage(kv, layer, m, positions, tile_stride, stage_lo, n_stage_tiles, stage, s);
-  launch_attention(m, vectors, impl, a, s);
-  if (kv_splits > 1) {
-    const dim3 grid((unsigned)(n_kv * n_rb * vectors / 8));
-    const int n_cb = vectors / 8, q_stride = (int)(n_q_heads * kD);
+  const TimedPair tp = timing_pair(kv, s);
+  if (!split_mode) {
+    const P32Args a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows, (int)start, group, n_rb,
+                    n_rb * n_kv, per_xcd, kv_splits, scale * kLog2e, qn ? qn->w : nullptr, qn ? qn->eps : 0.f,
+                    qn ? qn->tab : nullptr, qn ? qn->prepped : nullptr, part,
+                    (uint32_t)std::min<size_t>(part_bytes, 0xFFFFFFF0u),
+                    kv->pf_tickets, out, tp};
+    if (m == RV_PREFILL_BF16)
+      launch_p32<kBF16>(a, vectors, s);
+    else
+      launch_p32<kF16>(a, vectors, s);
+  } else {
+    PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
+                  (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,
+                  qn ? qn->w : nullptr, qn ? qn->eps : 0.f, qn ? qn->tab : nullptr, part, out, tp};
+    launch_exact(vectors, a, s);
+    if (kv_splits > 1) {
+      const int qr = vectors / group;
+      const dim3 grid((unsigned)(n_kv * n_rb * vectors / 8));
+      const int n_cb = vectors / 8, q_stride = (int)(n_q_heads * kD);
 #define RV_MERGE(S)                                                                                               \
   case S:                                                                                                         \
     hipLaunchKernelGGL(prefill_merge_kernel<S>, grid, dim3(256), 0, s, (const float*)part, n_rb, n_cb, qr, (int)rows, \
                        group, q_stride, out);                                                                    \
     break
-    switch (kv_splits) {
-      RV_MERGE(2);
-      RV_MERGE(3);
-      RV_MERGE(4);
-      RV_MERGE(5);
-      RV_MERGE(6);
-      RV_MERGE(7);
-      default: RV_MERGE(8);
-    }
+      switch (kv_splits) {
+        RV_MERGE(2);
+        RV_MERGE(3);
+        RV_MERGE(4);
+        RV_MERGE(5);
+        RV_MERGE(6);
+        RV_MERGE(7);
+        default: RV_MERGE(8);
+      }
 #undef RV_MERGE
+    }
   }
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prefill launch";
+  return st;
+}
+
+// The F16 / BF16 fold's ticket lines (one 128-byte line per unit), grown on
+// need outside capture, zeroed when allocated; every call's last split resets
+// its unit's counter, so they stay zero between calls.
+HipStatus ensure_prefill_tickets(rv_kv* kv, size_t units) {
+  HipStatus st;
+  if (units <= kv->pf_ticket_units) return st;
+  if (capturing(kv->stream)) {
+    st.e = hipErrorStreamCaptureUnsupported;
+    st.what = "prefill ticket growth under graph capture (run a call of this shape uncaptured first)";
+    return st;
+  }
+  const size_t want = std::max<size_t>(units, 1024);
+  void* p = nullptr;
+  st.e = hipMalloc(&p, want * 128);
+  if (st.e == hipSuccess) st.e = hipMemset(p, 0, want * 128);
+  if (st.e == hipSuccess) st.e = hipDeviceSynchronize();
+  if (st.e != hipSuccess) {
+    if (p) (void)hipFree(p);
+    st.what = "hipMalloc prefill tickets";
+    return st;
+  }
+  if (kv->pf_tickets) kv->retire(kv->pf_tickets, kv->pf_ticket_units * 128);
+  kv->pf_tickets = (unsigned*)p;
+  kv->pf_ticket_units = want;
   return st;
 }
 

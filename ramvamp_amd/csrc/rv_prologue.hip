@@ -72,7 +72,7 @@ __device__ __forceinline__ void stage_elem(const StagedRows& sr, int kind, int h
   constexpr int P = kPlanes<SM>;
   const int t = (int)(p % kBT);
   char* tile = sr.base + ((size_t)h * sr.tile_stride + (size_t)(p / kBT)) * (2 * P * kPlaneBytes);
-  char* dst = kind == 0 ? tile + k_off(t, d >> 3) + 2 * (d & 7) : tile + P * kPlaneBytes + vt_byte(d, t);
+  char* dst = kind == 0 ? tile + k_off(t, d >> 3) + 2 * (d & 7) : tile + P * kPlaneBytes + vt_byte_m<SM>(d, t);
   const E hi = (E)x;
   *reinterpret_cast<E*>(dst) = hi;
   if constexpr (Op<SM>::kSplit) *reinterpret_cast<E*>(dst + kPlaneBytes) = (E)(x - (float)hi);
@@ -116,7 +116,7 @@ __device__ __forceinline__ void stage_v_quad(const float* __restrict__ v, T* __r
   const int t = (int)(p0 % kBT);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
-    char* dst = plane + vt_byte(lane + 64 * k, t);  // positions t .. t + 3: 8 contiguous bytes
+    char* dst = plane + vt_byte_m<SM>(lane + 64 * k, t);  // positions t .. t + 3: 8 contiguous bytes
     V4 hi, lo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -156,12 +156,13 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
 // (i, i + half) with i = l + 64 j, j < NP, for every head of its slots, so
 // the row's sin/cos (f64, cast to f32) are computed once per wave rather than
 // once per head, while the wave's head loads are in flight.
-// SM >= 0 (a prefill chunk, n_q = 0, head_dim 128): k and v rows, as the
-// cache holds them, are also written into the staged tiles in mode SM, and
-// the rest of the chunk's last tile is zeroed. The slot list is then the k
-// heads only (grid rows past the chunk zero their K rows); v heads are
-// handled by the blocks y >= the k slot blocks, one per (quad of positions
-// x, head y - k slot blocks): stage_v_quad.
+// SM >= 0 (a prefill chunk, head_dim 128): k and v rows, as the cache holds
+// them, are also written into the staged tiles in mode SM, and the rest of
+// the chunk's last tile is zeroed. The slot list is then the q heads (none,
+// or into the prepared layout qp, rounded to SM's type) and the k heads
+// (grid rows past the chunk zero their K rows); v heads are handled by the
+// blocks y >= the q and k slot blocks, one per (quad of positions x, head y
+// - those blocks): stage_v_quad.
 constexpr int kSlots = 4;
 
 template <typename T, int NP, int SM>
@@ -171,7 +172,8 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
                                                           T* __restrict__ vp, int n_kv, int hd,
                                                           const float* __restrict__ q_w,
                                                           const float* __restrict__ k_w, float eps, InvFreq inv,
-                                                          long pos0, float* __restrict__ tab, StagedRows sr) {
+                                                          long pos0, float* __restrict__ tab, StagedRows sr,
+                                                          QPrep qp) {
 #pragma clang fp contract(off)
   const int r = blockIdx.x, lane = threadIdx.x;
   const int half = hd / 2;
@@ -297,6 +299,17 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
       const float a1 = x1[j][p] * inv_rms[j] * (is_q ? wq1[p] : wk1[p]);
       const float ya = a0 * cs[p] - a1 * sn[p], yb = a0 * sn[p] + a1 * cs[p];
       if (is_q) {
+        if constexpr (SM >= 0) {
+          if (qp.base) {  // the prepared layout: scaled and rounded to the MFMA type
+            typedef typename Op<SM>::E E;
+            const int unit = (s / qp.group) * qp.n_rb + r / qp.qr;
+            const size_t c = (size_t)unit * qp.qr * qp.group + (s % qp.group) * qp.qr + r % qp.qr;
+            E* qd = reinterpret_cast<E*>(qp.base);
+            qd[qprep_index(c, i)] = (E)(ya * qp.qscale);
+            qd[qprep_index(c, i + half)] = (E)(yb * qp.qscale);
+            continue;
+          }
+        }
         float* d = q_out + ((size_t)r * n_q + s) * hd;
         d[i] = ya;
         d[i + half] = yb;
@@ -316,10 +329,11 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
 template <typename T>
 void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int n_q, const float* k, const float* v,
                            T* kp, T* vp, int n_kv, int hd, const float* q_w, const float* k_w, float eps,
-                           const InvFreq& inv, long pos0, float* tab, int sm, const StagedRows& sr, hipStream_t s) {
+                           const InvFreq& inv, long pos0, float* tab, int sm, const StagedRows& sr, const QPrep& qp,
+                           hipStream_t s) {
 #define RV_PROLOGUE(NP, SM)                                                                                      \
   hipLaunchKernelGGL((row_prologue_kernel<T, NP, SM>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, \
-                     q_w, k_w, eps, inv, pos0, tab, sr)
+                     q_w, k_w, eps, inv, pos0, tab, sr, qp)
   if (sm == kF16)
     RV_PROLOGUE(1, kF16);
   else if (sm == kBF16)
@@ -356,7 +370,7 @@ HipStatus launch_append(const rv_kv* kv, size_t layer, size_t pos0, const float*
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
                               const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,
-                              const StageDst* sd, hipStream_t s) {
+                              const StageDst* sd, hipStream_t s, const QPrep* qp) {
   HipStatus st;
   if (rows == 0) return st;
   const int hd = (int)kv->head_dim, n_kv = (int)kv->n_kv_heads;
@@ -369,9 +383,12 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   // Staging: k and v heads only, head_dim 128; the grid covers the chunk's
   // last tile to its end.
   const bool staging = sd && sd->base;
+  const bool prep = qp && qp->base;
   // The split mode's tiles are staged whole by the stage kernel (their
-  // exponents span all of a tile's rows), never row by row here.
-  if (staging && (n_q != 0 || hd != 128 || (sd->mode != RV_PREFILL_F16 && sd->mode != RV_PREFILL_BF16))) {
+  // exponents span all of a tile's rows), never row by row here. q heads
+  // run in a staging launch only into the prepared layout.
+  if ((prep && !staging) ||
+      (staging && ((n_q != 0 && !prep) || hd != 128 || (sd->mode != RV_PREFILL_F16 && sd->mode != RV_PREFILL_BF16)))) {
     st.e = hipErrorInvalidValue;
     st.what = "staged prologue geometry";
     return st;
@@ -380,19 +397,21 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   const size_t grid_rows = staging ? rows + (kBT - end % kBT) % kBT : rows;
   const int sm = !staging ? -1 : sd->mode == RV_PREFILL_F16 ? kF16 : kBF16;
   const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
-  // Staging: k slot blocks, then one block row per v head (its quads of
-  // positions along x; grid_rows covers them).
-  const int slot_blocks = staging ? (n_kv + kSlots - 1) / kSlots + n_kv : (n_slots + kSlots - 1) / kSlots;
+  // Staging: q and k slot blocks, then one block row per v head (its quads
+  // of positions along x; grid_rows covers them).
+  const int slot_blocks =
+      staging ? ((int)n_q + n_kv + kSlots - 1) / kSlots + n_kv : (n_slots + kSlots - 1) / kSlots;
+  const QPrep qpv = prep ? *qp : QPrep{};
   const dim3 grid((unsigned)grid_rows, (unsigned)slot_blocks);
   const size_t off = cache_row * kv->kv_dim;
   if (kv->elem == RV_ELEM_F32)
     launch_row_prologue_t<float>(grid, np, q, q_out, (int)n_q, k, v, (float*)kv->k_layer(layer) + off,
                                  (float*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0, rope_tab,
-                                 sm, sr, s);
+                                 sm, sr, qpv, s);
   else
     launch_row_prologue_t<uint16_t>(grid, np, q, q_out, (int)n_q, k, v, (uint16_t*)kv->k_layer(layer) + off,
                                     (uint16_t*)kv->v_layer(layer) + off, n_kv, hd, q_w, k_w, eps, inv, (long)pos0,
-                                    rope_tab, sm, sr, s);
+                                    rope_tab, sm, sr, qpv, s);
   st.e = hipGetLastError();
   if (st.e != hipSuccess) st.what = "prologue launch";
   return st;

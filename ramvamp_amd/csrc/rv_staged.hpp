@@ -81,9 +81,15 @@ __device__ __forceinline__ void split2v(float x, V& hi, V& lo, int e) {
 // 16-byte chunks (8 elements).
 //   K plane: row t (64) x chunk c (16): elements d = 8c .. 8c+7, stored at
 //     byte 256 t + 16 (c ^ (t & 15)).
-//   V^T plane: row d (128) x chunk c (8): chunk c = 4 s2 + k holds, in slot
-//     j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
-//     (j >= 4); stored at byte 128 d + 16 (c ^ ((d >> 1) & 7)).
+//   V^T plane: row d (128) x chunk c (8), stored at byte
+//     128 d + 16 (c ^ ((d >> 1) & 7)); which positions a chunk holds follows
+//     the order the mode's attention kernel produces P in (vt_pos_m):
+//     the split mode (16x16 MFMA tiles): chunk c = 4 s2 + k holds, in slot
+//       j, position t = 32 s2 + 4k + j (j < 4) or 32 s2 + 16 + 4k + j - 4
+//       (j >= 4);
+//     F16 / BF16 (32x32 MFMA tiles): chunk c = 4 pb + 2 h + g holds, in
+//       slot j, position t = 32 pb + 16 h + 4 g + 8 (j / 4) + j % 4.
+//   In both, positions 4i .. 4i + 3 fill 8 contiguous bytes of one chunk.
 // The swizzles put the 16 lanes of one operand read on 16 distinct 16-byte
 // bank groups; the counters read no LDS bank conflicts for either plane
 // (an alternative V^T layout with each 32-position half contiguous,
@@ -100,6 +106,37 @@ __device__ __forceinline__ int vt_pos(int c, int j) {
 __device__ __forceinline__ int vt_byte(int d, int t) {
   const int u = t & 31;
   return vt_off(d, 4 * (t >> 5) + ((u & 15) >> 2)) + 2 * ((u & 3) + ((u >> 4) << 2));
+}
+// The F16 / BF16 map: chunk 4 pb + 2 h + g, slot 4 (w / 8) + w % 4 for
+// t = 32 pb + 16 h + w, g = (w / 4) % 2.
+__device__ __forceinline__ int vt_pos32(int c, int j) {
+  return 32 * (c >> 2) + 16 * ((c >> 1) & 1) + 4 * (c & 1) + 8 * (j >> 2) + (j & 3);
+}
+__device__ __forceinline__ int vt_byte32(int d, int t) {
+  const int w = t & 15;
+  return vt_off(d, 4 * (t >> 5) + 2 * ((t >> 4) & 1) + ((w >> 2) & 1)) + 2 * (4 * (w >> 3) + (w & 3));
+}
+template <int MODE>
+__device__ __forceinline__ int vt_pos_m(int c, int j) {
+  return Op<MODE>::kSplit ? vt_pos(c, j) : vt_pos32(c, j);
+}
+template <int MODE>
+__device__ __forceinline__ int vt_byte_m(int d, int t) {
+  return Op<MODE>::kSplit ? vt_byte(d, t) : vt_byte32(d, t);
+}
+
+// Prepared queries of the F16 / BF16 prefill: a chunk's row prologue writes
+// each query head's row after RMSNorm and RoPE, times log2(e) * scale,
+// rounded to the MFMA type, straight into the attention kernel's operand
+// order, so that kernel's query loads are eight coalesced 16-byte loads per
+// lane. The kernel's units (kv head * n_rb + rb) hold V = 128 or 256 columns
+// each: column m of unit u is query head kv head * group + m / qr of row
+// rb * qr + m % qr (qr = V / group), global column c = u * V + m. Element d
+// of column c sits in 16-byte chunk ((c / 32) * 8 + d / 16) * 64 + 32 * ((d /
+// 8) & 1) + c % 32 at position d % 8: the B operand (Q^T) of the QK step
+// d / 16 of the wave owning columns c - c % 32 .. + 31, in lane order.
+__host__ __device__ inline size_t qprep_index(size_t c, int d) {
+  return ((((c >> 5) * 8 + (size_t)(d >> 4)) * 64 + 32 * ((d >> 3) & 1) + (c & 31)) * 8 + (d & 7));
 }
 
 }  // namespace rv

@@ -37,12 +37,12 @@ def twin(rng, n_kv, hd, n_pos, cap, elem):
     return kv, ref
 
 
-@pytest.mark.parametrize("impl", [1, 2])
+@pytest.mark.parametrize("splits", [0, 1, 3])
 @pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
 @pytest.mark.parametrize("elem", ["f32", "f16"])
-def test_rows_match_per_row_attention_at(mode, elem, impl):
-    # impl (RV_TUNE_PREFILL_IMPL): 1 two wave groups, 2 software-pipelined
-    # (f16/bf16; the split mode has one kernel).
+def test_rows_match_per_row_attention_at(mode, elem, splits):
+    # splits (RV_TUNE_PREFILL_KV_SPLIT): 0 the launch plan's choice, 1 none,
+    # 3 (the F16/BF16 kernel folds a block's splits inside its launch).
     torch_cuda()
     rng = Rng(0xC0FFEE)
     for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (4, 32, 128, 100, 70), (2, 8, 128, 5, 16),
@@ -51,7 +51,7 @@ def test_rows_match_per_row_attention_at(mode, elem, impl):
                                        (1, 8, 16, 4, 9), (3, 6, 9, 0, 7)]:
         say(f"case rows {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem}")
         kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, elem)
-        kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
+        kv.set_tuning(rv.RV_TUNE_PREFILL_KV_SPLIT, splits)
         q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
         scale = np.float32(1.0) / np.sqrt(np.float32(hd))
         out = dev(np.zeros(q.shape))
@@ -66,9 +66,8 @@ def test_rows_match_per_row_attention_at(mode, elem, impl):
 
 @pytest.mark.parametrize("mode", ["f16", "bf16"])
 def test_ragged_chunk_shapes_match_the_oracle(mode):
-    # Chunk sizes the F16/BF16 launch plan maps to other shapes than 512
-    # rows: 224 workgroups without a KV split (448 rows), 128-vector blocks
-    # where 64-vector ones would spill past one workgroup per CU (520, 768).
+    # Chunk sizes other than 512 rows: partial 256-vector blocks and KV
+    # split counts the launch plan picks for them (448, 520, 768 rows).
     torch_cuda()
     rng = Rng(0x4A66ED)
     for start, rows in [(700, 448), (700, 520), (200, 768)]:
@@ -103,22 +102,22 @@ def test_config3_prefill_chunk_matches_the_oracle(mode):
         gate(kv.k_row(0, pos), ref.read_row(False, 0, pos), rel=2e-7, floor=1e-6, what="cache K")
 
 
-@pytest.mark.parametrize("impl", [1, 2])
+@pytest.mark.parametrize("splits", [0, 2])
 @pytest.mark.parametrize("mode", ["exact", "f16"])
 @pytest.mark.parametrize("elem", ["f32", "f16"])
-def test_prefill_chunk_matches_the_oracle_across_geometries(mode, elem, impl):
+def test_prefill_chunk_matches_the_oracle_across_geometries(mode, elem, splits):
     """The fused path (k/v prologue + append, q prologue inside the attention
     kernels' query loads) for groups 1..8, and the fallback path (full row
     prologue, then per-row decode) where the prefill kernels do not apply
     (group 3, head_dim 16 and 256)."""
     torch_cuda()
-    rng = Rng(0xFEED + 7 * impl + (elem == "f16"))
+    rng = Rng(0xFEED + 7 * splits + (elem == "f16"))
     for n_kv, n_q, hd, start, rows in [(4, 32, 128, 0, 37), (2, 8, 128, 5, 16), (1, 1, 128, 3, 20),
                                        (4, 16, 128, 100, 9), (2, 4, 128, 31, 33), (3, 9, 128, 2, 5),
                                        (1, 8, 16, 4, 9), (2, 4, 256, 7, 6)]:
-        say(f"case prefill_chunk {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem} impl={impl}")
+        say(f"case prefill_chunk {(n_kv, n_q, hd, start, rows)} mode={mode} elem={elem} splits={splits}")
         kv, ref = twin(rng, n_kv, hd, start, start + rows, elem)
-        kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
+        kv.set_tuning(rv.RV_TUNE_PREFILL_KV_SPLIT, splits)
         q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
         k = rng.vec_in(rows * n_kv * hd, -2.0, 2.0).reshape(rows, -1)
         v = rng.vec_in(rows * n_kv * hd, -1.0, 1.0).reshape(rows, -1)
@@ -283,31 +282,36 @@ def test_prefill_errors_and_first_row_semantics():
                        atol=0)
 
 
-@pytest.mark.parametrize("impl", [1, 2])
-@pytest.mark.parametrize("mode", ["exact", "f16"])
+@pytest.mark.parametrize("mode", ["exact", "f16", "bf16"])
 @pytest.mark.parametrize("vectors_rows,splits", [(0, 0), (8, 1), (16, 1), (16, 2), (8, 3), (8, 4), (16, 5), (8, 6),
                                                  (16, 7), (16, 8)])
-def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits, impl):
-    """64 or 128 query vectors per workgroup and 1..8 KV splits (some empty;
-    each split count has its own merge kernel),
-    over a chunk whose rows cross several 64-position tiles and end in a
-    partial row block, for both f16/bf16 attention kernels."""
+def test_tile_shapes_and_kv_splits_agree(mode, vectors_rows, splits):
+    """1..8 KV splits (some empty) over a chunk whose rows cross several
+    64-position tiles and end in a partial block of query vectors: EXACT at
+    64 or 128 query vectors per workgroup (each split count has its own
+    merge kernel), F16/BF16 at 256 (the splits folded inside the launch;
+    the vector count is EXACT's knob only)."""
     torch_cuda()
-    say(f"case tiles rows={vectors_rows} splits={splits} mode={mode} impl={impl}")
+    say(f"case tiles rows={vectors_rows} splits={splits} mode={mode}")
     rng = Rng(0x711E + 31 * splits + vectors_rows)
     n_kv, n_q, hd, start, rows = 4, 32, 128, 200, 130
     kv, ref = twin(rng, n_kv, hd, start + rows, start + rows, "f32")
-    kv.set_tuning(4, vectors_rows)
-    kv.set_tuning(2, splits)
-    kv.set_tuning(rv.RV_TUNE_PREFILL_IMPL, impl)
+    kv.set_tuning(rv.RV_TUNE_PREFILL_ROWS, vectors_rows)
+    kv.set_tuning(rv.RV_TUNE_PREFILL_KV_SPLIT, splits)
     q = rng.vec_in(rows * n_q * hd, -2.0, 2.0).reshape(rows, -1)
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     out = dev(np.full(q.shape, np.nan))
     rv.attention_at_rows(dev(q), kv, 0, start, scale, out, mode=mode)
     want = ref.scatter_attention(q, 0, start, scale, THREADS)
-    e = gate(host(out), want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode],
+    got = host(out)
+    e = gate(got, want, rel=BOUNDS[mode], abs_tol=ABS[mode], scale=SCALE[mode],
              what=f"tiles {vectors_rows}/{splits} {mode}")
     say(f"  max rel err {e:.3e}")
+    # Again: the same bits (each split fold's ticket is reset by its last
+    # arriver, and the fold runs in split order whichever split finishes last).
+    out2 = dev(np.full(q.shape, np.nan))
+    rv.attention_at_rows(dev(q), kv, 0, start, scale, out2, mode=mode)
+    assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
 
 
 def weighted_magnitude(q, K, V, n_kv, hd, start, scale):
