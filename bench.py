@@ -823,6 +823,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--prefill-case", action="append", default=[], metavar="CFG:MODE",
+                    help="with --prefill-only: run only these cases (e.g. 4:f16), repeatable")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the prefill legs (configs 3 and 4, every mode), log them and exit (for profiling)")
     ap.add_argument("--projections-only", action="store_true",
@@ -893,7 +895,9 @@ def main():
         log(f"config 5 default over one MALL-resident cache: {r5['default']['us_per_call_one_cache_mall']:.2f} us/call")
         return
     if args.prefill_only:
-        for cfg, mode in ((3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")):
+        cases = [(int(c.split(":")[0]), c.split(":")[1]) for c in args.prefill_case] or \
+            [(3, "f16"), (3, "bf16"), (3, "exact"), (4, "f16"), (4, "bf16"), (4, "exact")]
+        for cfg, mode in cases:
             r = bench_prefill(torch, rv, synth, cfg, mode)
             log(f"config {cfg} {mode}: {r['us_per_call']:.1f} us/call, kernel {r['us_attention_kernel']:.1f} us, "
                 f"{r['tflops_kernel']:.1f} TFLOP/s")

@@ -1036,9 +1036,12 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
     hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
     const bool prep = sd.base != nullptr;
     if (hs.e == hipSuccess)
-      hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, start + rows, kv->n_kv_heads, p.group)
-                                    : rows * hd * sizeof(float));
-    const rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, start + rows, p.group, scale) : rv::QPrep{};
+      hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, kv->n_kv_heads, p.group) : rows * hd * sizeof(float));
+    rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, p.group, scale) : rv::QPrep{};
+    if (prep && hs.e == hipSuccess) {
+      hs = rv::ensure_rope_tab(kv, theta, start + rows);
+      qp.rope = kv->rope_tab;
+    }
     if (hs.e == hipSuccess)
       hs = rv::launch_row_prologue(kv, layer, len, prep ? dq : nullptr, nullptr, prep ? p.n_q_heads : 0, dk, dv, rows,
                                    prep ? dwq : nullptr, dwk, eps, inv, start, prep ? nullptr : kv->qbuf, &sd,

@@ -179,26 +179,6 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
 // (max, sum)[128 columns].
 constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
 
-// Eight consecutive floats: two 16-byte loads when `vec` (p 16-byte
-// aligned), else eight 4-byte loads.
-__device__ __forceinline__ void ld8(const float* p, bool vec, float (&o)[8]) {
-  if (vec) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o[e] = a[e];
-      o[4 + e] = b[e];
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = p[e];
-  }
-}
-
-__device__ __forceinline__ bool aligned16(const void* a, const void* b = nullptr, const void* c = nullptr) {
-  return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0;
-}
-
 // Units of a launch: (split, row block, kv head) of a unit index, by
 // blockIdx (each XCD a contiguous run, kv-head-major).
 struct Unit {
@@ -670,16 +650,21 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 
 // ---- F16 / BF16: v_mfma_f32_32x32x16 tiles --------------------------------------------
 //
-// prefill32_kernel: one workgroup of 8 waves per (kv head, block of 256 query
-// vectors, KV split); wave w owns the 32 columns [32 w, 32 w + 32) (column m
-// is head m / qr, row m % qr of the block, qr = 256 / group). Every wave
-// computes every 64-position tile of the workgroup's range for its columns,
-// so one staged tile in LDS feeds 256 columns and each operand read feeds an
-// MFMA of 32 columns (twice the columns per LDS byte of a 16x16 tile). The
-// two waves sharing a SIMD are left to the hardware's interleaving: with
-// both issuing QK, softmax and PV in the same order one's VALU work runs
-// under the other's MFMAs (a prototype that offset the two wave groups by a
-// tile phase measured 12-16 % slower). Per tile, per wave:
+// prefill32_kernel<MODE, W, G>: one workgroup of W waves per (kv head, block
+// of V = 32 W / G query vectors, KV split), in G groups of W / G waves; wave
+// wv of each group owns the 32 columns [32 wv, 32 wv + 32) (column m is head
+// m / qr, row m % qr of the block, qr = V / group). Group gi computes the
+// tiles G j + gi of the workgroup's range for its columns, and the groups'
+// (O, max, sum) merge through LDS at the end, so one step of the ring feeds
+// V columns from each of G tiles and the causal chain of the block's longest
+// range is 1 / G as long. Each operand read feeds an MFMA of 32 columns
+// (twice the columns per LDS byte of a 16x16 tile). The two waves sharing a
+// SIMD are left to the hardware's interleaving (a prototype that offset them
+// by a tile phase measured 12-16 % slower). The instantiation is W = 8, G =
+// 2: 128-column units, the same throughput at 3.9k positions as 256-column
+// units with twice the KV splits (47.1 vs 48.3 us), and a chain half as long
+// where the chunk's own rows dominate (config 3: 14.4 vs 16.0 us). Per
+// tile, per wave:
 //   S^T[t][m] = sum_d K[t][d] Q[m][d]: A = K (32 positions x 16 d, one
 //     16-byte chunk of a staged K row per lane), B = Q^T (this lane's column
 //     lc = lane % 32 at d = 16 ks + 8 g + i, g = lane / 32), in registers;
@@ -691,14 +676,19 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 //     pb, rounded, are exactly the B operand P^T of PV step (pb, h) (the V^T
 //     tile is staged with its positions in that order, vt_pos32);
 //   O^T[d][m] += sum_t V^T[d][t] P^T[t][m]: 4 d blocks x 4 steps = 16 MFMAs.
-// Tiles stream through a 4-stage ring by direct-to-LDS loads, 3 tiles ahead.
-// The KV range is split across workgroups when the chunk has too few query
+// Tiles stream through a 4-stage ring by direct-to-LDS loads (inline
+// assembly, so the compiler adds no wait for them before LDS reads), the
+// next step's tiles in flight during a step. The KV range is split across
+// workgroups when the chunk has too few query
 // blocks to fill the chip; the splits of a block run on one XCD (blockIdx
 // agreeing mod 8: the dispatcher deals workgroups to the XCDs round robin),
 // write their partial (O, max, sum) columns with plain stores and take a
 // ticket, and the last to finish folds them in split order from that XCD's
 // L2 (no second launch, no workgroup waits on another).
 constexpr int kP32Stages = 4;
+constexpr int kP32Waves = 8;   // per workgroup
+constexpr int kP32Groups = 2;  // wave groups splitting a unit's tiles
+static_assert(32 * kP32Waves / kP32Groups == kQPrepVectors, "unit columns");
 constexpr int kP32TileBytes = 2 * kPlaneBytes;
 constexpr int kP32Part = 130;  // floats per partial column: O[128], max, sum
 constexpr int kPolicyL2 = 1;   // the sc0 bit: the load misses the CU's L1 and reads its XCD's L2
@@ -715,54 +705,6 @@ template <>
 struct Op32<kBF16> {
   __device__ static f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
-// This lane's 64 elements of one query vector, x[ks][i] = q[16 ks + 8 g + i]
-// (its partner lane, 32 apart, holds the other 64), with the q prologue's
-// operands when qn_w is given: the loads only (Q32Loads::issue), so the
-// caller can queue the first tiles' loads behind them before anything
-// waits, then the prologue (finish): RMSNorm with an f64 sum of squares over
-// the pair, then `x * inv * w` and the rotation of the pairs (d, d + 64)
-// (both in this lane: ks and ks + 4), in the reference's separately rounded
-// f32 operations, with the row's (cos, sin) from tab_row (64 cos, then 64
-// sin), as the row prologue would.
-struct Q32Loads {
-  float x[8][8];
-  float w0[4][8], w1[4][8], cs[4][8], sn[4][8];
-  __device__ __forceinline__ void issue(const float* qp, int g, const float* __restrict__ qn_w,
-                                        const float* __restrict__ tab_row) {
-    const bool vec = aligned16(qp, qn_w, tab_row);
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) ld8(qp + 16 * ks + 8 * g, vec, x[ks]);
-    if (!qn_w) return;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int i = 16 * ks + 8 * g;
-      ld8(qn_w + i, vec, w0[ks]);
-      ld8(qn_w + i + 64, vec, w1[ks]);
-      ld8(tab_row + i, vec, cs[ks]);
-      ld8(tab_row + 64 + i, vec, sn[ks]);
-    }
-  }
-  __device__ __forceinline__ void finish(bool norm, float qn_eps) {
-#pragma clang fp contract(off)
-    if (!norm) return;
-    double ss = 0.0;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += (double)x[ks][e] * (double)x[ks][e];
-    ss = swap_sum_f64<32>(ss);
-    const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)qn_eps));
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a0 = x[ks][e] * inv * w0[ks][e], a1 = x[ks + 4][e] * inv * w1[ks][e];
-        x[ks][e] = a0 * cs[ks][e] - a1 * sn[ks][e];
-        x[ks + 4][e] = a0 * sn[ks][e] + a1 * cs[ks][e];
-      }
   }
 };
 
@@ -820,7 +762,7 @@ __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o
   }
 }
 
-template <int MODE, int W>
+template <int MODE, int W, int G>
 __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restrict__ q, const char* __restrict__ stage,
                                                         int n_stage_tiles, int q_stride, int rows, int start,
                                                         int group, int n_rb, int n_units, int per_xcd, int kv_splits,
@@ -832,13 +774,15 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   typedef typename Op<MODE>::E E;
   typedef typename Op<MODE>::V8 V8;
   constexpr int TB = kP32TileBytes, NS = kP32Stages;
-  constexpr int V = 32 * W;        // columns per unit
+  constexpr int VG = W / G;        // waves per group
+  constexpr int V = 32 * VG;       // columns per unit
   constexpr int PW = 32 / W;       // 1 KiB pieces per wave per tile
   // Scores may exceed the running maximum by 2^kRescale (log2 units) before
   // it moves: P stays below 2^8 and most tiles skip rescaling O.
   constexpr float kRescale = 8.0f;
   __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
   __shared__ unsigned sm_ticket;
+  __shared__ float sm_ml[G > 1 ? 2 * VG * 64 : 1];
 
   // Unit (kv head, row block) and split: the splits of a unit share blockIdx
   // mod 8 (one XCD); each XCD takes a contiguous run of units, kv-head-major,
@@ -850,6 +794,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   const int kvh = u / n_rb, rb = u % n_rb;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = w / VG, wv = w % VG;  // group, wave within it
   const int g = lane >> 5, lc = lane & 31;
   const int qr = V / group;
   const int r0 = rb * qr, rows_here = min(qr, rows - r0);
@@ -858,7 +803,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   const int n_tiles = (wg_limit + kBT - 1) / kBT;
   const int tt_lo = (int)((long)n_tiles * split / kv_splits);
   const int n = (int)((long)n_tiles * (split + 1) / kv_splits) - tt_lo;
-  const int m = 32 * w + lc;  // this lane's column
+  const int m = 32 * wv + lc;  // this lane's column
   const int head = m / qr, row = r0 + m % qr;
   const bool col_ok = m % qr < rows_here;
   const int my_limit = start + row + 1;
@@ -870,7 +815,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   V8 qv[8];
   const int q_row = col_ok ? row : r0;
   if (qprep) {
-    const V8* qp = reinterpret_cast<const V8*>(qprep) + ((size_t)u * W + w) * 8 * 64 + lane;
+    const V8* qp = reinterpret_cast<const V8*>(qprep) + ((size_t)u * VG + wv) * 8 * 64 + lane;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qv[ks] = qp[64 * ks];
   } else {
@@ -883,16 +828,18 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   // do not all request the same lines of that XCD's L2 at once.
   const int rot = n > 0 ? (int)((long)ui * n / per_xcd) : 0;
   auto tile_of = [&](int j) { return j + rot < n ? j + rot : j + rot - n; };
-  // Step j's tile into stage j % NS: 32 pieces of 1 KiB, wave w copies w, w + 8, ...
-  auto issue = [&](int j) {
-    const char* t = src + (size_t)tile_of(j) * TB;
+  // Tile t (in issue order) into stage t % NS: 32 pieces of 1 KiB, wave w
+  // copies w, w + W, ... Step j computes tiles G j .. G j + G - 1, group gi
+  // the tile G j + gi; the NS - G tiles after them are in flight meanwhile.
+  auto issue = [&](int t) {
+    const char* tp = src + (size_t)tile_of(t) * TB;
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
       const int piece = 1024 * (w + W * i);
-      lds_dma16(t + piece, lds_offset(&lds[j % NS][piece]));
+      lds_dma16(tp + piece, lds_offset(&lds[t % NS][piece]));
     }
   };
-  for (int j = 0; j < 3 && j < n; ++j) issue(j);
+  for (int t = 0; t < NS - G && t < n; ++t) issue(t);
   if (qprep) {
     if (!col_ok) {
 #pragma unroll
@@ -912,18 +859,24 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   for (int db = 0; db < 4; ++db) o[db] = f32x16{};
   float m_run = kNegSentinel, l_run = 0.f;
   float negm = 0.f;  // -m_run, or 0 while the column has seen no position
-  for (int j = 0; j < n; ++j) {
-    // Tile j has landed once at most the later tiles issued are in flight;
-    // the barrier makes every wave's pieces visible and retires stage
-    // (j - 1) % NS, which the loads below overwrite.
-    if (j + 2 < n) wait_vmcnt<2 * PW>();
-    else if (j + 1 < n) wait_vmcnt<PW>();
+  const int steps = (n + G - 1) / G;
+  for (int j = 0; j < steps; ++j) {
+    // Step j's tiles have landed once at most the later tiles issued are in
+    // flight; the barrier makes every wave's pieces visible and retires the
+    // previous step's stages, which the loads below overwrite.
+    const int ahead = min(n - G * (j + 1), NS - 2 * G);
+    if (ahead >= 2) wait_vmcnt<2 * PW>();
+    else if (ahead == 1) wait_vmcnt<PW>();
     else wait_vmcnt<0>();
     __syncthreads();
-    if (j + 3 < n) issue(j + 3);
-    const char* kt = lds[j % NS];
+#pragma unroll
+    for (int k = 0; k < G; ++k)
+      if (G * j + NS - G + k < n) issue(G * j + NS - G + k);
+    const int tl = G * j + gi;
+    if (tl >= n) continue;
+    const char* kt = lds[tl % NS];
     const char* vt = kt + kPlaneBytes;
-    const int t0 = (tt_lo + tile_of(j)) * kBT;
+    const int t0 = (tt_lo + tile_of(tl)) * kBT;
     f32x16 sc[2];
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
@@ -993,6 +946,33 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     }
   }
   l_run = swap_sum<32>(l_run);  // the column's other half of the positions
+  if constexpr (G > 1) {
+    // The second group's (O, max, sum) into the first's: O through the
+    // upper half of the ring, (max, sum) through sm_ml; the first group
+    // continues with the merged column.
+    __syncthreads();  // every wave is past the ring
+    float* xo = reinterpret_cast<float*>(&lds[2][0]) + (size_t)wv * 64 * 64 + lane;
+    if (gi == 1) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xo[(16 * db + r) * 64] = o[db][r];
+      sm_ml[wv * 64 + lane] = m_run;
+      sm_ml[(VG + wv) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (gi == 0) {
+      const float m2 = sm_ml[wv * 64 + lane], l2 = sm_ml[(VG + wv) * 64 + lane];
+      const float M = fmaxf(m_run, m2);
+      const float a1 = __builtin_amdgcn_exp2f(m_run - M), a2 = __builtin_amdgcn_exp2f(m2 - M);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a1 + xo[(16 * db + r) * 64] * a2;
+      l_run = l_run * a1 + l2 * a2;
+      m_run = M;
+    }
+  }
 
   // The output goes through LDS (the tile ring is free once every wave is
   // past its last tile): put() writes 32 d of this lane's column, o-layout
@@ -1001,7 +981,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   // (the 32 lanes of one chunk hit distinct banks); flush() then reads whole
   // rows back, 512 contiguous bytes per half-wave, and stores each column's
   // row of out with 16-byte stores.
-  float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)w * 32 * kD;
+  float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)wv * 32 * kD;
   auto put = [&](int db, const f32x16& v, float inv) {
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
@@ -1012,22 +992,28 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   };
   auto flush = [&]() {
     const bool vec = aligned16(out) && q_stride % 4 == 0;
-#pragma unroll 4
+    f32x4 x[16];
+#pragma unroll
     for (int it = 0; it < 16; ++it) {
-      const int r = 2 * it + g, mm = 32 * w + r;  // row r of the region: column mm
+      const int r = 2 * it + g;  // row r of the region: column 32 wv + r
+      x[it] = *reinterpret_cast<const f32x4*>(obuf + r * kD + 4 * (lc ^ r));
+    }
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + g, mm = 32 * wv + r;
       if (mm % qr >= rows_here) continue;
-      const f32x4 x = *reinterpret_cast<const f32x4*>(obuf + r * kD + 4 * (lc ^ r));
       float* op = out + (size_t)(r0 + mm % qr) * q_stride + (size_t)(kvh * group + mm / qr) * kD + 4 * lc;
       if (vec) {
-        *reinterpret_cast<f32x4*>(op) = x;
+        *reinterpret_cast<f32x4*>(op) = x[it];
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) op[e] = x[e];
+        for (int e = 0; e < 4; ++e) op[e] = x[it][e];
       }
     }
   };
   if (kv_splits == 1) {
-    __syncthreads();  // every wave is past the ring
+    if constexpr (G == 1) __syncthreads();  // every wave is past the ring
+    if (gi != 0) return;
     const float inv = 1.0f / l_run;
 #pragma unroll
     for (int db = 0; db < 4; ++db) put(db, o[db], inv);
@@ -1035,12 +1021,12 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     return;
   }
   // This split's partial, laid out so a wave's stores and loads are
-  // contiguous: O as 16-byte chunks c (d = 4c .. 4c + 3) of all 256 columns,
-  // chunk-major, then (max, sum) per column. Lane (lc, g) holds chunks
-  // c = 8 db + 2 jj + g of its column.
+  // contiguous: O as 16-byte chunks c (d = 4c .. 4c + 3) of the unit's V
+  // columns, chunk-major, then (max, sum) per column. Lane (lc, g) holds
+  // chunks c = 8 db + 2 jj + g of its column.
   const size_t slice = (size_t)u * kv_splits;  // this unit's first split
   const size_t ml_base = (size_t)n_units * kv_splits * 32 * V;  // f32x4 units
-  {
+  if (gi == 0) {
     f32x4* ob = reinterpret_cast<f32x4*>(part) + (slice + split) * 32 * V + m;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -1062,7 +1048,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     sm_ticket = got;
   }
   __syncthreads();
-  if (sm_ticket != (unsigned)kv_splits - 1) return;
+  if (sm_ticket != (unsigned)kv_splits - 1 || gi != 0) return;
   // Fold in split order from this XCD's L2 (the same bits whichever split
   // finishes last; this split's own partial was stored above like the
   // others').
@@ -1164,17 +1150,11 @@ struct P32Args {
   TimedPair tp;
 };
 template <int MODE>
-void launch_p32(const P32Args& a, int vectors, hipStream_t s) {
+void launch_p32(const P32Args& a, hipStream_t s) {
   const unsigned blocks = (unsigned)(8 * a.per_xcd * a.kv_splits);
-#define RV_P32(W)                                                                                                  \
-  launch_timed(a.tp, prefill32_kernel<MODE, W>, dim3(blocks), dim3(64 * W), s, a.q, a.stage, a.n_stage_tiles,      \
-               a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.per_xcd, a.kv_splits, a.qscale, a.qn_w, \
-               a.qn_eps, a.qn_tab, a.qprep, a.part, a.part_bytes, a.tickets, a.out)
-  if (vectors == 128)
-    RV_P32(4);
-  else
-    RV_P32(8);
-#undef RV_P32
+  launch_timed(a.tp, prefill32_kernel<MODE, kP32Waves, kP32Groups>, dim3(blocks), dim3(64 * kP32Waves), s, a.q,
+               a.stage, a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.per_xcd,
+               a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.qprep, a.part, a.part_bytes, a.tickets, a.out);
 }
 
 // Stage tiles [lo, hi) of every kv head of `layer` (positions at or past
@@ -1208,17 +1188,12 @@ void launch_stage(const rv_kv* kv, size_t layer, uint32_t mode, size_t positions
 
 }  // namespace
 
-// 128 columns (4 waves) while the chunk's rows see at most 16 tiles: there
-// the longest unit's chain of tiles bounds the launch, and halving the
-// columns per tile halves its length; 256 (8 waves) beyond, where one staged
-// tile feeding twice the columns halves the L2 traffic.
-int p32_vectors(size_t positions) { return (positions + kBT - 1) / kBT <= 16 ? 128 : 256; }
-size_t qprep_bytes(size_t rows, size_t positions, size_t n_kv_heads, size_t group) {
-  const size_t v = (size_t)p32_vectors(positions), qr = v / group;
-  return n_kv_heads * ((rows + qr - 1) / qr) * v * 128 * 2;
+size_t qprep_bytes(size_t rows, size_t n_kv_heads, size_t group) {
+  const size_t qr = kQPrepVectors / group;
+  return n_kv_heads * ((rows + qr - 1) / qr) * kQPrepVectors * kD * 2;
 }
-QPrep qprep_plan(char* base, size_t rows, size_t positions, size_t group, float scale) {
-  const int qr = p32_vectors(positions) / (int)group;
+QPrep qprep_plan(char* base, size_t rows, size_t group, float scale) {
+  const int qr = kQPrepVectors / (int)group;
   return QPrep{base, (int)group, qr, (int)((rows + qr - 1) / qr), scale * kLog2e};
 }
 
@@ -1294,14 +1269,16 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   int vectors, n_rb, per_xcd = 0;
   size_t part_bytes = 0;
   if (!split_mode) {
-    // F16 / BF16 (prefill32_kernel): 256-vector blocks; the KV axis is split
-    // until about kCUs workgroups run, each split keeping at least 4 tiles of
-    // the longest block, and only where the XCD fold is available.
-    vectors = p32_vectors(positions);
+    // F16 / BF16 (prefill32_kernel): 128-column units; the KV axis is split
+    // across workgroups until about kCUs of them run, each split keeping at
+    // least 4 tiles of the longest block per wave group, and only where the
+    // XCD fold is available.
+    vectors = kQPrepVectors;
     const int qr = vectors / group;
     n_rb = (int)((rows + qr - 1) / qr);
     const long units = (long)n_rb * n_kv;
-    if (kv_splits <= 0) kv_splits = (int)std::min<long>((kCUs + units - 1) / units, std::max(1, n_stage_tiles / 4));
+    if (kv_splits <= 0)
+      kv_splits = (int)std::min<long>((kCUs + units - 1) / units, std::max(1, n_stage_tiles / (4 * kP32Groups)));
     if (!kv->xcd_ok) kv_splits = 1;
     kv_splits = std::max(1, std::min(kv_splits, kMaxKvSplits));
     per_xcd = (int)((units + 7) / 8);
@@ -1336,7 +1313,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
   // about kCUs workgroups' worth (256 rows of 128 columns in EXACT, 256
   // units of 256 columns for F16 / BF16), and a call stages at most every
   // tile of the capacity in the split mode's (largest) layout.
-  const size_t bound = std::max<size_t>(part_bytes, (size_t)kCUs * 256 * kP32Part * sizeof(float)) +
+  const size_t bound = std::max<size_t>(part_bytes, (size_t)kCUs * kQPrepVectors * kP32Part * sizeof(float)) +
                        (size_t)n_kv * ((kv->capacity + kBT - 1) / kBT) * tile_bytes_of(RV_PREFILL_EXACT);
   st = ensure_workspace(kv, part_bytes + call_stage_bytes, bound);
   if (st.e != hipSuccess) return st;
@@ -1373,9 +1350,9 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
                     (uint32_t)std::min<size_t>(part_bytes, 0xFFFFFFF0u),
                     kv->pf_tickets, out, tp};
     if (m == RV_PREFILL_BF16)
-      launch_p32<kBF16>(a, vectors, s);
+      launch_p32<kBF16>(a, s);
     else
-      launch_p32<kF16>(a, vectors, s);
+      launch_p32<kF16>(a, s);
   } else {
     PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
                   (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,

@@ -149,6 +149,40 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
   }
 }
 
+// One wave of a staging launch's query preparation: the 32 columns
+// [32 wv, 32 wv + 32) of unit u (qw = u * VG + wv) in the prepared layout.
+// Lane (lc, g) takes half of column lc's query (Q32Loads' layout: the rope
+// pairs (d, d + 64) in one lane), RMSNorms and rotates it with its row's
+// (cos, sin) from the cache's table, scales and rounds it, and the wave
+// stores its eight 1 KiB operand blocks whole. Columns past the chunk's rows
+// are zeros.
+template <int SM>
+__device__ __forceinline__ void prep_q_wave(int qw, const float* __restrict__ q, int n_q,
+                                            const float* __restrict__ q_w, float eps, long pos0, int rows,
+                                            const QPrep& qp, int lane) {
+  typedef typename Op<SM>::E E;
+  typedef typename Op<SM>::V8 V8;
+  constexpr int VG = kQPrepVectors / 32;
+  const int u = qw / VG, wv = qw % VG;
+  const int kvh = u / qp.n_rb, rb = u % qp.n_rb;
+  const int lc = lane & 31, g = lane >> 5;
+  const int m = 32 * wv + lc, head = m / qp.qr, row = rb * qp.qr + m % qp.qr;
+  const bool ok = row < rows;
+  const int q_row = ok ? row : rb * qp.qr;  // a row of the unit (its first is in the chunk)
+  Q32Loads ql;
+  ql.issue(q + ((size_t)q_row * n_q + (size_t)(kvh * qp.group + head)) * 128, g, q_w,
+           qp.rope + (size_t)(pos0 + q_row) * 128);
+  ql.finish(true, eps);
+  V8* dst = reinterpret_cast<V8*>(qp.base) + (size_t)qw * 8 * 64 + lane;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    V8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = ok ? (E)(ql.x[ks][e] * qp.qscale) : (E)0.f;
+    dst[64 * ks] = x;
+  }
+}
+
 // One decode or prefill row's prologue: q heads RMSNormed + rotated into
 // q_out, k heads RMSNormed + rotated into the cache, v heads copied into the
 // cache. grid (rows, slot blocks), one wave per 4 head slots of the row's
@@ -164,9 +198,14 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
 // blocks y >= the q and k slot blocks, one per (quad of positions x, head y
 // - those blocks): stage_v_quad.
 constexpr int kSlots = 4;
+// Waves per block of a staging launch (the slot blocks of one row side by
+// side: a prefill chunk's q, k and v heads are 8 + 1 + 4 blocks of a row at
+// GQA 32/4, each short, so blocks of one wave spend more on dispatch than on
+// work); other launches use one-wave blocks.
+constexpr int kPrologueWaves = 4;
 
 template <typename T, int NP, int SM>
-__global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
+__global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const float* __restrict__ q, float* __restrict__ q_out,
                                                           int n_q, const float* __restrict__ k,
                                                           const float* __restrict__ v, T* __restrict__ kp,
                                                           T* __restrict__ vp, int n_kv, int hd,
@@ -175,22 +214,49 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
                                                           long pos0, float* __restrict__ tab, StagedRows sr,
                                                           QPrep qp) {
 #pragma clang fp contract(off)
-  const int r = blockIdx.x, lane = threadIdx.x;
+  const int r = blockIdx.x, lane = threadIdx.x & 63;
   const int half = hd / 2;
-  const int n_slots = SM >= 0 ? n_q + n_kv : n_q + 2 * n_kv;
-  const int s0 = (int)blockIdx.y * kSlots;
+  // This wave's slot block: blockIdx.y in one-wave blocks, the block's
+  // waves side by side in a staging launch's (no block-wide barrier: each
+  // wave is independent).
+  const int wib = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // With prepared queries the first block rows prepare them, one unit's 32
+  // columns per wave (dispatched first, so their loads overlap the k and v
+  // blocks'); the rest are the row slots.
+  int by = (int)blockIdx.y;
+  if constexpr (SM >= 0) {
+    if (qp.base) {
+      const int q_waves = n_kv * qp.n_rb * (kQPrepVectors / 32);
+      const int qy = (q_waves + (int)gridDim.x * kPrologueWaves - 1) / ((int)gridDim.x * kPrologueWaves);
+      if (by < qy) {
+        const int qw = (by * (int)gridDim.x + r) * kPrologueWaves + wib;
+        if (qw < q_waves) prep_q_wave<SM>(qw, q, n_q, q_w, eps, pos0, sr.rows, qp, lane);
+        return;
+      }
+      by -= qy;
+    }
+  }
+  const int sy = by * (int)(blockDim.x >> 6) + wib;
+  const int n_q_row = (SM >= 0 && qp.base) ? 0 : n_q;
+  const int n_slots = SM >= 0 ? n_q_row + n_kv : n_q + 2 * n_kv;
+  const int s0 = sy * kSlots;
   if constexpr (SM >= 0) {
     const int kb = (n_slots + kSlots - 1) / kSlots;
-    if ((int)blockIdx.y >= kb) {
-      stage_v_quad<T, SM>(v, vp, n_kv, (int)blockIdx.y - kb, sr, r, lane);
+    if (sy >= kb + n_kv) return;
+    if (sy >= kb) {
+      stage_v_quad<T, SM>(v, vp, n_kv, sy - kb, sr, r, lane);
       return;
     }
+  } else {
+    if (s0 >= n_slots) return;
+  }
+  if constexpr (SM >= 0) {
     if (r >= sr.rows) {
 #pragma unroll
       for (int j = 0; j < kSlots; ++j) {
         const int s = s0 + j;
-        if (s < n_q || s >= n_slots) continue;
-        const int kind = s >= n_q + n_kv, h = s - n_q - kind * n_kv;
+        if (s < n_q_row || s >= n_slots) continue;
+        const int kind = s >= n_q_row + n_kv, h = s - n_q_row - kind * n_kv;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
           const int i = lane + 64 * p;
@@ -204,9 +270,9 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
   }
   // Source of slot s (q, k or v head of row r); its destination is below.
   auto src = [&](int s) -> const float* {
-    if (s < n_q) return q + ((size_t)r * n_q + s) * hd;
-    if (s < n_q + n_kv) return k + ((size_t)r * n_kv + (s - n_q)) * hd;
-    return v + ((size_t)r * n_kv + (s - n_q - n_kv)) * hd;
+    if (s < n_q_row) return q + ((size_t)r * n_q + s) * hd;
+    if (s < n_q_row + n_kv) return k + ((size_t)r * n_kv + (s - n_q_row)) * hd;
+    return v + ((size_t)r * n_kv + (s - n_q_row - n_kv)) * hd;
   };
   // inv_freq first: the sin/cos below wait only for it, not the heads.
   double freq[NP];
@@ -242,16 +308,21 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
   __builtin_amdgcn_sched_barrier(0);
   const double pos = (double)(pos0 + r);
   // Blocks of v heads only need no angles.
-  const bool rotates = s0 < n_q + n_kv;
+  const bool rotates = s0 < n_q_row + n_kv;
   float sn[NP], cs[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int i = lane + 64 * p;
     double sd = 0.0, cd = 1.0;
-    if (rotates && i < half) sincos(pos * freq[p], &sd, &cd);
+    if (qp.rope && i < half) {  // the same f32 values, computed once per position on the host
+      cd = qp.rope[(size_t)(pos0 + r) * hd + i];
+      sd = qp.rope[(size_t)(pos0 + r) * hd + half + i];
+    } else if (rotates && i < half) {
+      sincos(pos * freq[p], &sd, &cd);
+    }
     sn[p] = (float)sd;
     cs[p] = (float)cd;
-    if (tab && blockIdx.y == 0 && i < half) {
+    if (tab && sy == 0 && i < half) {
       tab[(size_t)r * hd + i] = cs[p];
       tab[(size_t)r * hd + half + i] = sn[p];
     }
@@ -274,8 +345,8 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
   for (int j = 0; j < kSlots; ++j) {
     const int s = s0 + j;
     if (s >= n_slots) break;
-    if (s >= n_q + n_kv) {  // v head: copied into the cache
-      T* d = vp + ((size_t)r * n_kv + (s - n_q - n_kv)) * hd;
+    if (s >= n_q_row + n_kv) {  // v head: copied into the cache
+      T* d = vp + ((size_t)r * n_kv + (s - n_q_row - n_kv)) * hd;
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
         const int i = lane + 64 * p;
@@ -283,14 +354,14 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
           const float c0 = store_cached<T>(d + i, x0[j][p]);
           const float c1 = store_cached<T>(d + i + half, x1[j][p]);
           if constexpr (SM >= 0) {
-            stage_elem<SM>(sr, 1, s - n_q - n_kv, sr.row0 + r, i, c0);
-            stage_elem<SM>(sr, 1, s - n_q - n_kv, sr.row0 + r, i + half, c1);
+            stage_elem<SM>(sr, 1, s - n_q_row - n_kv, sr.row0 + r, i, c0);
+            stage_elem<SM>(sr, 1, s - n_q_row - n_kv, sr.row0 + r, i + half, c1);
           }
         }
       }
       continue;
     }
-    const bool is_q = s < n_q;
+    const bool is_q = s < n_q_row;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const int i = lane + 64 * p;
@@ -299,27 +370,16 @@ __global__ __launch_bounds__(64) void row_prologue_kernel(const float* __restric
       const float a1 = x1[j][p] * inv_rms[j] * (is_q ? wq1[p] : wk1[p]);
       const float ya = a0 * cs[p] - a1 * sn[p], yb = a0 * sn[p] + a1 * cs[p];
       if (is_q) {
-        if constexpr (SM >= 0) {
-          if (qp.base) {  // the prepared layout: scaled and rounded to the MFMA type
-            typedef typename Op<SM>::E E;
-            const int unit = (s / qp.group) * qp.n_rb + r / qp.qr;
-            const size_t c = (size_t)unit * qp.qr * qp.group + (s % qp.group) * qp.qr + r % qp.qr;
-            E* qd = reinterpret_cast<E*>(qp.base);
-            qd[qprep_index(c, i)] = (E)(ya * qp.qscale);
-            qd[qprep_index(c, i + half)] = (E)(yb * qp.qscale);
-            continue;
-          }
-        }
         float* d = q_out + ((size_t)r * n_q + s) * hd;
         d[i] = ya;
         d[i + half] = yb;
       } else {
-        T* d = kp + ((size_t)r * n_kv + (s - n_q)) * hd;
+        T* d = kp + ((size_t)r * n_kv + (s - n_q_row)) * hd;
         const float c0 = store_cached<T>(d + i, ya);
         const float c1 = store_cached<T>(d + i + half, yb);
         if constexpr (SM >= 0) {
-          stage_elem<SM>(sr, 0, s - n_q, sr.row0 + r, i, c0);
-          stage_elem<SM>(sr, 0, s - n_q, sr.row0 + r, i + half, c1);
+          stage_elem<SM>(sr, 0, s - n_q_row, sr.row0 + r, i, c0);
+          stage_elem<SM>(sr, 0, s - n_q_row, sr.row0 + r, i + half, c1);
         }
       }
     }
@@ -332,7 +392,8 @@ void launch_row_prologue_t(dim3 grid, int np, const float* q, float* q_out, int 
                            const InvFreq& inv, long pos0, float* tab, int sm, const StagedRows& sr, const QPrep& qp,
                            hipStream_t s) {
 #define RV_PROLOGUE(NP, SM)                                                                                      \
-  hipLaunchKernelGGL((row_prologue_kernel<T, NP, SM>), grid, dim3(64), 0, s, q, q_out, n_q, k, v, kp, vp, n_kv, hd, \
+  hipLaunchKernelGGL((row_prologue_kernel<T, NP, SM>), grid, dim3(SM >= 0 ? 64 * kPrologueWaves : 64), 0, s, q, q_out, \
+                     n_q, k, v, kp, vp, n_kv, hd,                                                                \
                      q_w, k_w, eps, inv, pos0, tab, sr, qp)
   if (sm == kF16)
     RV_PROLOGUE(1, kF16);
@@ -387,7 +448,7 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   // The split mode's tiles are staged whole by the stage kernel (their
   // exponents span all of a tile's rows), never row by row here. q heads
   // run in a staging launch only into the prepared layout.
-  if ((prep && !staging) ||
+  if ((prep && (!staging || !qp->rope)) ||
       (staging && ((n_q != 0 && !prep) || hd != 128 || (sd->mode != RV_PREFILL_F16 && sd->mode != RV_PREFILL_BF16)))) {
     st.e = hipErrorInvalidValue;
     st.what = "staged prologue geometry";
@@ -399,8 +460,16 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
   // Staging: q and k slot blocks, then one block row per v head (its quads
   // of positions along x; grid_rows covers them).
-  const int slot_blocks =
-      staging ? ((int)n_q + n_kv + kSlots - 1) / kSlots + n_kv : (n_slots + kSlots - 1) / kSlots;
+  // Staging: with prepared queries first enough block rows for one wave per
+  // 32 columns of each unit, then (k blocks + v blocks) / kPrologueWaves.
+  int slot_blocks = (n_slots + kSlots - 1) / kSlots;
+  if (staging) {
+    slot_blocks = ((n_kv + kSlots - 1) / kSlots + n_kv + kPrologueWaves - 1) / kPrologueWaves;
+    if (prep) {
+      const size_t q_waves = (size_t)n_kv * qp->n_rb * (kQPrepVectors / 32);
+      slot_blocks += (int)((q_waves + grid_rows * kPrologueWaves - 1) / (grid_rows * kPrologueWaves));
+    }
+  }
   const QPrep qpv = prep ? *qp : QPrep{};
   const dim3 grid((unsigned)grid_rows, (unsigned)slot_blocks);
   const size_t off = cache_row * kv->kv_dim;

@@ -125,16 +125,85 @@ __device__ __forceinline__ int vt_byte_m(int d, int t) {
   return Op<MODE>::kSplit ? vt_byte(d, t) : vt_byte32(d, t);
 }
 
+// Eight consecutive floats: two 16-byte loads when `vec` (p 16-byte
+// aligned), else eight 4-byte loads.
+__device__ __forceinline__ void ld8(const float* p, bool vec, float (&o)[8]) {
+  if (vec) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = a[e];
+      o[4 + e] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = p[e];
+  }
+}
+
+__device__ __forceinline__ bool aligned16(const void* a, const void* b = nullptr, const void* c = nullptr) {
+  return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0;
+}
+
+// This lane's 64 elements of one query vector, x[ks][i] = q[16 ks + 8 g + i]
+// (its partner lane, 32 apart, holds the other 64), with the q prologue's
+// operands when qn_w is given: the loads only (Q32Loads::issue), so the
+// caller can queue the first tiles' loads behind them before anything
+// waits, then the prologue (finish): RMSNorm with an f64 sum of squares over
+// the pair, then `x * inv * w` and the rotation of the pairs (d, d + 64)
+// (both in this lane: ks and ks + 4), in the reference's separately rounded
+// f32 operations, with the row's (cos, sin) from tab_row (64 cos, then 64
+// sin), as the row prologue would.
+struct Q32Loads {
+  float x[8][8];
+  float w0[4][8], w1[4][8], cs[4][8], sn[4][8];
+  __device__ __forceinline__ void issue(const float* qp, int g, const float* __restrict__ qn_w,
+                                        const float* __restrict__ tab_row) {
+    const bool vec = aligned16(qp, qn_w, tab_row);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) ld8(qp + 16 * ks + 8 * g, vec, x[ks]);
+    if (!qn_w) return;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int i = 16 * ks + 8 * g;
+      ld8(qn_w + i, vec, w0[ks]);
+      ld8(qn_w + i + 64, vec, w1[ks]);
+      ld8(tab_row + i, vec, cs[ks]);
+      ld8(tab_row + 64 + i, vec, sn[ks]);
+    }
+  }
+  __device__ __forceinline__ void finish(bool norm, float qn_eps) {
+#pragma clang fp contract(off)
+    if (!norm) return;
+    double ss = 0.0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (double)x[ks][e] * (double)x[ks][e];
+    ss = swap_sum_f64<32>(ss);
+    const float inv = (float)(1.0 / sqrt(ss / 128.0 + (double)qn_eps));  // head_dim 128
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a0 = x[ks][e] * inv * w0[ks][e], a1 = x[ks + 4][e] * inv * w1[ks][e];
+        x[ks][e] = a0 * cs[ks][e] - a1 * sn[ks][e];
+        x[ks + 4][e] = a0 * sn[ks][e] + a1 * cs[ks][e];
+      }
+  }
+};
+
 // Prepared queries of the F16 / BF16 prefill: a chunk's row prologue writes
 // each query head's row after RMSNorm and RoPE, times log2(e) * scale,
 // rounded to the MFMA type, straight into the attention kernel's operand
 // order, so that kernel's query loads are eight coalesced 16-byte loads per
-// lane. The kernel's units (kv head * n_rb + rb) hold V = 128 or 256 columns
-// each: column m of unit u is query head kv head * group + m / qr of row
-// rb * qr + m % qr (qr = V / group), global column c = u * V + m. Element d
+// lane. The kernel's units (kv head * n_rb + rb) hold V = kQPrepVectors
+// columns each: column m of unit u is query head kv head * group + m / qr of
+// row rb * qr + m % qr (qr = V / group), global column c = u * V + m. Element d
 // of column c sits in 16-byte chunk ((c / 32) * 8 + d / 16) * 64 + 32 * ((d /
 // 8) & 1) + c % 32 at position d % 8: the B operand (Q^T) of the QK step
 // d / 16 of the wave owning columns c - c % 32 .. + 31, in lane order.
+constexpr int kQPrepVectors = 128;
 __host__ __device__ inline size_t qprep_index(size_t c, int d) {
   return ((((c >> 5) * 8 + (size_t)(d >> 4)) * 64 + 32 * ((d >> 3) & 1) + (c & 31)) * 8 + (d & 7));
 }
