@@ -13,11 +13,15 @@ per second of wall time (GB/s). The eager (one host call per layer) step time
 is reported beside it.
 
 `roofline` is for the dominant kernel (the decode tile kernel): algorithmic
-bytes per launch over its average duration, timed live over eager steps with
-HIP events that the kernel launch itself fills with the kernel's start and
-end on the launch stream (RV_TUNE_KERNEL_TIMING, hipExtLaunchKernelGGL).
-`traffic` is the HBM bytes per launch read from the committed rocprofv3
-counter summary, when present.
+bytes per launch over its average duration, given two ways. `trace` is the
+rocprofv3 kernel-trace average recorded in the committed summary of this
+same command (profiles/decode_tile_ctx4096_f32.md: the kernel's execution
+window); `events` is this run's own, timed live over eager steps with HIP
+events that the kernel launch itself fills on the launch stream
+(RV_TUNE_KERNEL_TIMING, hipExtLaunchKernelGGL), which also hold the launch's
+dispatch latency. `frac_source` names the one `frac` uses (the trace when
+the summary records it). `traffic` is the HBM bytes per launch from the same
+summary's counter passes.
 
 `roofline.whole_call` is the same bytes over the whole call's time per layer
 (tile kernel + split-merge kernel, from the graph replay).
@@ -52,6 +56,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 DECODE_PROFILE = os.path.join(ROOT, "profiles", "decode_tile_ctx4096_f32.md")
+CONFIG5_PROFILE = os.path.join(ROOT, "profiles", "decode_tile_ctx32768_f16.md")
 
 
 def log(*a):
@@ -102,14 +107,19 @@ def kernel_avg(torch, kv, fn, iters: int, lead_cycles: int = 0):
     return (ms / 1e3 / n) if n else None, n
 
 
-def traffic_from_profile(path: str):
-    """HBM bytes per launch recorded in a committed counter summary."""
+def profile_value(path: str, key: str):
+    """A `key: value` figure recorded in a committed rocprofv3 summary."""
     try:
         with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", f.read())
+            m = re.search(key + r":\s*([0-9.]+)", f.read())
         return float(m.group(1)) if m else None
     except OSError:
         return None
+
+
+def traffic_from_profile(path: str):
+    """HBM bytes per launch recorded in a committed counter summary."""
+    return profile_value(path, "traffic_bytes_per_launch")
 
 
 def bench_config2(torch, rv, synth, steps, warmup):
@@ -297,6 +307,7 @@ def bench_config5(torch, rv, synth, iters=50, n_caches=5, split_lens=(0, 1024, 2
             kv.set_tuning(rv.RV_TUNE_KERNEL_TIMING, 1)
             kv.kernel_time()
         for _ in range(iters):
+            torch.cuda._sleep(400_000)  # the host queues the five calls ahead of the GPU
             once()
         for kv in caches:
             ms, c = kv.kernel_time()
@@ -921,6 +932,12 @@ def main():
         log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us, "
             f"token graph {r1['token_graph']['us_per_step']:.2f} us/step")
         r5 = bench_config5(torch, rv, synth)
+        c5_trace = profile_value(CONFIG5_PROFILE, "trace_us_per_launch")
+        if c5_trace:
+            d5 = r5["default"]
+            d5["us_tile_kernel_trace"] = c5_trace
+            d5["hbm_frac_tile_kernel_trace"] = round(d5["bytes_per_call"] / (c5_trace * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            d5["trace_profile"] = os.path.relpath(CONFIG5_PROFILE, ROOT)
         extra["config5_decode_f16_ctx32768"] = r5
         for name, r in r5.items():
             log(f"config 5 {name} ({r['splits_per_kv_head']} splits/kv head): {r['us_per_call']:.2f} us/call, "
@@ -962,6 +979,31 @@ def main():
                     if key.startswith(name + "_"):
                         extra[key]["cpu_baseline"] = r
     traffic = traffic_from_profile(DECODE_PROFILE)
+    # Two figures for the tile kernel's launch duration: the committed
+    # rocprofv3 kernel-trace average of this same command (the kernel's
+    # execution window), and this run's HIP events around each launch
+    # (which also hold the launch's dispatch latency, ~0.5-1 us longer).
+    # frac uses the trace figure when the profile records one.
+    trace_us = profile_value(DECODE_PROFILE, "trace_us_per_launch")
+    byts = r2["bytes_per_launch"]
+    ev = {"us_per_launch": round(r2["kernel_us"], 3), "achieved": round(r2["achieved_gbs"], 1),
+          "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "launches_timed": r2["kernel_launches_timed"]}
+    if trace_us:
+        tr_gbs = byts / (trace_us * 1e-6) / 1e9
+        tr = {"us_per_launch": trace_us, "achieved": round(tr_gbs, 1), "frac": round(tr_gbs / HBM_PEAK_GBS, 4),
+              "profile": os.path.relpath(DECODE_PROFILE, ROOT)}
+        head, source = tr, "trace"
+    else:
+        tr, head, source = None, ev, "events"
+    roofline = {"bound": "hbm", "achieved": head["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": head["frac"], "frac_source": source, "traffic": traffic,
+                "kernel": "decode_tile_kernel<float, 4, 1>", "us_per_launch": head["us_per_launch"],
+                "bytes_per_launch": byts, "trace": tr, "events": ev,
+                "events_over_trace": round(r2["kernel_us"] / trace_us, 3) if trace_us and r2["kernel_us"] else None,
+                "whole_call": {"kernels": "decode_tile_kernel + decode_merge_kernel",
+                               "achieved": round(r2["whole_call_gbs"], 1),
+                               "frac": round(r2["whole_call_gbs"] / HBM_PEAK_GBS, 4),
+                               "us_per_call": round(r2["us_per_layer"], 3)}}
     line = {
         "metric": "decode attn µs/layer + HBM GB/s at ctx 4096; prefill attn TFLOP/s (512 tok)",
         "value": round(r2["value_gbs"], 2),
@@ -980,15 +1022,7 @@ def main():
                    "layers": 48, "context": 4096, "n_q_heads": 32, "n_kv_heads": 4, "head_dim": 128,
                    "kv_elem": "f32", "parallelism": "single GPU"},
         "us_per_layer": round(r2["us_per_layer"], 3),
-        "roofline": {"bound": "hbm", "achieved": round(r2["achieved_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r2["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_tile_kernel<float, 4, 1>",
-                     "us_per_launch": round(r2["kernel_us"], 3), "launches_timed": r2["kernel_launches_timed"],
-                     "bytes_per_launch": r2["bytes_per_launch"],
-                     "whole_call": {"kernels": "decode_tile_kernel + decode_merge_kernel",
-                                    "achieved": round(r2["whole_call_gbs"], 1),
-                                    "frac": round(r2["whole_call_gbs"] / HBM_PEAK_GBS, 4),
-                                    "us_per_call": round(r2["us_per_layer"], 3)}},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": extra,
     }
