@@ -823,23 +823,30 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
              qn_tab ? qn_tab + (size_t)q_row * kD : nullptr);
   }
   const char* src = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB + 16 * lane;
-  // The units sharing an XCD walk their splits' tiles from different
-  // starting points (the online softmax takes tiles in any order), so they
-  // do not all request the same lines of that XCD's L2 at once.
-  const int rot = n > 0 ? (int)((long)ui * n / per_xcd) : 0;
-  auto tile_of = [&](int j) { return j + rot < n ? j + rot : j + rot - n; };
-  // Tile t (in issue order) into stage t % NS: 32 pieces of 1 KiB, wave w
-  // copies w, w + W, ... Step j computes tiles G j .. G j + G - 1, group gi
-  // the tile G j + gi; the NS - G tiles after them are in flight meanwhile.
+  // Tile t into stage t % NS: 32 pieces of 1 KiB, wave w copies w, w + W,
+  // ... Step j computes tiles G j .. G j + G - 1, group gi the tile G j +
+  // gi; the NS - G tiles after them are in flight meanwhile. (The units of
+  // an XCD walk their tiles in the same order: their requests for a tile
+  // meet in that XCD's L2. Rotated starting points measured 1.5 us slower
+  // at config 4.)
+  auto issue_piece = [&](int t, int i) {
+    const int piece = 1024 * (w + W * i);
+    lds_dma16(src + (size_t)t * TB + piece, lds_offset(&lds[t % NS][piece]));
+  };
   auto issue = [&](int t) {
-    const char* tp = src + (size_t)tile_of(t) * TB;
 #pragma unroll
-    for (int i = 0; i < PW; ++i) {
-      const int piece = 1024 * (w + W * i);
-      lds_dma16(tp + piece, lds_offset(&lds[t % NS][piece]));
-    }
+    for (int i = 0; i < PW; ++i) issue_piece(t, i);
   };
   for (int t = 0; t < NS - G && t < n; ++t) issue(t);
+  // A step's copies are spread through its compute (kIssueSlots points, one
+  // copy each, in order) rather than issued at once after the barrier: the
+  // address unit takes ~16 cycles per 1 KiB copy, and a wave whose copies
+  // queue behind the other waves' stalls at its next memory instruction.
+  constexpr int kCopies = G * PW;  // copies per wave per step
+  auto issue_copy = [&](int j, int c) {
+    const int t = G * j + NS - G + c / PW;
+    if (c < kCopies && t < n) issue_piece(t, c % PW);
+  };
   if (qprep) {
     if (!col_ok) {
 #pragma unroll
@@ -869,14 +876,15 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     else if (ahead == 1) wait_vmcnt<PW>();
     else wait_vmcnt<0>();
     __syncthreads();
-#pragma unroll
-    for (int k = 0; k < G; ++k)
-      if (G * j + NS - G + k < n) issue(G * j + NS - G + k);
     const int tl = G * j + gi;
-    if (tl >= n) continue;
+    if (tl >= n) {
+#pragma unroll
+      for (int c = 0; c < kCopies; ++c) issue_copy(j, c);
+      continue;
+    }
     const char* kt = lds[tl % NS];
     const char* vt = kt + kPlaneBytes;
-    const int t0 = (tt_lo + tile_of(tl)) * kBT;
+    const int t0 = (tt_lo + tl) * kBT;
     f32x16 sc[2];
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {
@@ -886,7 +894,10 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[pb][r] = negm;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) sc[pb] = Op32<MODE>::mfma(ka[ks], qv[ks], sc[pb]);
+      for (int ks = 0; ks < 8; ++ks) {
+        sc[pb] = Op32<MODE>::mfma(ka[ks], qv[ks], sc[pb]);
+        if (ks == 3 || ks == 7) issue_copy(j, 2 * pb + ks / 4);  // copies 0 .. 3
+      }
     }
     // Causal mask only where some row of the block stops inside the tile.
     if (t0 + kBT > all_see) {
@@ -943,7 +954,10 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
       for (int c = 0; c < 4; ++c) va[c] = *reinterpret_cast<const V8*>(vt + vt_off(32 * db + lc, 2 * c + g));
 #pragma unroll
       for (int c = 0; c < 4; ++c) o[db] = Op32<MODE>::mfma(va[c], ph[c >> 1][c & 1], o[db]);
+      issue_copy(j, 4 + db);  // copies 4 .. 7
     }
+#pragma unroll
+    for (int c = 8; c < kCopies; ++c) issue_copy(j, c);
   }
   l_run = swap_sum<32>(l_run);  // the column's other half of the positions
   if constexpr (G > 1) {
