@@ -135,24 +135,27 @@ def test_device_bytes_account_for_everything_the_cache_allocates(elem):
     assert planes < now0 < bound0
     rng = Rng(0xB17E)
     rows = 64
-    q = dev(rng.vec_in(rows * 32 * hd, -1, 1))
-    k, v = dev(rng.vec_in(rows * n_kv * hd, -1, 1)), dev(rng.vec_in(rows * n_kv * hd, -1, 1))
+    q = dev(rng.vec_in(rows * 32 * hd, -1, 1)).reshape(rows, 32 * hd)
+    k = dev(rng.vec_in(rows * n_kv * hd, -1, 1)).reshape(rows, n_kv * hd)
+    v = dev(rng.vec_in(rows * n_kv * hd, -1, 1)).reshape(rows, n_kv * hd)
     w = dev(np.ones(hd, np.float32))
-    out = torch.zeros(rows * 32 * hd, device="cuda")
-    rv.prefill_chunk(kv, 0, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="exact")
-    rv.prefill_chunk(kv, 1, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="f16")
-    torch.cuda.synchronize()
-    now1, bound1 = kv.device_bytes()
-    tiles = (cap + 63) // 64
-    exact_copy, f16_copy = n_kv * tiles * (4 * 16384 + 4096), n_kv * tiles * 2 * 16384
-    qbuf = rows * hd * 4  # the chunk's (cos, sin) rows
-    assert now1 - now0 >= exact_copy + f16_copy + qbuf, (now1 - now0)
-    assert now1 <= bound1 and bound1 >= bound0
-    pos = torch.tensor([rows], dtype=torch.int32, device="cuda")
+    out = torch.zeros(rows, 32 * hd, device="cuda")
+    # The device-position step first: it builds the cache's (cos, sin)
+    # table for the capacity (the F16 chunk below reads the same table).
+    pos = torch.tensor([0], dtype=torch.int32, device="cuda")
     q1 = dev(rng.vec_in(32 * hd, -1, 1))
     k1, v1 = dev(rng.vec_in(n_kv * hd, -1, 1)), dev(rng.vec_in(n_kv * hd, -1, 1))
     o1 = torch.zeros(32 * hd, device="cuda")
-    rv.decode_step_dev(kv, 0, q1, k1, v1, w, w, 1e-6, 1e6, pos, cap - 1, 0.088, o1)
+    rv.decode_step_dev(kv, 2, q1, k1, v1, w, w, 1e-6, 1e6, pos, cap - 1, 0.088, o1)
+    torch.cuda.synchronize()
+    now1, bound1 = kv.device_bytes()
+    assert now1 - now0 >= cap * hd * 4 and now1 <= bound1, (now1 - now0)
+    rv.prefill_chunk(kv, 0, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="exact")
+    rv.prefill_chunk(kv, 1, q, k, v, w, w, 1e-6, 1e6, 0, 0.088, out, mode="f16")
     torch.cuda.synchronize()
     now2, bound2 = kv.device_bytes()
-    assert now2 - now1 >= cap * hd * 4 and now2 <= bound2
+    tiles = (cap + 63) // 64
+    exact_copy, f16_copy = n_kv * tiles * (4 * 16384 + 4096), n_kv * tiles * 2 * 16384
+    qbuf = rows * hd * 4  # at least the chunk's (cos, sin) rows, or its prepared queries
+    assert now2 - now1 >= exact_copy + f16_copy + qbuf, (now2 - now1)
+    assert now2 <= bound2 and bound2 >= bound0
