@@ -1034,7 +1034,9 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
     // prologue runs inside the attention kernel's query loads.
     rv::StageDst sd;
     hs = rv::prepare_prefill_stage(kv, layer, len, rows, flags, kv->stream, &sd);
-    const bool prep = sd.base != nullptr;
+    // (The preparation reads q and its norm weight with 16-byte loads.)
+    const bool prep = sd.base != nullptr && ((uintptr_t)dq % 16) == 0 && ((uintptr_t)dwq % 16) == 0 &&
+                      q_dim % 4 == 0;
     if (hs.e == hipSuccess)
       hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, kv->n_kv_heads, p.group) : rows * hd * sizeof(float));
     rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, p.group, scale) : rv::QPrep{};

@@ -149,37 +149,92 @@ __global__ __launch_bounds__(64) void append_kernel(const float* __restrict__ k,
   }
 }
 
-// One wave of a staging launch's query preparation: the 32 columns
-// [32 wv, 32 wv + 32) of unit u (qw = u * VG + wv) in the prepared layout.
-// Lane (lc, g) takes half of column lc's query (Q32Loads' layout: the rope
-// pairs (d, d + 64) in one lane), RMSNorms and rotates it with its row's
-// (cos, sin) from the cache's table, scales and rounds it, and the wave
-// stores its eight 1 KiB operand blocks whole. Columns past the chunk's rows
-// are zeros.
+// One workgroup of a staging launch's query preparation: the 32 columns
+// [32 wv, 32 wv + 32) of unit u (qw = u * VG + wv) in the prepared layout,
+// wave wib taking columns 8 wib .. 8 wib + 7. Loads are whole vectors: load
+// k brings column 8 wib + 2 k + (lane / 32) with lane l holding d = 4 (l %
+// 32) .. + 3, so each load is 1 KiB contiguous (two columns' 512 bytes of
+// q; a row's (cos, sin) pair halves), and the rope pair (d, d + 64) sits in
+// lanes 16 apart (exchanged with one permlane16 swap). RMSNorm sums the
+// column's squares in f64 over its 32 lanes (DPP within 16-lane rows, then
+// the swap), then `x * inv * w` and the rotation in the reference's
+// separately rounded f32 operations, times log2(e) * scale, rounded to the
+// MFMA type. The columns turn around through the workgroup's 8 KiB of LDS
+// (lq: column c's 16-byte chunk k at byte 256 c + 16 (k ^ (c & 15))), and
+// wave wib stores operand blocks 2 wib and 2 wib + 1 whole. Columns past the
+// chunk's rows are zeros. Every wave of the workgroup calls it (a barrier).
 template <int SM>
-__device__ __forceinline__ void prep_q_wave(int qw, const float* __restrict__ q, int n_q,
-                                            const float* __restrict__ q_w, float eps, long pos0, int rows,
-                                            const QPrep& qp, int lane) {
+__device__ __forceinline__ void prep_q_block(int qw, bool live, const float* __restrict__ q, int n_q,
+                                             const float* __restrict__ q_w, float eps, long pos0, int rows,
+                                             const QPrep& qp, int wib, int lane, uint16_t* lq) {
+#pragma clang fp contract(off)
   typedef typename Op<SM>::E E;
   typedef typename Op<SM>::V8 V8;
+  typedef E E4 __attribute__((ext_vector_type(4)));
   constexpr int VG = kQPrepVectors / 32;
   const int u = qw / VG, wv = qw % VG;
   const int kvh = u / qp.n_rb, rb = u % qp.n_rb;
+  const int hl = lane >> 5, dl = lane & 31;  // column parity of a load, d = 4 dl .. 4 dl + 3
+  const bool first = dl < 16;                // d < 64: the first element of its rope pair
+  if (live) {
+    const f32x4 w_own = *reinterpret_cast<const f32x4*>(q_w + 4 * dl);
+    f32x4 x[4], t[4];
+    bool ok[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = 8 * wib + 2 * k + hl, m = 32 * wv + c;
+      const int row = rb * qp.qr + m % qp.qr;
+      ok[k] = row < rows;
+      const int q_row = ok[k] ? row : rb * qp.qr;  // a row of the unit (its first is in the chunk)
+      x[k] = *reinterpret_cast<const f32x4*>(q + ((size_t)q_row * n_q + (size_t)(kvh * qp.group + m / qp.qr)) * 128 +
+                                             4 * dl);
+      // cos of pairs 4 dl .. + 3 in the first lanes, sin in their partners
+      t[k] = *reinterpret_cast<const f32x4*>(qp.rope + (size_t)(pos0 + q_row) * 128 + 4 * dl);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (!ok[k]) x[k] = f32x4{};
+      double ss = 0.0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += (double)x[k][e] * (double)x[k][e];
+      ss += dpp_f64<DPP_QUAD_XOR1>(ss);
+      ss += dpp_f64<DPP_QUAD_XOR2>(ss);
+      ss += dpp_f64<DPP_ROW_HALF_MIRROR>(ss);
+      ss += dpp_f64<DPP_ROW_MIRROR>(ss);
+      ss = swap_sum_f64<16>(ss);  // the column's 32 lanes
+      const float inv = (float)(1.0 / sqrt(ss / 128.0 + (double)eps));
+      f32x4 a, ap, tp, y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = x[k][e] * inv * w_own[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const auto ra = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[e]), __float_as_uint(a[e]), false, false);
+        const auto rt = __builtin_amdgcn_permlane16_swap(__float_as_uint(t[k][e]), __float_as_uint(t[k][e]), false,
+                                                         false);
+        ap[e] = __uint_as_float(first ? ra[1] : ra[0]);
+        tp[e] = __uint_as_float(first ? rt[1] : rt[0]);
+      }
+      // first lanes: y = a0 cos - a1 sin; partners: y = a0 sin + a1 cos.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float cs = first ? t[k][e] : tp[e], sn = first ? tp[e] : t[k][e];
+        y[e] = first ? a[e] * cs - ap[e] * sn : ap[e] * sn + a[e] * cs;
+      }
+      E4 h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = (E)(y[e] * qp.qscale);
+      const int c = 8 * wib + 2 * k + hl, d = 4 * dl;
+      *reinterpret_cast<E4*>(lq + 128 * c + 8 * ((d >> 3) ^ (c & 15)) + (d & 7)) = h;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
   const int lc = lane & 31, g = lane >> 5;
-  const int m = 32 * wv + lc, head = m / qp.qr, row = rb * qp.qr + m % qp.qr;
-  const bool ok = row < rows;
-  const int q_row = ok ? row : rb * qp.qr;  // a row of the unit (its first is in the chunk)
-  Q32Loads ql;
-  ql.issue(q + ((size_t)q_row * n_q + (size_t)(kvh * qp.group + head)) * 128, g, q_w,
-           qp.rope + (size_t)(pos0 + q_row) * 128);
-  ql.finish(true, eps);
   V8* dst = reinterpret_cast<V8*>(qp.base) + (size_t)qw * 8 * 64 + lane;
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    V8 x;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = ok ? (E)(ql.x[ks][e] * qp.qscale) : (E)0.f;
-    dst[64 * ks] = x;
+  for (int i = 0; i < 2; ++i) {
+    const int ks = 2 * wib + i;
+    dst[64 * ks] = *reinterpret_cast<const V8*>(lq + 128 * lc + 8 * ((2 * ks + g) ^ (lc & 15)));
   }
 }
 
@@ -217,20 +272,22 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   const int r = blockIdx.x, lane = threadIdx.x & 63;
   const int half = hd / 2;
   // This wave's slot block: blockIdx.y in one-wave blocks, the block's
-  // waves side by side in a staging launch's (no block-wide barrier: each
-  // wave is independent).
+  // waves side by side in a staging launch's (each wave independent; only
+  // the query-preparation workgroups below share a barrier, all four of
+  // their waves taking it).
   const int wib = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // With prepared queries the first block rows prepare them, one unit's 32
-  // columns per wave (dispatched first, so their loads overlap the k and v
-  // blocks'); the rest are the row slots.
+  // columns per workgroup (dispatched first, so their loads overlap the k
+  // and v blocks'); the rest are the row slots.
   int by = (int)blockIdx.y;
   if constexpr (SM >= 0) {
+    __shared__ __attribute__((aligned(16))) uint16_t qlds[32 * 128];
     if (qp.base) {
-      const int q_waves = n_kv * qp.n_rb * (kQPrepVectors / 32);
-      const int qy = (q_waves + (int)gridDim.x * kPrologueWaves - 1) / ((int)gridDim.x * kPrologueWaves);
+      const int q_groups = n_kv * qp.n_rb * (kQPrepVectors / 32);  // 32-column groups, one workgroup each
+      const int qy = (q_groups + (int)gridDim.x - 1) / (int)gridDim.x;
       if (by < qy) {
-        const int qw = (by * (int)gridDim.x + r) * kPrologueWaves + wib;
-        if (qw < q_waves) prep_q_wave<SM>(qw, q, n_q, q_w, eps, pos0, sr.rows, qp, lane);
+        const int qw = by * (int)gridDim.x + r;
+        prep_q_block<SM>(qw, qw < q_groups, q, n_q, q_w, eps, pos0, sr.rows, qp, wib, lane, qlds);
         return;
       }
       by -= qy;
@@ -460,14 +517,15 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   const StagedRows sr{staging ? sd->base : nullptr, staging ? sd->tile_stride : 0, (int)rows, (long)cache_row};
   // Staging: q and k slot blocks, then one block row per v head (its quads
   // of positions along x; grid_rows covers them).
-  // Staging: with prepared queries first enough block rows for one wave per
-  // 32 columns of each unit, then (k blocks + v blocks) / kPrologueWaves.
+  // Staging: with prepared queries first enough block rows for one
+  // workgroup per 32 columns of each unit, then (k blocks + v blocks) /
+  // kPrologueWaves.
   int slot_blocks = (n_slots + kSlots - 1) / kSlots;
   if (staging) {
     slot_blocks = ((n_kv + kSlots - 1) / kSlots + n_kv + kPrologueWaves - 1) / kPrologueWaves;
     if (prep) {
-      const size_t q_waves = (size_t)n_kv * qp->n_rb * (kQPrepVectors / 32);
-      slot_blocks += (int)((q_waves + grid_rows * kPrologueWaves - 1) / (grid_rows * kPrologueWaves));
+      const size_t q_groups = (size_t)n_kv * qp->n_rb * (kQPrepVectors / 32);
+      slot_blocks += (int)((q_groups + grid_rows - 1) / grid_rows);
     }
   }
   const QPrep qpv = prep ? *qp : QPrep{};
