@@ -846,6 +846,8 @@ def main():
                     help="only run the attention-block leg (48 layers, ctx 4096), log it and exit (for profiling)")
     ap.add_argument("--router-only", action="store_true",
                     help="only run the router leg (1, 512 and 1024 rows), log it and exit (for profiling)")
+    ap.add_argument("--config1-only", action="store_true",
+                    help="only config 1 (the fused decode step, eager and token graph), for profiling")
     ap.add_argument("--config5-only", action="store_true",
                     help="only run the config 5 leg (ctx 32768, f16, every split shape), log it and exit (for profiling)")
     ap.add_argument("--floors", action="store_true",
@@ -897,6 +899,11 @@ def main():
         for mode in ("f16", "exact"):
             rbp = bench_attn_block_prefill(torch, rv, synth, mode)
             log(f"attention block prefill {mode}: {rbp['us_per_layer']:.1f} us/layer for {rbp['rows']} rows")
+        return
+    if args.config1_only:
+        r1 = bench_config1(torch, rv, synth)
+        log(f"config 1: {r1['us_per_call']:.2f} us/call, kernel {r1['us_attention_kernel']:.2f} us, "
+            f"token graph {r1['token_graph']['us_per_step']:.2f} us/step")
         return
     if args.config5_only:
         r5 = bench_config5(torch, rv, synth)
