@@ -179,6 +179,11 @@ __device__ __forceinline__ void lds_dma16(const void* g, uint32_t l) {
 #endif
 }
 __device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
+// The same copy with a wave-uniform base in scalar registers and the lane's
+// byte offset in a vector register (no per-copy 64-bit vector add).
+__device__ __forceinline__ void lds_dma16s(const void* sbase, uint32_t voff, uint32_t l) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(l) : "memory");
+}
 
 // s_waitcnt with vmcnt(n) and the other counters left alone (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).

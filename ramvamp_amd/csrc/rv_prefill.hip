@@ -49,6 +49,7 @@
 #include "rv_staged.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace rv {
 namespace {
@@ -263,6 +264,17 @@ __device__ __forceinline__ float sum8(bf16x8 v, float acc) {
   acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
   acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+}
+
+// The sum of P values i and i + 1 of a B operand added to acc (one v_dot2).
+__device__ __forceinline__ float sum2(f16x8 v, int i, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(h2{v[i], v[i + 1]}, h2{1, 1}, acc, false);
+}
+__device__ __forceinline__ float sum2(bf16x8 v, int i, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(b2{v[i], v[i + 1]}, one, acc, false);
 }
 
 // G groups of W waves. Every group covers all M = 16 W MT columns of the
@@ -658,10 +670,8 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 // (O, max, sum) merge through LDS at the end, so one step of the ring feeds
 // V columns from each of G tiles and the causal chain of the block's longest
 // range is 1 / G as long. Each operand read feeds an MFMA of 32 columns
-// (twice the columns per LDS byte of a 16x16 tile). The two waves sharing a
-// SIMD are left to the hardware's interleaving (a prototype that offset them
-// by a tile phase measured 12-16 % slower). The instantiation is W = 8, G =
-// 2: 128-column units, the same throughput at 3.9k positions as 256-column
+// (twice the columns per LDS byte of a 16x16 tile). The instantiation is
+// W = 8, G = 2: 128-column units, the same throughput at 3.9k positions as 256-column
 // units with twice the KV splits (47.1 vs 48.3 us), and a chain half as long
 // where the chunk's own rows dominate (config 3: 14.4 vs 16.0 us). Per
 // tile, per wave:
@@ -676,9 +686,16 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 //     pb, rounded, are exactly the B operand P^T of PV step (pb, h) (the V^T
 //     tile is staged with its positions in that order, vt_pos32);
 //   O^T[d][m] += sum_t V^T[d][t] P^T[t][m]: 4 d blocks x 4 steps = 16 MFMAs.
-// Tiles stream through a 4-stage ring by direct-to-LDS loads (inline
-// assembly, so the compiler adds no wait for them before LDS reads), the
-// next step's tiles in flight during a step. The KV range is split across
+// The loop is software-pipelined inside each wave: tile j's exponentials run
+// between the MFMAs of tile j + 1's scores and tile j + 1's maximum between
+// tile j's PV MFMAs, written out chunk by chunk in issue order. On gfx950 an
+// MFMA 32x32x16 hides only about four full-rate VALU instructions (two
+// exponentials) of the same SIMD; a phase of softmax work between phases of
+// MFMAs costs its full length (measured: the two waves of a SIMD run their
+// phases in step, so the other wave does not fill the gap). Tiles stream
+// through a 4-stage ring by direct-to-LDS loads (inline assembly, so the
+// compiler adds no wait for them before LDS reads), the next step's planes
+// in flight during a step. The KV range is split across
 // workgroups when the chunk has too few query
 // blocks to fill the chip; the splits of a block run on one XCD (blockIdx
 // agreeing mod 8: the dispatcher deals workgroups to the XCDs round robin),
@@ -710,30 +727,42 @@ struct Op32<kBF16> {
 
 // The last split's fold of a unit's columns over its S splits: split sp's
 // partial column (O chunks 8 db + 2 jj + g of this lane from
-// o_off(sp, chunk), max and sum from ml_off(sp); this split's own stored
-// like the others), weighted by 2^(max_sp - M) over M = the splits' maximum
-// and summed in split order, 32 d (one db block) at a time;
-// emit(db, block, 1 / L) for each. S is fixed at compile time so every load
-// is unconditional and the next block's loads (S <= 4) are in flight while
-// one is folded.
+// o_off(sp, chunk), max and sum from ml_off(sp); split `own`, the folding
+// one, from its registers oo, m_own, l_own, which hold exactly what it
+// stored), weighted by 2^(max_sp - M) over M = the splits' maximum and
+// summed in split order, 32 d (one db block) at a time; emit(db, block,
+// 1 / L) for each. S is fixed at compile time so the loads are issued
+// without data-dependent branches and the next block's loads (S <= 4) are
+// in flight while one is folded.
 template <int S, typename OffFn, typename MlFn, typename Emit>
 __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o_off, MlFn ml_off, int g,
-                                       Emit emit) {
+                                       Emit emit, int own, const f32x16 (&oo)[4], float m_own, float l_own) {
   constexpr bool kAhead = S <= 4;
   f32x4 buf[kAhead ? 2 : 1][S][4];
   auto load_block = [&](int db, f32x4 (&b)[S][4]) {
 #pragma unroll
     for (int sp = 0; sp < S; ++sp)
+      if (sp != own) {
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        b[sp][jj] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(sp, 8 * db + 2 * jj + g), 0, kPolicyL2);
+        for (int jj = 0; jj < 4; ++jj)
+          b[sp][jj] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(sp, 8 * db + 2 * jj + g), 0, kPolicyL2);
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          b[sp][jj] = f32x4{oo[db][4 * jj], oo[db][4 * jj + 1], oo[db][4 * jj + 2], oo[db][4 * jj + 3]};
+      }
   };
   float ms[S], ls[S];
 #pragma unroll
   for (int sp = 0; sp < S; ++sp) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, ml_off(sp), 0, kPolicyL2);
-    ms[sp] = __builtin_bit_cast(float, (uint32_t)v[0]);
-    ls[sp] = __builtin_bit_cast(float, (uint32_t)v[1]);
+    if (sp != own) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, ml_off(sp), 0, kPolicyL2);
+      ms[sp] = __builtin_bit_cast(float, (uint32_t)v[0]);
+      ls[sp] = __builtin_bit_cast(float, (uint32_t)v[1]);
+    } else {
+      ms[sp] = m_own;
+      ls[sp] = l_own;
+    }
   }
   load_block(0, buf[0]);
   float M = ms[0];
@@ -776,7 +805,6 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   constexpr int TB = kP32TileBytes, NS = kP32Stages;
   constexpr int VG = W / G;        // waves per group
   constexpr int V = 32 * VG;       // columns per unit
-  constexpr int PW = 32 / W;       // 1 KiB pieces per wave per tile
   // Scores may exceed the running maximum by 2^kRescale (log2 units) before
   // it moves: P stays below 2^8 and most tiles skip rescaling O.
   constexpr float kRescale = 8.0f;
@@ -822,31 +850,34 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     ql.issue(q + (size_t)q_row * q_stride + (size_t)(kvh * group + head) * kD, g, qn_w,
              qn_tab ? qn_tab + (size_t)q_row * kD : nullptr);
   }
-  const char* src = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB + 16 * lane;
-  // Tile t into stage t % NS: 32 pieces of 1 KiB, wave w copies w, w + W,
-  // ... Step j computes tiles G j .. G j + G - 1, group gi the tile G j +
-  // gi; the NS - G tiles after them are in flight meanwhile. (The units of
-  // an XCD walk their tiles in the same order: their requests for a tile
-  // meet in that XCD's L2. Rotated starting points measured 1.5 us slower
-  // at config 4.)
-  auto issue_piece = [&](int t, int i) {
-    const int piece = 1024 * (w + W * i);
-    lds_dma16(src + (size_t)t * TB + piece, lds_offset(&lds[t % NS][piece]));
+  // Tile t of the range lands in stage 2 (t % 2) + (t / 2) % 2 as 32
+  // pieces of 1 KiB (wave w copies pieces w, w + W, w + 2W, w + 3W: two in
+  // the K plane, two in the V plane), so each group's two stages are
+  // adjacent and every operand read below is a per-lane base plus an
+  // immediate offset. The tile's address is wave-uniform (scalar
+  // registers), the lane's 16 bytes an offset. A tile past the range copies
+  // the range's last tile into its stage (free at that point either way):
+  // the copies stay unconditional, so the loop body has no branch between
+  // its MFMAs. (The units of an XCD walk their tiles in the same order:
+  // their requests for a tile meet in that XCD's L2. Rotated starting
+  // points measured 1.5 us slower at config 4.)
+  const char* const srcw = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB + 1024 * w;
+  const uint32_t voff = 16u * (uint32_t)lane;
+  auto stage_of = [](int t) { return 2 * (t & 1) + ((t >> 1) & 1); };
+  auto copy_piece = [&](int t, int i) {
+    lds_dma16s(srcw + (size_t)min(t, n - 1) * TB + 8192 * i, voff,
+               lds_offset(&lds[stage_of(t)][1024 * (w + W * i)]));
   };
-  auto issue = [&](int t) {
+  // Tiles 0 and 1 whole, then the K planes of tiles 2 and 3. A split with no
+  // tiles (more splits than the unit has tiles) copies nothing.
+  if (n > 0) {
 #pragma unroll
-    for (int i = 0; i < PW; ++i) issue_piece(t, i);
-  };
-  for (int t = 0; t < NS - G && t < n; ++t) issue(t);
-  // A step's copies are spread through its compute (kIssueSlots points, one
-  // copy each, in order) rather than issued at once after the barrier: the
-  // address unit takes ~16 cycles per 1 KiB copy, and a wave whose copies
-  // queue behind the other waves' stalls at its next memory instruction.
-  constexpr int kCopies = G * PW;  // copies per wave per step
-  auto issue_copy = [&](int j, int c) {
-    const int t = G * j + NS - G + c / PW;
-    if (c < kCopies && t < n) issue_piece(t, c % PW);
-  };
+    for (int t = 0; t < G; ++t) copy_piece(t, 0), copy_piece(t, 1);
+#pragma unroll
+    for (int t = 0; t < G; ++t) copy_piece(t, 2), copy_piece(t, 3);
+#pragma unroll
+    for (int t = G; t < 2 * G; ++t) copy_piece(t, 0), copy_piece(t, 1);
+  }
   if (qprep) {
     if (!col_ok) {
 #pragma unroll
@@ -867,97 +898,176 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   float m_run = kNegSentinel, l_run = 0.f;
   float negm = 0.f;  // -m_run, or 0 while the column has seen no position
   const int steps = (n + G - 1) / G;
-  for (int j = 0; j < steps; ++j) {
-    // Step j's tiles have landed once at most the later tiles issued are in
-    // flight; the barrier makes every wave's pieces visible and retires the
-    // previous step's stages, which the loads below overwrite.
-    const int ahead = min(n - G * (j + 1), NS - 2 * G);
-    if (ahead >= 2) wait_vmcnt<2 * PW>();
-    else if (ahead == 1) wait_vmcnt<PW>();
-    else wait_vmcnt<0>();
-    __syncthreads();
-    const int tl = G * j + gi;
-    if (tl >= n) {
+  {
+    static_assert(W == 8 && G == 2 && NS == 4, "two tiles per step; a wave's K pieces w, w + 8, V pieces w + 16, w + 24");
+    // Software-pipelined: iteration j exponentiates tile j's scores while the
+    // MFMAs of tile j + 1's scores run, then takes tile j + 1's maximum while
+    // tile j's PV MFMAs run, each chunk written out in issue order so a
+    // wave's softmax work fills the shadow of its own MFMAs. Iteration j
+    // reads the V planes of step j and the K planes of step j + 1 and copies
+    // in the V planes of step j + 1 and the K planes of step j + 2 (into the
+    // halves the previous iteration finished with). Two iterations per trip
+    // of the loop, so the two score arrays alternate roles in place and each
+    // stage's parity is known at compile time. A group whose tile lies past
+    // the range (group 1 when n is odd) computes on the copy of the range's
+    // last tile in its stage, fully masked: P = 0, nothing added.
+    if (n > 0) {
+      const char* kp[8];
+      const char* vp[4];
 #pragma unroll
-      for (int c = 0; c < kCopies; ++c) issue_copy(j, c);
-      continue;
-    }
-    const char* kt = lds[tl % NS];
-    const char* vt = kt + kPlaneBytes;
-    const int t0 = (tt_lo + tl) * kBT;
-    f32x16 sc[2];
+      for (int ks = 0; ks < 8; ++ks) kp[ks] = &lds[2 * gi][0] + 256 * lc + 16 * ((2 * ks + g) ^ (lc & 15));
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb) {
-      V8 ka[8];
+      for (int c = 0; c < 4; ++c) vp[c] = &lds[2 * gi][kPlaneBytes] + 128 * lc + 16 * ((2 * c + g) ^ ((lc >> 1) & 7));
+      // Operand k of a tile in the group's stage of parity par: K rows
+      // 32 (k / 8) + lc at d step k % 8; V^T rows 32 (k / 4) + lc at step k % 4.
+      auto kread = [&](int par, int k) {
+        return *reinterpret_cast<const V8*>(kp[k & 7] + TB * par + 8192 * (k >> 3));
+      };
+      auto vread = [&](int par, int k) {
+        return *reinterpret_cast<const V8*>(vp[k & 3] + TB * par + 4096 * (k >> 2));
+      };
+      // Copy c of iteration jj: c < 4 the V pieces of step jj + 1, else the K
+      // pieces of step jj + 2.
+      auto copy = [&](int jj, int c) {
+        const int t = c < 4 ? G * (jj + 1) + c / 2 : G * (jj + 2) + (c - 4) / 2;
+        copy_piece(t, c < 4 ? 2 + c % 2 : c % 2);
+      };
+      auto mask = [&](int jj, f32x16 (&s)[2]) {
+        const int tl = G * jj + gi;
+        const int t0 = tl < n ? (tt_lo + tl) * kBT : (1 << 29);
+        if (t0 + kBT > all_see) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) ka[ks] = *reinterpret_cast<const V8*>(kt + k_off(32 * pb + lc, 2 * ks + g));
+          for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[pb][r] = negm;
+            for (int r = 0; r < 16; ++r)
+              if (t0 + 32 * pb + 8 * (r >> 2) + 4 * g + (r & 3) >= my_limit) s[pb][r] = -INFINITY;
+        }
+      };
+      auto lane_max = [&](float mx) {
+        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        return __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      };
+      auto adjust = [&](float mx, f32x16 (&s)[2]) {
+        if (__builtin_amdgcn_ballot_w64(mx > kRescale || m_run == kNegSentinel)) {
+          const bool fresh = m_run == kNegSentinel;
+          const float d = fresh ? fmaxf(mx, kNegSentinel) : fmaxf(mx, 0.f);
+          if (!fresh) {
+            const float alpha = __builtin_amdgcn_exp2f(-d);
+            l_run *= alpha;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        sc[pb] = Op32<MODE>::mfma(ka[ks], qv[ks], sc[pb]);
-        if (ks == 3 || ks == 7) issue_copy(j, 2 * pb + ks / 4);  // copies 0 .. 3
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            m_run += d;
+          } else {
+            m_run = d;
+          }
+          s[0] -= d;
+          s[1] -= d;
+          negm = m_run == kNegSentinel ? 0.f : -m_run;
+        }
+      };
+      // One full iteration jj of parity P: scores sc of tile jj in, scores
+      // sn of tile jj + 1 out.
+      auto iter = [&](int jj, f32x16 (&sc)[2], f32x16 (&sn)[2], auto par_c) {
+        constexpr int P = decltype(par_c)::value;
+        wait_vmcnt<0>();  // step jj's V planes and step jj + 1's K planes
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        V8 ph[2][2];
+        // Phase A: MFMA k of tile jj + 1's scores, the K operand read for
+        // MFMA k + 4, and P pair k of tile jj (two exponentials, one
+        // conversion, one dot for the sum), each chunk fenced.
+        {
+          V8 ka[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ka[k] = kread(1 - P, k);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sn[0][r] = negm, sn[1][r] = negm;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            sn[k >> 3] = Op32<MODE>::mfma(ka[k & 3], qv[k & 7], sn[k >> 3]);
+            if (k + 4 < 16) ka[k & 3] = kread(1 - P, k + 4);
+            const int qb = k >> 3, h = (k >> 2) & 1, i = 2 * (k & 3);
+            ph[qb][h][i] = (E)__builtin_amdgcn_exp2f(sc[qb][8 * h + i]);
+            ph[qb][h][i + 1] = (E)__builtin_amdgcn_exp2f(sc[qb][8 * h + i + 1]);
+            l_run = sum2(ph[qb][h], i, l_run);
+            // An empty asm consuming the pair and the sum keeps them here:
+            // otherwise they are sunk past the mask's branch to the PV MFMAs.
+            asm("" : "+v"(ph[qb][h]), "+v"(l_run));
+            if (k & 1) copy(jj, (4 + (k >> 1)) & 7);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        mask(jj + 1, sn);
+        // Phase B: PV MFMA k of tile jj, the V operand read for MFMA k + 4,
+        // and two of tile jj + 1's 32 scores into its running maximum.
+        float mx = -INFINITY;
+        {
+          V8 va[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) va[k] = vread(P, k);
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const int c = k & 3;
+            o[k >> 2] = Op32<MODE>::mfma(va[c], ph[c >> 1][c & 1], o[k >> 2]);
+            if (k + 4 < 16) va[c] = vread(P, k + 4);
+            mx = max3f(mx, sn[k >> 3][2 * (k & 7)], sn[k >> 3][2 * (k & 7) + 1]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        adjust(lane_max(mx), sn);
+      };
+      // The last iteration: tile jj's P and PV MFMAs only.
+      auto last = [&](f32x16 (&sc)[2], auto par_c) {
+        constexpr int P = decltype(par_c)::value;
+        wait_vmcnt<0>();
+        __syncthreads();
+        V8 ph[2][2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ph[pb][h][i] = (E)__builtin_amdgcn_exp2f(sc[pb][8 * h + i]);
+            l_run = sum8(ph[pb][h], l_run);
+          }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int c = k & 3;
+          o[k >> 2] = Op32<MODE>::mfma(vread(P, k), ph[c >> 1][c & 1], o[k >> 2]);
+        }
+      };
+      wait_vmcnt<4 * G>();  // the V planes of step 0 and K planes of step 1 may still fly
+      __syncthreads();
+      f32x16 sA[2], sB[2];
+#pragma unroll
+      for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sA[pb][r] = negm;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) sA[pb] = Op32<MODE>::mfma(kread(0, 8 * pb + ks), qv[ks], sA[pb]);
       }
-    }
-    // Causal mask only where some row of the block stops inside the tile.
-    if (t0 + kBT > all_see) {
+      mask(0, sA);
+      {
+        float mx = max3f(sA[0][0], sA[0][1], sA[0][2]);
 #pragma unroll
-      for (int pb = 0; pb < 2; ++pb)
+        for (int r = 3; r < 15; r += 2) mx = max3f(mx, sA[0][r], sA[0][r + 1]);
+        mx = max3f(mx, sA[0][15], sA[1][0]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (t0 + 32 * pb + 8 * (r >> 2) + 4 * g + (r & 3) >= my_limit) sc[pb][r] = -INFINITY;
-    }
-    float mx = max3f(sc[0][0], sc[0][1], sc[0][2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = max3f(mx, sc[0][r], sc[0][r + 1]);
-    mx = max3f(mx, sc[0][15], sc[1][0]);
-#pragma unroll
-    for (int r = 1; r < 15; r += 2) mx = max3f(mx, sc[1][r], sc[1][r + 1]);
-    mx = __builtin_elementwise_maximum(mx, sc[1][15]);
-    {
-      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-    }
-    if (__builtin_amdgcn_ballot_w64(mx > kRescale || m_run == kNegSentinel)) {
-      // A column still at the sentinel takes the tile's maximum outright (its
-      // O and sum are zero); others move up by d >= 0 and rescale.
-      const bool fresh = m_run == kNegSentinel;
-      const float d = fresh ? fmaxf(mx, kNegSentinel) : fmaxf(mx, 0.f);
-      if (!fresh) {
-        const float alpha = __builtin_amdgcn_exp2f(-d);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[db] *= alpha;
-        m_run += d;
+        for (int r = 1; r < 15; r += 2) mx = max3f(mx, sA[1][r], sA[1][r + 1]);
+        adjust(lane_max(__builtin_elementwise_maximum(mx, sA[1][15])), sA);
+      }
+      int j = 0;
+      for (; j + 2 < steps; j += 2) {
+        iter(j, sA, sB, std::integral_constant<int, 0>{});
+        iter(j + 1, sB, sA, std::integral_constant<int, 1>{});
+      }
+      if (j + 1 < steps) {
+        iter(j, sA, sB, std::integral_constant<int, 0>{});
+        last(sB, std::integral_constant<int, 1>{});
       } else {
-        m_run = d;
+        last(sA, std::integral_constant<int, 0>{});
       }
-      sc[0] -= d;
-      sc[1] -= d;
-      negm = m_run == kNegSentinel ? 0.f : -m_run;
     }
-    // P^T of PV step (pb, h): registers 8 h .. 8 h + 7 of block pb, rounded;
-    // the row sums are of exactly the rounded P the products use.
-    V8 ph[2][2];
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ph[pb][h][i] = (E)__builtin_amdgcn_exp2f(sc[pb][8 * h + i]);
-        l_run = sum8(ph[pb][h], l_run);
-      }
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      V8 va[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) va[c] = *reinterpret_cast<const V8*>(vt + vt_off(32 * db + lc, 2 * c + g));
-#pragma unroll
-      for (int c = 0; c < 4; ++c) o[db] = Op32<MODE>::mfma(va[c], ph[c >> 1][c & 1], o[db]);
-      issue_copy(j, 4 + db);  // copies 4 .. 7
-    }
-#pragma unroll
-    for (int c = 8; c < kCopies; ++c) issue_copy(j, c);
   }
   l_run = swap_sum<32>(l_run);  // the column's other half of the positions
   if constexpr (G > 1) {
@@ -965,12 +1075,13 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     // upper half of the ring, (max, sum) through sm_ml; the first group
     // continues with the merged column.
     __syncthreads();  // every wave is past the ring
-    float* xo = reinterpret_cast<float*>(&lds[2][0]) + (size_t)wv * 64 * 64 + lane;
+    f32x4* xo = reinterpret_cast<f32x4*>(&lds[2][0]) + (size_t)wv * 16 * 64 + lane;
     if (gi == 1) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xo[(16 * db + r) * 64] = o[db][r];
+        for (int jj = 0; jj < 4; ++jj)
+          xo[(4 * db + jj) * 64] = f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
       sm_ml[wv * 64 + lane] = m_run;
       sm_ml[(VG + wv) * 64 + lane] = l_run;
     }
@@ -982,7 +1093,11 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * a1 + xo[(16 * db + r) * 64] * a2;
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 x = xo[(4 * db + jj) * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[db][4 * jj + e] = o[db][4 * jj + e] * a1 + x[e] * a2;
+        }
       l_run = l_run * a1 + l2 * a2;
       m_run = M;
     }
@@ -992,9 +1107,10 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   // past its last tile): put() writes 32 d of this lane's column, o-layout
   // o[db][4 jj + e] = O^T[32 db + 8 jj + 4 g + e][m], into the wave's 16 KiB
   // region as 16-byte chunks c = d / 4 of row lc, swizzled to chunk c ^ lc
-  // (the 32 lanes of one chunk hit distinct banks); flush() then reads whole
-  // rows back, 512 contiguous bytes per half-wave, and stores each column's
-  // row of out with 16-byte stores.
+  // (the 32 lanes of one chunk hit distinct banks); after a barrier,
+  // flush() has every wave of the workgroup read whole rows back (group gi
+  // takes half the rows of wave wv's region), 512 contiguous bytes per
+  // half-wave, and store each column's row of out with 16-byte stores.
   float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)wv * 32 * kD;
   auto put = [&](int db, const f32x16& v, float inv) {
 #pragma unroll
@@ -1005,16 +1121,17 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     }
   };
   auto flush = [&]() {
+    static_assert(G == 2, "two groups share the output rows");
     const bool vec = aligned16(out) && q_stride % 4 == 0;
-    f32x4 x[16];
+    f32x4 x[8];
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int r = 2 * it + g;  // row r of the region: column 32 wv + r
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + 2 * gi + g;  // row r of the region: column 32 wv + r
       x[it] = *reinterpret_cast<const f32x4*>(obuf + r * kD + 4 * (lc ^ r));
     }
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int r = 2 * it + g, mm = 32 * wv + r;
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + 2 * gi + g, mm = 32 * wv + r;
       if (mm % qr >= rows_here) continue;
       float* op = out + (size_t)(r0 + mm % qr) * q_stride + (size_t)(kvh * group + mm / qr) * kD + 4 * lc;
       if (vec) {
@@ -1026,11 +1143,12 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     }
   };
   if (kv_splits == 1) {
-    if constexpr (G == 1) __syncthreads();  // every wave is past the ring
-    if (gi != 0) return;
-    const float inv = 1.0f / l_run;
+    if (gi == 0) {
+      const float inv = 1.0f / l_run;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) put(db, o[db], inv);
+      for (int db = 0; db < 4; ++db) put(db, o[db], inv);
+    }
+    __syncthreads();
     flush();
     return;
   }
@@ -1062,22 +1180,25 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     sm_ticket = got;
   }
   __syncthreads();
-  if (sm_ticket != (unsigned)kv_splits - 1 || gi != 0) return;
-  // Fold in split order from this XCD's L2 (the same bits whichever split
-  // finishes last; this split's own partial was stored above like the
-  // others').
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)part_bytes, 0x00020000);
-  auto o_off = [&](int sp, int c) { return (uint32_t)((((slice + sp) * 32 + c) * V + m) * 16); };
-  auto ml_off = [&](int sp) { return (uint32_t)(ml_base * 16 + ((slice + sp) * V + m) * 8); };
-  switch (kv_splits) {
-    case 2: fold32<2>(rs, o_off, ml_off, g, put); break;
-    case 3: fold32<3>(rs, o_off, ml_off, g, put); break;
-    case 4: fold32<4>(rs, o_off, ml_off, g, put); break;
-    case 5: fold32<5>(rs, o_off, ml_off, g, put); break;
-    case 6: fold32<6>(rs, o_off, ml_off, g, put); break;
-    case 7: fold32<7>(rs, o_off, ml_off, g, put); break;
-    default: fold32<8>(rs, o_off, ml_off, g, put); break;
+  if (sm_ticket != (unsigned)kv_splits - 1) return;
+  // Fold in split order, the other splits' partials from this XCD's L2 and
+  // this split's own from its registers (the same bits whichever split
+  // finishes last: the registers hold exactly what was stored).
+  if (gi == 0) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)part_bytes, 0x00020000);
+    auto o_off = [&](int sp, int c) { return (uint32_t)((((slice + sp) * 32 + c) * V + m) * 16); };
+    auto ml_off = [&](int sp) { return (uint32_t)(ml_base * 16 + ((slice + sp) * V + m) * 8); };
+    switch (kv_splits) {
+      case 2: fold32<2>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 3: fold32<3>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 4: fold32<4>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 5: fold32<5>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 6: fold32<6>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 7: fold32<7>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      default: fold32<8>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+    }
   }
+  __syncthreads();
   flush();
 }
 
