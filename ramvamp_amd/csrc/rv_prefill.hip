@@ -725,21 +725,21 @@ struct Op32<kBF16> {
   }
 };
 
-// The last split's fold of a unit's columns over its S splits: split sp's
-// partial column (O chunks 8 db + 2 jj + g of this lane from
-// o_off(sp, chunk), max and sum from ml_off(sp); split `own`, the folding
-// one, from its registers oo, m_own, l_own, which hold exactly what it
-// stored), weighted by 2^(max_sp - M) over M = the splits' maximum and
-// summed in split order, 32 d (one db block) at a time; emit(db, block,
-// 1 / L) for each. S is fixed at compile time so the loads are issued
-// without data-dependent branches and the next block's loads (S <= 4) are
-// in flight while one is folded.
-template <int S, typename OffFn, typename MlFn, typename Emit>
+// The last split's fold of a unit's columns over its S splits, d blocks DB0
+// and DB0 + 1 (32 d each): split sp's partial column (O chunks 8 db + 2 jj +
+// g of this lane from o_off(sp, chunk), max and sum from ml_off(sp); split
+// `own`, the folding one, from its registers oo, m_own, l_own, which hold
+// exactly what it stored), weighted by 2^(max_sp - M) over M = the splits'
+// maximum and summed in split order; emit(db, block, 1 / L) for each block.
+// S is fixed at compile time so the loads are issued without data-dependent
+// branches; up to 4 splits every load is issued before the first is used.
+template <int S, int DB0, typename OffFn, typename MlFn, typename Emit>
 __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o_off, MlFn ml_off, int g,
                                        Emit emit, int own, const f32x16 (&oo)[4], float m_own, float l_own) {
-  constexpr bool kAhead = S <= 4;
-  f32x4 buf[kAhead ? 2 : 1][S][4];
-  auto load_block = [&](int db, f32x4 (&b)[S][4]) {
+  constexpr int NB = S <= 4 ? 2 : 1;  // blocks in flight
+  f32x4 buf[NB][S][4];
+  auto load_block = [&](auto bkc, f32x4 (&b)[S][4]) {
+    constexpr int db = DB0 + decltype(bkc)::value;
 #pragma unroll
     for (int sp = 0; sp < S; ++sp)
       if (sp != own) {
@@ -764,7 +764,8 @@ __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o
       ls[sp] = l_own;
     }
   }
-  load_block(0, buf[0]);
+  load_block(std::integral_constant<int, 0>{}, buf[0]);
+  if constexpr (NB == 2) load_block(std::integral_constant<int, 1>{}, buf[NB - 1]);
   float M = ms[0];
 #pragma unroll
   for (int sp = 1; sp < S; ++sp) M = fmaxf(M, ms[sp]);
@@ -775,10 +776,7 @@ __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o
     L += ls[sp] * a[sp];
   }
   const float inv = 1.0f / L;
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    f32x4 (&cur)[S][4] = buf[kAhead ? (db & 1) : 0];
-    if (kAhead && db + 1 < 4) load_block(db + 1, buf[(db + 1) & 1]);
+  auto fold_block = [&](const f32x4 (&cur)[S][4]) {
     f32x16 acc{};
 #pragma unroll
     for (int sp = 0; sp < S; ++sp)
@@ -786,9 +784,11 @@ __device__ __forceinline__ void fold32(const __amdgpu_buffer_rsrc_t& rs, OffFn o
       for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[4 * jj + e] += cur[sp][jj][e] * a[sp];
-    emit(db, acc, inv);
-    if (!kAhead && db + 1 < 4) load_block(db + 1, buf[0]);
-  }
+    return acc;
+  };
+  emit(DB0, fold_block(buf[0]), inv);
+  if constexpr (NB == 1) load_block(std::integral_constant<int, 1>{}, buf[0]);
+  emit(DB0 + 1, fold_block(buf[NB - 1]), inv);
 }
 
 template <int MODE, int W, int G>
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   constexpr float kRescale = 8.0f;
   __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
   __shared__ unsigned sm_ticket;
-  __shared__ float sm_ml[G > 1 ? 2 * VG * 64 : 1];
+  __shared__ float sm_ml[4 * VG * 64];
 
   // Unit (kv head, row block) and split: the splits of a unit share blockIdx
   // mod 8 (one XCD); each XCD takes a contiguous run of units, kv-head-major,
@@ -1070,47 +1070,16 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     }
   }
   l_run = swap_sum<32>(l_run);  // the column's other half of the positions
-  if constexpr (G > 1) {
-    // The second group's (O, max, sum) into the first's: O through the
-    // upper half of the ring, (max, sum) through sm_ml; the first group
-    // continues with the merged column.
-    __syncthreads();  // every wave is past the ring
-    f32x4* xo = reinterpret_cast<f32x4*>(&lds[2][0]) + (size_t)wv * 16 * 64 + lane;
-    if (gi == 1) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          xo[(4 * db + jj) * 64] = f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
-      sm_ml[wv * 64 + lane] = m_run;
-      sm_ml[(VG + wv) * 64 + lane] = l_run;
-    }
-    __syncthreads();
-    if (gi == 0) {
-      const float m2 = sm_ml[wv * 64 + lane], l2 = sm_ml[(VG + wv) * 64 + lane];
-      const float M = fmaxf(m_run, m2);
-      const float a1 = __builtin_amdgcn_exp2f(m_run - M), a2 = __builtin_amdgcn_exp2f(m2 - M);
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 x = xo[(4 * db + jj) * 64];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[db][4 * jj + e] = o[db][4 * jj + e] * a1 + x[e] * a2;
-        }
-      l_run = l_run * a1 + l2 * a2;
-      m_run = M;
-    }
-  }
 
   // The output goes through LDS (the tile ring is free once every wave is
   // past its last tile): put() writes 32 d of this lane's column, o-layout
-  // o[db][4 jj + e] = O^T[32 db + 8 jj + 4 g + e][m], into the wave's 16 KiB
-  // region as 16-byte chunks c = d / 4 of row lc, swizzled to chunk c ^ lc
-  // (the 32 lanes of one chunk hit distinct banks); after a barrier,
-  // flush() has every wave of the workgroup read whole rows back (group gi
-  // takes half the rows of wave wv's region), 512 contiguous bytes per
-  // half-wave, and store each column's row of out with 16-byte stores.
+  // o[db][4 jj + e] = O^T[32 db + 8 jj + 4 g + e][m], into region wv (16
+  // KiB) as 16-byte chunks c = d / 4 of row lc, swizzled to chunk c ^ lc (the
+  // 32 lanes of one chunk hit distinct banks); after a barrier, flush() has
+  // every wave of the workgroup read whole rows back (group gi takes half the
+  // rows of region wv), 512 contiguous bytes per half-wave, and store each
+  // column's row of out with 16-byte stores.
+  static_assert(G == 2, "the two groups share the epilogue by halves");
   float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)wv * 32 * kD;
   auto put = [&](int db, const f32x16& v, float inv) {
 #pragma unroll
@@ -1121,7 +1090,6 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     }
   };
   auto flush = [&]() {
-    static_assert(G == 2, "two groups share the output rows");
     const bool vec = aligned16(out) && q_stride % 4 == 0;
     f32x4 x[8];
 #pragma unroll
@@ -1142,64 +1110,108 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
       }
     }
   };
-  if (kv_splits == 1) {
-    if (gi == 0) {
-      const float inv = 1.0f / l_run;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) put(db, o[db], inv);
-    }
-    __syncthreads();
-    flush();
-    return;
-  }
-  // This split's partial, laid out so a wave's stores and loads are
-  // contiguous: O as 16-byte chunks c (d = 4c .. 4c + 3) of the unit's V
-  // columns, chunk-major, then (max, sum) per column. Lane (lc, g) holds
-  // chunks c = 8 db + 2 jj + g of its column.
+  // A split's partial, laid out so a wave's stores and loads are contiguous:
+  // O as 16-byte chunks c (d = 4c .. 4c + 3) of the unit's V columns,
+  // chunk-major, then (max, sum) per column. Lane (lc, g) holds chunks
+  // c = 8 db + 2 jj + g of its column.
   const size_t slice = (size_t)u * kv_splits;  // this unit's first split
   const size_t ml_base = (size_t)n_units * kv_splits * 32 * V;  // f32x4 units
-  if (gi == 0) {
-    f32x4* ob = reinterpret_cast<f32x4*>(part) + (slice + split) * 32 * V + m;
+
+  // The rest runs per group with its d blocks known at compile time (the
+  // accumulators stay in registers). The two groups' (O, max, sum) merge by
+  // halves: group GI keeps d blocks 2 GI, 2 GI + 1 of its columns and passes
+  // the other two to its partner wave (same wv, other group) through the
+  // upper half of the ring, (max, sum) through sm_ml; both compute the merged
+  // sums with group 0's term first, so they agree to the bit, and every
+  // later step (output, partial store, fold) runs on all W waves, each on
+  // half of its columns' d.
+  auto epilogue = [&](auto gc) {
+    constexpr int GI = decltype(gc)::value, KEEP = 2 * GI, SEND = 2 - KEEP;
+    __syncthreads();  // every wave is past the ring
+    {
+      f32x4* const xo = reinterpret_cast<f32x4*>(&lds[2][0]) + (size_t)w * 8 * 64 + lane;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+      for (int bk = 0; bk < 2; ++bk)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        ob[(size_t)(8 * db + 2 * jj + g) * V] =
-            f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
-    if (g == 0)
-      reinterpret_cast<float2*>(reinterpret_cast<f32x4*>(part) + ml_base)[(slice + split) * V + m] =
-          float2{m_run, l_run};
-  }
-  // The last split to finish (its ticket the unit's last) folds the unit.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    unsigned* t = tickets + (size_t)u * 32;  // one 128-byte line per unit
-    const unsigned got = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (got == (unsigned)kv_splits - 1) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm_ticket = got;
-  }
-  __syncthreads();
-  if (sm_ticket != (unsigned)kv_splits - 1) return;
-  // Fold in split order, the other splits' partials from this XCD's L2 and
-  // this split's own from its registers (the same bits whichever split
-  // finishes last: the registers hold exactly what was stored).
-  if (gi == 0) {
+        for (int jj = 0; jj < 4; ++jj)
+          xo[(4 * bk + jj) * 64] = f32x4{o[SEND + bk][4 * jj], o[SEND + bk][4 * jj + 1], o[SEND + bk][4 * jj + 2],
+                                         o[SEND + bk][4 * jj + 3]};
+      sm_ml[w * 64 + lane] = m_run;
+      sm_ml[(W + w) * 64 + lane] = l_run;
+      __syncthreads();
+      const int pw = (1 - GI) * VG + wv;  // partner wave
+      const f32x4* const xp = reinterpret_cast<const f32x4*>(&lds[2][0]) + (size_t)pw * 8 * 64 + lane;
+      const float m2 = sm_ml[pw * 64 + lane], l2 = sm_ml[(W + pw) * 64 + lane];
+      const float M = fmaxf(m_run, m2);
+      const float a1 = __builtin_amdgcn_exp2f(m_run - M), a2 = __builtin_amdgcn_exp2f(m2 - M);
+      const float ma = GI == 0 ? a1 : a2, mb = GI == 0 ? a2 : a1;
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 x = xp[(4 * bk + jj) * 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float mine = o[KEEP + bk][4 * jj + e];
+            const float t0 = GI == 0 ? mine : x[e], t1 = GI == 0 ? x[e] : mine;
+            o[KEEP + bk][4 * jj + e] = __builtin_fmaf(t0, ma, t1 * mb);
+          }
+        }
+      // Written as one explicit fma so both groups round it identically.
+      l_run = GI == 0 ? __builtin_fmaf(l_run, ma, l2 * mb) : __builtin_fmaf(l2, ma, l_run * mb);
+      m_run = M;
+    }
+    if (kv_splits == 1) {
+      const float inv = 1.0f / l_run;
+      put(KEEP, o[KEEP], inv);
+      put(KEEP + 1, o[KEEP + 1], inv);
+      __syncthreads();
+      flush();
+      return;
+    }
+    {
+      f32x4* ob = reinterpret_cast<f32x4*>(part) + (slice + split) * 32 * V + m;
+#pragma unroll
+      for (int bk = 0; bk < 2; ++bk)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          ob[(size_t)(8 * (KEEP + bk) + 2 * jj + g) * V] = f32x4{o[KEEP + bk][4 * jj], o[KEEP + bk][4 * jj + 1],
+                                                                  o[KEEP + bk][4 * jj + 2], o[KEEP + bk][4 * jj + 3]};
+      if (GI == 0 && g == 0)
+        reinterpret_cast<float2*>(reinterpret_cast<f32x4*>(part) + ml_base)[(slice + split) * V + m] =
+            float2{m_run, l_run};
+    }
+    // The last split to finish (its ticket the unit's last) folds the unit.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      unsigned* t = tickets + (size_t)u * 32;  // one 128-byte line per unit
+      const unsigned got = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (got == (unsigned)kv_splits - 1) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm_ticket = got;
+    }
+    __syncthreads();
+    if (sm_ticket != (unsigned)kv_splits - 1) return;
+    // Fold in split order, the other splits' partials from this XCD's L2 and
+    // this split's own from its registers (the same bits whichever split
+    // finishes last: the registers hold exactly what was stored).
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, (int)part_bytes, 0x00020000);
     auto o_off = [&](int sp, int c) { return (uint32_t)((((slice + sp) * 32 + c) * V + m) * 16); };
     auto ml_off = [&](int sp) { return (uint32_t)(ml_base * 16 + ((slice + sp) * V + m) * 8); };
     switch (kv_splits) {
-      case 2: fold32<2>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      case 3: fold32<3>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      case 4: fold32<4>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      case 5: fold32<5>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      case 6: fold32<6>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      case 7: fold32<7>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
-      default: fold32<8>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 2: fold32<2, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 3: fold32<3, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 4: fold32<4, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 5: fold32<5, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 6: fold32<6, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      case 7: fold32<7, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
+      default: fold32<8, KEEP>(rs, o_off, ml_off, g, put, split, o, m_run, l_run); break;
     }
-  }
-  __syncthreads();
-  flush();
+    __syncthreads();
+    flush();
+  };
+  if (gi == 0) epilogue(std::integral_constant<int, 0>{});
+  else epilogue(std::integral_constant<int, 1>{});
 }
 
 template <int S>
