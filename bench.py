@@ -630,7 +630,8 @@ def bench_floors(torch, iters=50):
     buffers: 807 MB, past the 256 MB MALL) and of one config-5 call's (67.1
     MB, 5 rotating buffers: 336 MB) at several workgroup counts; and the
     issue rate of the MFMA forms (independent chains, 1 and 4 waves per
-    SIMD), timed with events around one long launch."""
+    SIMD) and the VALU work one 32x32x16 MFMA hides, timed with events
+    around one long launch."""
     from ctypes import byref, c_void_p
 
     from ramvamp_amd import _lib as L
@@ -698,6 +699,23 @@ def bench_floors(torch, iters=50):
             row[f"tflops_{waves_per_simd}_waves_per_simd"] = round(tf, 1)
             row[f"ns_per_mfma_per_simd_{waves_per_simd}_waves"] = round(s_ / (waves_per_simd * it * 4) * 1e9, 2)
         res[f"mfma_{name}"] = row
+    # How much VALU work one v_mfma_f32_32x32x16_f16 hides on its SIMD: ns per
+    # MFMA per SIMD with k independent VALU instructions after each, at two
+    # waves per SIMD (the prefill kernel's occupancy).
+    row = {}
+    for kind, kname, ks in ((L.RV_FLOOR_VALU_FMA, "fma", (0, 2, 4, 8)), (L.RV_FLOOR_VALU_EXP, "exp", (2, 4, 8))):
+        for k in ks:
+            n_wg, it = 512, 1000
+            for _ in range(2):  # warm-up
+                ok(lib.rv_floor_mfma_valu(kind, k, it, n_wg, c_void_p(sink.data_ptr()), stream(), byref(err)))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ok(lib.rv_floor_mfma_valu(kind, k, it, n_wg, c_void_p(sink.data_ptr()), stream(), byref(err)))
+            e1.record()
+            torch.cuda.synchronize()
+            s_ = e0.elapsed_time(e1) / 1e3
+            row[f"ns_per_mfma_{kname}_{k}"] = round(s_ / (2 * it * 4) * 1e9, 2)
+    res["mfma_32x32x16_valu_overlap_2_waves"] = row
     return res
 
 

@@ -1,11 +1,12 @@
 /*
  * ramvamp_floors.h — measurement floors (no reference counterpart).
  *
- * Three probe launches that bench.py times (`--floors`, and `extra.floors`
+ * Four probe launches that bench.py times (`--floors`, and `extra.floors`
  * in its default run) to measure the limits the attention kernels are judged
  * against on the box they run on: the cost of a launch in a graph, a plain
- * streaming read of a decode call's bytes, and the issue rate of the MFMA
- * forms the kernels use. They compute nothing the library needs.
+ * streaming read of a decode call's bytes, the issue rate of the MFMA forms
+ * the kernels use, and how much VALU work an MFMA hides. They compute
+ * nothing the library needs.
  *
  * Device pointers; work on `stream` (a hipStream_t, null for the null
  * stream).
@@ -44,6 +45,18 @@ int32_t rv_floor_stream_read(const void* src, size_t bytes, uint32_t n_wg, float
 #define RV_FLOOR_MFMA_F32_16X16X4 2
 int32_t rv_floor_mfma(int32_t form, uint32_t chains, uint32_t iters, uint32_t n_wg, float* sink, void* stream,
                       rv_error* err);
+
+/* MFMA / VALU overlap: n_wg workgroups of 256 threads, every wave issuing
+ * `iters` rounds of 4 independent v_mfma_f32_32x32x16_f16 chains, each MFMA
+ * followed in issue order by `valu_per_mfma` (0, 2, 4 or 8) independent VALU
+ * instructions of one kind: RV_FLOOR_VALU_FMA (v_fma_f32) or
+ * RV_FLOOR_VALU_EXP (v_exp_f32). The time per MFMA against valu_per_mfma = 0
+ * shows how much VALU work an MFMA hides on the same SIMD. Each wave writes
+ * one float to sink[wave]. iters >= 1; n_wg in [1, 65536]. */
+#define RV_FLOOR_VALU_FMA 0
+#define RV_FLOOR_VALU_EXP 1
+int32_t rv_floor_mfma_valu(int32_t kind, uint32_t valu_per_mfma, uint32_t iters, uint32_t n_wg, float* sink,
+                           void* stream, rv_error* err);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,8 @@ RV_QF_Q8_K = 5
 RV_FLOOR_MFMA_F16_16X16X32 = 0
 RV_FLOOR_MFMA_F16_32X32X16 = 1
 RV_FLOOR_MFMA_F32_16X16X4 = 2
+RV_FLOOR_VALU_FMA = 0
+RV_FLOOR_VALU_EXP = 1
 
 
 class RvError(ctypes.Structure):
@@ -151,6 +153,7 @@ SIGNATURES = {
     "rv_floor_empty": (c_int32, [_P, _E]),
     "rv_floor_stream_read": (c_int32, [_P, c_size_t, c_uint32, _P, _P, _E]),
     "rv_floor_mfma": (c_int32, [c_int32, c_uint32, c_uint32, c_uint32, _P, _P, _E]),
+    "rv_floor_mfma_valu": (c_int32, [c_int32, c_uint32, c_uint32, c_uint32, _P, _P, _E]),
 }
 
 _lib = None

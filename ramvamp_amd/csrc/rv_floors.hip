@@ -91,6 +91,59 @@ __global__ __launch_bounds__(256) void floor_mfma_kernel(uint32_t iters, float* 
   if (lane == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = total;
 }
 
+// MFMA / VALU overlap: 4 independent chains of v_mfma_f32_32x32x16_f16, each
+// MFMA followed in issue order by K independent VALU instructions of one
+// kind (KIND 0: v_fma_f32, 1: v_exp_f32) on 8 registers; a scheduling fence
+// after each chunk keeps that order.
+template <int KIND, int K>
+__global__ __launch_bounds__(256) void floor_overlap_kernel(uint32_t iters, float* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  f16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = (_Float16)(0.001f * (float)(lane + e));
+    b[e] = (_Float16)(0.002f * (float)(lane - e));
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = 0.25f * (float)(lane + i) / 64.f;
+  const float y = 0.999f, z = 0.0001f * (float)lane;
+  for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if constexpr (KIND == 0) x[k & 7] = __builtin_fmaf(x[k & 7], y, z);
+        else x[k & 7] = __builtin_amdgcn_exp2f(-x[k & 7]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  float total = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) total += acc[c][r];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) total += x[i];
+  if (lane == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = total;
+}
+
+template <int KIND>
+void launch_overlap(uint32_t k, uint32_t iters, uint32_t n_wg, float* sink, hipStream_t s) {
+  switch (k) {
+    case 0: hipLaunchKernelGGL((floor_overlap_kernel<KIND, 0>), dim3(n_wg), dim3(256), 0, s, iters, sink); break;
+    case 2: hipLaunchKernelGGL((floor_overlap_kernel<KIND, 2>), dim3(n_wg), dim3(256), 0, s, iters, sink); break;
+    case 4: hipLaunchKernelGGL((floor_overlap_kernel<KIND, 4>), dim3(n_wg), dim3(256), 0, s, iters, sink); break;
+    default: hipLaunchKernelGGL((floor_overlap_kernel<KIND, 8>), dim3(n_wg), dim3(256), 0, s, iters, sink); break;
+  }
+}
+
 template <int FORM>
 void launch_mfma(uint32_t chains, uint32_t iters, uint32_t n_wg, float* sink, hipStream_t s) {
   if (chains == 1)
@@ -131,6 +184,19 @@ int32_t rv_floor_mfma(int32_t form, uint32_t chains, uint32_t iters, uint32_t n_
   else if (form == RV_FLOOR_MFMA_F16_32X32X16) launch_mfma<1>(chains, iters, n_wg, sink, s);
   else launch_mfma<2>(chains, iters, n_wg, sink, s);
   return done(err, "mfma launch");
+}
+
+int32_t rv_floor_mfma_valu(int32_t kind, uint32_t valu_per_mfma, uint32_t iters, uint32_t n_wg, float* sink,
+                           void* stream, rv_error* err) {
+  if (!sink) return fail(err, RV_ERR_NULL_ARG, 0, "sink");
+  if (kind != RV_FLOOR_VALU_FMA && kind != RV_FLOOR_VALU_EXP) return fail(err, RV_ERR_UNSUPPORTED, (uint64_t)kind, "kind");
+  if (valu_per_mfma != 0 && valu_per_mfma != 2 && valu_per_mfma != 4 && valu_per_mfma != 8)
+    return fail(err, RV_ERR_UNSUPPORTED, valu_per_mfma, "valu_per_mfma 0, 2, 4 or 8");
+  if (iters == 0 || n_wg == 0 || n_wg > 65536) return fail(err, RV_ERR_UNSUPPORTED, n_wg, "iters >= 1, n_wg in [1, 65536]");
+  const hipStream_t s = (hipStream_t)stream;
+  if (kind == RV_FLOOR_VALU_FMA) launch_overlap<0>(valu_per_mfma, iters, n_wg, sink, s);
+  else launch_overlap<1>(valu_per_mfma, iters, n_wg, sink, s);
+  return done(err, "mfma/valu overlap launch");
 }
 
 }  // extern "C"
