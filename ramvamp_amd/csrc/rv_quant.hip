@@ -383,7 +383,11 @@ template <bool NORM>
 __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjArgs a) {
   __shared__ rv_block_q8_k lk[kFusedMaxKBlocks];
   __shared__ rv_block_q8_0 l0[kFusedMax0Blocks];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave index as a scalar: the row, its segment and the segment's
+  // fields are then wave-uniform, read with scalar loads from the kernel
+  // arguments (indexed from a vector register, each was a vector load of
+  // the argument segment that every later load waited behind).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (a.gate_pos && *a.gate_pos > a.gate_max) return;  // the whole grid: its decode step was refused
   const int first = (int)blockIdx.x * kFusedWaves;
   // The segments this workgroup's rows touch decide which forms it needs.
@@ -398,18 +402,23 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
   }
   int i = first + wave, sg = 0;
   while (sg < a.n_seg && i >= a.n_rows[sg]) i -= a.n_rows[sg++];
-  // This wave's weight row starts streaming now, while the workgroup
-  // quantizes: one dword from each of its 128-byte lines (lane l: byte
-  // 128 l, clamped to the row and aligned down; the matrix base is 4-byte
-  // aligned, so the address stays inside it). The value is consumed only
-  // after the barrier, so nothing waits for it here.
+  // This wave's weight row starts streaming while the workgroup quantizes:
+  // one dword from each of its 128-byte lines (lane l: byte 128 l, clamped
+  // to the row and aligned down; the matrix base is 4-byte aligned, so the
+  // address stays inside it). The value is consumed only after the barrier,
+  // so nothing waits for it. With the norm it is issued after the loads of
+  // x and the norm weight, which the norm waits for first (loads retire in
+  // order).
   uint32_t touch = 0;
-  if (sg < a.n_seg) {
-    const FusedSeg& s = a.seg[sg];
-    const uint8_t* row = s.w + (size_t)i * s.row_bytes;
-    const size_t off = min((size_t)128 * lane, s.row_bytes - 4);
-    touch = *reinterpret_cast<const uint32_t*>((uintptr_t)(row + off) & ~(uintptr_t)3);
-  }
+  auto touch_row = [&]() {
+    if (sg < a.n_seg) {
+      const FusedSeg& s = a.seg[sg];
+      const uint8_t* row = s.w + (size_t)i * s.row_bytes;
+      const size_t off = min((size_t)128 * lane, s.row_bytes - 4);
+      touch = *reinterpret_cast<const uint32_t*>((uintptr_t)(row + off) & ~(uintptr_t)3);
+    }
+  };
+  if constexpr (!NORM) touch_row();
   // The residual an output row is added to is read now, under the rest.
   float addv = 0.f;
   if (sg < a.n_seg && a.seg[sg].add && lane == 0) addv = a.seg[sg].add[i];
@@ -431,6 +440,8 @@ __global__ __launch_bounds__(64 * kFusedWaves) void fused_proj_kernel(FusedProjA
       xr[r] = j < n ? a.x[j] : 0.f;
       wr[r] = j < n ? a.norm_w[j] : 0.f;
     }
+    asm volatile("" ::: "memory");  // the row loads above issue first
+    touch_row();
     double ss = 0.0;
 #pragma unroll
     for (int r = 0; r < PER; ++r) ss += (double)xr[r] * (double)xr[r];
