@@ -248,8 +248,8 @@ __device__ __forceinline__ void prep_q_block(int qw, bool live, const float* __r
 // SM >= 0 (a prefill chunk, head_dim 128): k and v rows, as the cache holds
 // them, are also written into the staged tiles in mode SM, and the rest of
 // the chunk's last tile is zeroed. The slot list is then the q heads (none,
-// or into the prepared layout qp, rounded to SM's type) and the k heads
-// (grid rows past the chunk zero their K rows); v heads are handled by the
+// or into the prepared layout qp, rounded to SM's type) and the k heads, one
+// per wave (grid rows past the chunk zero their K rows); v heads are handled by the
 // blocks y >= the q and k slot blocks, one per (quad of positions x, head y
 // - those blocks): stage_v_quad.
 constexpr int kSlots = 4;
@@ -269,6 +269,10 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
                                                           long pos0, float* __restrict__ tab, StagedRows sr,
                                                           QPrep qp) {
 #pragma clang fp contract(off)
+  // Slots per wave: a staging launch gives each k head a wave of its own
+  // (its f64 norm is a dependent chain of ~100 instructions; four of them
+  // in one wave took 2.1-2.6 us after the loads landed), the others four.
+  constexpr int KS = SM >= 0 ? 1 : kSlots;
   const int r = blockIdx.x, lane = threadIdx.x & 63;
   const int half = hd / 2;
   // This wave's slot block: blockIdx.y in one-wave blocks, the block's
@@ -296,9 +300,9 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   const int sy = by * (int)(blockDim.x >> 6) + wib;
   const int n_q_row = (SM >= 0 && qp.base) ? 0 : n_q;
   const int n_slots = SM >= 0 ? n_q_row + n_kv : n_q + 2 * n_kv;
-  const int s0 = sy * kSlots;
+  const int s0 = sy * KS;
   if constexpr (SM >= 0) {
-    const int kb = (n_slots + kSlots - 1) / kSlots;
+    const int kb = (n_slots + KS - 1) / KS;
     if (sy >= kb + n_kv) return;
     if (sy >= kb) {
       stage_v_quad<T, SM>(v, vp, n_kv, sy - kb, sr, r, lane);
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   if constexpr (SM >= 0) {
     if (r >= sr.rows) {
 #pragma unroll
-      for (int j = 0; j < kSlots; ++j) {
+      for (int j = 0; j < KS; ++j) {
         const int s = s0 + j;
         if (s < n_q_row || s >= n_slots) continue;
         const int kind = s >= n_q_row + n_kv, h = s - n_q_row - kind * n_kv;
@@ -335,9 +339,9 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   double freq[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) freq[p] = inv.f[min(lane + 64 * p, half - 1)];
-  float x0[kSlots][NP], x1[kSlots][NP];
+  float x0[KS][NP], x1[KS][NP];
 #pragma unroll
-  for (int j = 0; j < kSlots; ++j) {
+  for (int j = 0; j < KS; ++j) {
     const bool live = s0 + j < n_slots;
     const float* x = src(live ? s0 + j : 0);
     // Unconditional loads from clamped (valid) addresses, so the wait
@@ -387,9 +391,9 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   // The slots' norms first, branch-free within a block that rotates (its v
   // and dead slots compute a norm they do not use), so the f64 reductions
   // and square roots overlap.
-  float inv_rms[kSlots];
+  float inv_rms[KS];
 #pragma unroll
-  for (int j = 0; j < kSlots; ++j) {
+  for (int j = 0; j < KS; ++j) {
     inv_rms[j] = 1.0f;
     if (!rotates) continue;
     double ss = 0.0;
@@ -399,7 +403,7 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
     inv_rms[j] = (float)(1.0 / sqrt(ss / (double)hd + (double)eps));
   }
 #pragma unroll
-  for (int j = 0; j < kSlots; ++j) {
+  for (int j = 0; j < KS; ++j) {
     const int s = s0 + j;
     if (s >= n_slots) break;
     if (s >= n_q_row + n_kv) {  // v head: copied into the cache
@@ -522,7 +526,7 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   // kPrologueWaves.
   int slot_blocks = (n_slots + kSlots - 1) / kSlots;
   if (staging) {
-    slot_blocks = ((n_kv + kSlots - 1) / kSlots + n_kv + kPrologueWaves - 1) / kPrologueWaves;
+    slot_blocks = (2 * n_kv + kPrologueWaves - 1) / kPrologueWaves;  // a wave per k head, then per v head
     if (prep) {
       const size_t q_groups = (size_t)n_kv * qp->n_rb * (kQPrepVectors / 32);
       slot_blocks += (int)((q_groups + grid_rows - 1) / grid_rows);
