@@ -973,9 +973,9 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         V8 ph[2][2];
-        // Phase A: MFMA k of tile jj + 1's scores, the K operand read for
-        // MFMA k + 4, and P pair k of tile jj (two exponentials, one
-        // conversion, one dot for the sum), each chunk fenced.
+        // Phase A: MFMA k of tile jj + 1's scores (started at -max), the K
+        // operand read for MFMA k + 4, and P pair k of tile jj (two
+        // exponentials, one conversion), each chunk fenced.
         {
           V8 ka[4];
 #pragma unroll
@@ -989,17 +989,17 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
             const int qb = k >> 3, h = (k >> 2) & 1, i = 2 * (k & 3);
             ph[qb][h][i] = (E)__builtin_amdgcn_exp2f(sc[qb][8 * h + i]);
             ph[qb][h][i + 1] = (E)__builtin_amdgcn_exp2f(sc[qb][8 * h + i + 1]);
-            l_run = sum2(ph[qb][h], i, l_run);
-            // An empty asm consuming the pair and the sum keeps them here:
-            // otherwise they are sunk past the mask's branch to the PV MFMAs.
-            asm("" : "+v"(ph[qb][h]), "+v"(l_run));
+            // An empty asm consuming the pair keeps it here: otherwise it is
+            // sunk past the mask's branch to the PV MFMAs.
+            asm("" : "+v"(ph[qb][h]));
             if (k & 1) copy(jj, (4 + (k >> 1)) & 7);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
         mask(jj + 1, sn);
         // Phase B: PV MFMA k of tile jj, the V operand read for MFMA k + 4,
-        // and two of tile jj + 1's 32 scores into its running maximum.
+        // two of tile jj + 1's 32 scores into its running maximum, and pair k
+        // of tile jj's P into the sum (in the order the pairs were made).
         float mx = -INFINITY;
         {
           V8 va[4];
@@ -1011,6 +1011,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
             o[k >> 2] = Op32<MODE>::mfma(va[c], ph[c >> 1][c & 1], o[k >> 2]);
             if (k + 4 < 16) va[c] = vread(P, k + 4);
             mx = max3f(mx, sn[k >> 3][2 * (k & 7)], sn[k >> 3][2 * (k & 7) + 1]);
+            l_run = sum2(ph[k >> 3][(k >> 2) & 1], 2 * (k & 3), l_run);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
