@@ -342,7 +342,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     const int tile = tt_lo + G * min(j, n_load - 1) + grp;
     const char* g = src + (size_t)tile * TB;
     const int piece = 1024 * (wv + W * i);
-    lds_load16(g + piece, (lds_void*)&lds[grp][s][piece]);
+    lds_dma16(g + piece, lds_offset(&lds[grp][s][piece]));
   };
 #pragma unroll
   for (int j = 0; j < NS - 1; ++j)
@@ -416,50 +416,57 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     const char* vt = kt + P * kPlaneBytes;
     const int t0 = (tt_lo + G * j + grp) * kBT;
 
-    // S^T for the tile's four 16-position blocks. The tile's K operands are
-    // read from LDS ahead of the MFMAs; the next tile's loads are issued
-    // between them, so the address queue drains while the MFMAs run.
-    V8 ka[4][4], kal[4][4];
+    // S^T for the tile's four 16-position blocks in 16 fenced chunks c =
+    // (pb, ks), pb-major: chunk c's three split products (hi·hi, lo·hi,
+    // hi·lo) for every column block, the K operand reads of chunk c + 2 (a
+    // ring of three: reading all 32 operands first kept 128 registers and
+    // left the first MFMAs waiting on the last reads), and one of the next
+    // tile's pieces every other chunk. Each accumulator sums in the same
+    // order as before. The tile's K row exponents are read up front.
+    static_assert(kSplit && G == 1, "the split mode's single group");
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    f32x4 sc[MT][4];
+    i32x4 ke[4];
+    {
+      V8 ka[3], kal[3];
+      auto kread = [&](int c, int slot) {
+        const int off = k_off(16 * (c >> 2) + lm, 4 * (c & 3) + kk);
+        ka[slot] = *reinterpret_cast<const V8*>(kt + off);
+        kal[slot] = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
+      };
+      kread(0, 0);
+      kread(1, 1);
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) ke[pb] = *reinterpret_cast<const i32x4*>(kt + kScaleOffset + 4 * (16 * pb + 4 * kk));
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const int pb = c >> 2, ks = c & 3, sl = c % 3;
+        if (c + 2 < 16) kread(c + 2, (c + 2) % 3);
+        if (ks == 0) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(ka[sl], qh[mt][ks], sc[mt][pb]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(kal[sl], qh[mt][ks], sc[mt][pb]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(ka[sl], ql[mt][ks], sc[mt][pb]);
+        if (c & 1) {
+#pragma unroll
+          for (int i = (c >> 1) * LQK / 8; i < ((c >> 1) + 1) * LQK / 8; ++i) issue_piece(j + NS - 1, nxt, i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // Undo the q and K row exponents (exactly), then scale in fp32; this
+    // lane's positions are 16 pb + 4 kk + e.
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int off = k_off(16 * pb + lm, 4 * ks + kk);
-        ka[pb][ks] = *reinterpret_cast<const V8*>(kt + off);
-        if constexpr (kSplit) kal[pb][ks] = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
-      }
-    f32x4 sc[MT][4];
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        sc[mt][pb] = kSplit ? f32x4{0.f, 0.f, 0.f, 0.f} : negm[mt];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          sc[mt][pb] = Op<MODE>::mfma(ka[pb][ks], qh[mt][ks], sc[mt][pb]);
-          if constexpr (kSplit) {
-            sc[mt][pb] = Op<MODE>::mfma(kal[pb][ks], qh[mt][ks], sc[mt][pb]);
-            sc[mt][pb] = Op<MODE>::mfma(ka[pb][ks], ql[mt][ks], sc[mt][pb]);
-          }
-        }
-      }
-      // Pieces [0, LQK) of the next tile, spread over the four blocks.
-#pragma unroll
-      for (int i = pb * LQK / 4; i < (pb + 1) * LQK / 4; ++i) issue_piece(j + NS - 1, nxt, i);
-    }
-    if constexpr (kSplit) {
-      // Undo the q and K row exponents (exactly), then scale in fp32; this
-      // lane's positions are 16 pb + 4 kk + e.
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        typedef int i32x4 __attribute__((ext_vector_type(4)));
-        const i32x4 ke = *reinterpret_cast<const i32x4*>(kt + kScaleOffset + 4 * (16 * pb + 4 * kk));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc[mt][pb][e] = ldexpf(sc[mt][pb][e], -(qe[mt] + ke[e])) * qscale + negm[mt][e];
-      }
-    }
+        for (int e = 0; e < 4; ++e) sc[mt][pb][e] = ldexpf(sc[mt][pb][e], -(qe[mt] + ke[pb][e])) * qscale + negm[mt][e];
     // Causal mask only where some row of the block stops inside the tile.
     if (t0 + kBT > all_see) {
 #pragma unroll
@@ -540,49 +547,54 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       if constexpr (!kSplit) psum = sum8(ph[mt][1], sum8(ph[mt][0], 0.f));
       l_run[mt] += psum;
     }
-    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's);
-    // the V operands are read ahead of the MFMAs. The split mode sums the
-    // tile into a fresh accumulator and folds it in with the tile's column
-    // exponents undone (this lane's O^T rows are d = 16 b + 4 kk + e).
-    V8 va[8][2], val[8][2];
+    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's),
+    // in 8 fenced d blocks b: block b's 6 MT MFMAs (two steps, the three
+    // split products, into a fresh accumulator), block b + 1's V operand
+    // reads and column exponents, block b - 1's fold into O with its
+    // exponents undone (this lane's O^T rows are d = 16 b + 4 kk + e), and
+    // the rest of the next tile's pieces.
+    {
+      V8 va[2][2], val[2][2];
+      i32x4 cx[3];
+      auto vread = [&](int b) {
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int off = vt_off(16 * b + lm, 4 * s2 + kk);
-        va[b][s2] = *reinterpret_cast<const V8*>(vt + off);
-        if constexpr (kSplit) val[b][s2] = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
-      }
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      f32x4 acc[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] = kSplit ? f32x4{0.f, 0.f, 0.f, 0.f} : o[mt][b];
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          acc[mt] = Op<MODE>::mfma(va[b][s2], ph[mt][s2], acc[mt]);
-          if constexpr (kSplit) {
-            acc[mt] = Op<MODE>::mfma(val[b][s2], ph[mt][s2], acc[mt]);
-            acc[mt] = Op<MODE>::mfma(va[b][s2], pl[mt][s2], acc[mt]);
-          }
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int off = vt_off(16 * b + lm, 4 * s2 + kk);
+          va[b & 1][s2] = *reinterpret_cast<const V8*>(vt + off);
+          val[b & 1][s2] = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
         }
-      }
-      if constexpr (kSplit) {
-        typedef int i32x4 __attribute__((ext_vector_type(4)));
-        const i32x4 cx = *reinterpret_cast<const i32x4*>(kt + kVScaleOffset + 4 * (16 * b + 4 * kk));
+        cx[b % 3] = *reinterpret_cast<const i32x4*>(kt + kVScaleOffset + 4 * (16 * b + 4 * kk));
+      };
+      f32x4 pend[MT];
+      auto fold = [&](int b) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[mt][b][e] += ldexpf(acc[mt][e], -cx[e]);
-      } else {
+          for (int e = 0; e < 4; ++e) o[mt][b][e] += ldexpf(pend[mt][e], -cx[b % 3][e]);
+      };
+      vread(0);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) o[mt][b] = acc[mt];
+      for (int b = 0; b < 8; ++b) {
+        if (b + 1 < 8) vread(b + 1);
+        f32x4 acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt] = Op<MODE>::mfma(va[b & 1][s2], ph[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(val[b & 1][s2], ph[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(va[b & 1][s2], pl[mt][s2], acc[mt]);
+          }
+        if (b > 0) fold(b - 1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) pend[mt] = acc[mt];
+#pragma unroll
+        for (int i = LQK + b * (LPW - LQK) / 8; i < LQK + (b + 1) * (LPW - LQK) / 8; ++i) issue_piece(j + NS - 1, nxt, i);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // Pieces [LQK, LPW), spread over the eight d blocks.
-#pragma unroll
-      for (int i = LQK + b * (LPW - LQK) / 8; i < LQK + (b + 1) * (LPW - LQK) / 8; ++i) issue_piece(j + NS - 1, nxt, i);
+      fold(7);
     }
   }
   // The clamped prefetches past the last tile may still be landing in LDS:
