@@ -8,42 +8,46 @@
 //
 // 1. prefill_stage_kernel converts the layer's K and V rows [0, positions)
 //    once into the MFMA element type (f16 / bf16, or for the split mode
-//    scaled hi + lo f16 K with each row's exponent, hi + lo bf16 V) and lays
-//    each 64-position tile out exactly as the attention
+//    hi + lo f16 with each K row and each V column of a tile scaled by its
+//    power of two) and lays each 64-position tile out exactly as the attention
 //    kernel wants it in LDS: K row-major, V transposed with its positions
 //    permuted into the order the S^T accumulator produces P, both with their
 //    16-byte chunks XOR-swizzled so the MFMA operand reads are free of bank
 //    conflicts. Every row block of the chunk then re-reads this compact copy
 //    (half the bytes of an fp32 cache) instead of converting on the fly.
 //
-// 2. prefill_kernel: one workgroup (W waves) per (kv head, block of M/group
-//    query rows, KV split). Its M = 128 (or 64) query vectors are every q head
-//    of the GQA group for each of its rows, so each staged K/V tile feeds all
-//    heads: column m is head m / qr, row m % qr (qr = M / group); wave w owns
-//    columns [16*MT*w, 16*MT*(w+1)). Tiles stream into a ring of NS LDS
-//    stages with direct-to-LDS loads (global_load_lds_dwordx4: no registers,
-//    no conversion), NS - 1 tiles ahead of the one being computed. Per tile:
-//      S^T[t][m] = sum_d K[t][d] Q[m][d]      (A = K from LDS, B = Q in VGPRs)
-//      O^T[d][m] += sum_t V[t][d] P[m][t]     (A = V^T from LDS, B = P in VGPRs)
-//    on v_mfma_f32_16x16x32_{f16,bf16}. Computing S transposed puts a query
-//    vector's scores in one lane (4 consecutive t per 16x16 block), which is
-//    the B-operand layout P^T needs, so P never leaves registers.
+// 2. The attention kernel: one workgroup per (kv head, block of query
+//    vectors, KV split). Its query vectors are every q head of the GQA group
+//    for each of its rows, so each staged K/V tile feeds all heads. Tiles
+//    stream into LDS with direct-to-LDS loads (global_load_lds_dwordx4: no
+//    registers, no conversion), issued from inline assembly so the compiler
+//    adds no wait for them before LDS reads. Per tile:
+//      S^T[t][m] = sum_d K[t][d] Q[m][d]      (A = K from LDS, B = Q in registers)
+//      O^T[d][m] += sum_t V[t][d] P[m][t]     (A = V^T from LDS, B = P in registers)
+//    Computing S transposed puts a query vector's scores in the lanes that
+//    hold it as the B operand P^T needs, so P never leaves registers. Both
+//    kernels are software-pipelined inside each wave: a tile's softmax work
+//    runs between the MFMAs of its neighbours.
+//    prefill_kernel (EXACT) works on v_mfma_f32_16x16x32_f16, 16 or 32
+//    columns per wave; prefill32_kernel (F16 / BF16) on
+//    v_mfma_f32_32x32x16_{f16,bf16}, 32 columns per wave.
 //
 // Arithmetic modes (flags RV_PREFILL_*):
-//   EXACT, the fp32 parity mode, for any finite fp32 operands: each K row
-//          and q vector scaled by a power of two that puts its largest
-//          magnitude in [2^13, 2^14), split as hi + lo f16, products hi*hi +
-//          hi*lo + lo*hi in fp32 (~2^-21 of the row and vector maxima), the
-//          exponents undone exactly on the fp32 score; V as bf16 hi + lo and
-//          P as bf16 hi + mid + lo (bf16 keeps fp32's exponent range), five
-//          products per term (~2^-18 relative).
+//   EXACT, the fp32 parity mode, for any finite fp32 operands: each K row,
+//          each V column of a tile and each q vector scaled by a power of
+//          two that puts its largest magnitude in [2^13, 2^14), split as hi
+//          + lo f16; products hi*hi + lo*hi + hi*lo in fp32 (~2^-21 of the
+//          row and vector maxima), the scales undone exactly on the fp32
+//          scores and on each tile's O^T rows; P (< 2^8) as f16 hi + lo,
+//          three products per PV term.
 //   F16 / BF16: one MFMA per product, fp32 accumulate.
 // Softmax is online in fp32 (exp2, log2(e) folded into the score scale), with
 // the running maximum moved only when a tile exceeds it by 2^8.
 //
 // KV splits (short chunks, too few row blocks to fill the chip): each split
-// writes partial (O, max, sum) columns; prefill_merge_kernel folds them with
-// an fp32 log-sum-exp in a further launch (the splits run on different XCDs).
+// writes partial (O, max, sum) columns; EXACT folds them with an fp32
+// log-sum-exp in a further launch (prefill_merge_kernel), F16 / BF16 in the
+// same launch (the last split of a unit to finish, on the splits' XCD).
 #include "rv_device.hpp"
 #include "rv_internal.hpp"
 #include "rv_staged.hpp"
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
   if (plane == 0) {
     // NE elements = a half (fp32) or a whole (f16) 16-byte chunk of row r,
     // whose kD / NE threads are adjacent lanes; the split mode scales the row
-    // by its exponent (from their max over the row) and records it.
+    // by its exponent e (from their max over the row) and records 2^-e.
     const int c = StageLoad<T>::col(tid);
 #pragma unroll
     for (int j = 0; j < StageLoad<T>::kN; ++j) {
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
 #pragma unroll
         for (int w = 1; w < kD / NE; w <<= 1) amax = fmaxf(amax, __shfl_xor(amax, w, 64));
         ex = scale_exponent(amax);
-        if (c == 0) *reinterpret_cast<int*>(dst + kScaleOffset + 4 * r) = ex;
+        if (c == 0) *reinterpret_cast<float*>(dst + kScaleOffset + 4 * r) = ldexpf(1.0f, -ex);
       }
       EN hi, lo;
 #pragma unroll
@@ -152,8 +156,8 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
     for (int e = 0; e < NE; ++e) vt[StageLoad<T>::row(j, tid)][StageLoad<T>::col(tid) + e] = ld.get(j, e);
   __syncthreads();
   // Thread -> V^T row d = tid / 2, chunks 4 (tid % 2) .. +3. The split mode
-  // scales the tile's column d by its exponent (from the column's max over
-  // the tile, both threads of d taking half) and records it.
+  // scales the tile's column d by its exponent c (from the column's max over
+  // the tile, both threads of d taking half) and records 2^-c.
   const int d = tid >> 1;
   char* vdst = dst + P * kPlaneBytes;
   int cx = 0;
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
 #pragma unroll 8
     for (int t = 32 * (tid & 1); t < 32 * (tid & 1) + 32; ++t) amax = fmaxf(amax, fabsf(vt[t][d]));
     cx = scale_exponent(fmaxf(amax, __shfl_xor(amax, 1, 64)));
-    if ((tid & 1) == 0) *reinterpret_cast<int*>(dst + kVScaleOffset + 4 * d) = cx;
+    if ((tid & 1) == 0) *reinterpret_cast<float*>(dst + kVScaleOffset + 4 * d) = ldexpf(1.0f, -cx);
   }
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) {
@@ -277,12 +281,19 @@ __device__ __forceinline__ float sum2(bf16x8 v, int i, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(b2{v[i], v[i + 1]}, one, acc, false);
 }
 
-// G groups of W waves. Every group covers all M = 16 W MT columns of the
-// workgroup; group g computes the tiles tt_lo + G j + g of the workgroup's
-// range from its own ring of NS stages, all groups in lockstep (one barrier
-// per iteration), and the groups' (O, max, sum) are merged through LDS at the
-// end. With G = 2 two waves share each SIMD, so one's softmax overlaps the
-// other's MFMAs.
+// prefill_kernel (the split mode): one group of W = 4 waves; column m of the
+// workgroup's M = 16 W MT is head m / qr, row m % qr of the block (qr = M /
+// group), wave w owning columns [16 MT w, 16 MT (w + 1)). A tile is 68 KiB
+// (K hi, K lo, V^T hi, V^T lo planes, then the exponents) and the ring holds
+// two. The loop is software-pipelined inside each wave, as the F16 / BF16
+// kernel's: iteration j exponentiates and splits tile j's P between the
+// MFMAs of tile j + 1's scores (phase A), then scales tile j + 1's scores and
+// takes their maximum between tile j's PV MFMAs (phase B), each chunk fenced
+// so the compiler keeps that issue order; the shadow of the MFMAs holds the
+// softmax work, which otherwise ran between the MFMA phases on the SIMD's
+// single wave. Tile j + 1's V half is copied in during phase A and tile j +
+// 2's K half during phase B, into the halves of the ring the previous
+// iteration finished with.
 template <int MODE, int G, int W, int MT, int NS>
 __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __restrict__ q,
                                                              const char* __restrict__ stage, int n_stage_tiles,
@@ -295,30 +306,22 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   typedef typename Op<MODE>::V8 V8;
   typedef typename Op<MODE>::V4 V4;
   constexpr bool kSplit = Op<MODE>::kSplit;
-  constexpr int P = kSplit ? 2 : 1;
+  static_assert(kSplit && G == 1 && NS == 2 && W == 4, "the split mode: one group of 4 waves, two stages");
   constexpr int M = 16 * W * MT;       // query vectors per workgroup
   constexpr int TB = kTileBytes<MODE>;  // bytes per staged tile
-  constexpr int LPW = TB / 1024 / W;   // direct-to-LDS loads per wave per tile
-  // Pieces issued among the QK MFMAs (spread over the four position blocks);
-  // the rest go among the PV MFMAs (over the eight d blocks).
-  constexpr int LQK = LPW / 8 * 4;
-  static_assert(TB % (1024 * W) == 0 && LQK >= 4, "whole pieces per wave");
+  static_assert(TB == 68 * 1024 && kVScaleOffset == kScaleOffset + 1024, "68 pieces of 1 KiB");
   // Scores are kept relative to a running maximum that only moves when a
   // tile's maximum exceeds it by more than this (log2 units): P values stay
   // below 2^8 and most tiles skip rescaling the accumulators.
   constexpr float kRescale = 8.0f;
-  // Per-lane floats a later group hands to group 0: O, then (max, sum) per mt.
-  constexpr int kX = MT * 32 + 2 * MT;
-  static_assert((size_t)(G - 1) * W * 64 * kX * 4 <= (size_t)G * NS * TB, "group exchange fits the ring");
 
-  __shared__ __attribute__((aligned(1024))) char lds[G][NS][TB];
+  __shared__ __attribute__((aligned(1024))) char lds[NS][TB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const Unit un = unit_of(n_units, n_rb, kv_splits);
   if (!un.live) return;
   const int split = un.split, rb = un.rb, kvh = un.kvh;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave / W, wv = wave % W;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lm = lane & 15, kk = lane >> 4;
   const int qr = M / group;  // rows per workgroup
   const int r0 = rb * qr;
@@ -327,39 +330,58 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   const int all_see = start + r0 + 1;           // positions every row of the block sees
   const int n_tiles = (wg_limit + kBT - 1) / kBT;
   const int tt_lo = (int)((long)n_tiles * split / kv_splits);
-  const int tt_hi = (int)((long)n_tiles * (split + 1) / kv_splits);
-  const int n = tt_hi - tt_lo;
-  const int n_mine = (n - grp + G - 1) / G;  // this group's tiles: tt_lo + G j + grp
-  const int n_iter = (n + G - 1) / G;        // iterations (every group, lockstep)
-  const int n_load = n_mine;
+  const int n = (int)((long)n_tiles * (split + 1) / kv_splits) - tt_lo;
 
-  // The group's tile j (clamped to its last loaded one, so every wave issues
-  // the same number of loads per iteration) into stage s: wave w copies the
-  // 1 KiB pieces w, w + W, ...; lane l's 16 bytes land at piece + 16 l.
-  const char* src = stage + (size_t)kvh * n_stage_tiles * TB + 16 * lane;
-  auto issue_piece = [&](int j, int s, int i) {
-    if (n_load <= 0) return;
-    const int tile = tt_lo + G * min(j, n_load - 1) + grp;
-    const char* g = src + (size_t)tile * TB;
-    const int piece = 1024 * (wv + W * i);
-    lds_dma16(g + piece, lds_offset(&lds[grp][s][piece]));
+  // Half h of tile t (0: the K planes, pieces 0-31, and the K factors,
+  // piece 64; 1: the V planes, 32-63, and the V factors, 65) into stage s,
+  // in 9 parts per wave: part i < 8 is piece 32 h + w + 4 i, part 8 piece
+  // 64 + h + 2 (w & 1) (waves 0 and 2 both copy the factors, 1 and 3 an
+  // unused piece: no branch). Lane l's 16 bytes land at piece + 16 l. A
+  // half's global and LDS bases are wave-uniform, set once per half and
+  // hidden from the compiler (so it computes each part's address where the
+  // part is issued, instead of holding every part's address in scalar
+  // registers across the loop). Tile indices are clamped to the range's last
+  // tile, so the copies stay unconditional (past the range they refill a
+  // half that nothing reads again).
+  const char* const srcw = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB;
+  const uint32_t voff = 16u * (uint32_t)lane;
+  struct HalfBase {
+    const char* g;
+    uint32_t l;
   };
+  auto half_base = [&](int t, int s, int h) {
+    HalfBase b{srcw + (size_t)min(t, n - 1) * TB + 1024 * (32 * h + wv),
+               (uint32_t)lds_offset(&lds[s][1024 * (32 * h + wv)])};
+    asm volatile("" : "+s"(b.g), "+s"(b.l));
+    return b;
+  };
+  auto copy_part = [&](const HalfBase& b, int h, int i) {
+    const int off = i < 8 ? 4096 * i : 1024 * (64 + h + 2 * (wv & 1) - 32 * h - wv);
+    lds_dma16s(b.g + off, voff, b.l + off);
+  };
+  // Tile 0 whole and tile 1's K half, ahead of the query loads.
+  if (n > 0) {
+    const HalfBase k0 = half_base(0, 0, 0), v0 = half_base(0, 0, 1), k1 = half_base(1, 1, 0);
 #pragma unroll
-  for (int j = 0; j < NS - 1; ++j)
+    for (int i = 0; i < 9; ++i) copy_part(k0, 0, i);
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) issue_piece(j, j, i);
+    for (int i = 0; i < 9; ++i) copy_part(v0, 1, i);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) copy_part(k1, 0, i);
+  }
 
   // This lane's query vector in column block mt: column m = 16*(wv*MT + mt) + lm.
   int my_row[MT], my_head[MT], my_limit[MT];
   bool col_ok[MT];
   V8 qh[MT][4], ql[MT][4];
-  int qe[MT];  // the split mode's q exponents
+  // log2(e) * scale * 2^-qe: undoes the vector's exponent qe and scales its
+  // fp32 scores.
+  float qf[MT];
   f32x4 o[MT][8];
   float m_run[MT], l_run[MT];
-  // -m_run, or 0 while a column has seen no unmasked position: the non-split
-  // modes start their QK MFMAs from it, so S^T arrives relative to the
-  // running max; the split mode adds it after scaling.
-  f32x4 negm[MT];
+  // -m_run, or 0 while a column has seen no unmasked position: added to the
+  // scores after scaling, so they are relative to the running max.
+  float negm[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * (wv * MT + mt) + lm;
@@ -370,235 +392,345 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
                       (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
     // q rows may be only 4-byte aligned: scalar loads (once per workgroup).
-    // log2(e) * scale is folded in before rounding to the MFMA type, except
-    // in the split mode, where rounding the scaled q would cost low bits of
-    // the lo half and the scores are scaled in fp32 instead.
-    const float qs = col_ok[mt] ? (kSplit ? 1.f : qscale) : 0.f;
+    // The scores are scaled by log2(e) * scale in fp32 (rounding the scaled q
+    // would cost low bits of the lo half).
+    const float qs = col_ok[mt] ? 1.f : 0.f;
     float x[4][8];
     load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
-    // The split mode scales the vector by its exponent (from its max over
-    // the column's four lanes), undone on the fp32 scores.
-    qe[mt] = 0;
-    if constexpr (kSplit) {
-      float amax = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[s][e] * qs));
-      qe[mt] = scale_exponent(swap_max<32>(swap_max<16>(amax)));
-    }
+    // The vector scaled by its exponent (from its max over the column's four
+    // lanes), undone on the fp32 scores; capped at 100 so qscale * 2^-qe
+    // stays a normal float (a vector below 2^-86 throughout keeps its
+    // largest elements in f16's range and contributes scores below 2^-60).
+    float amax = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) split2v<E>(kSplit ? ldexpf(x[s][e] * qs, qe[mt]) : x[s][e] * qs, qh[mt][s], ql[mt][s], e);
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[s][e] * qs));
+    const int qe = scale_exponent(swap_max<32>(swap_max<16>(amax)), 100);
+    qf[mt] = ldexpf(qscale, -qe);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) split2v<E>(ldexpf(x[s][e] * qs, qe), qh[mt][s], ql[mt][s], e);
+      // Held in AGPRs: the QK MFMAs read them from there, which leaves the
+      // VGPRs to the loop's working set.
+      asm("" : "+a"(qh[mt][s]));
+      asm("" : "+a"(ql[mt][s]));
+    }
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m_run[mt] = kNegSentinel;
     l_run[mt] = 0.f;
-    negm[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    negm[mt] = 0.f;
   }
 
-  for (int j = 0; j < n_iter; ++j) {
-    const int s = j % NS;
-    // This wave's loads of the group's tile j are done once at most NS - 2
-    // tiles of its loads remain in flight; the barrier makes every wave's
-    // part visible and retires the stage the loads below overwrite
-    // (computed last iteration).
-    wait_vmcnt<(NS - 2) * LPW>();
-    __syncthreads();
-    const int nxt = (j + NS - 1) % NS;
-    if (j >= n_mine) {  // this group has no tile this iteration (wave-uniform)
+  if (n > 0) {
+    typedef __attribute__((address_space(3))) const char* LdsPtr;
+    // Scores of a tile: s[mt][pb][e] = S^T[16 pb + 4 kk + e][column block mt];
+    // element i = 4 (MT pb + mt) + e in the orders below.
+    typedef f32x4 Scores[MT][4];
+    // Per-lane LDS bases per stage (stage 1 lies past the reads' 16-bit
+    // immediate offsets, so each stage gets its own): K row lm at d chunk
+    // 4 ks + kk; V^T row lm at chunk 4 s2 + kk; this lane's four K factors
+    // (positions 4 kk .. + 3 of a 16-position block) and V^T factors.
+    // Every read below is one of these plus an immediate.
+    LdsPtr kb[2][4], vb[2][2], kfb[2], vfb[2];
 #pragma unroll
-      for (int i = 0; i < LPW; ++i) issue_piece(j + NS - 1, nxt, i);
-      continue;
+    for (int s = 0; s < 2; ++s) {
+      const LdsPtr st = (LdsPtr)&lds[s][0];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        kb[s][ks] = st + k_off(lm, 4 * ks + kk);
+        asm("" : "+v"(kb[s][ks]));
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        vb[s][s2] = st + 2 * kPlaneBytes + vt_off(lm, 4 * s2 + kk);
+        asm("" : "+v"(vb[s][s2]));
+      }
+      kfb[s] = st + kScaleOffset + 16 * kk;
+      vfb[s] = st + kVScaleOffset + 16 * kk;
+      asm("" : "+v"(kfb[s]));
+      asm("" : "+v"(vfb[s]));
     }
-    const char* kt = lds[grp][s];
-    const char* vt = kt + P * kPlaneBytes;
-    const int t0 = (tt_lo + G * j + grp) * kBT;
-
-    // S^T for the tile's four 16-position blocks in 16 fenced chunks c =
-    // (pb, ks), pb-major: chunk c's three split products (hi·hi, lo·hi,
-    // hi·lo) for every column block, the K operand reads of chunk c + 2 (a
-    // ring of three: reading all 32 operands first kept 128 registers and
-    // left the first MFMAs waiting on the last reads), and one of the next
-    // tile's pieces every other chunk. Each accumulator sums in the same
-    // order as before. The tile's K row exponents are read up front.
-    static_assert(kSplit && G == 1, "the split mode's single group");
-    typedef int i32x4 __attribute__((ext_vector_type(4)));
-    f32x4 sc[MT][4];
-    i32x4 ke[4];
-    {
-      V8 ka[3], kal[3];
-      auto kread = [&](int c, int slot) {
-        const int off = k_off(16 * (c >> 2) + lm, 4 * (c & 3) + kk);
-        ka[slot] = *reinterpret_cast<const V8*>(kt + off);
-        kal[slot] = *reinterpret_cast<const V8*>(kt + kPlaneBytes + off);
-      };
-      kread(0, 0);
-      kread(1, 1);
+    // K operands of QK chunk c = (pb, ks), pb-major: rows 16 pb + lm, d
+    // chunk 4 ks + kk (the swizzle k_off depends on the row only through lm),
+    // both planes.
+    auto kread = [&](int s, int c, V8& a, V8& al) {
+      const LdsPtr p = kb[s][c & 3] + 4096 * (c >> 2);
+      a = *reinterpret_cast<const __attribute__((address_space(3))) V8*>(p);
+      al = *reinterpret_cast<const __attribute__((address_space(3))) V8*>(p + kPlaneBytes);
+    };
+    // Chunk c's three split products (hi·hi, lo·hi, hi·lo) for every column
+    // block, into fresh accumulators at ks = 0.
+    auto qk_chunk = [&](int c, const V8& a, const V8& al, Scores& s) {
+      const int pb = c >> 2, ks = c & 3;
+      if (ks == 0) {
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb) ke[pb] = *reinterpret_cast<const i32x4*>(kt + kScaleOffset + 4 * (16 * pb + 4 * kk));
+        for (int mt = 0; mt < MT; ++mt) s[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) s[mt][pb] = Op<MODE>::mfma(a, qh[mt][ks], s[mt][pb]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) s[mt][pb] = Op<MODE>::mfma(al, qh[mt][ks], s[mt][pb]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) s[mt][pb] = Op<MODE>::mfma(a, ql[mt][ks], s[mt][pb]);
+    };
+    // A tile's 16 QK chunks from stage st with a ring of three K operand
+    // reads; between(c) runs in chunk c, each chunk fenced.
+    auto qk_tile = [&](int st, Scores& s, auto between) {
+      V8 ka[3], kal[3];
+      kread(st, 0, ka[0], kal[0]);
+      kread(st, 1, ka[1], kal[1]);
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
-        const int pb = c >> 2, ks = c & 3, sl = c % 3;
-        if (c + 2 < 16) kread(c + 2, (c + 2) % 3);
-        if (ks == 0) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(ka[sl], qh[mt][ks], sc[mt][pb]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(kal[sl], qh[mt][ks], sc[mt][pb]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) sc[mt][pb] = Op<MODE>::mfma(ka[sl], ql[mt][ks], sc[mt][pb]);
-        if (c & 1) {
-#pragma unroll
-          for (int i = (c >> 1) * LQK / 8; i < ((c >> 1) + 1) * LQK / 8; ++i) issue_piece(j + NS - 1, nxt, i);
-        }
+        if (c + 2 < 16) kread(st, c + 2, ka[(c + 2) % 3], kal[(c + 2) % 3]);
+        qk_chunk(c, ka[c % 3], kal[c % 3], s);
+        between(c);
         __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    // Undo the q and K row exponents (exactly), then scale in fp32; this
-    // lane's positions are 16 pb + 4 kk + e.
+    };
+    // Causal mask of tile jj's scores, only where some row of the block stops
+    // inside the tile.
+    auto mask = [&](int jj, Scores& s) {
+      const int t0 = (tt_lo + jj) * kBT;
+      if (t0 + kBT > all_see) {
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+          for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sc[mt][pb][e] = ldexpf(sc[mt][pb][e], -(qe[mt] + ke[pb][e])) * qscale + negm[mt][e];
-    // Causal mask only where some row of the block stops inside the tile.
-    if (t0 + kBT > all_see) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) sc[mt][pb][e] = -INFINITY;
-    }
-    // Online softmax per query vector; this lane holds t0 + 16pb + 4kk + e,
-    // relative to m_run (absolute while m_run is the sentinel). Column maxima
-    // over the lane's 16 values, then across the four lanes of the column
-    // (lanes 16 and 32 apart) with permlane swaps.
-    float mx[MT];
-    bool grow = false;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float x = max3f(sc[mt][0][0], sc[mt][0][1], sc[mt][0][2]);
-      x = max3f(x, sc[mt][0][3], sc[mt][1][0]);
-      x = max3f(x, sc[mt][1][1], sc[mt][1][2]);
-      x = max3f(x, sc[mt][1][3], sc[mt][2][0]);
-      x = max3f(x, sc[mt][2][1], sc[mt][2][2]);
-      x = max3f(x, sc[mt][2][3], sc[mt][3][0]);
-      x = max3f(x, sc[mt][3][1], sc[mt][3][2]);
-      x = __builtin_elementwise_maximum(x, sc[mt][3][3]);
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      x = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-      mx[mt] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-      grow = grow || mx[mt] > kRescale || m_run[mt] == kNegSentinel;
-    }
-    if (__builtin_amdgcn_ballot_w64(grow)) {
+            for (int e = 0; e < 4; ++e)
+              if (t0 + 16 * pb + 4 * kk + e >= my_limit[mt]) s[mt][pb][e] = -INFINITY;
+      }
+    };
+    // The K factors 2^-e_t of positions 16 pb + 4 kk + e.
+    auto read_kf = [&](int s, int pb) {
+      return *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(kfb[s] + 64 * pb);
+    };
+    // Elements i and i + 1 (one column block) of s: the K row and q
+    // exponents undone (exact powers of two), the fp32 scale and -max
+    // applied, both into that column's running maximum of the tile.
+    auto scale_pair = [&](Scores& s, const f32x4& kf, int i, float (&mx)[MT]) {
+      const int pb = i / (4 * MT), mt = (i / 4) % MT, e = i % 4;
+      s[mt][pb][e] = __builtin_fmaf(s[mt][pb][e] * kf[e], qf[mt], negm[mt]);
+      s[mt][pb][e + 1] = __builtin_fmaf(s[mt][pb][e + 1] * kf[e + 1], qf[mt], negm[mt]);
+      mx[mt] = max3f(mx[mt], s[mt][pb][e], s[mt][pb][e + 1]);
+    };
+    // Online softmax step of a tile whose scores are scaled and whose lane
+    // maxima are mx: the column maxima across the column's four lanes (16
+    // and 32 apart, permlane swaps); a column still at the sentinel takes the
+    // tile's maximum outright (its O and sum are zero), others move up by d
+    // >= 0 and rescale, only when some column of the wave grows by more than
+    // kRescale.
+    auto adjust = [&](float (&mx)[MT], Scores& s) {
+      bool grow = false;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        // A column still at the sentinel takes the tile's maximum outright
-        // (its O and sum are zero); others move up by d >= 0 and rescale.
-        const bool fresh = m_run[mt] == kNegSentinel;
-        const float d = fresh ? fmaxf(mx[mt], kNegSentinel) : fmaxf(mx[mt], 0.f);
-        if (!fresh) {
-          const float alpha = __builtin_amdgcn_exp2f(-d);
-          l_run[mt] *= alpha;
-#pragma unroll
-          for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
-          m_run[mt] += d;
-        } else {
-          m_run[mt] = d;
-        }
-#pragma unroll
-        for (int pb = 0; pb < 4; ++pb) sc[mt][pb] -= d;
-        const float nm = m_run[mt] == kNegSentinel ? 0.f : -m_run[mt];
-        negm[mt] = f32x4{nm, nm, nm, nm};
+        float x = mx[mt];
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __builtin_elementwise_maximum(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        mx[mt] = __builtin_elementwise_maximum(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+        grow = grow || mx[mt] > kRescale || m_run[mt] == kNegSentinel;
       }
-    }
-    // P^T operand for PV step s2: slots j<4 are t = 32s2 + 4kk + j, slots
-    // j>=4 are t = 32s2 + 16 + 4kk + j - 4 (blocks 2s2 and 2s2 + 1).
-    V8 ph[MT][2], pl[MT][2];
+      if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float psum = 0.f;
+        for (int mt = 0; mt < MT; ++mt) {
+          const bool fresh = m_run[mt] == kNegSentinel;
+          const float d = fresh ? fmaxf(mx[mt], kNegSentinel) : fmaxf(mx[mt], 0.f);
+          if (!fresh) {
+            const float alpha = __builtin_amdgcn_exp2f(-d);
+            l_run[mt] *= alpha;
 #pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        f32x4 p;
+            for (int b = 0; b < 8; ++b) o[mt][b] *= alpha;
+            m_run[mt] += d;
+          } else {
+            m_run[mt] = d;
+          }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = __builtin_amdgcn_exp2f(sc[mt][pb][e]);
-        const V4 hi = __builtin_convertvector(p, V4);
-        V4 lo;
-        if constexpr (kSplit) {
-          psum += (p[0] + p[1]) + (p[2] + p[3]);
-          lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
-          if constexpr (kSplit) pl[mt][pb / 2][4 * (pb % 2) + e] = lo[e];
+          for (int pb = 0; pb < 4; ++pb) s[mt][pb] -= d;
+          negm[mt] = m_run[mt] == kNegSentinel ? 0.f : -m_run[mt];
         }
       }
-      if constexpr (!kSplit) psum = sum8(ph[mt][1], sum8(ph[mt][0], 0.f));
-      l_run[mt] += psum;
-    }
-    // O^T += V^T P^T: A row d = 16b + lm, chunk 4 s2 + kk (slots as P's),
-    // in 8 fenced d blocks b: block b's 6 MT MFMAs (two steps, the three
-    // split products, into a fresh accumulator), block b + 1's V operand
-    // reads and column exponents, block b - 1's fold into O with its
-    // exponents undone (this lane's O^T rows are d = 16 b + 4 kk + e), and
-    // the rest of the next tile's pieces.
-    {
-      V8 va[2][2], val[2][2];
-      i32x4 cx[3];
-      auto vread = [&](int b) {
+    };
+    // P^T operands of PV step s2: slots j < 4 are t = 32 s2 + 4 kk + j, slots
+    // j >= 4 are t = 32 s2 + 16 + 4 kk + j - 4 (blocks 2 s2 and 2 s2 + 1),
+    // as f16 hi + lo of P (< 2^8).
+    typedef V8 POps[MT][2];
+    // Each exponential and split is pinned where it is written by an empty
+    // volatile asm (otherwise they are sunk past the mask's branch to the PV
+    // MFMAs that use them).
+    auto exp_el = [&](Scores& s, int i) {
+      const int pb = i / (4 * MT), mt = (i / 4) % MT, e = i % 4;
+      s[mt][pb][e] = __builtin_amdgcn_exp2f(s[mt][pb][e]);
+      asm volatile("" : "+v"(s[mt][pb][e]));
+    };
+    // Group g = MT pb + mt of exponentials (done) into the P operands and the
+    // column's sum.
+    auto split_grp = [&](const Scores& s, int g, POps& ph, POps& pl, float (&psum)[MT]) {
+      const int pb = g / MT, mt = g % MT;
+      const f32x4 p = s[mt][pb];
+      V4 hi = __builtin_convertvector(p, V4);
+      V4 lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
+      psum[mt] += (p[0] + p[1]) + (p[2] + p[3]);
+      asm volatile("" : "+v"(hi), "+v"(lo), "+v"(psum[mt]));
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const int off = vt_off(16 * b + lm, 4 * s2 + kk);
-          va[b & 1][s2] = *reinterpret_cast<const V8*>(vt + off);
-          val[b & 1][s2] = *reinterpret_cast<const V8*>(vt + kPlaneBytes + off);
-        }
-        cx[b % 3] = *reinterpret_cast<const i32x4*>(kt + kVScaleOffset + 4 * (16 * b + 4 * kk));
+      for (int e = 0; e < 4; ++e) {
+        ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
+        pl[mt][pb / 2][4 * (pb % 2) + e] = lo[e];
+      }
+    };
+    // O^T += V^T P^T from stage st in 8 fenced d blocks b: block b's 6 MT
+    // MFMAs (two steps, the three split products, into a fresh accumulator;
+    // the V operands of step h = 2 b + s2 read two steps ahead), block b +
+    // 1's V factors, block b - 1's fold into O with its factors (this lane's
+    // O^T rows are d = 16 b + 4 kk + e), and between(b).
+    auto pv_tile = [&](int st, const POps& ph, const POps& pl, auto between) {
+      V8 va[3], val[3];
+      f32x4 cf[3];
+      auto vread = [&](int h) {
+        const LdsPtr p = vb[st][h & 1] + 2048 * (h >> 1);
+        va[h % 3] = *reinterpret_cast<const __attribute__((address_space(3))) V8*>(p);
+        val[h % 3] = *reinterpret_cast<const __attribute__((address_space(3))) V8*>(p + kPlaneBytes);
+      };
+      auto cread = [&](int b) {
+        cf[b % 3] = *reinterpret_cast<const __attribute__((address_space(3))) f32x4*>(vfb[st] + 64 * b);
       };
       f32x4 pend[MT];
       auto fold = [&](int b) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[mt][b][e] += ldexpf(pend[mt][e], -cx[b % 3][e]);
+          for (int e = 0; e < 4; ++e) o[mt][b][e] = __builtin_fmaf(pend[mt][e], cf[b % 3][e], o[mt][b][e]);
       };
       vread(0);
+      vread(1);
+      cread(0);
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
-        if (b + 1 < 8) vread(b + 1);
         f32x4 acc[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int h = 2 * b + s2;
+          if (h + 2 < 16) vread(h + 2);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            acc[mt] = Op<MODE>::mfma(va[b & 1][s2], ph[mt][s2], acc[mt]);
-            acc[mt] = Op<MODE>::mfma(val[b & 1][s2], ph[mt][s2], acc[mt]);
-            acc[mt] = Op<MODE>::mfma(va[b & 1][s2], pl[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(va[h % 3], ph[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(val[h % 3], ph[mt][s2], acc[mt]);
+            acc[mt] = Op<MODE>::mfma(va[h % 3], pl[mt][s2], acc[mt]);
           }
+        }
+        if (b + 1 < 8) cread(b + 1);
         if (b > 0) fold(b - 1);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) pend[mt] = acc[mt];
-#pragma unroll
-        for (int i = LQK + b * (LPW - LQK) / 8; i < LQK + (b + 1) * (LPW - LQK) / 8; ++i) issue_piece(j + NS - 1, nxt, i);
+        between(b);
         __builtin_amdgcn_sched_barrier(0);
       }
       fold(7);
+    };
+
+    // Tile 0: scores, mask, scaling and maximum on their own.
+    Scores sA, sB;
+    wait_vmcnt<0>();
+    __syncthreads();
+    {
+      qk_tile(0, sA, [](int) {});
+      mask(0, sA);
+      float mx[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) mx[mt] = -INFINITY;
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) {
+        const f32x4 kf = read_kf(0, pb);
+#pragma unroll
+        for (int u = 0; u < 4 * MT; u += 2) scale_pair(sA, kf, 4 * MT * pb + u, mx);
+      }
+      adjust(mx, sA);
+    }
+    // One iteration jj of parity P (tile jj in stage P, tile jj + 1's K half
+    // in stage 1 - P): scores sc of tile jj in (scaled, adjusted), scores sn
+    // of tile jj + 1 out (scaled, adjusted).
+    auto iter = [&](int jj, Scores& sc, Scores& sn, auto par_c) {
+      constexpr int P = decltype(par_c)::value;
+      wait_vmcnt<0>();  // tile jj's V half and tile jj + 1's K half
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      POps ph, pl;
+      float psum[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) psum[mt] = 0.f;
+      // Phase A: tile jj + 1's QK chunks; chunk c takes MT of tile jj's
+      // exponentials and splits the groups whose exponentials an earlier
+      // chunk finished; tile jj + 1's V half is copied in.
+      const HalfBase vh = half_base(jj + 1, 1 - P, 1);
+      qk_tile(1 - P, sn, [&](int c) {
+#pragma unroll
+        for (int u = 0; u < MT; ++u) exp_el(sc, MT * c + u);
+#pragma unroll
+        for (int g = 0; g < 4 * MT; ++g)
+          if ((4 * g + 3) / MT + 1 == c) split_grp(sc, g, ph, pl, psum);
+        if (c & 1) copy_part(vh, 1, c >> 1);
+        if (c == 0) copy_part(vh, 1, 8);
+      });
+#pragma unroll
+      for (int g = 0; g < 4 * MT; ++g)
+        if ((4 * g + 3) / MT + 1 >= 16) split_grp(sc, g, ph, pl, psum);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) l_run[mt] += psum[mt];
+      mask(jj + 1, sn);
+      // Phase B: tile jj's PV blocks; block b scales 2 MT of tile jj + 1's
+      // scores into their maximum (K factors read a block ahead); tile jj +
+      // 2's K half is copied in.
+      float mx[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) mx[mt] = -INFINITY;
+      f32x4 kf[4];
+      kf[0] = read_kf(1 - P, 0);
+      const HalfBase kh = half_base(jj + 2, P, 0);
+      pv_tile(P, ph, pl, [&](int b) {
+        if ((b & 1) && b + 1 < 8) kf[(b + 1) / 2] = read_kf(1 - P, (b + 1) / 2);
+#pragma unroll
+        for (int u = 0; u < 2 * MT; u += 2) scale_pair(sn, kf[b / 2], 2 * MT * b + u, mx);
+        copy_part(kh, 0, b);
+        if (b == 7) copy_part(kh, 0, 8);
+      });
+      adjust(mx, sn);
+    };
+    // The last tile: its P and PV MFMAs only.
+    auto last = [&](Scores& sc, auto par_c) {
+      constexpr int P = decltype(par_c)::value;
+      wait_vmcnt<0>();
+      __syncthreads();
+      POps ph, pl;
+      float psum[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) psum[mt] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16 * MT; ++i) exp_el(sc, i);
+#pragma unroll
+      for (int g = 0; g < 4 * MT; ++g) split_grp(sc, g, ph, pl, psum);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) l_run[mt] += psum[mt];
+      pv_tile(P, ph, pl, [](int) {});
+    };
+    int j = 0;
+    for (; j + 2 < n; j += 2) {
+      iter(j, sA, sB, std::integral_constant<int, 0>{});
+      iter(j + 1, sB, sA, std::integral_constant<int, 1>{});
+    }
+    if (j + 1 < n) {
+      iter(j, sA, sB, std::integral_constant<int, 0>{});
+      last(sB, std::integral_constant<int, 1>{});
+    } else {
+      last(sA, std::integral_constant<int, 0>{});
     }
   }
-  // The clamped prefetches past the last tile may still be landing in LDS:
-  // retire them before the ring is reused or the workgroup ends.
+  // Every copy has landed (the last tile's step issues none); retire them
+  // before the workgroup ends.
   wait_vmcnt<0>();
 
   // Column sums: each lane holds a quarter of its column's positions.
@@ -606,43 +738,6 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   for (int mt = 0; mt < MT; ++mt) {
     l_run[mt] += __shfl_xor(l_run[mt], 16, 64);
     l_run[mt] += __shfl_xor(l_run[mt], 32, 64);
-  }
-
-  if constexpr (G > 1) {
-    // Groups 1.. hand (O, max, sum) to group 0 through the ring: item i of
-    // wave w's lane l at float (w * kX + i) * 64 + l (conflict-free).
-    float* xch = reinterpret_cast<float*>(&lds[0][0][0]);
-    __syncthreads();
-    if (grp > 0) {
-      float* mine = xch + (size_t)((grp - 1) * W + wv) * kX * 64 + lane;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mine[((mt * 8 + b) * 4 + e) * 64] = o[mt][b][e];
-        mine[(MT * 32 + 2 * mt) * 64] = m_run[mt];
-        mine[(MT * 32 + 2 * mt + 1) * 64] = l_run[mt];
-      }
-    }
-    __syncthreads();
-    if (grp > 0) return;
-#pragma unroll
-    for (int g2 = 1; g2 < G; ++g2) {
-      const float* theirs = xch + (size_t)((g2 - 1) * W + wv) * kX * 64 + lane;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float m2 = theirs[(MT * 32 + 2 * mt) * 64], l2 = theirs[(MT * 32 + 2 * mt + 1) * 64];
-        const float mn = fmaxf(m_run[mt], m2);
-        const float a1 = __builtin_amdgcn_exp2f(m_run[mt] - mn), a2 = __builtin_amdgcn_exp2f(m2 - mn);
-        m_run[mt] = mn;
-        l_run[mt] = l_run[mt] * a1 + l2 * a2;
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[mt][b][e] = o[mt][b][e] * a1 + theirs[((mt * 8 + b) * 4 + e) * 64] * a2;
-      }
-    }
   }
 
   if (kv_splits == 1) {

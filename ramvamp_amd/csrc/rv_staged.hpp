@@ -51,20 +51,25 @@ constexpr int kPlanes = Op<MODE>::kSplit ? 2 : 1;
 // scaling with powers of two: each K row t by its exponent e_t, each V
 // column d of a tile by its exponent c_d (so a tile's exponents depend on all
 // of its rows, and only the stage kernel, converting whole tiles from the
-// cache, writes split-mode tiles). The tile ends with a 4 KiB region (whole
-// 1 KiB pieces, so every wave copies the same number of pieces per tile):
-// int32 e_t at byte kScaleOffset + 4 t, int32 c_d at byte kVScaleOffset + 4 d.
+// cache, writes split-mode tiles). The tile ends with a 4 KiB region of
+// 1 KiB pieces holding the factors that undo the scaling, as floats: 2^-e_t
+// at byte kScaleOffset + 4 t (the first piece), 2^-c_d at byte
+// kVScaleOffset + 4 d (the second), two unused, so the K half of a tile (its
+// planes and factors) and the V half can be copied into LDS separately.
 constexpr int kScaleBytes = 4096;
 constexpr int kScaleOffset = 4 * kPlaneBytes;
-constexpr int kVScaleOffset = kScaleOffset + 4 * kBT;
+constexpr int kVScaleOffset = kScaleOffset + 1024;
 template <int MODE>
 constexpr int kTileBytes = 2 * kPlanes<MODE> * kPlaneBytes + (Op<MODE>::kSplit ? kScaleBytes : 0);
 
-// The power-of-two exponent e that puts amax * 2^e in [2^13, 2^14), or 0
-// for a zero or non-finite amax (such a row is staged as it is).
-__device__ __forceinline__ int scale_exponent(float amax) {
+// The power-of-two exponent e that puts amax * 2^e in [2^13, 2^14), at most
+// cap, or 0 for a zero or non-finite amax (such a row is staged as it is).
+// The default cap keeps 2^-e a float (2^-149 is its smallest subnormal); a
+// capped vector, all of whose elements are below 2^-135, is scaled to
+// magnitudes in [1, 2^14), inside f16's normal range.
+__device__ __forceinline__ int scale_exponent(float amax, int cap = 149) {
   if (!(amax > 0.f) || !__builtin_isfinite(amax)) return 0;
-  return 14 - __builtin_amdgcn_frexp_expf(amax);
+  return min(14 - __builtin_amdgcn_frexp_expf(amax), cap);
 }
 
 // hi = round(x); lo = round(x - hi), into element e of two vectors.
