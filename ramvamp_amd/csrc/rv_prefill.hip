@@ -205,46 +205,66 @@ __device__ __forceinline__ Unit unit_of(int n_units, int n_rb, int kv_splits) {
   return u;
 }
 
-// This lane's 32 elements of one query vector, d = 8kk + 32s + e, from qp
-// (already offset by 8kk). With qn_w, qp is the raw projection and the q
-// prologue runs here, as the row prologue would: RMSNorm with an f64 sum of
-// squares over the column's four lanes (lanes 16 and 32 apart), then
-// `x * inv * w` and the rotation of the pairs (i, i + 64) - both in this
-// lane, s and s + 2 - in the reference's separately rounded f32 operations,
-// with the row's (cos, sin) from tab_row (64 cos, then 64 sin).
-__device__ __forceinline__ void load_q(const float* qp, int kk, const float* __restrict__ qn_w, float qn_eps,
-                                       const float* __restrict__ tab_row, float (&x)[4][8]) {
-#pragma clang fp contract(off)
-  // Rows, weights and table 16-byte aligned (the common case): 16-byte loads.
-  const bool vec = aligned16(qp, qn_w, tab_row);
-#pragma unroll
-  for (int s = 0; s < 4; ++s) ld8(qp + 32 * s, vec, x[s]);
-  if (!qn_w) return;
+// This lane's 32 elements of one query vector, d = 8 kk + 32 s + e, from qp
+// (already offset by 8 kk), and with qn_w the q prologue's operands: the
+// loads only (issue), so the caller can queue other loads behind them before
+// anything waits; then (finish) the q prologue, as the row prologue would:
+// RMSNorm with an f64 sum of squares over the column's four lanes (lanes 16
+// and 32 apart), then `x * inv * w` and the rotation of the pairs (i, i +
+// 64) - both in this lane, s and s + 2 - in the reference's separately
+// rounded f32 operations, with the row's (cos, sin) from tab_row (64 cos,
+// then 64 sin).
+struct Q16Loads {
+  float x[4][8];
   float w0[2][8], w1[2][8], cs[2][8], sn[2][8];
+  __device__ __forceinline__ void issue(const float* qp, int kk, const float* __restrict__ qn_w,
+                                        const float* __restrict__ tab_row) {
+    // Rows, weights and table 16-byte aligned (the common case): 16-byte loads.
+    const bool vec = aligned16(qp, qn_w, tab_row);
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int i = 8 * kk + 32 * s;
-    ld8(qn_w + i, vec, w0[s]);
-    ld8(qn_w + i + 64, vec, w1[s]);
-    ld8(tab_row + i, vec, cs[s]);
-    ld8(tab_row + 64 + i, vec, sn[s]);
-  }
-  double ss = 0.0;
+    for (int s = 0; s < 4; ++s) ld8(qp + 32 * s, vec, x[s]);
+    if (!qn_w) return;
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += (double)x[s][e] * (double)x[s][e];
-  ss = swap_sum_f64<32>(swap_sum_f64<16>(ss));
-  const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)qn_eps));
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float a0 = x[s][e] * inv * w0[s][e], a1 = x[s + 2][e] * inv * w1[s][e];
-      x[s][e] = a0 * cs[s][e] - a1 * sn[s][e];
-      x[s + 2][e] = a0 * sn[s][e] + a1 * cs[s][e];
+    for (int s = 0; s < 2; ++s) {
+      const int i = 8 * kk + 32 * s;
+      ld8(qn_w + i, vec, w0[s]);
+      ld8(qn_w + i + 64, vec, w1[s]);
+      ld8(tab_row + i, vec, cs[s]);
+      ld8(tab_row + 64 + i, vec, sn[s]);
     }
-}
+  }
+  // The operands from LDS instead: the weights at w (128 floats) and the
+  // row's (cos, sin) at t.
+  __device__ __forceinline__ void operands_from(const float* w, const float* t, int kk) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int i = 8 * kk + 32 * s;
+      ld8(w + i, true, w0[s]);
+      ld8(w + i + 64, true, w1[s]);
+      ld8(t + i, true, cs[s]);
+      ld8(t + 64 + i, true, sn[s]);
+    }
+  }
+  __device__ __forceinline__ void finish(bool norm, float qn_eps) {
+#pragma clang fp contract(off)
+    if (!norm) return;
+    double ss = 0.0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (double)x[s][e] * (double)x[s][e];
+    ss = swap_sum_f64<32>(swap_sum_f64<16>(ss));
+    const float inv = (float)(1.0 / sqrt(ss / (double)kD + (double)qn_eps));
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a0 = x[s][e] * inv * w0[s][e], a1 = x[s + 2][e] * inv * w1[s][e];
+        x[s][e] = a0 * cs[s][e] - a1 * sn[s][e];
+        x[s + 2][e] = a0 * sn[s][e] + a1 * cs[s][e];
+      }
+  }
+};
 
 // NaN-propagating max of three (v_maximum3_f32: unlike fmaxf it needs no
 // operand canonicalisation).
@@ -281,6 +301,21 @@ __device__ __forceinline__ float sum2(bf16x8 v, int i, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(b2{v[i], v[i + 1]}, one, acc, false);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// p - h[i] for the f16 pair h, exactly (p - h is representable when h is p
+// rounded to f16): one v_fma_mix_f32 reading the f16 half in place, where
+// converting h to f32 and subtracting takes two instructions.
+template <int I>
+__device__ __forceinline__ float residual_f16(f16x2 h, float p) {
+  float r;
+  if constexpr (I == 0)
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(p));
+  else
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(p));
+  return r;
+}
+
 // prefill_kernel (the split mode): one group of W = 4 waves; column m of the
 // workgroup's M = 16 W MT is head m / qr, row m % qr of the block (qr = M /
 // group), wave w owning columns [16 MT w, 16 MT (w + 1)). A tile is 68 KiB
@@ -291,9 +326,9 @@ __device__ __forceinline__ float sum2(bf16x8 v, int i, float acc) {
 // takes their maximum between tile j's PV MFMAs (phase B), each chunk fenced
 // so the compiler keeps that issue order; the shadow of the MFMAs holds the
 // softmax work, which otherwise ran between the MFMA phases on the SIMD's
-// single wave. Tile j + 1's V half is copied in during phase A and tile j +
-// 2's K half during phase B, into the halves of the ring the previous
-// iteration finished with.
+// single wave. Tile j + 2's K half and tile j + 1's V half are copied in
+// early in phase A, into the halves of the ring the previous iteration
+// finished with.
 template <int MODE, int G, int W, int MT, int NS>
 __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __restrict__ q,
                                                              const char* __restrict__ stage, int n_stage_tiles,
@@ -306,7 +341,9 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   typedef typename Op<MODE>::V8 V8;
   typedef typename Op<MODE>::V4 V4;
   constexpr bool kSplit = Op<MODE>::kSplit;
-  static_assert(kSplit && G == 1 && NS == 2 && W == 4, "the split mode: one group of 4 waves, two stages");
+  static_assert(kSplit && G == 1 && NS == 2 && (W == 4 || W == 8), "the split mode: one group of 4 or 8 waves, two stages");
+  // (8 waves of 16 columns measured equal to 4 waves of 32 at config 4.)
+  constexpr int NPL = 32 / W;  // plane pieces per wave per half tile
   constexpr int M = 16 * W * MT;       // query vectors per workgroup
   constexpr int TB = kTileBytes<MODE>;  // bytes per staged tile
   static_assert(TB == 68 * 1024 && kVScaleOffset == kScaleOffset + 1024, "68 pieces of 1 KiB");
@@ -334,9 +371,9 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 
   // Half h of tile t (0: the K planes, pieces 0-31, and the K factors,
   // piece 64; 1: the V planes, 32-63, and the V factors, 65) into stage s,
-  // in 9 parts per wave: part i < 8 is piece 32 h + w + 4 i, part 8 piece
-  // 64 + h + 2 (w & 1) (waves 0 and 2 both copy the factors, 1 and 3 an
-  // unused piece: no branch). Lane l's 16 bytes land at piece + 16 l. A
+  // in NPL + 1 parts per wave (NPL = 32 / W): part i < NPL is piece 32 h + w
+  // + W i, part NPL piece 64 + h + 2 (w & 1) (even waves all copy the
+  // factors, odd waves an unused piece: no branch). Lane l's 16 bytes land at piece + 16 l. A
   // half's global and LDS bases are wave-uniform, set once per half and
   // hidden from the compiler (so it computes each part's address where the
   // part is issued, instead of holding every part's address in scalar
@@ -356,23 +393,65 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     return b;
   };
   auto copy_part = [&](const HalfBase& b, int h, int i) {
-    const int off = i < 8 ? 4096 * i : 1024 * (64 + h + 2 * (wv & 1) - 32 * h - wv);
+    const int off = i < NPL ? 1024 * W * i : 1024 * (64 + h + 2 * (wv & 1) - 32 * h - wv);
     lds_dma16s(b.g + off, voff, b.l + off);
   };
-  // Tile 0 whole and tile 1's K half, ahead of the query loads.
-  if (n > 0) {
-    const HalfBase k0 = half_base(0, 0, 0), v0 = half_base(0, 0, 1), k1 = half_base(1, 1, 0);
-#pragma unroll
-    for (int i = 0; i < 9; ++i) copy_part(k0, 0, i);
-#pragma unroll
-    for (int i = 0; i < 9; ++i) copy_part(v0, 1, i);
-#pragma unroll
-    for (int i = 0; i < 9; ++i) copy_part(k1, 0, i);
-  }
-
   // This lane's query vector in column block mt: column m = 16*(wv*MT + mt) + lm.
   int my_row[MT], my_head[MT], my_limit[MT];
   bool col_ok[MT];
+  Q16Loads qld[MT];
+  // With the q prologue, its operands (the block's (cos, sin) rows, then the
+  // norm weights) are copied once per workgroup into LDS (stage 1's V half,
+  // unused until the loop) by a few coalesced copies, instead of every lane
+  // loading its own: those scattered per-lane loads took ~4 us to issue at
+  // 32 columns per wave. Unaligned operands or blocks of more than 48 rows
+  // load per lane.
+  const bool pro_lds = qn_w != nullptr && aligned16(qn_w, qn_tab) && qr <= 48;
+  float* const pro = reinterpret_cast<float*>(&lds[1][2 * kPlaneBytes]);
+  const int pro_rows = (qr + 1) / 2 * 2;  // table rows held (the weights follow)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * (wv * MT + mt) + lm;
+    my_head[mt] = m / qr;
+    my_row[mt] = r0 + m % qr;
+    col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
+    my_limit[mt] = col_ok[mt] ? start + my_row[mt] + 1 : 0;
+    const int q_row = col_ok[mt] ? my_row[mt] : 0;
+    qld[mt].issue(q + (size_t)q_row * q_stride + (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk,
+                  kk, pro_lds ? nullptr : qn_w, pro_lds || !qn_tab ? nullptr : qn_tab + (size_t)q_row * kD);
+  }
+  if (pro_lds) {
+    // Copy i: table rows 2 i and 2 i + 1 of the block (512 bytes each;
+    // rows past the chunk read its last), the weights after them (wave 0).
+    for (int i = wv; i < pro_rows / 2; i += W) {
+      const int row = min(r0 + min(2 * i + (lane >> 5), qr - 1), rows - 1);
+      lds_dma16(qn_tab + (size_t)row * kD + 4 * (lane & 31), lds_offset(pro + 256 * i));
+    }
+    if (wv == 0) lds_dma16(qn_w + 4 * (lane & 31), lds_offset(pro + 128 * pro_rows));
+  }
+  // Tile 0 whole and tile 1's K half, queued behind the query loads (which
+  // return first, so the q prologue runs while the tiles land).
+  if (n > 0) {
+    const HalfBase k0 = half_base(0, 0, 0), v0 = half_base(0, 0, 1), k1 = half_base(1, 1, 0);
+#pragma unroll
+    for (int i = 0; i <= NPL; ++i) copy_part(k0, 0, i);
+#pragma unroll
+    for (int i = 0; i <= NPL; ++i) copy_part(v0, 1, i);
+#pragma unroll
+    for (int i = 0; i <= NPL; ++i) copy_part(k1, 0, i);
+  }
+  if (pro_lds) {
+    // The operand copies are done once only the tile copies may remain.
+    if (n > 0)
+      wait_vmcnt<3 * (NPL + 1)>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      qld[mt].operands_from(pro + 128 * pro_rows, pro + 128 * (my_row[mt] - r0), kk);
+  }
+
   V8 qh[MT][4], ql[MT][4];
   // log2(e) * scale * 2^-qe: undoes the vector's exponent qe and scales its
   // fp32 scores.
@@ -384,19 +463,11 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   float negm[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * (wv * MT + mt) + lm;
-    my_head[mt] = m / qr;
-    my_row[mt] = r0 + m % qr;
-    col_ok[mt] = my_row[mt] < rows && my_head[mt] < group;
-    my_limit[mt] = col_ok[mt] ? start + my_row[mt] + 1 : 0;
-    const float* qp = q + (size_t)(col_ok[mt] ? my_row[mt] : 0) * q_stride +
-                      (size_t)(kvh * group + (col_ok[mt] ? my_head[mt] : 0)) * kD + 8 * kk;
-    // q rows may be only 4-byte aligned: scalar loads (once per workgroup).
-    // The scores are scaled by log2(e) * scale in fp32 (rounding the scaled q
-    // would cost low bits of the lo half).
+    // The scores are scaled by log2(e) * scale in fp32 (rounding the scaled
+    // q would cost low bits of the lo half).
     const float qs = col_ok[mt] ? 1.f : 0.f;
-    float x[4][8];
-    load_q(qp, kk, qn_w, qn_eps, qn_tab ? qn_tab + (size_t)(col_ok[mt] ? my_row[mt] : 0) * kD : nullptr, x);
+    qld[mt].finish(qn_w != nullptr, qn_eps);
+    const float(&x)[4][8] = qld[mt].x;
     // The vector scaled by its exponent (from its max over the column's four
     // lanes), undone on the fp32 scores; capped at 100 so qscale * 2^-qe
     // stays a normal float (a vector below 2^-86 throughout keeps its
@@ -566,19 +637,32 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       s[mt][pb][e] = __builtin_amdgcn_exp2f(s[mt][pb][e]);
       asm volatile("" : "+v"(s[mt][pb][e]));
     };
-    // Group g = MT pb + mt of exponentials (done) into the P operands and the
-    // column's sum.
-    auto split_grp = [&](const Scores& s, int g, POps& ph, POps& pl, float (&psum)[MT]) {
+    // Group g = MT pb + mt of exponentials (done) into the P operands.
+    auto split_grp = [&](const Scores& s, int g, POps& ph, POps& pl) {
       const int pb = g / MT, mt = g % MT;
       const f32x4 p = s[mt][pb];
       V4 hi = __builtin_convertvector(p, V4);
-      V4 lo = __builtin_convertvector(p - __builtin_convertvector(hi, f32x4), V4);
-      psum[mt] += (p[0] + p[1]) + (p[2] + p[3]);
-      asm volatile("" : "+v"(hi), "+v"(lo), "+v"(psum[mt]));
+      const f16x2 h01 = {hi[0], hi[1]}, h23 = {hi[2], hi[3]};
+      const f32x4 r = {residual_f16<0>(h01, p[0]), residual_f16<1>(h01, p[1]), residual_f16<0>(h23, p[2]),
+                       residual_f16<1>(h23, p[3])};
+      V4 lo = __builtin_convertvector(r, V4);
+      asm volatile("" : "+v"(hi), "+v"(lo));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         ph[mt][pb / 2][4 * (pb % 2) + e] = hi[e];
         pl[mt][pb / 2][4 * (pb % 2) + e] = lo[e];
+      }
+    };
+    // Share b (of 8) of the column sums of P as the PV products use it (hi
+    // + lo), into l_run: term k of column block mt is the pair k % 4 of
+    // plane (k / 4) % 2 (hi, lo) of step k / 8, one v_dot2 each. It runs
+    // among the PV MFMAs, whose half of the loop has VALU to spare.
+    auto sum_share = [&](const POps& ph, const POps& pl, int b) {
+#pragma unroll
+      for (int u = 0; u < 2 * MT; ++u) {
+        const int idx = 2 * MT * b + u, mt = idx / 16, k = idx % 16;
+        const V8& v = ((k >> 2) & 1) ? pl[mt][k >> 3] : ph[mt][k >> 3];
+        l_run[mt] = sum2(v, 2 * (k & 3), l_run[mt]);
       }
     };
     // O^T += V^T P^T from stage st in 8 fenced d blocks b: block b's 6 MT
@@ -660,43 +744,38 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
       POps ph, pl;
-      float psum[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) psum[mt] = 0.f;
       // Phase A: tile jj + 1's QK chunks; chunk c takes MT of tile jj's
       // exponentials and splits the groups whose exponentials an earlier
-      // chunk finished; tile jj + 1's V half is copied in.
-      const HalfBase vh = half_base(jj + 1, 1 - P, 1);
+      // chunk finished. Tile jj + 2's K half (needed first, at the next
+      // iteration's start) and then tile jj + 1's V half are copied in over
+      // the first chunks, so every copy has most of the iteration to land
+      // before the next iteration's wait.
+      const HalfBase kh = half_base(jj + 2, P, 0), vh = half_base(jj + 1, 1 - P, 1);
       qk_tile(1 - P, sn, [&](int c) {
 #pragma unroll
         for (int u = 0; u < MT; ++u) exp_el(sc, MT * c + u);
 #pragma unroll
         for (int g = 0; g < 4 * MT; ++g)
-          if ((4 * g + 3) / MT + 1 == c) split_grp(sc, g, ph, pl, psum);
-        if (c & 1) copy_part(vh, 1, c >> 1);
-        if (c == 0) copy_part(vh, 1, 8);
+          if ((4 * g + 3) / MT + 1 == c) split_grp(sc, g, ph, pl);
+        if (c <= NPL) copy_part(kh, 0, c);
+        if (c >= 1 && c <= NPL + 1) copy_part(vh, 1, c - 1);
       });
 #pragma unroll
       for (int g = 0; g < 4 * MT; ++g)
-        if ((4 * g + 3) / MT + 1 >= 16) split_grp(sc, g, ph, pl, psum);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) l_run[mt] += psum[mt];
+        if ((4 * g + 3) / MT + 1 >= 16) split_grp(sc, g, ph, pl);
       mask(jj + 1, sn);
       // Phase B: tile jj's PV blocks; block b scales 2 MT of tile jj + 1's
-      // scores into their maximum (K factors read a block ahead); tile jj +
-      // 2's K half is copied in.
+      // scores into their maximum (K factors read a block ahead).
       float mx[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) mx[mt] = -INFINITY;
       f32x4 kf[4];
       kf[0] = read_kf(1 - P, 0);
-      const HalfBase kh = half_base(jj + 2, P, 0);
       pv_tile(P, ph, pl, [&](int b) {
+        sum_share(ph, pl, b);
         if ((b & 1) && b + 1 < 8) kf[(b + 1) / 2] = read_kf(1 - P, (b + 1) / 2);
 #pragma unroll
         for (int u = 0; u < 2 * MT; u += 2) scale_pair(sn, kf[b / 2], 2 * MT * b + u, mx);
-        copy_part(kh, 0, b);
-        if (b == 7) copy_part(kh, 0, 8);
       });
       adjust(mx, sn);
     };
@@ -706,16 +785,11 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       wait_vmcnt<0>();
       __syncthreads();
       POps ph, pl;
-      float psum[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) psum[mt] = 0.f;
 #pragma unroll
       for (int i = 0; i < 16 * MT; ++i) exp_el(sc, i);
 #pragma unroll
-      for (int g = 0; g < 4 * MT; ++g) split_grp(sc, g, ph, pl, psum);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) l_run[mt] += psum[mt];
-      pv_tile(P, ph, pl, [](int) {});
+      for (int g = 0; g < 4 * MT; ++g) split_grp(sc, g, ph, pl);
+      pv_tile(P, ph, pl, [&](int b) { sum_share(ph, pl, b); });
     };
     int j = 0;
     for (; j + 2 < n; j += 2) {
