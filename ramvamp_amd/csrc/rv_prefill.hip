@@ -712,6 +712,18 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) pend[mt] = acc[mt];
         between(b);
+        // Issue order inside the block: its LDS reads, two MFMAs, then two
+        // VALU instructions after each further MFMA (left to itself the
+        // scheduler put block b - 1's fold right behind the block's first
+        // MFMA, waiting on block b - 1's last; this order measured ~10 %
+        // faster for the half).
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+#pragma unroll
+        for (int i = 0; i < 6 * MT - 2; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       fold(7);
