@@ -729,9 +729,11 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       fold(7);
     };
 
-    // Tile 0: scores, mask, scaling and maximum on their own.
+    // Tile 0: scores, mask, scaling and maximum on their own, once its K
+    // half has landed (its V half and tile 1's K half, issued after it, may
+    // still be in flight: the first iteration waits for them).
     Scores sA, sB;
-    wait_vmcnt<0>();
+    wait_vmcnt<2 * (NPL + 1)>();
     __syncthreads();
     {
       qk_tile(0, sA, [](int) {});
