@@ -406,9 +406,12 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   // loading its own: those scattered per-lane loads took ~4 us to issue at
   // 32 columns per wave. Unaligned operands or blocks of more than 48 rows
   // load per lane.
-  const bool pro_lds = qn_w != nullptr && aligned16(qn_w, qn_tab) && qr <= 48;
+  // Row r of the table sits at float 260 r (1040 bytes: each row takes a
+  // copy of its own, and the 16-byte skew puts the 16 rows one read
+  // gathers on distinct banks), the weights after the rows.
+  const bool pro_lds = qn_w != nullptr && aligned16(qn_w, qn_tab) && qr <= 30;
   float* const pro = reinterpret_cast<float*>(&lds[1][2 * kPlaneBytes]);
-  const int pro_rows = (qr + 1) / 2 * 2;  // table rows held (the weights follow)
+  constexpr int kProRow = 260;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * (wv * MT + mt) + lm;
@@ -421,13 +424,12 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
                   kk, pro_lds ? nullptr : qn_w, pro_lds || !qn_tab ? nullptr : qn_tab + (size_t)q_row * kD);
   }
   if (pro_lds) {
-    // Copy i: table rows 2 i and 2 i + 1 of the block (512 bytes each;
-    // rows past the chunk read its last), the weights after them (wave 0).
-    for (int i = wv; i < pro_rows / 2; i += W) {
-      const int row = min(r0 + min(2 * i + (lane >> 5), qr - 1), rows - 1);
-      lds_dma16(qn_tab + (size_t)row * kD + 4 * (lane & 31), lds_offset(pro + 256 * i));
-    }
-    if (wv == 0) lds_dma16(qn_w + 4 * (lane & 31), lds_offset(pro + 128 * pro_rows));
+    // Copy i: table row i of the block (512 bytes, twice: the second half
+    // lands in the row's padding; rows past the chunk read its last), the
+    // weights after the rows (wave 0).
+    for (int i = wv; i < qr; i += W)
+      lds_dma16(qn_tab + (size_t)min(r0 + i, rows - 1) * kD + 4 * (lane & 31), lds_offset(pro + kProRow * i));
+    if (wv == 0) lds_dma16(qn_w + 4 * (lane & 31), lds_offset(pro + kProRow * qr));
   }
   // Tile 0 whole and tile 1's K half, queued behind the query loads (which
   // return first, so the q prologue runs while the tiles land).
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     __syncthreads();
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      qld[mt].operands_from(pro + 128 * pro_rows, pro + 128 * (my_row[mt] - r0), kk);
+      qld[mt].operands_from(pro + kProRow * qr, pro + kProRow * (my_row[mt] - r0), kk);
   }
 
   V8 qh[MT][4], ql[MT][4];
