@@ -431,21 +431,20 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
       lds_dma16(qn_tab + (size_t)min(r0 + i, rows - 1) * kD + 4 * (lane & 31), lds_offset(pro + kProRow * i));
     if (wv == 0) lds_dma16(qn_w + 4 * (lane & 31), lds_offset(pro + kProRow * qr));
   }
-  // Tile 0 whole and tile 1's K half, queued behind the query loads (which
-  // return first, so the q prologue runs while the tiles land).
+  // Tile 0's K half, queued behind the query loads (which return first, so
+  // the q prologue runs while it lands). Tile 0's V half and tile 1's K
+  // half are issued among tile 0's score MFMAs: issued here, their copies
+  // held the wave ~2.5 us (the memory pipeline is full at the start, and a
+  // wave issues in order) before it could start the q prologue.
   if (n > 0) {
-    const HalfBase k0 = half_base(0, 0, 0), v0 = half_base(0, 0, 1), k1 = half_base(1, 1, 0);
+    const HalfBase k0 = half_base(0, 0, 0);
 #pragma unroll
     for (int i = 0; i <= NPL; ++i) copy_part(k0, 0, i);
-#pragma unroll
-    for (int i = 0; i <= NPL; ++i) copy_part(v0, 1, i);
-#pragma unroll
-    for (int i = 0; i <= NPL; ++i) copy_part(k1, 0, i);
   }
   if (pro_lds) {
     // The operand copies are done once only the tile copies may remain.
     if (n > 0)
-      wait_vmcnt<3 * (NPL + 1)>();
+      wait_vmcnt<NPL + 1>();
     else
       wait_vmcnt<0>();
     __syncthreads();
@@ -732,13 +731,17 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
     };
 
     // Tile 0: scores, mask, scaling and maximum on their own, once its K
-    // half has landed (its V half and tile 1's K half, issued after it, may
-    // still be in flight: the first iteration waits for them).
+    // half has landed; its V half and tile 1's K half are copied in among
+    // the score MFMAs (the first iteration waits for them).
     Scores sA, sB;
-    wait_vmcnt<2 * (NPL + 1)>();
+    wait_vmcnt<0>();
     __syncthreads();
     {
-      qk_tile(0, sA, [](int) {});
+      const HalfBase v0 = half_base(0, 0, 1), k1 = half_base(1, 1, 0);
+      qk_tile(0, sA, [&](int c) {
+        if (c <= NPL) copy_part(v0, 1, c);
+        if (c >= 7 && c <= 7 + NPL) copy_part(k1, 0, c - 7);
+      });
       mask(0, sA);
       float mx[MT];
 #pragma unroll
