@@ -180,7 +180,10 @@ __global__ __launch_bounds__(kWG) void prefill_stage_kernel(const T* __restrict_
   }
 }
 
-// Partial layout per (kv head, row block, split): O[128 columns][kD], then
+// Partial layout per (kv head, row block, split): O in 16-byte chunks
+// (128 columns x kD floats), chunk (8 cb + b) * 64 + l holding O^T[16 b + 4
+// (l / 16) .. + 3][16 cb + l % 16] (lane l's four values of d block b for
+// column block cb: the writer's 64 lanes store 1 KiB contiguous), then
 // (max, sum)[128 columns].
 constexpr size_t kPartStride = (size_t)128 * kD + 2 * 128;
 
@@ -852,7 +855,7 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * (wv * MT + mt) + lm;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) *reinterpret_cast<f32x4*>(&mine[(size_t)m * kD + 16 * b + 4 * kk]) = o[mt][b];
+    for (int b = 0; b < 8; ++b) reinterpret_cast<f32x4*>(mine)[((wv * MT + mt) * 8 + b) * 64 + lane] = o[mt][b];
     if (kk == 0) {
       mine[128 * kD + 2 * m] = m_run[mt];
       mine[128 * kD + 2 * m + 1] = l_run[mt];
@@ -1419,34 +1422,43 @@ template <int S>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part, int n_rb, int n_cb,
                                                             int qr, int rows, int group, int q_stride,
                                                             float* __restrict__ out) {
+  // Workgroup (kv head, row block, column block cb of 16): thread t takes
+  // lane l = t % 64's chunks of d blocks t / 64 and t / 64 + 4 (1 KiB
+  // contiguous per wave and split).
   const int cb = blockIdx.x % n_cb, rb = (blockIdx.x / n_cb) % n_rb, kvh = blockIdx.x / (n_cb * n_rb);
-  const int m = 8 * cb + (threadIdx.x >> 5), d = 4 * (threadIdx.x & 31);
+  const int l = threadIdx.x & 63, b0 = threadIdx.x >> 6;
+  const int m = 16 * cb + (l & 15), kk = l >> 4;
   const int head = m / qr, row = rb * qr + m % qr;
   if (head >= group || row >= rows) return;
   const float* base = part + ((size_t)kvh * n_rb + rb) * S * kPartStride;
-  f32x4 o[S];
+  f32x4 o[S][2];
   float2 ml[S];
 #pragma unroll
   for (int sp = 0; sp < S; ++sp) {
-    o[sp] = *reinterpret_cast<const f32x4*>(base + sp * kPartStride + (size_t)m * kD + d);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      o[sp][h] = reinterpret_cast<const f32x4*>(base + sp * kPartStride)[(cb * 8 + b0 + 4 * h) * 64 + l];
     ml[sp] = *reinterpret_cast<const float2*>(base + sp * kPartStride + 128 * kD + 2 * m);
   }
   float M = ml[0].x;
 #pragma unroll
   for (int sp = 1; sp < S; ++sp) M = fmaxf(M, ml[sp].x);
   float L = 0.f;
-  f32x4 O = {0.f, 0.f, 0.f, 0.f};
+  f32x4 O[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int sp = 0; sp < S; ++sp) {
     const float w = __builtin_amdgcn_exp2f(ml[sp].x - M);
     L += ml[sp].y * w;
-    O += o[sp] * w;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) O[h] += o[sp][h] * w;
   }
   // The caller's rows may be only 4-byte aligned: scalar stores.
-  float* op = out + (size_t)row * q_stride + (size_t)(kvh * group + head) * kD + d;
+  float* op = out + (size_t)row * q_stride + (size_t)(kvh * group + head) * kD + 4 * kk;
   const float inv = 1.0f / L;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) op[e] = O[e] * inv;
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) op[16 * (b0 + 4 * h) + e] = O[h][e] * inv;
 }
 
 struct PrefillArgs {
@@ -1708,8 +1720,8 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
     launch_exact(vectors, a, s);
     if (kv_splits > 1) {
       const int qr = vectors / group;
-      const dim3 grid((unsigned)(n_kv * n_rb * vectors / 8));
-      const int n_cb = vectors / 8, q_stride = (int)(n_q_heads * kD);
+      const dim3 grid((unsigned)(n_kv * n_rb * vectors / 16));
+      const int n_cb = vectors / 16, q_stride = (int)(n_q_heads * kD);
 #define RV_MERGE(S)                                                                                               \
   case S:                                                                                                         \
     hipLaunchKernelGGL(prefill_merge_kernel<S>, grid, dim3(256), 0, s, (const float*)part, n_rb, n_cb, qr, (int)rows, \
