@@ -1037,9 +1037,11 @@ int32_t rv_prefill_chunk(rv_kv* kv, size_t layer, const float* q_rows, const flo
     // (The preparation reads q and its norm weight with 16-byte loads.)
     const bool prep = sd.base != nullptr && ((uintptr_t)dq % 16) == 0 && ((uintptr_t)dwq % 16) == 0 &&
                       q_dim % 4 == 0;
+    const int vectors = prep ? rv::prefill_vectors(kv, rows, start, p.group) : 0;
     if (hs.e == hipSuccess)
-      hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, kv->n_kv_heads, p.group) : rows * hd * sizeof(float));
-    rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, p.group, scale) : rv::QPrep{};
+      hs = rv::ensure_qbuf(kv, prep ? rv::qprep_bytes(rows, kv->n_kv_heads, p.group, vectors)
+                                    : rows * hd * sizeof(float));
+    rv::QPrep qp = prep ? rv::qprep_plan((char*)kv->qbuf, rows, p.group, scale, vectors) : rv::QPrep{};
     if (prep && hs.e == hipSuccess) {
       hs = rv::ensure_rope_tab(kv, theta, start + rows);
       qp.rope = kv->rope_tab;

@@ -189,13 +189,18 @@ struct QPrep {
   int qr = 0;          // rows per unit: its columns / group
   int n_rb = 0;        // units per kv head
   float qscale = 0.f;  // log2(e) * softmax scale
+  int vectors = 0;     // columns per unit (64 or 128)
   // The cache's (cos, sin) table by position (ensure_rope_tab), read instead
   // of each wave computing its row's angles in f64.
   const float* rope = nullptr;
 };
-// Bytes of the prepared queries of a chunk of `rows` rows, and their layout.
-size_t qprep_bytes(size_t rows, size_t n_kv_heads, size_t group);
-QPrep qprep_plan(char* base, size_t rows, size_t group, float scale);
+// Bytes of the prepared queries of a chunk of `rows` rows, and their layout,
+// for units of `vectors` columns (prefill_vectors).
+size_t qprep_bytes(size_t rows, size_t n_kv_heads, size_t group, int vectors);
+QPrep qprep_plan(char* base, size_t rows, size_t group, float scale, int vectors);
+// Columns per unit of the F16 / BF16 prefill kernel for a chunk of `rows`
+// rows at `start` (64 or 128; the prepared queries are laid out for it).
+int prefill_vectors(const rv_kv* kv, size_t rows, size_t start, size_t group);
 HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, const float* q, float* q_out,
                               size_t n_q, const float* k, const float* v, size_t rows, const float* q_w,
                               const float* k_w, float eps, const InvFreq& inv, size_t pos0, float* rope_tab,

@@ -1067,19 +1067,27 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   const char* const srcw = stage + ((size_t)kvh * n_stage_tiles + tt_lo) * TB + 1024 * w;
   const uint32_t voff = 16u * (uint32_t)lane;
   auto stage_of = [](int t) { return 2 * (t & 1) + ((t >> 1) & 1); };
+  // A wave's pieces of a tile: NK in the K plane (i < NK), NK in the V plane.
+  constexpr int NK = 16 / W;
   auto copy_piece = [&](int t, int i) {
-    lds_dma16s(srcw + (size_t)min(t, n - 1) * TB + 8192 * i, voff,
+    lds_dma16s(srcw + (size_t)min(t, n - 1) * TB + 1024 * W * i, voff,
                lds_offset(&lds[stage_of(t)][1024 * (w + W * i)]));
   };
   // Tiles 0 and 1 whole, then the K planes of tiles 2 and 3. A split with no
   // tiles (more splits than the unit has tiles) copies nothing.
   if (n > 0) {
 #pragma unroll
-    for (int t = 0; t < G; ++t) copy_piece(t, 0), copy_piece(t, 1);
+    for (int t = 0; t < G; ++t)
 #pragma unroll
-    for (int t = 0; t < G; ++t) copy_piece(t, 2), copy_piece(t, 3);
+      for (int i = 0; i < NK; ++i) copy_piece(t, i);
 #pragma unroll
-    for (int t = G; t < 2 * G; ++t) copy_piece(t, 0), copy_piece(t, 1);
+    for (int t = 0; t < G; ++t)
+#pragma unroll
+      for (int i = NK; i < 2 * NK; ++i) copy_piece(t, i);
+#pragma unroll
+    for (int t = G; t < 2 * G; ++t)
+#pragma unroll
+      for (int i = 0; i < NK; ++i) copy_piece(t, i);
   }
   if (qprep) {
     if (!col_ok) {
@@ -1102,7 +1110,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   float negm = 0.f;  // -m_run, or 0 while the column has seen no position
   const int steps = (n + G - 1) / G;
   {
-    static_assert(W == 8 && G == 2 && NS == 4, "two tiles per step; a wave's K pieces w, w + 8, V pieces w + 16, w + 24");
+    static_assert((W == 8 || W == 4) && G == 2 && NS == 4, "two tiles per step; a wave's K pieces w + W i, i < NK, then its V pieces");
     // Software-pipelined: iteration j exponentiates tile j's scores while the
     // MFMAs of tile j + 1's scores run, then takes tile j + 1's maximum while
     // tile j's PV MFMAs run, each chunk written out in issue order so a
@@ -1129,11 +1137,11 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
       auto vread = [&](int par, int k) {
         return *reinterpret_cast<const V8*>(vp[k & 3] + TB * par + 4096 * (k >> 2));
       };
-      // Copy c of iteration jj: c < 4 the V pieces of step jj + 1, else the K
-      // pieces of step jj + 2.
+      // Copy c (of 4 NK) of iteration jj: c < 2 NK the V pieces of step jj +
+      // 1, else the K pieces of step jj + 2.
       auto copy = [&](int jj, int c) {
-        const int t = c < 4 ? G * (jj + 1) + c / 2 : G * (jj + 2) + (c - 4) / 2;
-        copy_piece(t, c < 4 ? 2 + c % 2 : c % 2);
+        const int t = c < 2 * NK ? G * (jj + 1) + c / NK : G * (jj + 2) + (c - 2 * NK) / NK;
+        copy_piece(t, c < 2 * NK ? NK + c % NK : c % NK);
       };
       auto mask = [&](int jj, f32x16 (&s)[2]) {
         const int tl = G * jj + gi;
@@ -1195,7 +1203,12 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
             // An empty asm consuming the pair keeps it here: otherwise it is
             // sunk past the mask's branch to the PV MFMAs.
             asm("" : "+v"(ph[qb][h]));
-            if (k & 1) copy(jj, (4 + (k >> 1)) & 7);
+            // The K pieces first (needed first), 4 NK copies over the 16 chunks.
+            if constexpr (NK == 2) {
+              if (k & 1) copy(jj, (4 + (k >> 1)) & 7);
+            } else {
+              copy(jj, (8 + k) & 15);
+            }
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -1240,7 +1253,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
           o[k >> 2] = Op32<MODE>::mfma(vread(P, k), ph[c >> 1][c & 1], o[k >> 2]);
         }
       };
-      wait_vmcnt<4 * G>();  // the V planes of step 0 and K planes of step 1 may still fly
+      wait_vmcnt<2 * G * NK>();  // the V planes of step 0 and K planes of step 1 may still fly
       __syncthreads();
       f32x16 sA[2], sB[2];
 #pragma unroll
@@ -1509,12 +1522,20 @@ struct P32Args {
   float* out;
   TimedPair tp;
 };
-template <int MODE>
-void launch_p32(const P32Args& a, hipStream_t s) {
+template <int MODE, int W>
+void launch_p32_w(const P32Args& a, hipStream_t s) {
   const unsigned blocks = (unsigned)(8 * a.per_xcd * a.kv_splits);
-  launch_timed(a.tp, prefill32_kernel<MODE, kP32Waves, kP32Groups>, dim3(blocks), dim3(64 * kP32Waves), s, a.q,
-               a.stage, a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.per_xcd,
-               a.kv_splits, a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.qprep, a.part, a.part_bytes, a.tickets, a.out);
+  launch_timed(a.tp, prefill32_kernel<MODE, W, kP32Groups>, dim3(blocks), dim3(64 * W), s, a.q, a.stage,
+               a.n_stage_tiles, a.q_stride, a.rows, a.start, a.group, a.n_rb, a.n_units, a.per_xcd, a.kv_splits,
+               a.qscale, a.qn_w, a.qn_eps, a.qn_tab, a.qprep, a.part, a.part_bytes, a.tickets, a.out);
+}
+// 128-column units on 8 waves, 64-column units on 4.
+template <int MODE>
+void launch_p32(int vectors, const P32Args& a, hipStream_t s) {
+  if (vectors == 64)
+    launch_p32_w<MODE, 4>(a, s);
+  else
+    launch_p32_w<MODE, kP32Waves>(a, s);
 }
 
 // Stage tiles [lo, hi) of every kv head of `layer` (positions at or past
@@ -1548,13 +1569,27 @@ void launch_stage(const rv_kv* kv, size_t layer, uint32_t mode, size_t positions
 
 }  // namespace
 
-size_t qprep_bytes(size_t rows, size_t n_kv_heads, size_t group) {
-  const size_t qr = kQPrepVectors / group;
-  return n_kv_heads * ((rows + qr - 1) / qr) * kQPrepVectors * kD * 2;
+size_t qprep_bytes(size_t rows, size_t n_kv_heads, size_t group, int vectors) {
+  const size_t qr = vectors / group;
+  return n_kv_heads * ((rows + qr - 1) / qr) * vectors * kD * 2;
 }
-QPrep qprep_plan(char* base, size_t rows, size_t group, float scale) {
-  const int qr = kQPrepVectors / (int)group;
-  return QPrep{base, (int)group, qr, (int)((rows + qr - 1) / qr), scale * kLog2e};
+QPrep qprep_plan(char* base, size_t rows, size_t group, float scale, int vectors) {
+  const int qr = vectors / (int)group;
+  return QPrep{base, (int)group, qr, (int)((rows + qr - 1) / qr), scale * kLog2e, vectors};
+}
+// 64-column units (4 waves, one per SIMD) where 128-column units would leave
+// CUs idle and take no KV split (a short chunk on a short cache: config 3's
+// 128 units become 256 workgroups and its longest unit's steps run on one
+// wave per SIMD instead of two); 128 otherwise.
+int prefill_vectors(const rv_kv* kv, size_t rows, size_t start, size_t group) {
+  if (group == 0 || 64 % group) return kQPrepVectors;
+  const long units = (long)kv->n_kv_heads * (long)((rows + kQPrepVectors / group - 1) / (kQPrepVectors / group));
+  const int n_stage_tiles = (int)((start + rows + kBT - 1) / kBT);
+  int kv_splits = (int)kv->tune_prefill_kv_split;
+  if (kv_splits <= 0)
+    kv_splits = (int)std::min<long>((kCUs + units - 1) / units, std::max(1, n_stage_tiles / (4 * kP32Groups)));
+  if (!kv->xcd_ok) kv_splits = 1;
+  return kv_splits <= 1 && units * 2 <= kCUs ? 64 : kQPrepVectors;
 }
 
 namespace {
@@ -1633,7 +1668,7 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
     // across workgroups until about kCUs of them run, each split keeping at
     // least 4 tiles of the longest block per wave group, and only where the
     // XCD fold is available.
-    vectors = kQPrepVectors;
+    vectors = prefill_vectors(kv, rows, start, group);
     const int qr = vectors / group;
     n_rb = (int)((rows + qr - 1) / qr);
     const long units = (long)n_rb * n_kv;
@@ -1710,9 +1745,9 @@ HipStatus launch_prefill(rv_kv* kv, const float* q_rows, size_t rows, size_t n_q
                     (uint32_t)std::min<size_t>(part_bytes, 0xFFFFFFF0u),
                     kv->pf_tickets, out, tp};
     if (m == RV_PREFILL_BF16)
-      launch_p32<kBF16>(a, s);
+      launch_p32<kBF16>(vectors, a, s);
     else
-      launch_p32<kF16>(a, s);
+      launch_p32<kF16>(vectors, a, s);
   } else {
     PrefillArgs a{q_rows, stage, tile_stride, (int)(n_q_heads * kD), (int)rows,
                   (int)start, group, n_rb, n_kv * n_rb * kv_splits, kv_splits, scale * kLog2e,

@@ -171,7 +171,7 @@ __device__ __forceinline__ void prep_q_block(int qw, bool live, const float* __r
   typedef typename Op<SM>::E E;
   typedef typename Op<SM>::V8 V8;
   typedef E E4 __attribute__((ext_vector_type(4)));
-  constexpr int VG = kQPrepVectors / 32;
+  const int VG = qp.vectors / 32;
   const int u = qw / VG, wv = qw % VG;
   const int kvh = u / qp.n_rb, rb = u % qp.n_rb;
   const int hl = lane >> 5, dl = lane & 31;  // column parity of a load, d = 4 dl .. 4 dl + 3
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kPrologueWaves * 64) void row_prologue_kernel(const
   if constexpr (SM >= 0) {
     __shared__ __attribute__((aligned(16))) uint16_t qlds[32 * 128];
     if (qp.base) {
-      const int q_groups = n_kv * qp.n_rb * (kQPrepVectors / 32);  // 32-column groups, one workgroup each
+      const int q_groups = n_kv * qp.n_rb * (qp.vectors / 32);  // 32-column groups, one workgroup each
       const int qy = (q_groups + (int)gridDim.x - 1) / (int)gridDim.x;
       if (by < qy) {
         const int qw = by * (int)gridDim.x + r;
@@ -528,7 +528,7 @@ HipStatus launch_row_prologue(const rv_kv* kv, size_t layer, size_t cache_row, c
   if (staging) {
     slot_blocks = (2 * n_kv + kPrologueWaves - 1) / kPrologueWaves;  // a wave per k head, then per v head
     if (prep) {
-      const size_t q_groups = (size_t)n_kv * qp->n_rb * (kQPrepVectors / 32);
+      const size_t q_groups = (size_t)n_kv * qp->n_rb * (qp->vectors / 32);
       slot_blocks += (int)((q_groups + grid_rows - 1) / grid_rows);
     }
   }

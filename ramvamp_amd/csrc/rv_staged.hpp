@@ -202,8 +202,8 @@ struct Q32Loads {
 // each query head's row after RMSNorm and RoPE, times log2(e) * scale,
 // rounded to the MFMA type, straight into the attention kernel's operand
 // order, so that kernel's query loads are eight coalesced 16-byte loads per
-// lane. The kernel's units (kv head * n_rb + rb) hold V = kQPrepVectors
-// columns each: column m of unit u is query head kv head * group + m / qr of
+// lane. The kernel's units (kv head * n_rb + rb) hold V = 128 (kQPrepVectors)
+// or 64 columns each (prefill_vectors): column m of unit u is query head kv head * group + m / qr of
 // row rb * qr + m % qr (qr = V / group), global column c = u * V + m. Element d
 // of column c sits in 16-byte chunk ((c / 32) * 8 + d / 16) * 64 + 32 * ((d /
 // 8) & 1) + c % 32 at position d % 8: the B operand (Q^T) of the QK step
