@@ -1073,19 +1073,14 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
     lds_dma16s(srcw + (size_t)min(t, n - 1) * TB + 1024 * W * i, voff,
                lds_offset(&lds[stage_of(t)][1024 * (w + W * i)]));
   };
-  // Tiles 0 and 1 whole, then the K planes of tiles 2 and 3. A split with no
+  // The K planes of tiles 0 and 1 (the first scores need only them); the V
+  // planes of tiles 0 and 1 and the K planes of tiles 2 and 3 are issued
+  // among the first score MFMAs (issued here, their copies held each wave
+  // in the prologue while the memory pipeline was full). A split with no
   // tiles (more splits than the unit has tiles) copies nothing.
   if (n > 0) {
 #pragma unroll
     for (int t = 0; t < G; ++t)
-#pragma unroll
-      for (int i = 0; i < NK; ++i) copy_piece(t, i);
-#pragma unroll
-    for (int t = 0; t < G; ++t)
-#pragma unroll
-      for (int i = NK; i < 2 * NK; ++i) copy_piece(t, i);
-#pragma unroll
-    for (int t = G; t < 2 * G; ++t)
 #pragma unroll
       for (int i = 0; i < NK; ++i) copy_piece(t, i);
   }
@@ -1255,7 +1250,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
           o[k >> 2] = Op32<MODE>::mfma(vread(P, k), ph[c >> 1][c & 1], o[k >> 2]);
         }
       };
-      wait_vmcnt<2 * G * NK>();  // the V planes of step 0 and K planes of step 1 may still fly
+      wait_vmcnt<0>();  // the queries and step 0's K planes
       __syncthreads();
       f32x16 sA[2], sB[2];
 #pragma unroll
@@ -1263,7 +1258,15 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
 #pragma unroll
         for (int r = 0; r < 16; ++r) sA[pb][r] = negm;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) sA[pb] = Op32<MODE>::mfma(kread(0, 8 * pb + ks), qv[ks], sA[pb]);
+        for (int ks = 0; ks < 8; ++ks) {
+          sA[pb] = Op32<MODE>::mfma(kread(0, 8 * pb + ks), qv[ks], sA[pb]);
+          // Copy c: c < 2 NK the V planes of step 0, then the K planes of step 1.
+          const int c = 8 * pb + ks;
+          if (c < 2 * NK)
+            copy_piece(c / NK, NK + c % NK);
+          else if (c < 4 * NK)
+            copy_piece(G + (c - 2 * NK) / NK, (c - 2 * NK) % NK);
+        }
       }
       mask(0, sA);
       {
