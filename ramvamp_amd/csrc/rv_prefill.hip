@@ -1198,11 +1198,13 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
             // An empty asm consuming the pair keeps it here: otherwise it is
             // sunk past the mask's branch to the PV MFMAs.
             asm("" : "+v"(ph[qb][h]));
-            // The K pieces first (needed first), 4 NK copies over the 16 chunks.
+            // The K pieces first (needed first), 4 NK copies over the 16 chunks;
+            // with 4 waves (one per SIMD) the V pieces go to the PV half,
+            // which has room for them (config 3: 10.46 -> 10.28 us).
             if constexpr (NK == 2) {
               if (k & 1) copy(jj, (4 + (k >> 1)) & 7);
             } else {
-              copy(jj, (8 + k) & 15);
+              if (k < 8) copy(jj, 8 + k);
             }
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -1223,6 +1225,9 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
             if (k + 4 < 16) va[c] = vread(P, k + 4);
             mx = max3f(mx, sn[k >> 3][2 * (k & 7)], sn[k >> 3][2 * (k & 7) + 1]);
             l_run = sum2(ph[k >> 3][(k >> 2) & 1], 2 * (k & 3), l_run);
+            if constexpr (NK == 4) {
+              if (k < 8) copy(jj, k);  // step jj + 1's V pieces
+            }
             // Fenced every two MFMAs (every one measured 0.4 us slower at
             // config 4: the scheduler places the pair's VALU better).
             if (k & 1) __builtin_amdgcn_sched_barrier(0);
