@@ -837,15 +837,25 @@ __global__ __launch_bounds__(G * W * 64) void prefill_kernel(const float* __rest
   }
 
   if (kv_splits == 1) {
+    // Non-temporal stores: nothing reads the output in this launch, and
+    // lines already on their way out leave less for the end-of-kernel
+    // write-back (config 3: 19.0 -> 18.6 us).
+    const bool vec = aligned16(out) && q_stride % 4 == 0;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       if (!col_ok[mt]) continue;
       const float inv = 1.0f / l_run[mt];
-      float* op = out + (size_t)my_row[mt] * q_stride + (size_t)(kvh * group + my_head[mt]) * kD;
+      float* op = out + (size_t)my_row[mt] * q_stride + (size_t)(kvh * group + my_head[mt]) * kD + 4 * kk;
 #pragma unroll
-      for (int b = 0; b < 8; ++b)
+      for (int b = 0; b < 8; ++b) {
+        const f32x4 y = o[mt][b] * inv;
+        if (vec) {
+          __builtin_nontemporal_store(y, reinterpret_cast<f32x4*>(op + 16 * b));
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) op[16 * b + 4 * kk + e] = o[mt][b][e] * inv;
+          for (int e = 0; e < 4; ++e) __builtin_nontemporal_store(y[e], op + 16 * b + e);
+        }
+      }
     }
     return;
   }
@@ -1305,7 +1315,7 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
   // 32 lanes of one chunk hit distinct banks); after a barrier, flush() has
   // every wave of the workgroup read whole rows back (group gi takes half the
   // rows of region wv), 512 contiguous bytes per half-wave, and store each
-  // column's row of out with 16-byte stores.
+  // column's row of out with 16-byte non-temporal stores.
   static_assert(G == 2, "the two groups share the epilogue by halves");
   float* const obuf = reinterpret_cast<float*>(&lds[0][0]) + (size_t)wv * 32 * kD;
   auto put = [&](int db, const f32x16& v, float inv) {
@@ -1330,10 +1340,10 @@ __global__ __launch_bounds__(64 * W) void prefill32_kernel(const float* __restri
       if (mm % qr >= rows_here) continue;
       float* op = out + (size_t)(r0 + mm % qr) * q_stride + (size_t)(kvh * group + mm / qr) * kD + 4 * lc;
       if (vec) {
-        *reinterpret_cast<f32x4*>(op) = x[it];
+        __builtin_nontemporal_store(x[it], reinterpret_cast<f32x4*>(op));
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) op[e] = x[it][e];
+        for (int e = 0; e < 4; ++e) __builtin_nontemporal_store(x[it][e], op + e);
       }
     }
   };
@@ -1475,13 +1485,21 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
 #pragma unroll
     for (int h = 0; h < 2; ++h) O[h] += o[sp][h] * w;
   }
-  // The caller's rows may be only 4-byte aligned: scalar stores.
+  // Non-temporal 16-byte stores where the caller's rows allow (they may be
+  // only 4-byte aligned).
   float* op = out + (size_t)row * q_stride + (size_t)(kvh * group + head) * kD + 4 * kk;
   const float inv = 1.0f / L;
+  const bool vec = aligned16(out) && q_stride % 4 == 0;
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int h = 0; h < 2; ++h) {
+    const f32x4 y = O[h] * inv;
+    if (vec) {
+      __builtin_nontemporal_store(y, reinterpret_cast<f32x4*>(op + 16 * (b0 + 4 * h)));
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) op[16 * (b0 + 4 * h) + e] = O[h][e] * inv;
+      for (int e = 0; e < 4; ++e) __builtin_nontemporal_store(y[e], op + 16 * (b0 + 4 * h) + e);
+    }
+  }
 }
 
 struct PrefillArgs {
